@@ -1,0 +1,111 @@
+"""ctypes binding of libevo2_hyena.so, the C ABI declared in include/evo2_hyena.h.
+
+The library is loaded after torch so that its HIP runtime dependency
+(soname libamdhip64.so.7) resolves to the runtime torch already mapped: a
+`hipStream_t` taken from torch is then valid inside the library.  There is no
+fallback: if the library is missing or fails to load, every operator raises.
+"""
+
+import ctypes
+import os
+import threading
+
+import torch  # noqa: F401  (must precede the library load, see above)
+
+from .build import LIB_PATH
+
+_c_i64 = ctypes.c_int64
+_c_i32 = ctypes.c_int32
+_c_p = ctypes.c_void_p
+_c_f = ctypes.c_float
+
+# name -> argtypes, in the order of include/evo2_hyena.h
+SIGNATURES = {
+    "evo2_last_error": [],
+    "evo2_abi_version": [],
+    "evo2_hyena_decode": [
+        _c_p, _c_i64, _c_p,                       # z, sz, short_w
+        _c_p, _c_i64, _c_i64, _c_i64,             # conv_state + strides
+        _c_p, _c_i64,                             # slots, ssl
+        _c_p, _c_i64, _c_i64,                     # inner + strides
+        _c_p, _c_i64, _c_i64,                     # log_poles + strides
+        _c_p, _c_i64, _c_i64, _c_i64,             # inner_state + strides
+        _c_p, _c_p, _c_i64,                       # D, out, so
+        _c_i64, _c_i64, _c_i32, _c_i32,           # B, H, K, is_iir
+        _c_i32, _c_i64, _c_p,                     # null_block, num_blocks, stream
+    ],
+}
+
+RESTYPES = {"evo2_last_error": ctypes.c_char_p}
+
+_lock = threading.Lock()
+_lib = None
+
+
+class Evo2Error(RuntimeError):
+    """A nonzero status from the C ABI."""
+
+    def __init__(self, fn, code, msg):
+        super().__init__(f"{fn} failed (code {code}): {msg}")
+        self.code = code
+
+
+def _hip_runtimes_mapped():
+    try:
+        with open("/proc/self/maps") as f:
+            return {line.split()[-1] for line in f if "libamdhip64" in line}
+    except OSError:
+        return set()
+
+
+def lib():
+    """The loaded library (loaded on first use).  Raises if it is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is not built; run `python -m evo2_flash_amd.build` "
+                "(or __graft_entry__.build()) first")
+        handle = ctypes.CDLL(LIB_PATH, mode=ctypes.RTLD_LOCAL)
+        for name, argtypes in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.argtypes = argtypes
+            fn.restype = RESTYPES.get(name, ctypes.c_int)
+        runtimes = _hip_runtimes_mapped()
+        if len(runtimes) > 1:
+            raise RuntimeError(f"more than one HIP runtime is mapped: {sorted(runtimes)}")
+        _lib = handle
+        return _lib
+
+
+def call(name, *args):
+    """Call a C-ABI entry point; raise Evo2Error on a nonzero status."""
+    l = lib()
+    rc = getattr(l, name)(*args)
+    if rc != 0:
+        msg = l.evo2_last_error().decode(errors="replace")
+        raise Evo2Error(name, rc, msg)
+
+
+def ptr(t):
+    """Device pointer of a tensor (None for None)."""
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def stream_of(t=None):
+    """The current torch stream on t's device, as a void* for the C ABI."""
+    dev = t.device if t is not None else None
+    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def require_device(*tensors):
+    """The HIP path runs on ROCm devices only: raise for CPU tensors."""
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError(
+                "evo2_flash_amd operators run on the GPU only (got a CPU tensor); "
+                "there is no CPU fallback")

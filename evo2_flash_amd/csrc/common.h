@@ -1,0 +1,48 @@
+// Shared helpers for the gfx950 Hyena kernels: bf16 rounding, error reporting,
+// launch checking.  Included by every .hip translation unit of the library.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/evo2_hyena.h"
+
+namespace evo2 {
+
+// ---------------------------------------------------------------- bf16 / fp32
+typedef uint16_t bf16_t;  // raw bfloat16 bits in memory
+
+__device__ __forceinline__ float bf2f(bf16_t b) {
+  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+
+// fp32 -> bf16 with round-to-nearest-even (hardware v_cvt_pk_bf16_f32), the
+// rounding torch applies when an op writes a bf16 tensor.
+__device__ __forceinline__ bf16_t f2bf(float x) {
+  return __builtin_bit_cast(bf16_t, static_cast<__bf16>(x));
+}
+
+// Round fp32 to bf16 and back: the value a bf16 torch tensor would hold.
+__device__ __forceinline__ float rbf(float x) { return bf2f(f2bf(x)); }
+
+__device__ __forceinline__ float lo_bf(uint32_t packed) {
+  return __uint_as_float(packed << 16);
+}
+__device__ __forceinline__ float hi_bf(uint32_t packed) {
+  return __uint_as_float(packed & 0xffff0000u);
+}
+__device__ __forceinline__ uint32_t pack_bf(float lo, float hi) {
+  return static_cast<uint32_t>(f2bf(lo)) | (static_cast<uint32_t>(f2bf(hi)) << 16);
+}
+
+// ---------------------------------------------------------------- host side
+void set_error(const char *fmt, ...);
+int fail(int code, const char *fmt, ...);
+
+// Checks the launch that was just enqueued; EVO2_ERR_LAUNCH with the runtime's
+// message on failure.
+int check_launch(const char *what);
+
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace evo2

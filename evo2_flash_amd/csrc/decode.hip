@@ -1,0 +1,243 @@
+// Fused single-token Hyena decode step for gfx950.
+//
+// One thread per (row b, channel h).  Lanes run along channels, so every
+// state column, z triple and output row is read and written as one coalesced
+// sweep across the wavefront; the hcm window shift is a column-by-column
+// read / write-one-column-lower pass over the channel-contiguous native
+// layout.  Each state element is read and written by exactly one thread, so
+// the in-place update needs no barrier: within a thread, every load of a
+// column precedes the store that overwrites it in program order.
+//
+// Rounding points follow evo2_flash/triton_decode.py:10-22, 44-53, 57-164:
+// fp32 products are rounded separately from the sums (no FMA contraction in
+// this file), reductions use the same association trees, and every value a
+// bf16 torch tensor would hold is rounded to bf16.
+#include "common.h"
+
+#pragma clang fp contract(off)
+
+namespace evo2 {
+
+enum { KIND_HCS = 0, KIND_HCM = 1, KIND_HCL = 2 };
+
+struct DecodeArgs {
+  const bf16_t *z; int64_t sz;
+  const bf16_t *ws;
+  bf16_t *cs; int64_t cs0, cs1, cs2;
+  const int32_t *slots; int64_t ssl;
+  const void *inner; int64_t wi0, wi1;
+  const float *lp; int64_t lp0, lp1;
+  float *st; int64_t is0, is1, is2;
+  const bf16_t *D;
+  bf16_t *out; int64_t so;
+  int H;
+  int null_block;
+  int64_t num_blocks;
+};
+
+// vLLM's K=3 conv update for one channel (triton_decode.py:44-53):
+// bf16(((0 + bf16(c0 w0)) + bf16(c1 w1)) + bf16(x w2)).
+__device__ __forceinline__ float short_tap(float x, float c0, float c1, const bf16_t *w) {
+  float acc = 0.0f + rbf(c0 * bf2f(w[0]));
+  acc = acc + rbf(c1 * bf2f(w[1]));
+  acc = acc + rbf(x * bf2f(w[2]));
+  return rbf(acc);
+}
+
+template <int KIND, bool HAS_D, bool CONTIG_S>
+__global__ __launch_bounds__(256) void hyena_decode_kernel(DecodeArgs a) {
+  const int h = blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t b = blockIdx.y;
+  if (h >= a.H) return;
+  const int64_t blk = a.slots[b * a.ssl];
+  bf16_t *o = a.out + b * a.so + h;
+  // The null block (CUDA/HIP-graph padding rows) and any slot outside the
+  // pool produce a zero row and touch no state.
+  if (blk == a.null_block || blk < 0 || blk >= a.num_blocks) {
+    *o = 0;
+    return;
+  }
+
+  // ---- short filter on the interleaved triple (3h, 3h+1, 3h+2) = (x2, x1, v)
+  const bf16_t *zr = a.z + b * a.sz + 3 * (int64_t)h;
+  bf16_t *c = a.cs + blk * a.cs0 + 3 * (int64_t)h * a.cs1;
+  bf16_t keep_c1[3], keep_x[3];
+  float y3[3];
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    const bf16_t xb = zr[i];
+    const bf16_t c0b = c[i * a.cs1];
+    const bf16_t c1b = c[i * a.cs1 + a.cs2];
+    y3[i] = short_tap(bf2f(xb), bf2f(c0b), bf2f(c1b), a.ws + (3 * (int64_t)h + i) * 3);
+    keep_c1[i] = c1b;
+    keep_x[i] = xb;
+  }
+  const float x2 = y3[0];
+  const float u = rbf(y3[1] * y3[2]);
+  float y;
+
+  float *s = a.st + blk * a.is0 + (int64_t)h * a.is1;
+  if constexpr (KIND == KIND_HCL) {
+    // s <- s * exp(lp) + u; readout halving tree (triton_decode.py:81-96).
+    const float *res = static_cast<const float *>(a.inner) + (int64_t)h * a.wi0;
+    const float *lp = a.lp + (int64_t)h * a.lp0;
+    float sv[16], r[16];
+    if constexpr (CONTIG_S) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float4 v = reinterpret_cast<const float4 *>(s)[q];
+        sv[4 * q] = v.x; sv[4 * q + 1] = v.y; sv[4 * q + 2] = v.z; sv[4 * q + 3] = v.w;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) sv[i] = s[i * a.is2];
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float p = expf(lp[i * a.lp1]);
+      sv[i] = sv[i] * p + u;
+      r[i] = sv[i] * res[i * a.wi1];
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r[i] = r[i] + r[i + 8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r[i] = r[i] + r[i + 4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) r[i] = r[i] + r[i + 2];
+    y = rbf((r[0] + r[1]) + 0.0f);
+    if constexpr (CONTIG_S) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        reinterpret_cast<float4 *>(s)[q] =
+            make_float4(sv[4 * q], sv[4 * q + 1], sv[4 * q + 2], sv[4 * q + 3]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s[i * a.is2] = sv[i];
+    }
+  } else if constexpr (KIND == KIND_HCM) {
+    // Taps k = 16j + 4m + l: accumulator (m, l) sums j = 0..7 in order, then
+    // ((m0 + m1) + m2) + m3 per l, then (l0 + l2) + (l1 + l3)
+    // (triton_decode.py:97-124).  The window shifts down one column in place.
+    const bf16_t *w = static_cast<const bf16_t *>(a.inner) + (int64_t)h * a.wi0;
+    float acc[4][4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+      for (int l = 0; l < 4; ++l) acc[m][l] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float sv[16];
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        const int k = 16 * j + q;
+        sv[q] = (k < 127) ? s[k * a.is2] : 0.0f;
+      }
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        const int k = 16 * j + q;
+        const float wk = (k < 127) ? bf2f(w[k * a.wi1]) : 0.0f;
+        acc[q >> 2][q & 3] = acc[q >> 2][q & 3] + sv[q] * wk;
+      }
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        const int k = 16 * j + q;
+        if (k >= 1 && k < 127) s[(k - 1) * a.is2] = sv[q];
+      }
+    }
+    float p[4];
+#pragma unroll
+    for (int l = 0; l < 4; ++l) p[l] = ((acc[0][l] + acc[1][l]) + acc[2][l]) + acc[3][l];
+    const float last = bf2f(w[127 * a.wi1]);
+    y = rbf(((p[0] + p[2]) + (p[1] + p[3])) + last * u);
+    s[126 * a.is2] = u;
+  } else {
+    // K = 7: ((((s0w0 + s4w4) + (s1w1 + s5w5)) + s2w2) + s3w3) + w6 u
+    // (triton_decode.py:125-150).
+    const bf16_t *w = static_cast<const bf16_t *>(a.inner) + (int64_t)h * a.wi0;
+    float sv[6];
+#pragma unroll
+    for (int k = 0; k < 6; ++k) sv[k] = s[k * a.is2];
+    const float aa = (sv[0] * bf2f(w[0]) + 0.0f) + sv[4] * bf2f(w[4 * a.wi1]);
+    const float bb = (sv[1] * bf2f(w[a.wi1]) + 0.0f) + sv[5] * bf2f(w[5 * a.wi1]);
+    const float cc = sv[2] * bf2f(w[2 * a.wi1]) + 0.0f;
+    const float dd = sv[3] * bf2f(w[3 * a.wi1]) + 0.0f;
+    const float last = bf2f(w[6 * a.wi1]);
+    y = rbf((((aa + bb) + cc) + dd) + last * u);
+#pragma unroll
+    for (int k = 0; k < 5; ++k) s[k * a.is2] = sv[k + 1];
+    s[5 * a.is2] = u;
+  }
+
+  // Short-filter window (c0, c1) <- (c1, x).
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    c[i * a.cs1] = keep_c1[i];
+    c[i * a.cs1 + a.cs2] = keep_x[i];
+  }
+
+  if constexpr (HAS_D) y = rbf(y + rbf(bf2f(a.D[h]) * u));
+  *o = f2bf(x2 * y);
+}
+
+template <int KIND, bool HAS_D, bool CONTIG_S>
+static void launch(const DecodeArgs &a, int64_t B, hipStream_t stream) {
+  constexpr int BH = 256;
+  dim3 grid(static_cast<unsigned>(cdiv(a.H, BH)), static_cast<unsigned>(B));
+  hipLaunchKernelGGL((hyena_decode_kernel<KIND, HAS_D, CONTIG_S>), grid, dim3(BH), 0, stream, a);
+}
+
+}  // namespace evo2
+
+using namespace evo2;
+
+extern "C" int evo2_hyena_decode(const void *z, int64_t sz, const void *short_w,
+                                 void *conv_state, int64_t cs0, int64_t cs1, int64_t cs2,
+                                 const int32_t *slots, int64_t ssl,
+                                 const void *inner, int64_t wi0, int64_t wi1,
+                                 const float *log_poles, int64_t lp0, int64_t lp1,
+                                 float *inner_state, int64_t is0, int64_t is1, int64_t is2,
+                                 const void *D, void *out, int64_t so,
+                                 int64_t B, int64_t H, int32_t K, int32_t is_iir,
+                                 int32_t null_block, int64_t num_blocks, void *stream) {
+  if (B < 0 || H <= 0 || H > (1 << 30) || num_blocks <= 0)
+    return fail(EVO2_ERR_INVALID, "hyena_decode: bad sizes B=%lld H=%lld blocks=%lld",
+                (long long)B, (long long)H, (long long)num_blocks);
+  if (B == 0) return EVO2_OK;
+  if (B > 65535)
+    return fail(EVO2_ERR_UNSUPPORTED, "hyena_decode: B=%lld exceeds 65535 rows", (long long)B);
+  if (!z || !short_w || !conv_state || !slots || !inner || !inner_state || !out)
+    return fail(EVO2_ERR_INVALID, "hyena_decode: null pointer argument");
+  int kind;
+  if (is_iir) {
+    if (K != 16 || !log_poles)
+      return fail(EVO2_ERR_INVALID, "hyena_decode: LI needs 16 poles and log_poles (K=%d)", K);
+    kind = KIND_HCL;
+  } else if (K == 7) {
+    kind = KIND_HCS;
+  } else if (K == 128) {
+    kind = KIND_HCM;
+  } else {
+    return fail(EVO2_ERR_UNSUPPORTED, "hyena_decode: inner FIR length %d (7 or 128 only)", K);
+  }
+  DecodeArgs a{static_cast<const bf16_t *>(z), sz, static_cast<const bf16_t *>(short_w),
+               static_cast<bf16_t *>(conv_state), cs0, cs1, cs2, slots, ssl,
+               inner, wi0, wi1, log_poles, lp0, lp1, inner_state, is0, is1, is2,
+               static_cast<const bf16_t *>(D), static_cast<bf16_t *>(out), so,
+               static_cast<int>(H), null_block, num_blocks};
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool hasD = D != nullptr;
+  if (kind == KIND_HCL) {
+    const bool contig = is2 == 1 && (is1 % 4) == 0 && (is0 % 4) == 0 &&
+                        (reinterpret_cast<uintptr_t>(inner_state) % 16) == 0;
+    if (hasD) {
+      contig ? launch<KIND_HCL, true, true>(a, B, st) : launch<KIND_HCL, true, false>(a, B, st);
+    } else {
+      contig ? launch<KIND_HCL, false, true>(a, B, st) : launch<KIND_HCL, false, false>(a, B, st);
+    }
+  } else if (kind == KIND_HCM) {
+    hasD ? launch<KIND_HCM, true, false>(a, B, st) : launch<KIND_HCM, false, false>(a, B, st);
+  } else {
+    hasD ? launch<KIND_HCS, true, false>(a, B, st) : launch<KIND_HCS, false, false>(a, B, st);
+  }
+  return check_launch("hyena_decode");
+}

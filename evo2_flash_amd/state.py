@@ -1,0 +1,91 @@
+"""Paged Hyena state: the unified three-slice spec and a block pool laid out
+the way vLLM lays out a mamba layer's cache.
+
+Every Hyena layer declares one spec (mixers.py:870-917, model.py:277-333):
+  slice 0  conv state   native (blocks, K_short-1, 3H) bf16 -> view (blocks, 3H, 2)
+  slice 1  inner FIR    native (blocks, K_max-1, H) fp32    -> view (blocks, H, 127)
+  slice 2  LI state     (blocks, H, 16) fp32, not transposed
+The three slices of a block share one padded page, so each slice's block
+stride is the page size in that slice's element type, not its own size.
+Views are oldest-first windows; block 0 is the null block.
+"""
+
+import torch
+
+NULL_BLOCK = 0
+
+
+def unified_state_shape(hidden, k_short=3, k_inner_max=128, state_size=16):
+    """Native shapes per block: ((K_short-1, 3H), (K_max-1, H), (H, S)).
+
+    The first two are vLLM's (state_len, dim) conv layout, normalised to
+    (dim, state_len) by `conv_view` (mixers.py:858-868, 940-949).
+    """
+    return ((k_short - 1, 3 * hidden), (k_inner_max - 1, hidden), (hidden, state_size))
+
+
+def unified_state_dtype(model_dtype=torch.bfloat16):
+    """(model dtype, fp32, fp32) (mixers.py:908-910)."""
+    return (model_dtype, torch.float32, torch.float32)
+
+
+def page_bytes(hidden, k_short=3, k_inner_max=128, state_size=16, align=256):
+    shapes = unified_state_shape(hidden, k_short, k_inner_max, state_size)
+    dtypes = unified_state_dtype()
+    total = 0
+    for shp, dt in zip(shapes, dtypes):
+        n = 1
+        for d in shp:
+            n *= d
+        total += n * torch.tensor([], dtype=dt).element_size()
+    return (total + align - 1) // align * align
+
+
+class HyenaStatePool:
+    """One layer's state pool: a (blocks, page) byte buffer carved into three
+    strided slices, like vLLM's mamba KV cache for a layer.
+
+    `kv_cache` is the engine-facing 3-tuple of native-layout views;
+    `conv_view`, `inner_view` and `ssm_view` are the normalised dim-first
+    views the operators take.
+    """
+
+    def __init__(self, num_blocks, hidden, device, k_short=3, k_inner_max=128,
+                 state_size=16, page_align=256, dtype=torch.bfloat16):
+        self.num_blocks = num_blocks
+        self.hidden = hidden
+        shapes = unified_state_shape(hidden, k_short, k_inner_max, state_size)
+        dtypes = unified_state_dtype(dtype)
+        self.page = page_bytes(hidden, k_short, k_inner_max, state_size, page_align)
+        self.raw = torch.zeros(num_blocks, self.page, dtype=torch.uint8, device=device)
+        views, off = [], 0
+        for shp, dt in zip(shapes, dtypes):
+            es = torch.tensor([], dtype=dt).element_size()
+            assert off % es == 0 and self.page % es == 0
+            flat = self.raw.view(-1).view(dt)
+            inner_strides = []
+            acc = 1
+            for d in reversed(shp):
+                inner_strides.insert(0, acc)
+                acc *= d
+            v = flat.as_strided((num_blocks, *shp), (self.page // es, *inner_strides), off // es)
+            views.append(v)
+            off += acc * es
+        self.kv_cache = tuple(views)
+
+    def conv_view(self):
+        """(blocks, 3H, K_short-1) bf16, dim-first (mixers.py:940-949)."""
+        return self.kv_cache[0].transpose(-1, -2)
+
+    def inner_view(self, width=None):
+        """(blocks, H, K_max-1) fp32, or its leading `width` columns."""
+        v = self.kv_cache[1].transpose(-1, -2)
+        return v if width is None else v[..., :width]
+
+    def ssm_view(self):
+        """(blocks, H, 16) fp32 (mixers.py:1334-1342)."""
+        return self.kv_cache[2]
+
+    def zero_(self):
+        self.raw.zero_()
+        return self

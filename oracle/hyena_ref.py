@@ -1,0 +1,347 @@
+"""CPU restatement of evo2_flash's Hyena mixer math (TEST INFRASTRUCTURE ONLY).
+
+Citations are relative to the reference package `evo2_flash/`.  Tensors are
+CPU torch tensors; bf16 values are carried as fp32 holding bf16-representable
+numbers where the reference rounds, via `bf`.
+
+State views follow the reference's normalised, dim-first orientation:
+conv_state (blocks, 3H, 2) bf16, inner FIR state (blocks, H, K-1) fp32,
+LI state (blocks, H, 16) fp32 (mixers.py:892-917, 940-949).
+"""
+
+import torch
+import torch.nn.functional as F
+
+__all__ = [
+    "bf", "depthwise_prefill", "hcl_compute_filter", "iir_segment",
+    "fir_mixer_prefill", "iir_mixer_prefill", "fir_decode_one", "iir_decode_one",
+    "short_conv_update", "hyena_decode_emulated", "mixer_decode_unfused",
+    "rms_norm", "quantize_input", "fp8_linear_dequant", "prefill_tables",
+    "STATE_ACC_BUDGET",
+]
+
+# mixers.py:72-74: bound on the (H, blk, L) temporary of the LI final state.
+STATE_ACC_BUDGET = 64 << 20
+
+
+def bf(x):
+    """Round fp32 to bf16 and back: the value a bf16 torch tensor holds."""
+    return x.to(torch.bfloat16).to(torch.float32)
+
+
+# ------------------------------------------------------------------ prefill
+def depthwise_prefill(x_p, w, qsl, slots, has_init, state, k):
+    """Per-segment depthwise causal conv over packed rows, carrying state.
+
+    Follows `_depthwise_prefill_torch` (mixers.py:350-383), which is also the
+    reference's torch form of the short filter's `causal_conv1d_fn`
+    (`_short_fir_torch`, mixers.py:1210-1212).  `w` (dim, k) is in
+    cross-correlation order: w[:, -1] multiplies the current sample.  The left
+    context is the cached window (has_init) or zeros; the window written back
+    is always the last k-1 inputs of cat(prev, seq), even for a segment
+    shorter than k-1 (mixers.py:380-382).  Empty segments touch nothing.
+
+    x_p: (T, dim); qsl: n+1 segment starts; slots: n state blocks;
+    has_init: n flags; state: (blocks, dim, >=k-1) view, updated in place.
+    Returns (T, dim) in x_p's dtype.
+    """
+    dim = x_p.shape[1]
+    out = torch.empty_like(x_p)
+    wt = w.float().unsqueeze(1)  # (dim, 1, k)
+    for j in range(len(qsl) - 1):
+        a, b = int(qsl[j]), int(qsl[j + 1])
+        if b <= a:
+            continue
+        idx = int(slots[j])
+        seq = x_p[a:b].transpose(0, 1).float()
+        if has_init[j]:
+            prev = state[idx, :, : k - 1].float()
+        else:
+            prev = torch.zeros(dim, k - 1, dtype=torch.float32)
+        seq_in = torch.cat([prev, seq], dim=-1)
+        y = F.conv1d(seq_in.unsqueeze(0), wt, padding=0, groups=dim)
+        out[a:b] = y[0].transpose(0, 1).to(out.dtype)
+        state[idx, :, : k - 1] = seq_in[..., -(k - 1):].to(state.dtype)
+    return out
+
+
+def hcl_compute_filter(residues, log_poles, t):
+    """h[d, l] = sum_s residues[d, s] * exp(log_poles[d, s] * t[l]), fp32.
+
+    The torch form `_compute_filter_torch` (triton_hcl.py:77-85): accumulate
+    over state channels, never materialising (D, S, L).
+    """
+    D, S = residues.shape
+    h = torch.zeros(D, t.shape[0], dtype=torch.float32)
+    for s in range(S):
+        h += residues[:, s:s + 1].float() * torch.exp(log_poles[:, s:s + 1].float() * t.float())
+    return h
+
+
+def iir_segment(seq, res, lp, s_prev):
+    """One prefill segment of s_t = p*s_{t-1} + x_t (mixers.py:144-210).
+
+    seq (H, L) fp32, res/lp (H, S), s_prev (H, S) or None.  Returns
+    (y (H, L), s_last (H, S)).  y is the causal convolution with the modal
+    filter, evaluated by FFT of length 2L (mixers.py:197-202); the final state
+    is the closed form sum_t x_t p^(L-1-t), blocked over state channels to
+    the reference's byte budget (mixers.py:181-195).  A continuation adds
+    p^L s_prev to the state and sum_s res_s s_prev,s p_s^(t+1) to y
+    (mixers.py:204-209).
+    """
+    H, L = seq.shape
+    S = res.shape[1]
+    t = torch.arange(L, dtype=torch.float32)
+    h = hcl_compute_filter(res, lp, t)
+    lag = t.flip(0)
+    blk = min(S, max(1, int(STATE_ACC_BUDGET // max(H * L * 4, 1))))
+    st = torch.empty(H, S, dtype=torch.float32)
+    for s0 in range(0, S, blk):
+        sl = slice(s0, min(s0 + blk, S))
+        st[:, sl] = (seq.unsqueeze(1) * torch.exp(lp[:, sl].unsqueeze(-1) * lag)).sum(-1)
+    n = 2 * L
+    y = torch.fft.irfft(
+        torch.fft.rfft(seq, n=n) * (torch.fft.rfft(h, n=n) / n), n=n, norm="forward"
+    )[..., :L]
+    if s_prev is not None:
+        st = st + torch.exp(lp * L) * s_prev
+        y = y + hcl_compute_filter(res * s_prev, lp, t + 1.0)
+    return y, st
+
+
+def _split(zf):
+    """(x2, x1, v) from the interleaved projection (mixers.py:1206-1208)."""
+    return zf[:, 0::3], zf[:, 1::3], zf[:, 2::3]
+
+
+def fir_mixer_prefill(z_p, short_w, conv_state, w_inner, inner_state, D, qsl, slots,
+                      has_init):
+    """Prefill rows of HyenaFIRMixer between in_proj and out_proj.
+
+    mixers.py:1277-1305 with the torch short filter (mixers.py:1121-1212) and
+    the torch inner FIR (mixers.py:350-383): bf16 z -> short conv (bf16) ->
+    u = x1*v (bf16) -> FIR (bf16) -> [+ D*u] -> g = x2*y, all bf16 ops.
+    inner_state: (blocks, H, >= K-1) fp32 view.  Returns g (T, H) bf16.
+    """
+    k_short = short_w.shape[1]
+    zf = depthwise_prefill(z_p, short_w, qsl, slots, has_init, conv_state, k_short)
+    x2, x1, v = _split(zf)
+    u = x1 * v
+    K = w_inner.shape[1]
+    y = depthwise_prefill(u, w_inner, qsl, slots, has_init, inner_state, K)
+    if D is not None:
+        y = y + D.to(y.dtype) * u
+    return x2 * y
+
+
+def iir_mixer_prefill(z_p, short_w, conv_state, res, lp, ssm, D, qsl, slots, has_init):
+    """Prefill rows of HyenaIIRMixer between in_proj and out_proj.
+
+    mixers.py:1327-1401: short conv, x1v = x1*v (bf16), per segment
+    `iir_segment` on x1v as fp32 -> y (bf16), ssm[slot] <- final state, then
+    g = (y + x1v*D) * x2 in bf16.  res, lp: (H, 16) fp32.  Returns g (T, H) bf16.
+    """
+    k_short = short_w.shape[1]
+    zf = depthwise_prefill(z_p, short_w, qsl, slots, has_init, conv_state, k_short)
+    x2, x1, v = _split(zf)
+    x1v = x1 * v
+    y = torch.empty_like(x1v)
+    for j in range(len(qsl) - 1):
+        a, b = int(qsl[j]), int(qsl[j + 1])
+        if b <= a:
+            continue
+        seq = x1v[a:b].float().transpose(0, 1)
+        idx = int(slots[j])
+        s_prev = ssm[idx].float() if has_init[j] else None
+        conv, st = iir_segment(seq, res, lp, s_prev)
+        y[a:b] = conv.transpose(0, 1).to(y.dtype)
+        ssm[idx] = st
+    return (y + x1v * D.to(y.dtype)) * x2
+
+
+# ------------------------------------------------------------------ decode
+def fir_decode_one(x, weight, indices, state):
+    """Unfused torch FIR decode (mixers.py:555-565), fp32 sums in torch's order."""
+    st = state[indices].float()
+    wf = weight.float()
+    y = (st * wf[None, :, :-1]).sum(-1) + wf[None, :, -1] * x.float()
+    state[indices] = torch.cat([st[..., 1:], x.float().unsqueeze(-1)], dim=-1).to(state.dtype)
+    return y.to(x.dtype)
+
+
+def iir_decode_one(x, poles, residues, indices, state):
+    """Unfused torch LI decode (mixers.py:568-575)."""
+    st = state[indices] * poles[None] + x[..., None]
+    state[indices] = st
+    return (residues[None] * st).sum(-1).to(x.dtype)
+
+
+def short_conv_update(z, short_w, conv_state, slots):
+    """The K=3 conv update as the fused decode rounds it (triton_decode.py:44-53).
+
+    Per channel: bf16(((0 + bf16(c0 w0)) + bf16(c1 w1)) + bf16(x w2)), then
+    window (c0, c1) <- (c1, x).  conv_state (blocks, 3H, 2) is updated in
+    place for each row's slot.  Returns (B, 3H) fp32 holding bf16 values.
+    """
+    B, C = z.shape
+    w = short_w.float()
+    out = torch.empty(B, C, dtype=torch.float32)
+    for b in range(B):
+        blk = int(slots[b])
+        c = conv_state[blk].float()
+        x = z[b].float()
+        acc = (0.0 + bf(c[:, 0] * w[:, 0])) + bf(c[:, 1] * w[:, 1])
+        acc = acc + bf(x * w[:, 2])
+        out[b] = bf(acc)
+        conv_state[blk, :, 0] = conv_state[blk, :, 1]
+        conv_state[blk, :, 1] = z[b].to(conv_state.dtype)
+    return out
+
+
+def _hcm_sum(s, wf, u):
+    """K=128 readout in the fused kernel's order (triton_decode.py:97-123)."""
+    H = s.shape[0]
+    acc = [[torch.zeros(H) for _ in range(4)] for _ in range(4)]
+    for j in range(8):
+        for m in range(4):
+            for l in range(4):
+                k = 16 * j + 4 * m + l
+                if k < 127:
+                    acc[m][l] = acc[m][l] + s[:, k] * wf[:, k]
+                else:
+                    acc[m][l] = acc[m][l] + 0.0
+    p = [((acc[0][l] + acc[1][l]) + acc[2][l]) + acc[3][l] for l in range(4)]
+    return bf(((p[0] + p[2]) + (p[1] + p[3])) + wf[:, 127] * u)
+
+
+def _hcs_sum(s, wf, u):
+    """K=7 readout in the fused kernel's order (triton_decode.py:125-143)."""
+    a = (s[:, 0] * wf[:, 0] + 0.0) + s[:, 4] * wf[:, 4]
+    b = (s[:, 1] * wf[:, 1] + 0.0) + s[:, 5] * wf[:, 5]
+    c = s[:, 2] * wf[:, 2] + 0.0
+    d = s[:, 3] * wf[:, 3] + 0.0
+    return bf((((a + b) + c) + d) + wf[:, 6] * u)
+
+
+def hyena_decode_emulated(z, short_w, conv_state, slots, inner, inner_state, D=None,
+                          log_poles=None, null_block=0, poles=None):
+    """The fused q=1 decode step with the reference kernel's rounding points.
+
+    triton_decode.py:57-164 restated op by op in fp32 torch (no FMA on the
+    CPU): rows whose slot is the null block output 0 and write no state; all
+    three state slices are updated in place.  `poles` overrides exp(log_poles)
+    so a caller can feed the exact fp32 poles a device computed.
+    Returns (B, H) bf16.
+    """
+    B = z.shape[0]
+    H = inner.shape[0]
+    out = torch.zeros(B, H, dtype=torch.bfloat16)
+    iir = log_poles is not None
+    if iir and poles is None:
+        poles = torch.exp(log_poles.float())
+    for b in range(B):
+        blk = int(slots[b])
+        if blk == null_block:
+            continue
+        y3 = short_conv_update(z[b:b + 1], short_w, conv_state, [blk])[0].view(H, 3)
+        x2, x1, v = y3[:, 0], y3[:, 1], y3[:, 2]
+        u = bf(x1 * v)
+        if iir:
+            s = inner_state[blk].float() * poles + u[:, None]
+            r = s * inner.float()
+            r = r[:, :8] + r[:, 8:]
+            r = r[:, :4] + r[:, 4:]
+            r = r[:, :2] + r[:, 2:]
+            y = bf((r[:, 0] + r[:, 1]) + 0.0)
+            inner_state[blk] = s
+        else:
+            K = inner.shape[1]
+            s = inner_state[blk, :, : K - 1].float()
+            wf = inner.float()
+            y = _hcm_sum(s, wf, u) if K == 128 else _hcs_sum(s, wf, u)
+            inner_state[blk, :, : K - 1] = torch.cat([s[:, 1:], u[:, None]], dim=1)
+        if D is not None:
+            y = bf(y + bf(D.float() * u))
+        out[b] = (x2 * y).to(torch.bfloat16)
+    return out
+
+
+def mixer_decode_unfused(z, short_w, conv_state, slots, inner, inner_state, D=None,
+                         log_poles=None):
+    """The reference's unfused decode (fp32 torch sums), for tolerance checks.
+
+    FIR: mixers.py:1285-1305 with `_fir_decode_one`; LI: mixers.py:1355-1397
+    with `_iir_decode_one`.  The short filter uses the fused rounding
+    (`short_conv_update`), which is what vLLM's update kernel computes.
+    """
+    H = inner.shape[0]
+    zf = bf(short_conv_update(z, short_w, conv_state, slots)).to(torch.bfloat16)
+    x2, x1, v = _split(zf)
+    u = x1 * v
+    idx = torch.as_tensor([int(s) for s in slots], dtype=torch.long)
+    if log_poles is not None:
+        y = iir_decode_one(u.float(), torch.exp(log_poles.float()), inner.float(), idx,
+                           inner_state).to(torch.bfloat16)
+        y = (y + u * D.to(y.dtype)) * x2
+        return y
+    K = inner.shape[1]
+    view = inner_state[..., : K - 1]
+    st = view[idx].float()
+    wf = inner.float()
+    yf = (st * wf[None, :, :-1]).sum(-1) + wf[None, :, -1] * u.float()
+    inner_state[idx, :, : K - 1] = torch.cat([st[..., 1:], u.float().unsqueeze(-1)], dim=-1)
+    y = yf.to(torch.bfloat16)
+    if D is not None:
+        y = y + D.to(y.dtype) * u
+    return x2 * y
+
+
+# ------------------------------------------------------------------ norm, fp8
+def rms_norm(x, weight, eps, residual=None):
+    """Evo2RMSNorm (model.py:47-74) with the rounding points of triton_norm.py:6-11.
+
+    s = bf(x + r); n = bf(sqrt(sum s^2)) (fp32 sum); n = bf(n H^-1/2);
+    n = bf(n + eps); y = bf(w * bf(s / n)).  eps sits outside the sqrt.
+    Returns y, or (y, s) with a residual.  bf16 in and out.
+    """
+    H = x.shape[-1]
+    s = x.float()
+    if residual is not None:
+        s = bf(s + residual.float())
+    n = bf(torch.sqrt((s.double() * s.double()).sum(-1, keepdim=True)).float())
+    n = bf(n * (H ** -0.5))
+    n = bf(n + eps)
+    y = bf(weight.float() * bf(s / n)).to(torch.bfloat16)
+    if residual is None:
+        return y
+    return y, s.to(torch.bfloat16)
+
+
+def quantize_input(x, input_scale):
+    """Static per-tensor E4M3 activation quantisation (fp8_emul.py:76-78)."""
+    return (x.float() / input_scale).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
+
+
+def fp8_linear_dequant(x, w8, input_scale, weight_scale, bias=None):
+    """bf16( (e4m3(x/s_in) @ W8^T) * s_in * s_w [+ b] ) in fp32 (convert.py:195-201)."""
+    xq = quantize_input(x, input_scale).float()
+    acc = xq @ w8.float().t()
+    out = acc * float(input_scale) * float(weight_scale)
+    if bias is not None:
+        out = out + bias.float()
+    return out.to(torch.bfloat16)
+
+
+# ------------------------------------------------------------------ tables
+def prefill_tables(qsl, has_init, block_t):
+    """(seq (n,3) [start, end, has_init], tiles (ntiles,2) [segment, row0]).
+
+    `_prefill_tables` (mixers.py:386-415) on host lists.
+    """
+    seq, tiles = [], []
+    for j in range(len(qsl) - 1):
+        a, b = int(qsl[j]), int(qsl[j + 1])
+        seq.append((a, b, int(bool(has_init[j]))))
+        tiles.extend((j, t) for t in range(a, b, block_t))
+    return (torch.tensor(seq, dtype=torch.int32).reshape(-1, 3),
+            torch.tensor(tiles, dtype=torch.int32).reshape(-1, 2))
