@@ -186,6 +186,274 @@ static void launch(const DecodeArgs &a, int64_t B, hipStream_t stream) {
   hipLaunchKernelGGL((hyena_decode_kernel<KIND, HAS_D, CONTIG_S>), grid, dim3(BH), 0, stream, a);
 }
 
+// ---------------------------------------------------------------------------
+// Fast path for the engine's native layouts: each lane owns a channel pair
+// (h0, h0+1), so every operand moves as 4/8/16-byte vectors: the z triple
+// pair and both conv-state columns as three dwords each, FIR window columns
+// as float2 (channel-contiguous native storage), LI states, residues and
+// log-poles as float4.  The hcm window is streamed in 16-column chunks with
+// the next chunk's loads issued before the current chunk's arithmetic and
+// shifted stores.  Arithmetic and rounding are exactly the generic kernel's.
+//
+// WT: FIR taps in channel-contiguous (K, H) storage (wi0 == 1), one dword
+// per tap for the pair; otherwise tap-contiguous (H, K) rows (wi1 == 1).
+
+__device__ __forceinline__ void unpack3(const uint32_t *p, float f[6]) {
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    const uint32_t v = p[i];
+    f[2 * i] = lo_bf(v);
+    f[2 * i + 1] = hi_bf(v);
+  }
+}
+
+template <int KIND, bool HAS_D, bool WT>
+__global__ __launch_bounds__(128) void hyena_decode_pair_kernel(DecodeArgs a) {
+  const int pair = blockIdx.x * blockDim.x + threadIdx.x;
+  const int h0 = 2 * pair;
+  const int64_t b = blockIdx.y;
+  if (h0 >= a.H) return;
+  const int64_t blk = a.slots[b * a.ssl];
+  uint32_t *o = reinterpret_cast<uint32_t *>(a.out + b * a.so + h0);
+  if (blk == a.null_block || blk < 0 || blk >= a.num_blocks) {
+    *o = 0u;
+    return;
+  }
+
+  // ---- short filter: z triples and both window columns for 6 sub-channels
+  const uint32_t *zr = reinterpret_cast<const uint32_t *>(a.z + b * a.sz + 3 * (int64_t)h0);
+  bf16_t *cbase = a.cs + blk * a.cs0 + 3 * (int64_t)h0;
+  uint32_t *c0p = reinterpret_cast<uint32_t *>(cbase);
+  uint32_t *c1p = reinterpret_cast<uint32_t *>(cbase + a.cs2);
+  uint32_t zraw[3], c0raw[3], c1raw[3];
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    zraw[i] = zr[i];
+    c0raw[i] = c0p[i];
+    c1raw[i] = c1p[i];
+  }
+  float xf[6], c0f[6], c1f[6], wsf[18];
+  unpack3(zraw, xf);
+  unpack3(c0raw, c0f);
+  unpack3(c1raw, c1f);
+  const uint32_t *wsp = reinterpret_cast<const uint32_t *>(a.ws + 9 * (int64_t)h0);
+#pragma unroll
+  for (int i = 0; i < 9; ++i) {
+    const uint32_t v = wsp[i];
+    wsf[2 * i] = lo_bf(v);
+    wsf[2 * i + 1] = hi_bf(v);
+  }
+  float y6[6];
+#pragma unroll
+  for (int i = 0; i < 6; ++i) {
+    float acc = 0.0f + rbf(c0f[i] * wsf[3 * i]);
+    acc = acc + rbf(c1f[i] * wsf[3 * i + 1]);
+    acc = acc + rbf(xf[i] * wsf[3 * i + 2]);
+    y6[i] = rbf(acc);
+  }
+  const float x2[2] = {y6[0], y6[3]};
+  const float u[2] = {rbf(y6[1] * y6[2]), rbf(y6[4] * y6[5])};
+  float y[2];
+
+  if constexpr (KIND == KIND_HCL) {
+    float sv[2][16], res[2][16], lpv[2][16];
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const float4 *sp = reinterpret_cast<const float4 *>(a.st + blk * a.is0 + (int64_t)(h0 + c) * a.is1);
+      const float4 *rp = reinterpret_cast<const float4 *>(static_cast<const float *>(a.inner) + (int64_t)(h0 + c) * a.wi0);
+      const float4 *lq = reinterpret_cast<const float4 *>(a.lp + (int64_t)(h0 + c) * a.lp0);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float4 s4 = sp[q], r4 = rp[q], l4 = lq[q];
+        sv[c][4 * q] = s4.x; sv[c][4 * q + 1] = s4.y; sv[c][4 * q + 2] = s4.z; sv[c][4 * q + 3] = s4.w;
+        res[c][4 * q] = r4.x; res[c][4 * q + 1] = r4.y; res[c][4 * q + 2] = r4.z; res[c][4 * q + 3] = r4.w;
+        lpv[c][4 * q] = l4.x; lpv[c][4 * q + 1] = l4.y; lpv[c][4 * q + 2] = l4.z; lpv[c][4 * q + 3] = l4.w;
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      float r[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        sv[c][i] = sv[c][i] * expf(lpv[c][i]) + u[c];
+        r[i] = sv[c][i] * res[c][i];
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) r[i] = r[i] + r[i + 8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) r[i] = r[i] + r[i + 4];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) r[i] = r[i] + r[i + 2];
+      y[c] = rbf((r[0] + r[1]) + 0.0f);
+      float4 *sp = reinterpret_cast<float4 *>(a.st + blk * a.is0 + (int64_t)(h0 + c) * a.is1);
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        sp[q] = make_float4(sv[c][4 * q], sv[c][4 * q + 1], sv[c][4 * q + 2], sv[c][4 * q + 3]);
+    }
+  } else if constexpr (KIND == KIND_HCM) {
+    float *s = a.st + blk * a.is0 + h0;  // is1 == 1: the pair is one float2
+    const bf16_t *w = static_cast<const bf16_t *>(a.inner);
+    float acc[2][16];
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int q = 0; q < 16; ++q) acc[c][q] = 0.0f;
+    float2 cur[16], nxt[16];
+#pragma unroll
+    for (int q = 0; q < 16; ++q) cur[q] = *reinterpret_cast<const float2 *>(s + q * a.is2);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (j < 7) {
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+          const int k = 16 * (j + 1) + q;
+          nxt[q] = (k < 127) ? *reinterpret_cast<const float2 *>(s + k * a.is2) : make_float2(0.f, 0.f);
+        }
+      }
+      float wf[2][16];
+      if constexpr (WT) {
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+          const int k = 16 * j + q;
+          const uint32_t v = *reinterpret_cast<const uint32_t *>(w + (int64_t)k * a.wi1 + h0);
+          wf[0][q] = lo_bf(v);
+          wf[1][q] = hi_bf(v);
+        }
+      } else {
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          const uint4 *wp = reinterpret_cast<const uint4 *>(w + (int64_t)(h0 + c) * a.wi0 + 16 * j);
+#pragma unroll
+          for (int v4 = 0; v4 < 2; ++v4) {
+            const uint4 v = wp[v4];
+            const uint32_t d[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              wf[c][8 * v4 + 2 * e] = lo_bf(d[e]);
+              wf[c][8 * v4 + 2 * e + 1] = hi_bf(d[e]);
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        const int k = 16 * j + q;
+        const float w0 = (k < 127) ? wf[0][q] : 0.0f;
+        const float w1 = (k < 127) ? wf[1][q] : 0.0f;
+        acc[0][q] = acc[0][q] + cur[q].x * w0;
+        acc[1][q] = acc[1][q] + cur[q].y * w1;
+      }
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        const int k = 16 * j + q;
+        if (k >= 1 && k < 127) *reinterpret_cast<float2 *>(s + (k - 1) * a.is2) = cur[q];
+      }
+      if (j < 7) {
+#pragma unroll
+        for (int q = 0; q < 16; ++q) cur[q] = nxt[q];
+      }
+    }
+    float last[2];
+    if constexpr (WT) {
+      const uint32_t v = *reinterpret_cast<const uint32_t *>(w + (int64_t)127 * a.wi1 + h0);
+      last[0] = lo_bf(v);
+      last[1] = hi_bf(v);
+    } else {
+      last[0] = bf2f(w[(int64_t)h0 * a.wi0 + 127]);
+      last[1] = bf2f(w[(int64_t)(h0 + 1) * a.wi0 + 127]);
+    }
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      float p[4];
+#pragma unroll
+      for (int l = 0; l < 4; ++l)
+        p[l] = ((acc[c][l] + acc[c][4 + l]) + acc[c][8 + l]) + acc[c][12 + l];
+      y[c] = rbf(((p[0] + p[2]) + (p[1] + p[3])) + last[c] * u[c]);
+    }
+    *reinterpret_cast<float2 *>(s + 126 * a.is2) = make_float2(u[0], u[1]);
+  } else {
+    float *s = a.st + blk * a.is0 + h0;
+    const bf16_t *w = static_cast<const bf16_t *>(a.inner);
+    float2 sv[6];
+#pragma unroll
+    for (int k = 0; k < 6; ++k) sv[k] = *reinterpret_cast<const float2 *>(s + k * a.is2);
+    float wf[2][7];
+    if constexpr (WT) {
+#pragma unroll
+      for (int k = 0; k < 7; ++k) {
+        const uint32_t v = *reinterpret_cast<const uint32_t *>(w + (int64_t)k * a.wi1 + h0);
+        wf[0][k] = lo_bf(v);
+        wf[1][k] = hi_bf(v);
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int k = 0; k < 7; ++k) wf[c][k] = bf2f(w[(int64_t)(h0 + c) * a.wi0 + k]);
+    }
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      float s6[6];
+#pragma unroll
+      for (int k = 0; k < 6; ++k) s6[k] = c ? sv[k].y : sv[k].x;
+      const float aa = (s6[0] * wf[c][0] + 0.0f) + s6[4] * wf[c][4];
+      const float bb = (s6[1] * wf[c][1] + 0.0f) + s6[5] * wf[c][5];
+      const float cc = s6[2] * wf[c][2] + 0.0f;
+      const float dd = s6[3] * wf[c][3] + 0.0f;
+      y[c] = rbf((((aa + bb) + cc) + dd) + wf[c][6] * u[c]);
+    }
+#pragma unroll
+    for (int k = 0; k < 5; ++k) *reinterpret_cast<float2 *>(s + k * a.is2) = sv[k + 1];
+    *reinterpret_cast<float2 *>(s + 5 * a.is2) = make_float2(u[0], u[1]);
+  }
+
+  // Short-filter windows (c0, c1) <- (c1, x) for the 6 sub-channels.
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    c0p[i] = c1raw[i];
+    c1p[i] = zraw[i];
+  }
+  if constexpr (HAS_D) {
+    const uint32_t dv = *reinterpret_cast<const uint32_t *>(a.D + h0);
+    y[0] = rbf(y[0] + rbf(lo_bf(dv) * u[0]));
+    y[1] = rbf(y[1] + rbf(hi_bf(dv) * u[1]));
+  }
+  *o = pack_bf(x2[0] * y[0], x2[1] * y[1]);
+}
+
+template <int KIND, bool HAS_D, bool WT>
+static void launch_pair(const DecodeArgs &a, int64_t B, hipStream_t stream) {
+  constexpr int BT = 128;  // 256 channels per block
+  dim3 grid(static_cast<unsigned>(cdiv(a.H / 2, BT)), static_cast<unsigned>(B));
+  hipLaunchKernelGGL((hyena_decode_pair_kernel<KIND, HAS_D, WT>), grid, dim3(BT), 0, stream, a);
+}
+
+static bool aligned(const void *p, uintptr_t n) {
+  return p == nullptr || (reinterpret_cast<uintptr_t>(p) % n) == 0;
+}
+
+// Which fast-path variant applies: -1 none, 0 row-major taps, 1 transposed.
+static int pair_variant(const DecodeArgs &a, int kind) {
+  if (a.H % 2) return -1;
+  if (a.sz % 2 || !aligned(a.z, 4)) return -1;
+  if (a.cs1 != 1 || a.cs0 % 2 || a.cs2 % 2 || !aligned(a.cs, 4)) return -1;
+  if (!aligned(a.ws, 4) || !aligned(a.D, 4)) return -1;
+  if (a.so % 2 || !aligned(a.out, 4)) return -1;
+  if (kind == KIND_HCL) {
+    const bool ok = a.is2 == 1 && a.is1 % 4 == 0 && a.is0 % 4 == 0 && aligned(a.st, 16) &&
+                    a.wi1 == 1 && a.wi0 % 4 == 0 && aligned(a.inner, 16) &&
+                    a.lp1 == 1 && a.lp0 % 4 == 0 && aligned(a.lp, 16);
+    return ok ? 0 : -1;
+  }
+  if (a.is1 != 1 || a.is0 % 2 || a.is2 % 2 || !aligned(a.st, 8)) return -1;
+  if (a.wi0 == 1 && a.wi1 % 2 == 0 && aligned(a.inner, 4)) return 1;
+  if (a.wi1 == 1) {
+    if (kind == KIND_HCS) return 0;
+    if (a.wi0 % 8 == 0 && aligned(a.inner, 16)) return 0;
+  }
+  return -1;
+}
+
 }  // namespace evo2
 
 using namespace evo2;
@@ -226,6 +494,19 @@ extern "C" int evo2_hyena_decode(const void *z, int64_t sz, const void *short_w,
                static_cast<int>(H), null_block, num_blocks};
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool hasD = D != nullptr;
+  const int pv = pair_variant(a, kind);
+  if (pv >= 0) {
+    if (kind == KIND_HCL) {
+      hasD ? launch_pair<KIND_HCL, true, false>(a, B, st) : launch_pair<KIND_HCL, false, false>(a, B, st);
+    } else if (kind == KIND_HCM) {
+      if (pv) hasD ? launch_pair<KIND_HCM, true, true>(a, B, st) : launch_pair<KIND_HCM, false, true>(a, B, st);
+      else hasD ? launch_pair<KIND_HCM, true, false>(a, B, st) : launch_pair<KIND_HCM, false, false>(a, B, st);
+    } else {
+      if (pv) hasD ? launch_pair<KIND_HCS, true, true>(a, B, st) : launch_pair<KIND_HCS, false, true>(a, B, st);
+      else hasD ? launch_pair<KIND_HCS, true, false>(a, B, st) : launch_pair<KIND_HCS, false, false>(a, B, st);
+    }
+    return check_launch("hyena_decode");
+  }
   if (kind == KIND_HCL) {
     const bool contig = is2 == 1 && (is1 % 4) == 0 && (is0 % 4) == 0 &&
                         (reinterpret_cast<uintptr_t>(inner_state) % 16) == 0;

@@ -114,6 +114,39 @@ def test_decode_multi_step_and_permutation(kind):
     assert torch.equal(gp.raw, gp2.raw)
 
 
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("H", [1024, 255])
+def test_decode_layouts_agree(kind, H):
+    """Native pool views with (H, K) taps, channel-contiguous (K, H) taps, and
+    dense dim-first state tensors (the generic strided kernel) give identical
+    bits; odd H always takes the generic kernel."""
+    B, nblk = 12, 20
+    prm, z, slots, pool = decode_case(kind, H, B, nblk, seed=31, n_null=2)
+    dev = "cuda"
+    sw = prm["short_filter"].view(3 * H, 3).to(dev)
+    D = prm.get("D")
+    D = None if D is None else D.to(dev)
+    outs, states = [], []
+    for layout in ("native", "taps_t", "dense"):
+        gp = clone_pool(pool, dev)
+        inner, lp, st, _ = _args(kind, prm, gp, H)
+        inner = inner.to(dev)
+        lp = None if lp is None else lp.to(dev)
+        conv = gp.conv_view()
+        if layout == "taps_t":
+            inner = inner.t().contiguous().t()
+        if layout == "dense":
+            conv = conv.contiguous()
+            st = st.contiguous()
+        out = hyena_decode(z.to(dev), sw, conv, slots.to(dev), inner, st, D, lp)
+        outs.append(out.cpu())
+        states.append((conv.cpu().clone(), st.cpu().clone()))
+    for o, (c, s) in zip(outs[1:], states[1:]):
+        assert torch.equal(outs[0].view(torch.int16), o.view(torch.int16))
+        assert torch.equal(states[0][0], c)
+        assert torch.equal(states[0][1], s)
+
+
 def test_decode_empty_batch():
     H = 256
     prm, z, slots, pool = decode_case("hcs", H, 1, 4, seed=1)
