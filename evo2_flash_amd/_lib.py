@@ -34,6 +34,25 @@ SIGNATURES = {
         _c_i64, _c_i64, _c_i32, _c_i32,           # B, H, K, is_iir
         _c_i32, _c_i64, _c_p,                     # null_block, num_blocks, stream
     ],
+    "evo2_fir_prefill": [
+        _c_p, _c_i64, _c_p, _c_i64, _c_i64,       # u, su, w, w0, w1
+        _c_i32, _c_p, _c_i64, _c_i64, _c_i64,     # K, state + strides
+        _c_p, _c_i64, _c_p, _c_i64,               # seq_table, nseq, blocks, sblk
+        _c_p, _c_i64, _c_i32,                     # tile_table, ntiles, block_t
+        _c_p, _c_i64, _c_i64, _c_i64,             # out, so, T, H
+        _c_i64, _c_p,                             # num_blocks, stream
+    ],
+    "evo2_hyena_fir_prefill": [
+        _c_p, _c_i64, _c_p,                       # z, sz, short_w
+        _c_p, _c_i64, _c_i64, _c_i64,             # conv_state + strides
+        _c_p, _c_i64, _c_i64, _c_i32,             # w, w0, w1, K
+        _c_p, _c_i64, _c_i64, _c_i64,             # inner_state + strides
+        _c_p,                                     # D
+        _c_p, _c_i64, _c_p, _c_i64,               # seq_table, nseq, blocks, sblk
+        _c_p, _c_i64, _c_i32,                     # tile_table, ntiles, block_t
+        _c_p, _c_i64, _c_i64, _c_i64,             # out, so, T, H
+        _c_i64, _c_p,                             # num_blocks, stream
+    ],
 }
 
 RESTYPES = {"evo2_last_error": ctypes.c_char_p}

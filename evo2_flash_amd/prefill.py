@@ -1,0 +1,105 @@
+"""Varlen Hyena FIR prefill (HIP, gfx950).
+
+`fir_prefill` and `fir_prefill_block_t` keep the signatures of
+evo2_flash/triton_prefill.py:462-501; `hyena_fir_prefill` is the fused
+prefill core of HyenaFIRMixer (mixers.py:1277-1305) between in_proj and
+out_proj.  Kernels: csrc/prefill_fir.hip.
+"""
+
+import torch
+
+from . import _lib
+
+# Rows per tile.  A tile is swept in 64-row sub-tiles with the FIR history in
+# LDS, so longer tiles amortise the (K-1)-row halo; shorter ones add
+# parallelism when there are few tokens.
+_MAX_BLOCK_T = {7: 1024, 128: 2048}
+_TARGET_WORKGROUPS = 2048
+
+
+def fir_prefill_block_t(k, num_tokens=None, hidden=None):
+    """Rows per prefill tile for filter length k; the tile table is built for
+    this value.  With `num_tokens` and `hidden` it shrinks (to a multiple of
+    64) until the launch has enough workgroups to fill the GPU."""
+    bt = _MAX_BLOCK_T.get(int(k), 1024)
+    if num_tokens is not None and hidden is not None:
+        cblocks = max(1, (int(hidden) + 63) // 64)
+        while bt > 64 and ((int(num_tokens) + bt - 1) // bt) * cblocks < _TARGET_WORKGROUPS:
+            bt //= 2
+    return bt
+
+
+def _check_tables(seq_table, tile_table):
+    for name, t, w in (("seq_table", seq_table, 3), ("tile_table", tile_table, 2)):
+        if t.dtype != torch.int32 or t.dim() != 2 or t.shape[1] != w or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous (n, {w}) int32 tensor")
+
+
+def fir_prefill(u, w, state, seq_table, blocks, tile_table, block_t):
+    """Depthwise causal FIR over packed prefill rows, carrying per-sequence state.
+
+    u: (T, H) bf16 packed rows.  w: (H, K) cross-correlation order (w[:, -1]
+    pairs with the current sample).  state: (blocks, H, >=K-1) fp32, any
+    strides.  seq_table: (n, 3) int32 [start, end, has_initial_state].
+    blocks: (n,) state block per segment, any stride.  tile_table: (ntiles, 2)
+    int32 [segment, first row] built for `block_t` (`fir_prefill_block_t`).
+
+    Returns the filter output (T, H) bf16 and writes each segment's final
+    (K-1)-input window into `state` (triton_prefill.py:462-496).
+    """
+    _lib.require_device(u, w, state, seq_table, blocks, tile_table)
+    T, H = u.shape
+    K = w.shape[1]
+    if u.stride(1) != 1:
+        raise ValueError("rows are addressed as t * stride(0) + channel")
+    if u.dtype != torch.bfloat16 or w.dtype != torch.bfloat16 or state.dtype != torch.float32:
+        raise ValueError("u and w must be bf16, state fp32")
+    _check_tables(seq_table, tile_table)
+    blocks = blocks if blocks.dtype == torch.int32 else blocks.to(torch.int32)
+    out = torch.empty(T, H, dtype=u.dtype, device=u.device)
+    _lib.call(
+        "evo2_fir_prefill",
+        _lib.ptr(u), u.stride(0), _lib.ptr(w), w.stride(0), w.stride(1),
+        K, _lib.ptr(state), *state.stride(),
+        _lib.ptr(seq_table), seq_table.shape[0], _lib.ptr(blocks), blocks.stride(0),
+        _lib.ptr(tile_table), tile_table.shape[0], int(block_t),
+        _lib.ptr(out), out.stride(0), T, H, state.shape[0], _lib.stream_of(u))
+    return out
+
+
+def hyena_fir_prefill(z, short_w, conv_state, w, inner_state, D, seq_table, blocks,
+                      tile_table, block_t):
+    """g = x2 * (FIR(x1*v) [+ D*(x1*v)]) over packed prefill rows of z.
+
+    z: (T, 3H) bf16 in_proj rows (interleaved x2, x1, v per channel).
+    short_w: (3H, 3) bf16.  conv_state: (blocks, 3H, 2) bf16 view.  w: (H, K)
+    bf16 inner taps (K = 7 or 128).  inner_state: (blocks, H, >=K-1) fp32
+    view.  D: (H,) bf16 or None.  Tables as for `fir_prefill`.
+    Returns g (T, H) bf16; both windows are rewritten for every segment.
+    """
+    _lib.require_device(z, short_w, conv_state, w, inner_state, seq_table, blocks, tile_table)
+    T = z.shape[0]
+    H, K = w.shape
+    if z.shape[1] != 3 * H or z.stride(1) != 1 or z.dtype != torch.bfloat16:
+        raise ValueError("z must be (T, 3H) bf16 with unit column stride")
+    if short_w.shape != (3 * H, 3) or not short_w.is_contiguous():
+        raise ValueError("short_w must be a contiguous (3H, 3) tensor")
+    if conv_state.dtype != torch.bfloat16 or inner_state.dtype != torch.float32:
+        raise ValueError("conv_state must be bf16 and inner_state fp32")
+    _check_tables(seq_table, tile_table)
+    if D is not None and (D.dtype != torch.bfloat16 or D.stride(0) != 1):
+        D = D.to(torch.bfloat16).contiguous()
+    blocks = blocks if blocks.dtype == torch.int32 else blocks.to(torch.int32)
+    out = torch.empty(T, H, dtype=z.dtype, device=z.device)
+    _lib.call(
+        "evo2_hyena_fir_prefill",
+        _lib.ptr(z), z.stride(0), _lib.ptr(short_w),
+        _lib.ptr(conv_state), *conv_state.stride(),
+        _lib.ptr(w), w.stride(0), w.stride(1), K,
+        _lib.ptr(inner_state), *inner_state.stride(),
+        _lib.ptr(D),
+        _lib.ptr(seq_table), seq_table.shape[0], _lib.ptr(blocks), blocks.stride(0),
+        _lib.ptr(tile_table), tile_table.shape[0], int(block_t),
+        _lib.ptr(out), out.stride(0), T, H, min(conv_state.shape[0], inner_state.shape[0]),
+        _lib.stream_of(z))
+    return out

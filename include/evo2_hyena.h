@@ -67,6 +67,54 @@ int evo2_hyena_decode(const void *z, int64_t sz, const void *short_w,
                       int64_t B, int64_t H, int32_t K, int32_t is_iir,
                       int32_t null_block, int64_t num_blocks, void *stream);
 
+/*
+ * Varlen depthwise causal FIR over packed prefill rows, carrying per-segment
+ * windows: y = FIR(u) (bf16 out), and each segment's last K-1 inputs of
+ * cat(window, segment) written back into `state`.
+ *
+ * Replaces triton_prefill.fir_prefill (evo2_flash/triton_prefill.py:391-496).
+ *
+ *   u          (T, H) bf16, row stride su          w  (H, K) bf16, strides w0, w1
+ *   state      (blocks, H, >=K-1) fp32 view, strides st0, st1, st2
+ *   seq_table  (nseq, 3) int32 [start, end, has_initial_state], contiguous
+ *   blocks     (nseq,) int32 state block per segment, stride sblk
+ *   tile_table (ntiles, 2) int32 [segment, first row], rows step block_t
+ *   out        (T, H) bf16, row stride so
+ * K is 7 or 128; H must be even; block_t a positive multiple of 64.
+ */
+int evo2_fir_prefill(const void *u, int64_t su, const void *w, int64_t w0, int64_t w1,
+                     int32_t K, float *state, int64_t st0, int64_t st1, int64_t st2,
+                     const int32_t *seq_table, int64_t nseq,
+                     const int32_t *blocks, int64_t sblk,
+                     const int32_t *tile_table, int64_t ntiles, int32_t block_t,
+                     void *out, int64_t so, int64_t T, int64_t H,
+                     int64_t num_blocks, void *stream);
+
+/*
+ * Fused Hyena FIR mixer prefill (hcs K=7 / hcm K=128) between in_proj and
+ * out_proj: z -> short K=3 filter (left context from conv_state) ->
+ * u = x1*v -> FIR(u) (left context from inner_state) [+ D*u] -> g = x2*y.
+ * Both windows are rewritten for every segment.
+ *
+ * Replaces the prefill rows of HyenaFIRMixer._forward_impl
+ * (evo2_flash/mixers.py:1277-1305): vLLM causal_conv1d_fn (mixers.py:1140-1150),
+ * the gate, _depthwise_prefill_triton (mixers.py:418-428) and the bf16 tail.
+ *
+ *   z          (T, 3H) bf16, row stride sz    short_w (3H, 3) bf16 contiguous
+ *   conv_state (blocks, 3H, 2) bf16 view      D (H,) bf16 or NULL (hcs)
+ *   other arguments as evo2_fir_prefill; out = g (T, H) bf16.
+ */
+int evo2_hyena_fir_prefill(const void *z, int64_t sz, const void *short_w,
+                           void *conv_state, int64_t cs0, int64_t cs1, int64_t cs2,
+                           const void *w, int64_t w0, int64_t w1, int32_t K,
+                           float *inner_state, int64_t st0, int64_t st1, int64_t st2,
+                           const void *D,
+                           const int32_t *seq_table, int64_t nseq,
+                           const int32_t *blocks, int64_t sblk,
+                           const int32_t *tile_table, int64_t ntiles, int32_t block_t,
+                           void *out, int64_t so, int64_t T, int64_t H,
+                           int64_t num_blocks, void *stream);
+
 #ifdef __cplusplus
 }
 #endif
