@@ -23,6 +23,8 @@
 // when the segment continues a sequence (has_initial_state), else zero
 // (mixers.py:126-141, 350-383).  The windows are rewritten by a second
 // launch after every tile has read them (as triton_prefill.py:489-495).
+#include <type_traits>
+
 #include "featurize.h"
 
 namespace evo2 {
@@ -55,15 +57,21 @@ struct FirGeom {
   static constexpr int KP = (K + 1) & ~1;  // taps padded to even (zero tap first)
   static constexpr int NP = KP / 2;        // tap pairs
   static constexpr int RS = 64;            // rows per sub-tile
-  static constexpr int RW = 16;            // rows per wave in the FIR phase
+  static constexpr int RW = 16;            // rows per wave per sub-tile
   static constexpr int NE = NP + RW / 2;   // pairs in one wave's window
   static constexpr int RING = (KP + RS <= 128) ? 128 : 256;
-  static constexpr int PITCH = RING + 8;   // bf16 per channel row (16-byte rows)
+  // Row pitches are 4 dwords mod 32 banks, so the b128 accesses of 8 lanes
+  // (one LDS cycle) cover all banks once.
+  static constexpr int PITCH = RING + 8;   // bf16 per channel row of the u ring
+  static constexpr int XPITCH = RS + 8;    // bf16 per channel row of x2
+  static constexpr int ZROWS = RS + 2;     // staged z rows: sub-tile + 2-row short halo
+  static constexpr int ZPITCH = 192;       // bf16 per staged z row (3 x 64 sub-channels)
   static_assert(KP + RS <= RING, "ring too small");
 };
 
 struct SegInfo {
-  int64_t a, e, t0, t_end, blk;
+  int a, e, t0, t_end;
+  int64_t blk;
   bool init;
 };
 
@@ -75,170 +83,337 @@ __device__ __forceinline__ SegInfo seg_of_tile(const FirArgs &p) {
   s.e = p.seq[3 * seg + 1];
   s.blk = p.blocks[seg * p.sblk];
   s.init = p.seq[3 * seg + 2] != 0 && s.blk >= 0 && s.blk < p.num_blocks;
-  s.t_end = min(s.t0 + (int64_t)p.block_t, s.e);
+  s.t_end = min(s.t0 + p.block_t, s.e);
   return s;
+}
+
+// bf16 pair (lo, hi) from two fp32 values, one v_cvt_pk_bf16_f32.
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16v2_t;
+__device__ __forceinline__ uint32_t cvt_pk(float lo, float hi) {
+  bf16v2_t v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+  return __builtin_bit_cast(uint32_t, v);
 }
 
 template <int K, bool HAS_D, bool FUSED>
 __global__ __launch_bounds__(256) void fir_prefill_kernel(FirArgs p) {
   using G = FirGeom<K>;
   __shared__ __align__(16) bf16_t ring[64][G::PITCH];
-  __shared__ __align__(16) bf16_t x2s[64][G::RS + 8];
+  __shared__ __align__(16) bf16_t x2s[FUSED ? 64 : 1][G::XPITCH];
+  __shared__ __align__(16) bf16_t zst[FUSED ? G::ZROWS : 1][G::ZPITCH];
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int c = blockIdx.y * 64 + lane;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c0 = blockIdx.y * 64;
+  const int c = c0 + lane;
   const bool active = c < p.H;
+  const int cl = active ? c : p.H - 1;  // clamped channel for loads
   const SegInfo S = seg_of_tile(p);
   if (S.t0 >= S.t_end) return;  // uniform across the block
 
-  // Taps as bf16 pairs, one zero tap in front when K is odd.
+  // Taps as bf16 pairs, one zero tap in front when K is odd.  K=128 taps are
+  // contiguous rows (the host guarantees it) and load as 16-byte vectors.
   uint32_t W[G::NP];
+  if constexpr (K % 8 == 0) {
+    const uint4 *wp = reinterpret_cast<const uint4 *>(p.w + (int64_t)cl * p.w0);
 #pragma unroll
-  for (int m = 0; m < G::NP; ++m) {
-    const int k0 = 2 * m - (G::KP - K), k1 = k0 + 1;
-    uint32_t lo = 0, hi = 0;
-    if (active) {
-      if (k0 >= 0) lo = p.w[(int64_t)c * p.w0 + (int64_t)k0 * p.w1];
-      hi = p.w[(int64_t)c * p.w0 + (int64_t)k1 * p.w1];
+    for (int q = 0; q < G::NP / 4; ++q) {
+      const uint4 v = wp[q];
+      W[4 * q] = active ? v.x : 0u;
+      W[4 * q + 1] = active ? v.y : 0u;
+      W[4 * q + 2] = active ? v.z : 0u;
+      W[4 * q + 3] = active ? v.w : 0u;
     }
-    W[m] = lo | (hi << 16);
+  } else {
+#pragma unroll
+    for (int m = 0; m < G::NP; ++m) {
+      const int k0 = 2 * m - (G::KP - K), k1 = k0 + 1;
+      uint32_t lo = 0, hi = 0;
+      if (active) {
+        if (k0 >= 0) lo = p.w[(int64_t)c * p.w0 + (int64_t)k0 * p.w1];
+        hi = p.w[(int64_t)c * p.w0 + (int64_t)k1 * p.w1];
+      }
+      W[m] = lo | (hi << 16);
+    }
   }
   float wsf[3][3];
-  ShortCtx ctx{};
   if constexpr (FUSED) {
 #pragma unroll
     for (int i = 0; i < 3; ++i)
 #pragma unroll
-      for (int j = 0; j < 3; ++j)
-        wsf[i][j] = active ? bf2f(p.ws[(3 * (int64_t)c + i) * 3 + j]) : 0.0f;
-    ctx.z = p.x;
-    ctx.sz = p.sx;
-    ctx.conv = S.init ? p.cs + S.blk * p.cs0 : nullptr;
-    ctx.cs1 = p.cs1;
-    ctx.cs2 = p.cs2;
-    ctx.a = S.a;
-    ctx.init = S.init;
+      for (int j = 0; j < 3; ++j) wsf[i][j] = bf2f(p.ws[(3 * (int64_t)cl + i) * 3 + j]);
   }
-  const float *stc = (S.init && active) ? p.st + S.blk * p.st0 + (int64_t)c * p.st1 : nullptr;
+  const float *stc = S.init ? p.st + S.blk * p.st0 + (int64_t)cl * p.st1 : nullptr;
+  const bool vec_z = FUSED && (c0 + 64 <= p.H) && (p.sx % 8 == 0) &&
+                     ((reinterpret_cast<uintptr_t>(p.x) & 15) == 0);
 
-  // u (and x2) for rows [r0, r0 + n) by this wave, lane = channel.
-  auto produce = [&](int64_t r0, int n, bool keep_x2) {
-    float zm2[3] = {0.f, 0.f, 0.f}, zm1[3] = {0.f, 0.f, 0.f};
-    if constexpr (FUSED) {
-      if (active) {
+  // ---- stage z rows [rs, rs + ZROWS) of this block's 192 sub-channels into
+  // LDS with direct-to-LDS loads: chunk i = row*24 + col (16 bytes), and one
+  // wave instruction moves 64 consecutive chunks (1 KB of the unpadded tile),
+  // so the data never passes through VGPRs and the next sub-tile's loads fly
+  // while the current one computes.  `prefetch` issues them; `fix` (after the
+  // loads have landed) fills the rows the loads skip: the short filter's left
+  // context (conv window rows a-2, a-1 when continuing, else zeros) and, when
+  // z is not 16-byte addressable, every row element by element.  Rows at or
+  // past the tile end keep stale (finite) values; only discarded rows read them.
+  constexpr int ZCH = G::ZROWS * 24;             // 16-byte chunks per tile
+  constexpr int ZW = (ZCH + 63) / 64;            // wave instructions per tile
+  auto prefetch = [&](int rs) {
+    if (!vec_z) return;
 #pragma unroll
-        for (int i = 0; i < 3; ++i) {
-          zm2[i] = z_at(ctx, r0 - 2, 3 * (int64_t)c + i);
-          zm1[i] = z_at(ctx, r0 - 1, 3 * (int64_t)c + i);
-        }
-      }
-    }
-    for (int r = 0; r < n; ++r) {
-      const int64_t t = r0 + r;
-      float u = 0.0f, x2 = 0.0f;
-      if (active) {
-        if (t < S.a) {
-          const int64_t col = (K - 1) + (t - S.a);
-          if (stc && col >= 0) u = stc[col * p.st2];
-        } else if (t < S.t_end) {
-          if constexpr (FUSED) {
-            float z0[3], y3[3];
-#pragma unroll
-            for (int i = 0; i < 3; ++i) {
-              z0[i] = bf2f(p.x[t * p.sx + 3 * (int64_t)c + i]);
-              y3[i] = short_out(zm2[i], zm1[i], z0[i], wsf[i]);
-              zm2[i] = zm1[i];
-              zm1[i] = z0[i];
-            }
-            x2 = y3[0];
-            u = rbf(y3[1] * y3[2]);
-          } else {
-            u = bf2f(p.x[t * p.sx + c]);
-          }
-        }
-        if constexpr (FUSED) {
-          if (t < S.a) {
-            // keep the short-filter window sliding through the left context
-#pragma unroll
-            for (int i = 0; i < 3; ++i) {
-              zm2[i] = zm1[i];
-              zm1[i] = z_at(ctx, t, 3 * (int64_t)c + i);
-            }
-          }
-        }
-      }
-      const int pos = static_cast<int>((t - S.t0 + G::KP) & (G::RING - 1));
-      ring[lane][pos] = f2bf(u);
-      if (keep_x2) x2s[lane][(t - S.t0) & (G::RS - 1)] = f2bf(x2);
+    for (int j = 0; j < (ZW + 3) / 4; ++j) {
+      const int cw = wave + 4 * j;  // wave-uniform
+      if (cw >= ZW) break;
+      const int i = cw * 64 + lane;
+      const int row = i / 24, col = i - 24 * (i / 24);
+      const int t = rs + row;
+      if (i < ZCH && t >= S.a && t < S.t_end)
+        __builtin_amdgcn_global_load_lds(
+            reinterpret_cast<const uint4 *>(p.x + (int64_t)t * p.sx + 3 * c0) + col,
+            (__attribute__((address_space(3))) void *)(&zst[0][0] + cw * 512), 16, 0, 0);
     }
   };
+  auto fix = [&](int rs) {
+    const bf16_t *conv = S.init ? p.cs + S.blk * p.cs0 : nullptr;
+    if (vec_z && rs >= S.a) return;  // uniform: nothing to patch
+#pragma unroll 1
+    for (int i = threadIdx.x; i < ZCH; i += 256) {
+      const int row = i / 24, col = i - 24 * (i / 24);
+      const int t = rs + row;
+      const bool inside = t >= S.a && t < S.t_end;
+      const bool left = t < S.a && t >= S.a - 2;
+      if ((vec_z && inside) || !(inside || left)) continue;
+#pragma unroll 1
+      for (int e = 0; e < 8; ++e) {
+        const int ch = 3 * c0 + 8 * col + e;
+        bf16_t b = 0;
+        if (ch < 3 * p.H) {
+          if (inside) b = p.x[(int64_t)t * p.sx + ch];
+          else if (conv) b = conv[ch * p.cs1 + (t - S.a + 2) * p.cs2];
+        }
+        zst[row][8 * col + e] = b;
+      }
+    }
+  };
+  auto land = [&]() { __builtin_amdgcn_s_waitcnt(0); };
 
-  // Halo: rows t0-KP .. t0-1, split over the four waves.
-  {
-    constexpr int per = G::KP / 4 > 0 ? G::KP / 4 : 1;
-    if (wave * per < G::KP) produce(S.t0 - G::KP + wave * per, min(per, G::KP - wave * per), false);
+  // ---- one row of u (and x2) at a segment or tile boundary, lane = channel:
+  // rows before the segment start take u from the inner window
+  // (continuation) or zero; rows at or past the tile end give zeros.
+  auto produce_row = [&](int t, int rs, bool keep_x2) {
+    float u = 0.0f, x2 = 0.0f;
+    if (t < S.a) {
+      const int col = (K - 1) + (t - S.a);
+      if (stc && col >= 0) u = stc[(int64_t)col * p.st2];
+    } else if (t < S.t_end) {
+      if constexpr (FUSED) {
+        float y3[3];
+        for (int i = 0; i < 3; ++i)
+          y3[i] = short_out(bf2f(zst[t - 2 - rs][3 * lane + i]), bf2f(zst[t - 1 - rs][3 * lane + i]),
+                            bf2f(zst[t - rs][3 * lane + i]), wsf[i]);
+        x2 = y3[0];
+        u = rbf(y3[1] * y3[2]);
+      } else {
+        u = active ? bf2f(p.x[(int64_t)t * p.sx + cl]) : 0.0f;
+      }
+    }
+    ring[lane][(t - S.t0 + G::KP) & (G::RING - 1)] = f2bf(u);
+    if (keep_x2) x2s[lane][(t - S.t0) & (G::RS - 1)] = f2bf(x2);
+  };
+
+  // ---- u (and x2) for NR consecutive rows [r0, r0 + NR) of this wave, lane =
+  // channel, written to the ring (and x2 buffer) as packed row pairs with
+  // b128 stores.  FUSED reads z from the staged rows (stage row of t is
+  // t - rs); U_IN loads u rows.  Groups touching a boundary go row by row.
+  auto produce = [&](int r0, int rs, auto nr_tag, bool keep_x2) {
+    constexpr int NR = decltype(nr_tag)::value;
+    static_assert(NR % 8 == 0, "rows are written as 8-row b128 groups");
+    if (!(r0 >= S.a && r0 + NR <= S.t_end)) {  // wave-uniform
+#pragma unroll 1
+      for (int r = 0; r < NR; ++r) produce_row(r0 + r, rs, keep_x2);
+      return;
+    }
+    uint32_t upk[NR / 2], xpk[NR / 2];
+    if constexpr (FUSED) {
+      const int rb = r0 - rs;
+      float zm2[3], zm1[3];
+#pragma unroll
+      for (int i = 0; i < 3; ++i) {
+        zm2[i] = bf2f(zst[rb - 2][3 * lane + i]);
+        zm1[i] = bf2f(zst[rb - 1][3 * lane + i]);
+      }
+#pragma unroll
+      for (int r = 0; r < NR; r += 2) {
+        float y[2][3];
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+#pragma unroll
+          for (int i = 0; i < 3; ++i) {
+            const float z0 = bf2f(zst[rb + r + q][3 * lane + i]);
+            float acc = wsf[i][0] * zm2[i];
+            acc = fmaf(wsf[i][1], zm1[i], acc);
+            y[q][i] = fmaf(wsf[i][2], z0, acc);
+            zm2[i] = zm1[i];
+            zm1[i] = z0;
+          }
+        }
+        const uint32_t px1 = cvt_pk(y[0][1], y[1][1]);
+        const uint32_t pv = cvt_pk(y[0][2], y[1][2]);
+        upk[r / 2] = cvt_pk(lo_bf(px1) * lo_bf(pv), hi_bf(px1) * hi_bf(pv));
+        xpk[r / 2] = cvt_pk(y[0][0], y[1][0]);
+      }
+    } else {
+      const bf16_t *xp = p.x + (int64_t)r0 * p.sx + cl;
+#pragma unroll
+      for (int r = 0; r < NR; r += 2) {
+        const uint32_t v0 = xp[(int64_t)r * p.sx], v1 = xp[(int64_t)(r + 1) * p.sx];
+        upk[r / 2] = active ? (v0 | (v1 << 16)) : 0u;
+        xpk[r / 2] = 0;
+      }
+    }
+    const int pos = (r0 - S.t0 + G::KP) & (G::RING - 1);
+#pragma unroll
+    for (int g = 0; g < NR / 8; ++g) {
+      *reinterpret_cast<uint4 *>(&ring[lane][(pos + 8 * g) & (G::RING - 1)]) =
+          make_uint4(upk[4 * g], upk[4 * g + 1], upk[4 * g + 2], upk[4 * g + 3]);
+      if (keep_x2)
+        *reinterpret_cast<uint4 *>(&x2s[lane][((r0 - S.t0) & (G::RS - 1)) + 8 * g]) =
+            make_uint4(xpk[4 * g], xpk[4 * g + 1], xpk[4 * g + 2], xpk[4 * g + 3]);
+    }
+  };
+  using R16 = std::integral_constant<int, 16>;
+  using R8 = std::integral_constant<int, 8>;
+
+  // ---- halo: rows t0-KP .. t0-1
+  if constexpr (G::KP == 128) {
+#pragma unroll 1
+    for (int h = 0; h < 2; ++h) {
+      const int rbase = S.t0 - G::KP + 64 * h;
+      if constexpr (FUSED) {
+        __syncthreads();
+        prefetch(rbase - 2);
+        land();
+        fix(rbase - 2);
+        __syncthreads();
+      }
+      produce(rbase + 16 * wave, rbase - 2, R16{}, false);
+    }
+  } else {
+    static_assert(G::KP == 8, "halo split assumes KP = 8 or 128");
+    const int rbase = S.t0 - G::KP;
+    if constexpr (FUSED) {
+      prefetch(rbase - 2);
+      land();
+      fix(rbase - 2);
+      __syncthreads();
+    }
+    if (wave == 0) produce(rbase, rbase - 2, R8{}, false);
+  }
+  if constexpr (FUSED) {
+    __syncthreads();
+    prefetch(S.t0 - 2);
+    land();
+    fix(S.t0 - 2);
+    __syncthreads();
   }
 
-  for (int64_t s0 = S.t0; s0 < S.t_end; s0 += G::RS) {
-    produce(s0 + wave * G::RW, G::RW, FUSED);
-    __syncthreads();
+  for (int s0 = S.t0; s0 < S.t_end; s0 += G::RS) {
+    produce(s0 + wave * G::RW, s0 - 2, R16{}, FUSED);
+    __syncthreads();  // ring / x2s complete; zst free
+    const bool more = s0 + G::RS < S.t_end;
+    if constexpr (FUSED) {
+      if (more) prefetch(s0 + G::RS - 2);
+    }
 
     // ---- FIR for rows s0 + 16*wave + r, r < 16
-    const int pbase = static_cast<int>(s0 - S.t0) + wave * G::RW;  // ring pos of row base
-    uint32_t E[G::NE];
-#pragma unroll
-    for (int q = 0; q < G::NE / 4; ++q) {
-      const uint4 v = *reinterpret_cast<const uint4 *>(&ring[lane][(pbase + 8 * q) & (G::RING - 1)]);
-      E[4 * q] = v.x; E[4 * q + 1] = v.y; E[4 * q + 2] = v.z; E[4 * q + 3] = v.w;
-    }
-#pragma unroll
-    for (int i = (G::NE / 4) * 4; i < G::NE; ++i)
-      E[i] = *reinterpret_cast<const uint32_t *>(&ring[lane][(pbase + 2 * i) & (G::RING - 1)]);
+    const int pbase = (s0 - S.t0) + wave * G::RW;  // ring pos of row base
+    // Tap pairs are consumed in order m = 0..NP-1.  At step m, row r reads
+    // window pair E[m + r/2 + 1] (odd r) or the pair re-aligned by one,
+    // O[m + r/2] = alignbit(E[m + r/2 + 1], E[m + r/2]) (even r); the eight
+    // O values in use slide by one per step, so each costs one alignbit.  The
+    // window is loaded per 16-step quarter and the steps are fenced in order,
+    // which keeps the live set to one quarter (otherwise the compiler runs
+    // each accumulator's whole chain in turn and holds the whole window).
+    constexpr int MQ = G::NP >= 16 ? 16 : G::NP;  // tap pairs per quarter
+    constexpr int EQ = MQ + G::RW / 2;            // window pairs per quarter
+    static_assert(EQ % 4 == 0, "window quarters are whole b128 loads");
     float acc[G::RW];
 #pragma unroll
     for (int r = 0; r < G::RW; ++r) acc[r] = 0.0f;
 #pragma unroll
-    for (int m = 0; m < G::NP; ++m) {
+    for (int m0 = 0; m0 < G::NP; m0 += MQ) {
+      uint32_t E[EQ];
 #pragma unroll
-      for (int r = 0; r < G::RW; r += 2) {
-        // row r (even) reads the odd-aligned pair starting at base+1+r+2m
-        const uint32_t o = __builtin_amdgcn_alignbit(E[r / 2 + m + 1], E[r / 2 + m], 16);
-        acc[r] = dot2(o, W[m], acc[r]);
-        acc[r + 1] = dot2(E[r / 2 + m + 1], W[m], acc[r + 1]);
+      for (int q = 0; q < EQ / 4; ++q) {
+        const uint4 v = *reinterpret_cast<const uint4 *>(
+            &ring[lane][(pbase + 2 * m0 + 8 * q) & (G::RING - 1)]);
+        E[4 * q] = v.x; E[4 * q + 1] = v.y; E[4 * q + 2] = v.z; E[4 * q + 3] = v.w;
+      }
+      uint32_t O[G::RW / 2];
+#pragma unroll
+      for (int j = 0; j < G::RW / 2 - 1; ++j) O[j] = __builtin_amdgcn_alignbit(E[j + 1], E[j], 16);
+#pragma unroll
+      for (int m = 0; m < MQ; ++m) {
+        O[G::RW / 2 - 1] = __builtin_amdgcn_alignbit(E[m + G::RW / 2], E[m + G::RW / 2 - 1], 16);
+        const uint32_t wm = W[m0 + m];
+#pragma unroll
+        for (int j = 0; j < G::RW / 2; ++j) {
+          acc[2 * j] = dot2(O[j], wm, acc[2 * j]);
+          acc[2 * j + 1] = dot2(E[m + j + 1], wm, acc[2 * j + 1]);
+        }
+#pragma unroll
+        for (int j = 0; j < G::RW / 2 - 1; ++j) O[j] = O[j + 1];
+        // Empty volatile asm on every accumulator: volatile statements keep
+        // their order, so step m+1 cannot start before step m is done.
+#pragma unroll
+        for (int r = 0; r < G::RW; ++r) asm volatile("" : "+v"(acc[r]));
       }
     }
 
-    // ---- epilogue: bf16(y) [+ D*u] then * x2; pair lanes to store dwords
-    uint32_t vals[G::RW];
+    // ---- epilogue on row pairs: bf16(y) [+ D*u] then * x2.
+    uint32_t xq[8], uq[8];
+    if constexpr (FUSED) {
+      const uint4 c4 = *reinterpret_cast<const uint4 *>(&ring[lane][(pbase + G::KP) & (G::RING - 1)]);
+      const uint4 d4 = *reinterpret_cast<const uint4 *>(&ring[lane][(pbase + G::KP + 8) & (G::RING - 1)]);
+      uq[0] = c4.x; uq[1] = c4.y; uq[2] = c4.z; uq[3] = c4.w;
+      uq[4] = d4.x; uq[5] = d4.y; uq[6] = d4.z; uq[7] = d4.w;
+      const uint4 a4 = *reinterpret_cast<const uint4 *>(&x2s[lane][wave * G::RW]);
+      const uint4 b4 = *reinterpret_cast<const uint4 *>(&x2s[lane][wave * G::RW + 8]);
+      xq[0] = a4.x; xq[1] = a4.y; xq[2] = a4.z; xq[3] = a4.w;
+      xq[4] = b4.x; xq[5] = b4.y; xq[6] = b4.z; xq[7] = b4.w;
+    }
     float dval = 0.0f;
-    if constexpr (HAS_D) dval = active ? bf2f(p.D[c]) : 0.0f;
-#pragma unroll
-    for (int r = 0; r < G::RW; ++r) {
-      float y = rbf(acc[r]);
-      if constexpr (FUSED) {
-        const int pos = pbase + G::KP + r;  // ring position of row t
-        const float u = bf2f(ring[lane][pos & (G::RING - 1)]);
-        if constexpr (HAS_D) y = rbf(y + rbf(dval * u));
-        y = bf2f(x2s[lane][(wave * G::RW + r) & (G::RS - 1)]) * y;
-      }
-      vals[r] = f2bf(y);
-    }
+    if constexpr (HAS_D) dval = bf2f(p.D[cl]);
     const bool odd = lane & 1;
+    const int cpair = c & ~1;
+    const int trow = s0 + wave * G::RW;
+    bf16_t *orow = p.out + (int64_t)trow * p.so + cpair;
 #pragma unroll
-    for (int r = 0; r < G::RW / 2; ++r) {
-      // even lanes keep rows 0..7 of the pair (c, c+1); odd lanes rows 8..15.
-      const uint32_t send = odd ? vals[r] : vals[r + G::RW / 2];
-      const uint32_t recv = __shfl_xor(send, 1);
-      const int rr = odd ? r + G::RW / 2 : r;
-      const uint32_t mine = vals[rr];
-      const uint32_t dw = odd ? (recv | (mine << 16)) : (mine | (recv << 16));
-      const int64_t t = s0 + wave * G::RW + rr;
-      const int cpair = c & ~1;
-      if (t < S.t_end && cpair < p.H)
-        *reinterpret_cast<uint32_t *>(p.out + t * p.so + cpair) = dw;
+    for (int r = 0; r < G::RW; r += 2) {
+      uint32_t py = cvt_pk(acc[r], acc[r + 1]);
+      if constexpr (FUSED) {
+        if constexpr (HAS_D) {
+          const uint32_t pu = uq[r / 2];
+          const uint32_t pd = cvt_pk(dval * lo_bf(pu), dval * hi_bf(pu));
+          py = cvt_pk(lo_bf(py) + lo_bf(pd), hi_bf(py) + hi_bf(pd));
+        }
+        const uint32_t px = xq[r / 2];
+        py = cvt_pk(lo_bf(px) * lo_bf(py), hi_bf(px) * hi_bf(py));
+      }
+      // py = (row r, row r+1) of channel c.  Even lanes store row r of the
+      // channel pair (c, c+1), odd lanes row r+1 of (c-1, c).
+      const uint32_t nb = __shfl_xor(py, 1);
+      const uint32_t dw = odd ? ((nb >> 16) | (py & 0xffff0000u)) : ((py & 0xffffu) | (nb << 16));
+      const int rr = r + (odd ? 1 : 0);
+      if (trow + rr < S.t_end && cpair < p.H)
+        *reinterpret_cast<uint32_t *>(orow + (int64_t)rr * p.so) = dw;
     }
-    __syncthreads();
+    if constexpr (FUSED) {
+      if (more) {
+        land();
+        fix(s0 + G::RS - 2);
+      }
+    }
+    __syncthreads();  // next produce may overwrite ring / x2s; zst committed
   }
 }
 
@@ -369,6 +544,8 @@ extern "C" int evo2_fir_prefill(const void *u, int64_t su, const void *w, int64_
             static_cast<const bf16_t *>(w), w0, w1, state, st0, st1, st2, nullptr,
             static_cast<bf16_t *>(out), so, seq_table, blocks, sblk, tile_table,
             static_cast<int>(H), block_t, num_blocks};
+  if (K == 128 && (w1 != 1 || w0 % 8 || reinterpret_cast<uintptr_t>(w) % 16))
+    return fail(EVO2_ERR_UNSUPPORTED, "fir_prefill: K=128 taps must be contiguous (H, 128) rows");
   if (ntiles) {
     if (K == 128) launch_fir<128, false, false>(a, ntiles, st);
     else launch_fir<7, false, false>(a, ntiles, st);
@@ -402,6 +579,8 @@ extern "C" int evo2_hyena_fir_prefill(const void *z, int64_t sz, const void *sho
             static_cast<const bf16_t *>(w), w0, w1, inner_state, st0, st1, st2,
             static_cast<const bf16_t *>(D), static_cast<bf16_t *>(out), so,
             seq_table, blocks, sblk, tile_table, static_cast<int>(H), block_t, num_blocks};
+  if (K == 128 && (w1 != 1 || w0 % 8 || reinterpret_cast<uintptr_t>(w) % 16))
+    return fail(EVO2_ERR_UNSUPPORTED, "hyena_fir_prefill: K=128 taps must be contiguous (H, 128) rows");
   if (ntiles) {
     const bool hasD = D != nullptr;
     if (K == 128) hasD ? launch_fir<128, true, true>(a, ntiles, st) : launch_fir<128, false, true>(a, ntiles, st);

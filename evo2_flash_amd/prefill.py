@@ -56,6 +56,7 @@ def fir_prefill(u, w, state, seq_table, blocks, tile_table, block_t):
         raise ValueError("u and w must be bf16, state fp32")
     _check_tables(seq_table, tile_table)
     blocks = blocks if blocks.dtype == torch.int32 else blocks.to(torch.int32)
+    w = w.contiguous()
     out = torch.empty(T, H, dtype=u.dtype, device=u.device)
     _lib.call(
         "evo2_fir_prefill",
@@ -90,6 +91,7 @@ def hyena_fir_prefill(z, short_w, conv_state, w, inner_state, D, seq_table, bloc
     if D is not None and (D.dtype != torch.bfloat16 or D.stride(0) != 1):
         D = D.to(torch.bfloat16).contiguous()
     blocks = blocks if blocks.dtype == torch.int32 else blocks.to(torch.int32)
+    w = w.contiguous()
     out = torch.empty(T, H, dtype=z.dtype, device=z.device)
     _lib.call(
         "evo2_hyena_fir_prefill",
