@@ -53,9 +53,37 @@ SIGNATURES = {
         _c_p, _c_i64, _c_i64, _c_i64,             # out, so, T, H
         _c_i64, _c_p,                             # num_blocks, stream
     ],
+    "evo2_hcl_workspace_bytes": [_c_i64, _c_i64],
+    "evo2_hyena_hcl_prefill": [
+        _c_p, _c_i64, _c_p,                       # z, sz, short_w
+        _c_p, _c_i64, _c_i64, _c_i64,             # conv_state + strides
+        _c_p, _c_i64, _c_i64,                     # residues + strides
+        _c_p, _c_i64, _c_i64,                     # log_poles + strides
+        _c_p, _c_i64, _c_i64, _c_i64,             # ssm + strides
+        _c_p,                                     # D
+        _c_p, _c_i64, _c_p, _c_i64,               # seq_table, nseq, blocks, sblk
+        _c_p, _c_i64, _c_p, _c_i32,               # tile_table, ntiles, tile_start, block_t
+        _c_p, _c_i64,                             # workspace, bytes
+        _c_p, _c_i64, _c_i64, _c_i64,             # out, so, T, H
+        _c_i64, _c_p,                             # num_blocks, stream
+    ],
+    "evo2_iir_segment": [
+        _c_p, _c_i64, _c_i64,                     # seq + strides
+        _c_p, _c_i64, _c_i64,                     # residues + strides
+        _c_p, _c_i64, _c_i64,                     # log_poles + strides
+        _c_p, _c_i64, _c_i64,                     # s_prev + strides
+        _c_p, _c_i64, _c_i64, _c_p,               # y + strides, st
+        _c_p, _c_i64,                             # workspace, bytes
+        _c_i64, _c_i64, _c_i32, _c_p,             # H, L, block_t, stream
+    ],
+    "evo2_hcl_compute_filter": [
+        _c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_i64,  # residues, log_poles + strides
+        _c_p, _c_i64, _c_p, _c_i64, _c_i64,           # t, st, h + strides
+        _c_i64, _c_i64, _c_i64, _c_p,                 # D, S, L, stream
+    ],
 }
 
-RESTYPES = {"evo2_last_error": ctypes.c_char_p}
+RESTYPES = {"evo2_last_error": ctypes.c_char_p, "evo2_hcl_workspace_bytes": ctypes.c_int64}
 
 _lock = threading.Lock()
 _lib = None

@@ -1,0 +1,492 @@
+// Hyena-LI (hcl) prefill for gfx950: the long convolution as a chunked modal
+// scan over 16 real poles per channel, replacing the reference's FFT
+// convolution with the modal filter plus closed-form final state
+// (mixers.py:144-210, triton_hcl.py:46-123, triton_prefill.py:351-387).
+//
+//   s_t = p (.) s_{t-1} + u_t,  y_t = sum_s r_s s_{t,s},  p = exp(lp)
+//
+// which equals the reference's y_t = (h * u)_t + sum_s r_s p_s^(t-a+1) s_{a-1,s}
+// with h_n = sum_s r_s p_s^n (mixers.py:150-155), and whose last state is the
+// reference's st = sum_t u_t p^(L-1-t) + p^L s_prev.
+//
+// Time is split into tiles of `block_t` rows (the same tile table as the FIR
+// prefill) so that the launch has parallelism beyond H/256 workgroups:
+//   phase 1  per tile, the end state of a scan started from zero;
+//   phase 2  per segment and channel, the carry into every tile
+//            C_j = p^(L_{j-1}) C_{j-1} + E_{j-1}, C_0 = the cached state
+//            (continuation) or 0; the segment's final state goes to the
+//            cache (mixers.py:1391-1394);
+//   phase 3  per tile, the scan again from its carry, the readout and the
+//            mixer tail g = bf16(bf16(bf16(y) + bf16(u D)) x2) (mixers.py:1397).
+// No workgroup waits on another, so the launch shape can never deadlock.
+//
+// Lanes run along channels (coalesced rows); a workgroup owns 256 channels
+// (4 waves) and sweeps its tile in 16-row sub-tiles staged into LDS with
+// direct-to-LDS loads, like the FIR prefill.
+#include <type_traits>
+
+#include "featurize.h"
+
+namespace evo2 {
+
+struct HclArgs {
+  const bf16_t *z; int64_t sz;              // (T, 3H) in_proj rows
+  const bf16_t *ws;                         // (3H, 3) short taps
+  const bf16_t *cs; int64_t cs0, cs1, cs2;  // conv window view (blocks, 3H, 2)
+  const float *res; int64_t r0, r1;         // residues (H, 16)
+  const float *lp; int64_t l0, l1;          // log-poles (H, 16)
+  float *ssm; int64_t m0, m1, m2;           // LI state view (blocks, H, 16)
+  const bf16_t *D;                          // (H,)
+  bf16_t *out; int64_t so;                  // g (T, H)
+  const int32_t *seq;                       // (n, 3) [start, end, has_init]
+  const int32_t *blocks; int64_t sblk;
+  const int32_t *tiles;                     // (ntiles, 2) [segment, first row]
+  const int32_t *tile_start;                // (n + 1) first tile of each segment
+  float *work;                              // (ntiles, H, 16) tile end states / carries
+  int H;
+  int block_t;
+  int64_t num_blocks;
+};
+
+constexpr int HCL_CH = 256;    // channels per workgroup (4 waves x 64 lanes)
+constexpr int HCL_RS = 16;     // rows per sub-tile
+constexpr int HCL_ZROWS = HCL_RS + 2;
+constexpr int HCL_ZPITCH = 3 * HCL_CH;  // bf16 per staged row, unpadded
+
+template <int PHASE>
+__global__ __launch_bounds__(256) void hcl_scan_kernel(HclArgs p) {
+  __shared__ __align__(16) bf16_t zst[HCL_ZROWS][HCL_ZPITCH];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int c0 = blockIdx.y * HCL_CH;
+  const int c = c0 + tid;  // lane = channel
+  const bool active = c < p.H;
+  const int cl = active ? c : p.H - 1;
+  const int seg = p.tiles[2 * blockIdx.x];
+  const int t0 = p.tiles[2 * blockIdx.x + 1];
+  const int a = p.seq[3 * seg], e = p.seq[3 * seg + 1];
+  const int64_t blk = p.blocks[seg * p.sblk];
+  const bool init = p.seq[3 * seg + 2] != 0 && blk >= 0 && blk < p.num_blocks;
+  const int t_end = min(t0 + p.block_t, e);
+  if (t0 >= t_end) return;  // uniform
+
+  float wsf[3][3];
+#pragma unroll
+  for (int i = 0; i < 3; ++i)
+#pragma unroll
+    for (int j = 0; j < 3; ++j) wsf[i][j] = bf2f(p.ws[(3 * (int64_t)cl + i) * 3 + j]);
+  float pole[16], res[16], s[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    pole[i] = expf(p.lp[(int64_t)cl * p.l0 + i * p.l1]);
+    res[i] = PHASE == 3 ? p.res[(int64_t)cl * p.r0 + i * p.r1] : 0.0f;
+    s[i] = PHASE == 3 ? p.work[((int64_t)blockIdx.x * p.H + cl) * 16 + i] : 0.0f;
+  }
+  const float dval = PHASE == 3 ? bf2f(p.D[cl]) : 0.0f;
+  const bool vec_z = (c0 + HCL_CH <= p.H) && (p.sz % 8 == 0) &&
+                     ((reinterpret_cast<uintptr_t>(p.z) & 15) == 0);
+  const bf16_t *conv = init ? p.cs + blk * p.cs0 : nullptr;
+
+  constexpr int ZCH = HCL_ZROWS * (HCL_ZPITCH / 8);  // 16-byte chunks per stage
+  constexpr int ZW = (ZCH + 63) / 64;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // stage rows [rs, rs + HCL_ZROWS): direct-to-LDS for interior rows, then
+  // element-wise left context / zeros (see the FIR prefill for the scheme).
+  auto stage = [&](int rs) {
+    if (vec_z) {
+#pragma unroll
+      for (int j = 0; j < (ZW + 3) / 4; ++j) {
+        const int cw = wave + 4 * j;
+        if (cw >= ZW) break;
+        const int i = cw * 64 + lane;
+        const int row = i / (HCL_ZPITCH / 8), col = i - (HCL_ZPITCH / 8) * row;
+        const int t = rs + row;
+        if (i < ZCH && t >= a && t < t_end)
+          __builtin_amdgcn_global_load_lds(
+              reinterpret_cast<const uint4 *>(p.z + (int64_t)t * p.sz + 3 * c0) + col,
+              (__attribute__((address_space(3))) void *)(&zst[0][0] + cw * 512), 16, 0, 0);
+      }
+      __builtin_amdgcn_s_waitcnt(0);
+    }
+    if (!vec_z || rs < a || rs + HCL_ZROWS > t_end) {
+#pragma unroll 1
+      for (int i = tid; i < ZCH; i += 256) {
+        const int row = i / (HCL_ZPITCH / 8), col = i - (HCL_ZPITCH / 8) * row;
+        const int t = rs + row;
+        const bool inside = t >= a && t < t_end;
+        if (vec_z && inside) continue;
+#pragma unroll 1
+        for (int q = 0; q < 8; ++q) {
+          const int ch = 3 * c0 + 8 * col + q;
+          bf16_t b = 0;
+          if (ch < 3 * p.H) {
+            if (inside) b = p.z[(int64_t)t * p.sz + ch];
+            else if (conv && t < a && t >= a - 2) b = conv[ch * p.cs1 + (t - a + 2) * p.cs2];
+          }
+          zst[row][8 * col + q] = b;
+        }
+      }
+    }
+  };
+
+  for (int s0 = t0; s0 < t_end; s0 += HCL_RS) {
+    __syncthreads();  // previous sub-tile's readers are done
+    stage(s0 - 2);
+    __syncthreads();
+    const int nr = min(HCL_RS, t_end - s0);
+    float zm2[3], zm1[3];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      zm2[i] = bf2f(zst[0][3 * tid + i]);
+      zm1[i] = bf2f(zst[1][3 * tid + i]);
+    }
+    uint32_t gpk[HCL_RS / 2];
+#pragma unroll
+    for (int r = 0; r < HCL_RS; r += 2) {
+      float ypair[2] = {0.f, 0.f}, upair[2], x2pair[2];
+      float yv[2][3];
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+          const float z0 = bf2f(zst[r + q + 2][3 * tid + i]);
+          float acc = wsf[i][0] * zm2[i];
+          acc = fmaf(wsf[i][1], zm1[i], acc);
+          yv[q][i] = fmaf(wsf[i][2], z0, acc);
+          zm2[i] = zm1[i];
+          zm1[i] = z0;
+        }
+      }
+      const uint32_t px1 = pack_bf(yv[0][1], yv[1][1]);
+      const uint32_t pv = pack_bf(yv[0][2], yv[1][2]);
+      upair[0] = rbf(lo_bf(px1) * lo_bf(pv));
+      upair[1] = rbf(hi_bf(px1) * hi_bf(pv));
+      x2pair[0] = rbf(yv[0][0]);
+      x2pair[1] = rbf(yv[1][0]);
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        if (r + q < nr) {  // uniform
+          float ya = 0.f, yb = 0.f, yc = 0.f, yd = 0.f;
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            s[i] = fmaf(pole[i], s[i], upair[q]);
+            if constexpr (PHASE == 3) {
+              if ((i & 3) == 0) ya = fmaf(res[i], s[i], ya);
+              if ((i & 3) == 1) yb = fmaf(res[i], s[i], yb);
+              if ((i & 3) == 2) yc = fmaf(res[i], s[i], yc);
+              if ((i & 3) == 3) yd = fmaf(res[i], s[i], yd);
+            }
+          }
+          ypair[q] = (ya + yb) + (yc + yd);
+        }
+      }
+      if constexpr (PHASE == 3) {
+        float g[2];
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          float y = rbf(ypair[q]);
+          y = rbf(y + rbf(upair[q] * dval));
+          g[q] = x2pair[q] * y;
+        }
+        gpk[r / 2] = pack_bf(g[0], g[1]);
+      }
+    }
+    if constexpr (PHASE == 3) {
+      // gpk[r/2] = (row r, row r+1) of channel c; even lanes store row r of
+      // the pair (c, c+1), odd lanes row r+1 of (c-1, c).
+      const bool odd = lane & 1;
+      const int cpair = c & ~1;
+      bf16_t *orow = p.out + (int64_t)s0 * p.so + cpair;
+#pragma unroll
+      for (int r = 0; r < HCL_RS; r += 2) {
+        const uint32_t py = gpk[r / 2];
+        const uint32_t nb = __shfl_xor(py, 1);
+        const uint32_t dw = odd ? ((nb >> 16) | (py & 0xffff0000u)) : ((py & 0xffffu) | (nb << 16));
+        const int rr = r + (odd ? 1 : 0);
+        if (rr < nr && cpair < p.H) *reinterpret_cast<uint32_t *>(orow + (int64_t)rr * p.so) = dw;
+      }
+    }
+  }
+  if constexpr (PHASE == 1) {
+    if (active) {
+      float4 *w = reinterpret_cast<float4 *>(p.work + ((int64_t)blockIdx.x * p.H + c) * 16);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) w[q] = make_float4(s[4 * q], s[4 * q + 1], s[4 * q + 2], s[4 * q + 3]);
+    }
+  }
+}
+
+// Phase 2: walk each segment's tiles in order, turning tile end states into
+// carries in place, and write the segment's final state to the cache.
+__global__ __launch_bounds__(64) void hcl_carry_kernel(HclArgs p) {
+  const int seg = blockIdx.x;
+  const int c = blockIdx.y * 64 + threadIdx.x;
+  if (c >= p.H) return;
+  const int a = p.seq[3 * seg], e = p.seq[3 * seg + 1];
+  if (e <= a) return;
+  const int64_t blk = p.blocks[seg * p.sblk];
+  if (blk < 0 || blk >= p.num_blocks) return;
+  const bool init = p.seq[3 * seg + 2] != 0;
+  float *st = p.ssm + blk * p.m0 + (int64_t)c * p.m1;
+  float S[16], lpv[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    S[i] = init ? st[i * p.m2] : 0.0f;
+    lpv[i] = p.lp[(int64_t)c * p.l0 + i * p.l1];
+  }
+  const int j0 = p.tile_start[seg], j1 = p.tile_start[seg + 1];
+  for (int j = j0; j < j1; ++j) {
+    const int tt0 = p.tiles[2 * j + 1];
+    const int len = min(tt0 + p.block_t, e) - tt0;
+    float4 *w = reinterpret_cast<float4 *>(p.work + ((int64_t)j * p.H + c) * 16);
+    float E[16];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float4 v = w[q];
+      E[4 * q] = v.x; E[4 * q + 1] = v.y; E[4 * q + 2] = v.z; E[4 * q + 3] = v.w;
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) w[q] = make_float4(S[4 * q], S[4 * q + 1], S[4 * q + 2], S[4 * q + 3]);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) S[i] = fmaf(expf(lpv[i] * static_cast<float>(len)), S[i], E[i]);
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) st[i * p.m2] = S[i];
+}
+
+// Conv window update for the LI prefill: same contract as the FIR window
+// kernel, conv slice only.
+__global__ __launch_bounds__(64) void hcl_conv_window_kernel(HclArgs p) {
+  const int seg = blockIdx.x;
+  const int c = blockIdx.y * 64 + threadIdx.x;
+  if (c >= p.H) return;
+  const int64_t a = p.seq[3 * seg], e = p.seq[3 * seg + 1];
+  if (e <= a) return;
+  const int64_t blk = p.blocks[seg * p.sblk];
+  if (blk < 0 || blk >= p.num_blocks) return;
+  const bool init = p.seq[3 * seg + 2] != 0;
+  bf16_t *cw = const_cast<bf16_t *>(p.cs) + blk * p.cs0;
+  for (int q = 0; q < 2; ++q) {
+    const int64_t src = e - 2 + q;
+    for (int i = 0; i < 3; ++i) {
+      const int64_t ch = 3 * (int64_t)c + i;
+      bf16_t v;
+      if (src >= a) v = p.z[src * p.sz + ch];
+      else v = init ? cw[ch * p.cs1 + (q + (e - a)) * p.cs2] : bf16_t(0);
+      cw[ch * p.cs1 + q * p.cs2] = v;
+    }
+  }
+}
+
+}  // namespace evo2
+
+using namespace evo2;
+
+extern "C" int64_t evo2_hcl_workspace_bytes(int64_t ntiles, int64_t H) {
+  return ntiles * H * 16 * static_cast<int64_t>(sizeof(float));
+}
+
+extern "C" int evo2_hyena_hcl_prefill(const void *z, int64_t sz, const void *short_w,
+                                      void *conv_state, int64_t cs0, int64_t cs1, int64_t cs2,
+                                      const float *residues, int64_t r0, int64_t r1,
+                                      const float *log_poles, int64_t l0, int64_t l1,
+                                      float *ssm, int64_t m0, int64_t m1, int64_t m2,
+                                      const void *D,
+                                      const int32_t *seq_table, int64_t nseq,
+                                      const int32_t *blocks, int64_t sblk,
+                                      const int32_t *tile_table, int64_t ntiles,
+                                      const int32_t *tile_start, int32_t block_t,
+                                      float *workspace, int64_t workspace_bytes,
+                                      void *out, int64_t so, int64_t T, int64_t H,
+                                      int64_t num_blocks, void *stream) {
+  if (T < 0 || H <= 0 || nseq < 0 || ntiles < 0 || num_blocks <= 0)
+    return fail(EVO2_ERR_INVALID, "hyena_hcl_prefill: bad sizes");
+  if (H % 2) return fail(EVO2_ERR_UNSUPPORTED, "hyena_hcl_prefill: H must be even");
+  if (block_t <= 0 || block_t % HCL_RS)
+    return fail(EVO2_ERR_INVALID, "hyena_hcl_prefill: block_t=%d must be a multiple of %d",
+                block_t, HCL_RS);
+  if (T == 0 || nseq == 0) return EVO2_OK;
+  if (!z || !short_w || !conv_state || !residues || !log_poles || !ssm || !D || !seq_table ||
+      !blocks || !out || !tile_start || (ntiles && (!tile_table || !workspace)))
+    return fail(EVO2_ERR_INVALID, "hyena_hcl_prefill: null pointer argument");
+  if (workspace_bytes < evo2_hcl_workspace_bytes(ntiles, H))
+    return fail(EVO2_ERR_INVALID, "hyena_hcl_prefill: workspace of %lld bytes, need %lld",
+                (long long)workspace_bytes, (long long)evo2_hcl_workspace_bytes(ntiles, H));
+  if (ntiles > 0x7fffffff || cdiv(H, HCL_CH) > 65535)
+    return fail(EVO2_ERR_UNSUPPORTED, "hyena_hcl_prefill: grid too large");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  HclArgs a{static_cast<const bf16_t *>(z), sz, static_cast<const bf16_t *>(short_w),
+            static_cast<const bf16_t *>(conv_state), cs0, cs1, cs2, residues, r0, r1,
+            log_poles, l0, l1, ssm, m0, m1, m2, static_cast<const bf16_t *>(D),
+            static_cast<bf16_t *>(out), so, seq_table, blocks, sblk, tile_table, tile_start,
+            workspace, static_cast<int>(H), block_t, num_blocks};
+  if (ntiles) {
+    dim3 grid(static_cast<unsigned>(ntiles), static_cast<unsigned>(cdiv(H, HCL_CH)));
+    hipLaunchKernelGGL(hcl_scan_kernel<1>, grid, dim3(256), 0, st, a);
+    int rc = check_launch("hcl phase 1");
+    if (rc) return rc;
+  }
+  dim3 sgrid(static_cast<unsigned>(nseq), static_cast<unsigned>(cdiv(H, 64)));
+  hipLaunchKernelGGL(hcl_carry_kernel, sgrid, dim3(64), 0, st, a);
+  int rc = check_launch("hcl phase 2");
+  if (rc) return rc;
+  if (ntiles) {
+    dim3 grid(static_cast<unsigned>(ntiles), static_cast<unsigned>(cdiv(H, HCL_CH)));
+    hipLaunchKernelGGL(hcl_scan_kernel<3>, grid, dim3(256), 0, st, a);
+    rc = check_launch("hcl phase 3");
+    if (rc) return rc;
+  }
+  hipLaunchKernelGGL(hcl_conv_window_kernel, sgrid, dim3(64), 0, st, a);
+  return check_launch("hcl conv window");
+}
+
+// ---------------------------------------------------------------------------
+// iir_segment (mixers.py:144-210): one segment of the LI recurrence over an
+// fp32 (H, L) input with any strides, from a cached state or zero.  Same
+// three phases as the mixer prefill, lane = channel, rows sequential per tile.
+namespace evo2 {
+
+struct IirArgs {
+  const float *x; int64_t xh, xl;           // seq (H, L)
+  const float *res; int64_t r0, r1;
+  const float *lp; int64_t l0, l1;
+  const float *sp; int64_t sp0, sp1;        // s_prev (H, 16) or null
+  float *y; int64_t yh, yl;                 // y (H, L)
+  float *st;                                // (H, 16) contiguous final state
+  float *work;                              // (ntiles, H, 16)
+  int H, L, block_t, ntiles;
+};
+
+template <int PHASE>
+__global__ __launch_bounds__(256) void iir_scan_kernel(IirArgs p) {
+  const int c = blockIdx.y * 256 + threadIdx.x;
+  if (c >= p.H) return;
+  const int j = blockIdx.x;
+  const int t0 = j * p.block_t, t1 = min(t0 + p.block_t, p.L);
+  float pole[16], res[16], s[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    pole[i] = expf(p.lp[(int64_t)c * p.l0 + i * p.l1]);
+    res[i] = p.res[(int64_t)c * p.r0 + i * p.r1];
+    s[i] = PHASE == 3 ? p.work[((int64_t)j * p.H + c) * 16 + i] : 0.0f;
+  }
+  const float *xr = p.x + (int64_t)c * p.xh;
+  float *yr = p.y + (int64_t)c * p.yh;
+#pragma unroll 4
+  for (int t = t0; t < t1; ++t) {
+    const float u = xr[(int64_t)t * p.xl];
+    float ya = 0.f, yb = 0.f, yc = 0.f, yd = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      s[i] = fmaf(pole[i], s[i], u);
+      if (PHASE == 3) {
+        if ((i & 3) == 0) ya = fmaf(res[i], s[i], ya);
+        if ((i & 3) == 1) yb = fmaf(res[i], s[i], yb);
+        if ((i & 3) == 2) yc = fmaf(res[i], s[i], yc);
+        if ((i & 3) == 3) yd = fmaf(res[i], s[i], yd);
+      }
+    }
+    if (PHASE == 3) yr[(int64_t)t * p.yl] = (ya + yb) + (yc + yd);
+  }
+  if (PHASE == 1) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) p.work[((int64_t)j * p.H + c) * 16 + i] = s[i];
+  }
+}
+
+__global__ __launch_bounds__(64) void iir_carry_kernel(IirArgs p) {
+  const int c = blockIdx.x * 64 + threadIdx.x;
+  if (c >= p.H) return;
+  float S[16], lpv[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    S[i] = p.sp ? p.sp[(int64_t)c * p.sp0 + i * p.sp1] : 0.0f;
+    lpv[i] = p.lp[(int64_t)c * p.l0 + i * p.l1];
+  }
+  for (int j = 0; j < p.ntiles; ++j) {
+    const int len = min((j + 1) * p.block_t, p.L) - j * p.block_t;
+    float *w = p.work + ((int64_t)j * p.H + c) * 16;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float E = w[i];
+      w[i] = S[i];
+      S[i] = fmaf(expf(lpv[i] * static_cast<float>(len)), S[i], E);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) p.st[(int64_t)c * 16 + i] = S[i];
+}
+
+// h[d, l] = sum_s residues[d, s] * exp(log_poles[d, s] * t[l])  (triton_hcl.py:46-74)
+__global__ __launch_bounds__(256) void hcl_filter_kernel(const float *res, int64_t r0, int64_t r1,
+                                                         const float *lp, int64_t l0, int64_t l1,
+                                                         const float *t, int64_t st,
+                                                         float *h, int64_t h0, int64_t h1,
+                                                         int D, int S, int L) {
+  const int l = blockIdx.x * 256 + threadIdx.x;
+  const int d = blockIdx.y;
+  if (l >= L) return;
+  const float tv = t[(int64_t)l * st];
+  float acc = 0.0f;
+  for (int s = 0; s < S; ++s)
+    acc = fmaf(res[(int64_t)d * r0 + s * r1], expf(lp[(int64_t)d * l0 + s * l1] * tv), acc);
+  h[(int64_t)d * h0 + (int64_t)l * h1] = acc;
+}
+
+}  // namespace evo2
+
+extern "C" int evo2_iir_segment(const float *seq, int64_t xh, int64_t xl,
+                                const float *residues, int64_t r0, int64_t r1,
+                                const float *log_poles, int64_t l0, int64_t l1,
+                                const float *s_prev, int64_t sp0, int64_t sp1,
+                                float *y, int64_t yh, int64_t yl, float *st,
+                                float *workspace, int64_t workspace_bytes,
+                                int64_t H, int64_t L, int32_t block_t, void *stream) {
+  if (H <= 0 || L < 0 || block_t <= 0)
+    return fail(EVO2_ERR_INVALID, "iir_segment: bad sizes H=%lld L=%lld block_t=%d",
+                (long long)H, (long long)L, block_t);
+  const int64_t ntiles = cdiv(L, block_t);
+  if (!seq || !residues || !log_poles || !y || !st || (ntiles && !workspace))
+    return fail(EVO2_ERR_INVALID, "iir_segment: null pointer argument");
+  if (workspace_bytes < evo2_hcl_workspace_bytes(ntiles, H))
+    return fail(EVO2_ERR_INVALID, "iir_segment: workspace too small");
+  if (ntiles > 65535 || L > 0x7fffffff)
+    return fail(EVO2_ERR_UNSUPPORTED, "iir_segment: L=%lld too long for block_t=%d",
+                (long long)L, block_t);
+  hipStream_t strm = static_cast<hipStream_t>(stream);
+  IirArgs a{seq, xh, xl, residues, r0, r1, log_poles, l0, l1, s_prev, sp0, sp1, y, yh, yl, st,
+            workspace, static_cast<int>(H), static_cast<int>(L), block_t,
+            static_cast<int>(ntiles)};
+  dim3 grid(static_cast<unsigned>(ntiles), static_cast<unsigned>(cdiv(H, 256)));
+  if (ntiles) {
+    hipLaunchKernelGGL(iir_scan_kernel<1>, grid, dim3(256), 0, strm, a);
+    int rc = check_launch("iir_segment phase 1");
+    if (rc) return rc;
+  }
+  hipLaunchKernelGGL(iir_carry_kernel, dim3(static_cast<unsigned>(cdiv(H, 64))), dim3(64), 0, strm, a);
+  int rc = check_launch("iir_segment phase 2");
+  if (rc) return rc;
+  if (ntiles) {
+    hipLaunchKernelGGL(iir_scan_kernel<3>, grid, dim3(256), 0, strm, a);
+    rc = check_launch("iir_segment phase 3");
+  }
+  return rc;
+}
+
+extern "C" int evo2_hcl_compute_filter(const float *residues, int64_t r0, int64_t r1,
+                                       const float *log_poles, int64_t l0, int64_t l1,
+                                       const float *t, int64_t st, float *h, int64_t h0, int64_t h1,
+                                       int64_t D, int64_t S, int64_t L, void *stream) {
+  if (D <= 0 || S <= 0 || L < 0 || D > 65535)
+    return fail(EVO2_ERR_INVALID, "hcl_compute_filter: bad sizes D=%lld S=%lld L=%lld",
+                (long long)D, (long long)S, (long long)L);
+  if (L == 0) return EVO2_OK;
+  if (!residues || !log_poles || !t || !h)
+    return fail(EVO2_ERR_INVALID, "hcl_compute_filter: null pointer argument");
+  dim3 grid(static_cast<unsigned>(cdiv(L, 256)), static_cast<unsigned>(D));
+  hipLaunchKernelGGL(hcl_filter_kernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream),
+                     residues, r0, r1, log_poles, l0, l1, t, st, h, h0, h1,
+                     static_cast<int>(D), static_cast<int>(S), static_cast<int>(L));
+  return check_launch("hcl_compute_filter");
+}

@@ -115,6 +115,68 @@ int evo2_hyena_fir_prefill(const void *z, int64_t sz, const void *short_w,
                            void *out, int64_t so, int64_t T, int64_t H,
                            int64_t num_blocks, void *stream);
 
+/*
+ * Bytes of workspace the LI prefill needs: one (H, 16) fp32 state per tile.
+ */
+int64_t evo2_hcl_workspace_bytes(int64_t ntiles, int64_t H);
+
+/*
+ * Fused Hyena LI (hcl) mixer prefill between in_proj and out_proj:
+ * z -> short K=3 filter -> u = x1*v -> s_t = p*s_{t-1} + u_t over 16 real
+ * poles p = exp(log_poles) (state from `ssm` when a segment continues) ->
+ * y_t = sum_s r_s s_t -> g = bf16(bf16(bf16(y) + bf16(u*D)) * x2).  Writes
+ * each segment's final state to `ssm` and its conv window.
+ *
+ * Replaces the prefill rows of HyenaIIRMixer._forward_impl
+ * (evo2_flash/mixers.py:1327-1401): iir_segment's FFT convolution and
+ * closed-form final state (mixers.py:144-210), hcl_compute_filter
+ * (triton_hcl.py:88-123) and iir_final_state (triton_prefill.py:351-387).
+ *
+ *   residues, log_poles (H, 16) fp32      ssm (blocks, H, 16) fp32 view
+ *   tile_start (nseq + 1) int32: index of each segment's first tile
+ *   workspace  >= evo2_hcl_workspace_bytes(ntiles, H) bytes of device memory
+ *   other arguments as evo2_hyena_fir_prefill; block_t a multiple of 16.
+ */
+int evo2_hyena_hcl_prefill(const void *z, int64_t sz, const void *short_w,
+                           void *conv_state, int64_t cs0, int64_t cs1, int64_t cs2,
+                           const float *residues, int64_t r0, int64_t r1,
+                           const float *log_poles, int64_t l0, int64_t l1,
+                           float *ssm, int64_t m0, int64_t m1, int64_t m2,
+                           const void *D,
+                           const int32_t *seq_table, int64_t nseq,
+                           const int32_t *blocks, int64_t sblk,
+                           const int32_t *tile_table, int64_t ntiles,
+                           const int32_t *tile_start, int32_t block_t,
+                           float *workspace, int64_t workspace_bytes,
+                           void *out, int64_t so, int64_t T, int64_t H,
+                           int64_t num_blocks, void *stream);
+
+/*
+ * One prefill segment of the LI recurrence s_t = p*s_{t-1} + x_t:
+ * y (H, L) fp32 and the final state st (H, 16) fp32 (contiguous), from
+ * s_prev (H, 16) or zero (NULL).  seq is (H, L) fp32 with any strides.
+ *
+ * Replaces iir_segment (evo2_flash/mixers.py:144-210).
+ */
+int evo2_iir_segment(const float *seq, int64_t xh, int64_t xl,
+                     const float *residues, int64_t r0, int64_t r1,
+                     const float *log_poles, int64_t l0, int64_t l1,
+                     const float *s_prev, int64_t sp0, int64_t sp1,
+                     float *y, int64_t yh, int64_t yl, float *st,
+                     float *workspace, int64_t workspace_bytes,
+                     int64_t H, int64_t L, int32_t block_t, void *stream);
+
+/*
+ * Modal filter h[d, l] = sum_s residues[d, s] * exp(log_poles[d, s] * t[l]).
+ *
+ * Replaces hcl_compute_filter / _hcl_compute_filter_kernel
+ * (evo2_flash/triton_hcl.py:46-123).
+ */
+int evo2_hcl_compute_filter(const float *residues, int64_t r0, int64_t r1,
+                            const float *log_poles, int64_t l0, int64_t l1,
+                            const float *t, int64_t st, float *h, int64_t h0, int64_t h1,
+                            int64_t D, int64_t S, int64_t L, void *stream);
+
 #ifdef __cplusplus
 }
 #endif
