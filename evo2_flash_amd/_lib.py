@@ -81,6 +81,13 @@ SIGNATURES = {
         _c_p, _c_i64, _c_p, _c_i64, _c_i64,           # t, st, h + strides
         _c_i64, _c_i64, _c_i64, _c_p,                 # D, S, L, stream
     ],
+    "evo2_fp8_quantize": [_c_p, _c_i64, _c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_p],
+    "evo2_fp8_gemm": [
+        _c_p, _c_i64, _c_p, _c_i64,               # x8, sx, w8, sw
+        _c_p, _c_p, _c_p,                         # x_scale, w_scale, bias
+        _c_p, _c_i64, _c_i64, _c_i64, _c_i64,     # out, so, M, N, K
+        _c_p,                                     # stream
+    ],
 }
 
 RESTYPES = {"evo2_last_error": ctypes.c_char_p, "evo2_hcl_workspace_bytes": ctypes.c_int64}

@@ -1,0 +1,91 @@
+"""fp8 e4m3 projections on gfx950 MFMA (static per-tensor scales, fp32 accumulate).
+
+The reference's in_proj is vLLM's static W8A8 `ReplicatedLinear` built from
+`Fp8Config(is_checkpoint_fp8_serialized=True, activation_scheme="static")`
+(mixers.py:741-757, 780-783): x is quantised as e4m3fn(clamp(x / input_scale,
++-448)) (fp8_emul.py:76-78), multiplied by the e4m3 weight with fp32
+accumulation, and scaled by input_scale * weight_scale (dequantisation
+convention, convert.py:195-201).  The checkpoint tensors are
+`in_proj.weight` (3H, H) float8_e4m3fn, `in_proj.weight_scale` (1,) and
+`in_proj.input_scale` (1,).  Kernels: csrc/fp8_gemm.hip.
+"""
+
+import torch
+from torch import nn
+
+from . import _lib
+
+FP8_MAX = 448.0
+E4M3 = torch.float8_e4m3fn
+
+
+def quantize_input(x, input_scale):
+    """e4m3fn(clamp(x / input_scale, -448, 448)) of a (..., K) bf16 tensor."""
+    _lib.require_device(x, input_scale)
+    K = x.shape[-1]
+    x2 = x.reshape(-1, K)
+    if x2.stride(-1) != 1 or x2.dtype != torch.bfloat16:
+        x2 = x2.to(torch.bfloat16).contiguous()
+    scale = input_scale.to(torch.float32).reshape(1)
+    q = torch.empty(x2.shape, dtype=E4M3, device=x.device)
+    _lib.call("evo2_fp8_quantize", _lib.ptr(x2), x2.stride(0), _lib.ptr(q), q.stride(0),
+              _lib.ptr(scale), x2.shape[0], K, _lib.stream_of(x))
+    return q.reshape(x.shape)
+
+
+def fp8_gemm(x8, w8, x_scale, w_scale, bias=None, out=None):
+    """bf16((x8 @ w8^T) * x_scale * w_scale [+ bias]) with x8 (M, K), w8 (N, K) e4m3."""
+    _lib.require_device(x8, w8, x_scale, w_scale, bias)
+    if x8.dtype != E4M3 or w8.dtype != E4M3:
+        raise ValueError("fp8_gemm operands must be float8_e4m3fn")
+    M, K = x8.shape
+    N, K2 = w8.shape
+    if K != K2:
+        raise ValueError(f"K mismatch: {K} vs {K2}")
+    if x8.stride(1) != 1:
+        x8 = x8.contiguous()
+    if w8.stride(1) != 1:
+        w8 = w8.contiguous()
+    xs = x_scale.to(torch.float32).reshape(1)
+    ws = w_scale.to(torch.float32).reshape(1)
+    if bias is not None:
+        bias = bias.to(torch.bfloat16).contiguous()
+    if out is None:
+        out = torch.empty(M, N, dtype=torch.bfloat16, device=x8.device)
+    _lib.call("evo2_fp8_gemm", _lib.ptr(x8), x8.stride(0), _lib.ptr(w8), w8.stride(0),
+              _lib.ptr(xs), _lib.ptr(ws), _lib.ptr(bias), _lib.ptr(out), out.stride(0),
+              M, N, K, _lib.stream_of(x8))
+    return out
+
+
+def static_fp8_linear(x, weight, input_scale, weight_scale, bias=None):
+    """vLLM's static W8A8 linear: (..., K) bf16 -> (..., N) bf16."""
+    K = x.shape[-1]
+    x8 = quantize_input(x.reshape(-1, K), input_scale)
+    out = fp8_gemm(x8, weight, input_scale, weight_scale, bias)
+    return out.reshape(*x.shape[:-1], weight.shape[0])
+
+
+class Fp8StaticLinear(nn.Module):
+    """Replicated static-W8A8 linear with the checkpoint's tensor names.
+
+    `forward(x) -> (y, None)` like vLLM's ReplicatedLinear, so mixer code and
+    forward hooks see the projection output unchanged.
+    """
+
+    def __init__(self, in_features, out_features, bias=False, device=None):
+        super().__init__()
+        self.in_features = in_features
+        self.out_features = out_features
+        self.weight = nn.Parameter(torch.empty(out_features, in_features, dtype=E4M3,
+                                               device=device), requires_grad=False)
+        self.weight_scale = nn.Parameter(torch.ones(1, dtype=torch.float32, device=device),
+                                         requires_grad=False)
+        self.input_scale = nn.Parameter(torch.ones(1, dtype=torch.float32, device=device),
+                                        requires_grad=False)
+        self.bias = (nn.Parameter(torch.zeros(out_features, dtype=torch.bfloat16, device=device),
+                                  requires_grad=False) if bias else None)
+
+    def forward(self, x):
+        return static_fp8_linear(x, self.weight, self.input_scale, self.weight_scale,
+                                 self.bias), None

@@ -177,6 +177,32 @@ int evo2_hcl_compute_filter(const float *residues, int64_t r0, int64_t r1,
                             const float *t, int64_t st, float *h, int64_t h0, int64_t h1,
                             int64_t D, int64_t S, int64_t L, void *stream);
 
+/*
+ * Static per-tensor activation quantisation for the fp8 projections:
+ * q = e4m3fn(clamp(x / scale[0], -448, 448)), round to nearest even.
+ *   x (rows, K) bf16, row stride sx; q (rows, K) e4m3 bytes, row stride sq.
+ *
+ * Replaces the activation side of vLLM's static fp8 linear
+ * (evo2_flash/fp8_emul.py:76-78 states the same contract).
+ */
+int evo2_fp8_quantize(const void *x, int64_t sx, void *q, int64_t sq,
+                      const float *scale, int64_t rows, int64_t K, void *stream);
+
+/*
+ * fp8 e4m3 GEMM on MFMA with fp32 accumulation:
+ * out[m, n] = bf16((sum_k x8[m, k] w8[n, k]) * x_scale[0] * w_scale[0] [+ bias[n]]).
+ *   x8 (M, K), w8 (N, K) e4m3 bytes with 16-byte aligned rows (strides in
+ *   bytes); bias (N,) bf16 or NULL; out (M, N) bf16, row stride so.
+ *   K must be a multiple of 128.
+ *
+ * Replaces the in_proj GEMM of vLLM's static W8A8 ReplicatedLinear
+ * (evo2_flash/mixers.py:741-757, 1076-1092) and, when quantised, out_proj
+ * (mixers.py:801-803).
+ */
+int evo2_fp8_gemm(const void *x8, int64_t sx, const void *w8, int64_t sw,
+                  const float *x_scale, const float *w_scale, const void *bias,
+                  void *out, int64_t so, int64_t M, int64_t N, int64_t K, void *stream);
+
 #ifdef __cplusplus
 }
 #endif
