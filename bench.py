@@ -1,21 +1,28 @@
 #!/usr/bin/env python3
 """Throughput of the Evo 2 Hyena mixer hot path on one MI355X.
 
-Workload (the headline): 7B-shaped decode, the 27 Hyena mixers of the 7B
-layer map (9 hcs, 9 hcm, 9 hcl; H=4096), batch 64, paged state in a
+Headline workload (`value`): 7B-shaped decode -- the 27 Hyena mixers of the
+7B layer map (9 hcs, 9 hcm, 9 hcl; H=4096), batch 64, paged state in a
 vLLM-layout pool with a seeded random slot table.  One step = one token for
-all 64 sequences through every mixer.  Inputs are resident in HBM before the
-timed region.  Prints one JSON line.
+all 64 sequences through every mixer core (the fused decode kernel).  Inputs
+are resident in HBM before the timed region.
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu]
+Also measured in the same run and reported in the same JSON line:
+  * prefill: the 27 mixer cores over one 32768-token sequence (fused
+    featurizer + FIR / modal scan + gate per layer), tokens/s;
+  * fp8: the e4m3 projection GEMMs M=8192, K=4096 -> N=12288 and N=4096,
+    TFLOP/s against the dense fp8 MFMA peak;
+  * roofline of the dominant decode kernel (hcm) from HIP events on the
+    stream it is launched on, and the CPU baseline: the oracle's restatement
+    of the reference torch decode path timed on the host cores.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--no-prefill] [--no-gemm]
 """
 
 import argparse
 import json
 import os
-import platform
 import statistics
-import subprocess
 import sys
 import time
 
@@ -26,12 +33,15 @@ import torch  # noqa: E402
 
 H_7B = 4096
 B_DECODE = 64
-LAYER_MAP_7B = {  # evo2_configs/evo2-7b-1m.yml:7-10
+L_PREFILL = 32768
+LAYER_MAP_7B = {  # evo2_configs/evo2-7b-1m.yml:7-9
     "hcs": [0, 4, 7, 11, 14, 18, 21, 25, 28],
     "hcm": [1, 5, 8, 12, 15, 19, 22, 26, 29],
     "hcl": [2, 6, 9, 13, 16, 20, 23, 27, 30],
 }
 HBM_PEAK_GBS = 8000.0
+FP8_PEAK_TFLOPS = 5000.0
+METRIC = "decode tok/s (7B-shape, bs=64) + prefill tok/s at 32k; % HBM/MFMA roofline"
 
 
 def decode_bytes_per_launch(kind, B, H):
@@ -49,6 +59,29 @@ def decode_bytes_per_launch(kind, B, H):
     return B * (conv + inner + z_out) + params
 
 
+def prefill_bytes(T, H):
+    """Fused minimum of one mixer-core prefill: read z (T, 3H) bf16 once and
+    write g (T, H) bf16 once; state and parameter bytes are < 0.1% and left out."""
+    return T * 3 * H * 2 + T * H * 2
+
+
+def _timed(fn, reps, stream):
+    """Average and median duration (us) of fn() over reps launches, each
+    bracketed by HIP events on `stream` (the stream the kernels run on)."""
+    evs = []
+    for _ in range(reps):
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        fn()
+        b.record(stream)
+        evs.append((a, b))
+    torch.cuda.synchronize()
+    d = [a.elapsed_time(b) * 1e3 for a, b in evs]
+    return statistics.mean(d), statistics.median(d)
+
+
+# ---------------------------------------------------------------- decode
 class DecodeLayer:
     def __init__(self, kind, idx, H, B, dev, seed):
         from evo2_flash_amd.state import HyenaStatePool
@@ -67,12 +100,8 @@ class DecodeLayer:
             self.lp = None
         self.pool = HyenaStatePool(B + 1, H, dev)
         g = torch.Generator(device=dev).manual_seed(seed + 1000 + idx)
-        self.pool.kv_cache[0].copy_(torch.randn(self.pool.kv_cache[0].shape, generator=g,
-                                                device=dev).to(torch.bfloat16))
-        self.pool.kv_cache[1].copy_(torch.randn(self.pool.kv_cache[1].shape, generator=g,
-                                                device=dev))
-        self.pool.kv_cache[2].copy_(torch.randn(self.pool.kv_cache[2].shape, generator=g,
-                                                device=dev))
+        for s in self.pool.kv_cache:
+            s.copy_(torch.randn(s.shape, generator=g, device=dev).to(s.dtype))
         self.state = (self.pool.ssm_view() if kind == "hcl"
                       else self.pool.inner_view(self.inner.shape[1] - 1))
         self.slots = random_slot_table(B, B + 1, seed + 2000 + idx, device=dev)
@@ -93,37 +122,115 @@ def bench_decode(steps, warmup, dev, seed=1234):
         for L in layers:
             L.step()
     torch.cuda.synchronize()
-
     stream = torch.cuda.current_stream()
-    ev = {k: [] for k in LAYER_MAP_7B}
+    # whole-step wall clock: every layer back to back, no per-launch events
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
     t0.record(stream)
     for _ in range(steps):
         for L in layers:
-            a = torch.cuda.Event(enable_timing=True)
-            b = torch.cuda.Event(enable_timing=True)
-            a.record(stream)
             L.step()
-            b.record(stream)
-            ev[L.kind].append((a, b))
     t1.record(stream)
     torch.cuda.synchronize()
-    total_ms = t0.elapsed_time(t1)
+    ms_per_step = t0.elapsed_time(t1) / steps
+    # per-kind kernel durations, each launch bracketed by events
     per_kind = {}
-    for k, pairs in ev.items():
-        durs = [a.elapsed_time(b) * 1e3 for a, b in pairs]  # us
-        nbytes = decode_bytes_per_launch(k, B, H)
-        avg = statistics.mean(durs)
-        per_kind[k] = {"avg_us": round(avg, 3), "median_us": round(statistics.median(durs), 3),
-                       "bytes_per_launch": nbytes,
-                       "achieved_GBs": round(nbytes / (avg * 1e-6) / 1e9, 1)}
-    ms_per_step = total_ms / steps
+    for kind in LAYER_MAP_7B:
+        Ls = [L for L in layers if L.kind == kind]
+        it = iter(range(10 ** 9))
+        avg, med = _timed(lambda: Ls[next(it) % len(Ls)].step(), steps * len(Ls), stream)
+        nbytes = decode_bytes_per_launch(kind, B, H)
+        per_kind[kind] = {"avg_us": round(avg, 3), "median_us": round(med, 3),
+                          "bytes_per_launch": nbytes,
+                          "achieved_GBs": round(nbytes / (avg * 1e-6) / 1e9, 1),
+                          "frac": round(nbytes / (avg * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    ideal_us = 9 * sum(decode_bytes_per_launch(k, B, H) for k in LAYER_MAP_7B) / (HBM_PEAK_GBS * 1e3)
+    kern_us = 9 * sum(v["avg_us"] for v in per_kind.values())
     return {"ms_per_step": ms_per_step, "tok_s": B / (ms_per_step * 1e-3), "per_kind": per_kind,
-            "layers": len(layers)}
+            "layers": len(layers), "kernel_us_per_step": round(kern_us, 2),
+            "ideal_us_per_step": round(ideal_us, 2),
+            "mixer_frac": round(ideal_us / kern_us, 4)}
 
 
+# ---------------------------------------------------------------- prefill
+def bench_prefill(reps, dev, L=L_PREFILL, H=H_7B, seed=77):
+    """One fresh L-token sequence through one mixer core of each kind; the
+    27-layer step is 9 x (hcs + hcm + hcl)."""
+    from evo2_flash_amd.hcl import hcl_block_t, hyena_hcl_prefill
+    from evo2_flash_amd.metadata import build_metadata, prefill_tables
+    from evo2_flash_amd.prefill import fir_prefill_block_t, hyena_fir_prefill
+    from evo2_flash_amd.state import HyenaStatePool
+    from evo2_flash_amd.synthetic import mixer_params
+
+    g = torch.Generator(device=dev).manual_seed(seed)
+    z = (torch.randn(L, 3 * H, generator=g, device=dev) * 1.3).to(torch.bfloat16)
+    m = build_metadata(prefill_lens=[L], prefill_slots=[1], has_init=[0], device=dev)
+    pool = HyenaStatePool(2, H, dev)
+    stream = torch.cuda.current_stream()
+    res = {}
+    for kind in ("hcs", "hcm", "hcl"):
+        prm = mixer_params(kind, H, seed, device=dev, in_proj_fp8=False)
+        sw = prm["short_filter"].view(3 * H, 3)
+        if kind == "hcl":
+            bt = hcl_block_t(L, H)
+            seq_t, til_t, ts_t = prefill_tables(m, bt, dev)
+
+            def fn(prm=prm, sw=sw, bt=bt, seq_t=seq_t, til_t=til_t, ts_t=ts_t):
+                return hyena_hcl_prefill(z, sw, pool.conv_view(), prm["residues"],
+                                         prm["log_poles"][..., 0], pool.ssm_view(), prm["D"],
+                                         seq_t, m.state_indices_tensor_p, til_t, ts_t, bt)
+        else:
+            K = prm["conv"].shape[-1]
+            bt = fir_prefill_block_t(K, L, H)
+            seq_t, til_t, _ = prefill_tables(m, bt, dev)
+            w = prm["conv"].view(H, K)
+
+            def fn(prm=prm, sw=sw, bt=bt, seq_t=seq_t, til_t=til_t, w=w, K=K):
+                return hyena_fir_prefill(z, sw, pool.conv_view(), w, pool.inner_view(K - 1),
+                                         prm.get("D"), seq_t, m.state_indices_tensor_p, til_t, bt)
+        fn()
+        torch.cuda.synchronize()
+        avg, med = _timed(fn, reps, stream)
+        nbytes = prefill_bytes(L, H)
+        res[kind] = {"avg_us": round(avg, 2), "median_us": round(med, 2), "block_t": bt,
+                     "bytes": nbytes, "achieved_GBs": round(nbytes / (avg * 1e-6) / 1e9, 1),
+                     "frac": round(nbytes / (avg * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    step_us = 9 * sum(v["avg_us"] for v in res.values())
+    ideal_us = 27 * prefill_bytes(L, H) / (HBM_PEAK_GBS * 1e3)
+    del z
+    return {"tok_s": round(L / (step_us * 1e-6), 1), "us_per_step": round(step_us, 1),
+            "L": L, "mixer_frac": round(ideal_us / step_us, 4), "per_kind": res}
+
+
+# ---------------------------------------------------------------- fp8 GEMMs
+def bench_gemm(reps, dev, M=8192, K=4096, seed=5):
+    from evo2_flash_amd.fp8 import fp8_gemm, quantize_input
+    from evo2_flash_amd.synthetic import quantize_weight_e4m3
+
+    g = torch.Generator(device=dev).manual_seed(seed)
+    x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
+    xs = (x.float().abs().max() / 448.0).reshape(1)
+    x8 = quantize_input(x, xs)
+    stream = torch.cuda.current_stream()
+    out = {}
+    for name, N in (("in_proj", 12288), ("out_proj", 4096)):
+        w8, ws = quantize_weight_e4m3(torch.randn(N, K, generator=g, device=dev) * 0.02)
+        o = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+        fn = lambda: fp8_gemm(x8, w8, xs, ws, out=o)  # noqa: E731
+        fn()
+        torch.cuda.synchronize()
+        avg, med = _timed(fn, reps, stream)
+        flop = 2 * M * N * K
+        tf = flop / (avg * 1e-6) / 1e12
+        out[name] = {"M": M, "N": N, "K": K, "avg_us": round(avg, 2), "median_us": round(med, 2),
+                     "TFLOPs": round(tf, 1), "frac": round(tf / FP8_PEAK_TFLOPS, 4)}
+    qavg, _ = _timed(lambda: quantize_input(x, xs), reps, stream)
+    out["quantize"] = {"avg_us": round(qavg, 2), "bytes": M * K * 3,
+                       "achieved_GBs": round(M * K * 3 / (qavg * 1e-6) / 1e9, 1)}
+    return out
+
+
+# ---------------------------------------------------------------- CPU baseline
 def _cpu_baseline_decode(budget_s=20.0):
     """The oracle's restatement of the reference torch decode path (unfused,
     mixers.py:555-575) for one layer of each kind at B=64, H=4096, timed on
@@ -151,7 +258,7 @@ def _cpu_baseline_decode(budget_s=20.0):
         D = prm.get("D")
         times = []
         with torch.inference_mode():
-            for rep in range(4):
+            for _ in range(4):
                 t = time.perf_counter()
                 oracle.mixer_decode_unfused(z, sw, pool.conv_view(), slots, inner, st, D, lp)
                 times.append(time.perf_counter() - t)
@@ -172,42 +279,63 @@ def main(argv=None):
     ap.add_argument("--steps", type=int, default=64)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the prefill leg")
+    ap.add_argument("--no-gemm", action="store_true", help="skip the fp8 GEMM leg")
+    ap.add_argument("--only", choices=["decode", "prefill", "gemm", "copy"], default=None,
+                    help="run one leg only (for profiling); `copy` runs a plain 1 GiB "
+                         "device copy, the reference dispatch for scaling HBM counters")
     args = ap.parse_args(argv)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(the sharding design is described in DESIGN.md). Run with --gpus 1.",
+              "(DESIGN.md describes how the path would shard). Run with --gpus 1.",
               file=sys.stderr)
         return 2
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         return 2
     dev = "cuda:0"
-    dec = bench_decode(args.steps, args.warmup, dev)
-    hcm = dec["per_kind"]["hcm"]
-    cpu = None if args.no_cpu else _cpu_baseline_decode()
+    if args.only == "copy":
+        src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        avg, _ = _timed(lambda: dst.copy_(src), max(3, args.steps), torch.cuda.current_stream())
+        print(json.dumps({"copy_bytes": 2 * src.numel() * 4, "avg_us": round(avg, 2),
+                          "GBs": round(2 * src.numel() * 4 / (avg * 1e-6) / 1e9, 1)}), flush=True)
+        return 0
+    run = lambda leg, flag: (args.only == leg) or (args.only is None and not flag)  # noqa: E731
+    dec = bench_decode(args.steps, args.warmup, dev) if run("decode", False) else None
+    pre = bench_prefill(max(3, args.steps // 8), dev) if run("prefill", args.no_prefill) else None
+    gem = bench_gemm(max(5, args.steps // 4), dev) if run("gemm", args.no_gemm) else None
+    cpu = None if (args.no_cpu or args.only) else _cpu_baseline_decode()
     line = {
-        "metric": "decode tok/s (7B-shape, bs=64) + prefill tok/s at 32k; % HBM/MFMA roofline",
-        "value": round(dec["tok_s"], 1),
+        "metric": METRIC,
+        "value": round(dec["tok_s"], 1) if dec else None,
         "unit": "tok/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(dec["ms_per_step"], 4),
+        "ms_per_step": round(dec["ms_per_step"], 4) if dec else None,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16/fp32",
+        "dtype": "bf16 I/O, fp32 arithmetic",
         "data": "synthetic (seeded random states, z rows and weights)",
         "config": {"workload": "7B-shape Hyena decode: 27 mixer cores (9 hcs, 9 hcm, 9 hcl), "
-                               "H=4096, B=64, paged state, fused decode kernel per layer",
-                   "global_batch": B_DECODE, "H": H_7B, "layers": dec["layers"]},
-        "roofline": {"bound": "hbm", "kernel": "hyena_decode_kernel<hcm>",
-                     "achieved": hcm["achieved_GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(hcm["achieved_GBs"] / HBM_PEAK_GBS, 4), "traffic": None},
-        "per_kind": dec["per_kind"],
-        "cpu_baseline": cpu,
+                               "H=4096, B=64, paged state (page per block, random slot table), "
+                               "one fused decode kernel per layer",
+                   "global_batch": B_DECODE, "H": H_7B, "layers": 27},
     }
-    print(json.dumps(line))
+    if dec:
+        hcm = dec["per_kind"]["hcm"]
+        line["roofline"] = {"bound": "hbm", "kernel": "hyena_decode_pair_kernel<hcm>",
+                            "achieved": hcm["achieved_GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                            "frac": hcm["frac"], "traffic": None}
+        line["decode"] = dec
+    if pre:
+        line["prefill"] = pre
+    if gem:
+        line["fp8_gemm"] = gem
+    line["cpu_baseline"] = cpu
+    print(json.dumps(line), flush=True)
     return 0
 
 

@@ -1,0 +1,114 @@
+"""The C ABI without a GPU: the built library loads, exports every entry point
+include/evo2_hyena.h declares (and the binding covers exactly those), and
+argument validation that runs before any HIP call returns the documented
+status codes.  The host wrappers refuse CPU tensors: there is no CPU path.
+"""
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from evo2_flash_amd import _lib
+from evo2_flash_amd.build import LIB_PATH
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "evo2_hyena.h")
+
+EVO2_OK, EVO2_ERR_INVALID, EVO2_ERR_UNSUPPORTED = 0, 1, 2
+
+
+def _declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"\b(evo2_\w+)\s*\(", text))
+
+
+def _codes():
+    text = open(HEADER).read()
+    return {k: int(v) for k, v in re.findall(r"\b(EVO2_\w+)\s*=\s*(\d+)", text)}
+
+
+needs_lib = pytest.mark.skipif(not os.path.exists(LIB_PATH), reason="library not built")
+
+
+def test_binding_covers_header():
+    assert _declared() == set(_lib.SIGNATURES), (
+        sorted(_declared() ^ set(_lib.SIGNATURES)))
+
+
+def test_status_codes():
+    c = _codes()
+    assert (c["EVO2_OK"], c["EVO2_ERR_INVALID"], c["EVO2_ERR_UNSUPPORTED"]) == (0, 1, 2)
+
+
+@needs_lib
+def test_library_exports_every_symbol():
+    handle = ctypes.CDLL(LIB_PATH, mode=ctypes.RTLD_LOCAL)
+    for name in sorted(_declared()):
+        assert hasattr(handle, name), name
+    lib = _lib.lib()
+    assert lib.evo2_abi_version() >= 1
+
+
+@needs_lib
+def test_workspace_bytes():
+    lib = _lib.lib()
+    assert lib.evo2_hcl_workspace_bytes(3, 4096) == 3 * 4096 * 16 * 4
+    assert lib.evo2_hcl_workspace_bytes(0, 4096) == 0
+
+
+@needs_lib
+def test_validation_before_launch():
+    """Calls rejected by argument checks never reach the HIP runtime."""
+    lib = _lib.lib()
+    n = None
+    rc = lib.evo2_hyena_decode(n, 0, n, n, 0, 0, 0, n, 0, n, 0, 0, n, 0, 0, n, 0, 0, 0, n, n, 0,
+                               -1, 4096, 128, 0, 0, 2, n)
+    assert rc == EVO2_ERR_INVALID
+    assert b"bad sizes" in lib.evo2_last_error()
+    rc = lib.evo2_hyena_decode(n, 0, n, n, 0, 0, 0, n, 0, n, 0, 0, n, 0, 0, n, 0, 0, 0, n, n, 0,
+                               0, 4096, 128, 0, 0, 2, n)
+    assert rc == EVO2_OK  # empty batch: nothing to do
+    rc = lib.evo2_hyena_decode(n, 0, n, n, 0, 0, 0, n, 0, n, 0, 0, n, 0, 0, n, 0, 0, 0, n, n, 0,
+                               4, 4096, 128, 0, 0, 2, n)
+    assert rc == EVO2_ERR_INVALID  # null pointers
+    rc = lib.evo2_fir_prefill(n, 0, n, 0, 0, 64, n, 0, 0, 0, n, 1, n, 0, n, 1, 64, n, 0, 10, 4096,
+                              2, n)
+    assert rc == EVO2_ERR_UNSUPPORTED and b"7 or 128" in lib.evo2_last_error()
+    rc = lib.evo2_fir_prefill(n, 0, n, 0, 0, 7, n, 0, 0, 0, n, 1, n, 0, n, 1, 48, n, 0, 10, 4096,
+                              2, n)
+    assert rc == EVO2_ERR_INVALID and b"block_t" in lib.evo2_last_error()
+    rc = lib.evo2_fp8_gemm(n, 16, n, 16, n, n, n, n, 0, 64, 4096, 4000, n)
+    assert rc == EVO2_ERR_INVALID  # null pointers are checked before K
+    rc = lib.evo2_hyena_hcl_prefill(n, 0, n, n, 0, 0, 0, n, 0, 0, n, 0, 0, n, 0, 0, 0, n, n, 1, n,
+                                    0, n, 1, n, 40, n, 0, n, 0, 10, 4096, 2, n)
+    assert rc == EVO2_ERR_INVALID and b"block_t" in lib.evo2_last_error()
+
+
+def test_wrappers_refuse_cpu_tensors():
+    from evo2_flash_amd.decode import hyena_decode
+    from evo2_flash_amd.fp8 import quantize_input
+    from evo2_flash_amd.hcl import hcl_compute_filter
+
+    H = 8
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        hyena_decode(torch.zeros(1, 3 * H, dtype=torch.bfloat16), torch.zeros(3 * H, 3),
+                     torch.zeros(2, 3 * H, 2), torch.ones(1, dtype=torch.int32),
+                     torch.zeros(H, 7), torch.zeros(2, H, 6))
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        quantize_input(torch.zeros(2, 16, dtype=torch.bfloat16), torch.ones(1))
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        hcl_compute_filter(torch.zeros(2, 16), torch.zeros(2, 16), torch.arange(4.0))
+
+
+def test_decode_supported_false_on_cpu():
+    from evo2_flash_amd.decode import decode_supported
+
+    H = 8
+    assert not decode_supported(torch.zeros(1, 3 * H, dtype=torch.bfloat16),
+                                torch.zeros(3 * H, 3, dtype=torch.bfloat16),
+                                torch.zeros(2, 3 * H, 2, dtype=torch.bfloat16),
+                                torch.zeros(H, 7, dtype=torch.bfloat16), torch.zeros(2, H, 6))

@@ -1,0 +1,485 @@
+"""Pins the CPU oracle (oracle/hyena_ref.py) against checks that do not share
+its code: float64 brute force written from the mathematics, closed forms,
+impulse responses, invariants and hand-computed known answers.  Each check is
+chosen so that a plausible mistake in the oracle (a flipped tap order, a
+dropped continuation term, eps inside the sqrt, a wrong window column) fails.
+
+CPU only; runs in seconds.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from evo2_flash_amd.metadata import build_metadata, host_tables
+from evo2_flash_amd.state import HyenaStatePool, page_bytes
+from evo2_flash_amd.synthetic import mixer_params, random_slot_table
+
+from _cases import bf16_ulp_diff, decode_case, max_rel_err
+
+
+def _qsl(lens):
+    q = [0]
+    for n in lens:
+        q.append(q[-1] + n)
+    return q
+
+
+# ---------------------------------------------------------------- bf16
+def test_bf_round_to_nearest_even():
+    one = 1.0
+    cases = {
+        one + 2 ** -8: 1.0,              # tie -> even mantissa (1.0)
+        one + 3 * 2 ** -8: 1.0 + 2 ** -6,  # tie -> even (up)
+        one + 2 ** -8 + 2 ** -20: 1.0 + 2 ** -7,  # above the tie -> up
+        -2.0 - 2 ** -7: -2.0,            # tie at exponent 1 -> even
+    }
+    for x, want in cases.items():
+        assert oracle.bf(torch.tensor([x], dtype=torch.float32)).item() == want, x
+
+
+# ---------------------------------------------------------------- depthwise FIR
+def _fir_f64(seq, w, prev):
+    """y_t = sum_k w[k] * x_{t-(K-1)+k} over cat(prev, seq), float64 loops."""
+    dim, L = seq.shape
+    K = w.shape[1]
+    full = np.concatenate([prev, seq], axis=1)
+    y = np.zeros((dim, L))
+    for t in range(L):
+        for k in range(K):
+            y[:, t] += w[:, k] * full[:, t + k]
+    return y
+
+
+@pytest.mark.parametrize("K", [3, 7, 128])
+def test_depthwise_prefill_vs_float64(K):
+    dim, nblk = 6, 8
+    lens, has_init = [40, 3, 0, 150, 1], [0, 1, 0, 1, 1]
+    qsl = _qsl(lens)
+    g = torch.Generator().manual_seed(K)
+    x = torch.randn(qsl[-1], dim, generator=g).to(torch.bfloat16)
+    w = (torch.randn(dim, K, generator=g) * 0.3).to(torch.bfloat16)
+    slots = [3, 5, 6, 1, 2]
+    state = torch.randn(nblk, dim, 127, generator=g)
+    state0 = state.clone()
+    y = oracle.depthwise_prefill(x, w, qsl, slots, has_init, state, K)
+    wd = w.double().numpy()
+    for j, (a, b) in enumerate(zip(qsl[:-1], qsl[1:])):
+        blk = slots[j]
+        if b == a:
+            assert torch.equal(state[blk], state0[blk])  # empty segment: untouched
+            continue
+        prev = state0[blk, :, :K - 1].double().numpy() if has_init[j] else np.zeros((dim, K - 1))
+        seq = x[a:b].double().numpy().T
+        ref = torch.from_numpy(_fir_f64(seq, wd, prev).T).float().to(torch.bfloat16)
+        assert bf16_ulp_diff(y[a:b], ref).max().item() <= 1, j
+        # new window: last K-1 inputs of cat(prev, seq), oldest first, full even if short
+        full = np.concatenate([prev, seq], axis=1)
+        want = torch.from_numpy(full[:, -(K - 1):]).float()
+        assert torch.equal(state[blk, :, :K - 1], want), j
+        assert torch.equal(state[blk, :, K - 1:], state0[blk, :, K - 1:])
+
+
+@pytest.mark.parametrize("K", [3, 7, 128])
+def test_depthwise_impulse_pins_tap_order(K):
+    """A unit impulse at t0 gives y[t0 + j] = w[K-1-j]: w[:, -1] pairs with
+    the current sample (cross-correlation order)."""
+    dim, L, t0 = 2, K + 10, 4
+    x = torch.zeros(L, dim, dtype=torch.bfloat16)
+    x[t0] = 1.0
+    w = torch.arange(1, K + 1, dtype=torch.float32).repeat(dim, 1).to(torch.bfloat16)
+    state = torch.zeros(2, dim, 127)
+    y = oracle.depthwise_prefill(x, w, [0, L], [1], [0], state, K)
+    for j in range(L - t0):
+        want = float(w[0, K - 1 - j]) if j < K else 0.0
+        assert y[t0 + j, 0].item() == want
+    assert (y[:t0] == 0).all()
+
+
+def test_depthwise_split_invariance():
+    """prefill(L) == prefill(a) then a continued prefill(L - a), within 1 ulp."""
+    dim, K, L = 5, 128, 300
+    g = torch.Generator().manual_seed(2)
+    x = torch.randn(L, dim, generator=g).to(torch.bfloat16)
+    w = (torch.randn(dim, K, generator=g) * 0.1).to(torch.bfloat16)
+    for a in (1, 50, 127, 200):
+        s1 = torch.zeros(2, dim, 127)
+        y1 = oracle.depthwise_prefill(x, w, [0, L], [1], [0], s1, K)
+        s2 = torch.zeros(2, dim, 127)
+        ya = oracle.depthwise_prefill(x[:a], w, [0, a], [1], [0], s2, K)
+        yb = oracle.depthwise_prefill(x[a:], w, [0, L - a], [1], [1], s2, K)
+        assert bf16_ulp_diff(y1, torch.cat([ya, yb])).max().item() <= 1
+        assert torch.equal(s1, s2)
+
+
+# ---------------------------------------------------------------- modal filter / LI
+def test_hcl_filter_single_pole_closed_form():
+    """S = 1: h[d, l] = r * p^t exactly as the geometric sequence."""
+    r = torch.tensor([[0.5], [-2.0]])
+    p = torch.tensor([[0.9], [0.5]])
+    t = torch.arange(20, dtype=torch.float32)
+    h = oracle.hcl_compute_filter(r, torch.log(p), t)
+    want = r.double() * p.double() ** t.double()
+    assert torch.allclose(h.double(), want, rtol=1e-5, atol=1e-7)
+
+
+def _recurrence_f64(seq, res, lp, s0):
+    p = np.exp(lp.astype(np.float64))
+    H, L = seq.shape
+    s = np.zeros(res.shape) if s0 is None else s0.astype(np.float64).copy()
+    y = np.empty((H, L))
+    for t in range(L):
+        s = p * s + seq[:, t:t + 1]
+        y[:, t] = (res * s).sum(1)
+    return y, s
+
+
+@pytest.mark.parametrize("with_prev", [False, True])
+@pytest.mark.parametrize("L", [1, 17, 400])
+def test_iir_segment_vs_sequential_recurrence(L, with_prev):
+    """The FFT form with the closed-form final state (and the continuation
+    terms) equals the sequential recurrence s_t = p s_{t-1} + x_t."""
+    H, S = 8, 16
+    g = torch.Generator().manual_seed(L)
+    prm = mixer_params("hcl", H, seed=L, in_proj_fp8=False)
+    res, lp = prm["residues"], prm["log_poles"][..., 0]
+    seq = torch.randn(H, L, generator=g)
+    s_prev = torch.randn(H, S, generator=g) * 3 if with_prev else None
+    y, st = oracle.iir_segment(seq, res, lp, s_prev)
+    yr, sr = _recurrence_f64(seq.double().numpy(), res.double().numpy(), lp.numpy(),
+                             None if s_prev is None else s_prev.numpy())
+    assert max_rel_err(y, torch.from_numpy(yr)) <= 1e-5
+    assert max_rel_err(st, torch.from_numpy(sr)) <= 1e-5
+
+
+def test_iir_segment_split_invariance():
+    H, L, a = 4, 300, 123
+    prm = mixer_params("hcl", H, seed=1, in_proj_fp8=False)
+    res, lp = prm["residues"], prm["log_poles"][..., 0]
+    seq = torch.randn(H, L, generator=torch.Generator().manual_seed(0))
+    y, st = oracle.iir_segment(seq, res, lp, None)
+    ya, sa = oracle.iir_segment(seq[:, :a], res, lp, None)
+    yb, sb = oracle.iir_segment(seq[:, a:], res, lp, sa)
+    assert max_rel_err(torch.cat([ya, yb], 1), y) <= 1e-5
+    assert max_rel_err(sb, st) <= 1e-5
+
+
+# ---------------------------------------------------------------- mixer prefill
+def _short_f64(z, w, prev2):
+    """K=3 short filter of one segment in float64, output rounded to bf16."""
+    return torch.from_numpy(_fir_f64(z.double().numpy().T, w.double().numpy(),
+                                     prev2).T).float().to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("kind", ["hcs", "hcm", "hcl"])
+def test_mixer_prefill_vs_float64(kind):
+    """Composition of the mixer prefill (A.2): short filter, gate, inner
+    operator, D, x2 -- recomputed here per segment in float64 from the
+    definitions, with bf16 rounding only where a bf16 tensor is written."""
+    H, nblk = 16, 6
+    lens, has_init = [70, 0, 9, 130], [0, 0, 1, 1]
+    qsl = _qsl(lens)
+    prm = mixer_params(kind, H, seed=4, in_proj_fp8=False)
+    g = torch.Generator().manual_seed(5)
+    z = (torch.randn(qsl[-1], 3 * H, generator=g) * 1.3).to(torch.bfloat16)
+    slots = [2, 3, 4, 5]
+    pool = HyenaStatePool(nblk, H, "cpu")
+    pool.kv_cache[0].copy_(torch.randn(pool.kv_cache[0].shape, generator=g).to(torch.bfloat16))
+    pool.kv_cache[1].copy_(torch.randn(pool.kv_cache[1].shape, generator=g).to(torch.bfloat16).float())
+    pool.kv_cache[2].copy_(torch.randn(pool.kv_cache[2].shape, generator=g))
+    conv0 = pool.conv_view().clone()
+    inner0 = pool.inner_view().clone()
+    ssm0 = pool.ssm_view().clone()
+    sw = prm["short_filter"].view(3 * H, 3)
+    D = prm.get("D")
+    if kind == "hcl":
+        res, lp = prm["residues"], prm["log_poles"][..., 0]
+        out = oracle.iir_mixer_prefill(z, sw, pool.conv_view(), res, lp, pool.ssm_view(), D,
+                                       qsl, slots, has_init)
+    else:
+        K = prm["conv"].shape[-1]
+        w = prm["conv"].view(H, K)
+        out = oracle.fir_mixer_prefill(z, sw, pool.conv_view(), w, pool.inner_view(K - 1), D,
+                                       qsl, slots, has_init)
+    for j, (a, b) in enumerate(zip(qsl[:-1], qsl[1:])):
+        if b == a:
+            continue
+        blk = slots[j]
+        prev2 = conv0[blk].double().numpy() if has_init[j] else np.zeros((3 * H, 2))
+        zf = _short_f64(z[a:b], sw, prev2).float()
+        x2, x1, v = zf[:, 0::3], zf[:, 1::3], zf[:, 2::3]
+        u = oracle.bf(x1 * v)
+        if kind == "hcl":
+            s0 = ssm0[blk].numpy() if has_init[j] else None
+            yv, sT = _recurrence_f64(u.double().numpy().T, res.double().numpy(), lp.numpy(), s0)
+            y = oracle.bf(torch.from_numpy(yv.T).float())
+            y = oracle.bf(y + oracle.bf(u * D.float()))
+            assert max_rel_err(pool.ssm_view()[blk], torch.from_numpy(sT)) <= 1e-5
+        else:
+            prev = inner0[blk, :, :K - 1].double().numpy() if has_init[j] else np.zeros((H, K - 1))
+            y = oracle.bf(torch.from_numpy(_fir_f64(u.double().numpy().T, w.double().numpy(),
+                                                    prev).T).float())
+            if D is not None:
+                y = oracle.bf(y + oracle.bf(D.float() * u))
+        ref = (x2 * y).to(torch.bfloat16)
+        assert max_rel_err(out[a:b], ref) <= 1e-2, j
+        # conv window: the last two z rows of cat(prev, segment), exactly
+        full = torch.cat([torch.from_numpy(prev2).float(), z[a:b].float().t()], 1)
+        assert torch.equal(pool.conv_view()[blk].float(), full[:, -2:]), j
+
+
+# ---------------------------------------------------------------- decode
+def _decode_f64(kind, prm, z, conv, inner_state, H):
+    """One decode token per row from the definitions in float64 (no rounding
+    inside the inner operator): returns (out, new conv window, new state)."""
+    # The short tap's rounding points are part of the decode contract (A.1:
+    # each product and the fp32 sum rounded to bf16); everything after the
+    # gate is float64.
+    sw = prm["short_filter"].view(3 * H, 3).float()
+    c = conv.float()
+    rb = lambda t: t.to(torch.bfloat16).float()  # noqa: E731
+    short = rb((rb(c[:, 0] * sw[:, 0]) + rb(c[:, 1] * sw[:, 1])) + rb(z.float() * sw[:, 2]))
+    short = short.double()
+    x2, x1, v = short[0::3], short[1::3], short[2::3]
+    u = (x1 * v).float().to(torch.bfloat16).double()
+    if kind == "hcl":
+        p = torch.exp(prm["log_poles"][..., 0].double())
+        s = inner_state.double() * p + u[:, None]
+        y = (s * prm["residues"].double()).sum(1)
+        new_state = s
+    else:
+        K = prm["conv"].shape[-1]
+        w = prm["conv"].view(H, K).double()
+        win = inner_state[:, :K - 1].double()
+        y = (win * w[:, :-1]).sum(1) + w[:, -1] * u
+        new_state = torch.cat([win[:, 1:], u[:, None]], 1)
+    if "D" in prm:
+        y = y + prm["D"].double() * u
+    return x2 * y, torch.stack([conv[:, 1].float(), z.float()], 1), new_state
+
+
+@pytest.mark.parametrize("kind", ["hcs", "hcm", "hcl"])
+def test_decode_emulated_vs_float64(kind):
+    H, B, nblk = 64, 6, 10
+    prm, z, slots, pool = decode_case(kind, H, B, nblk, seed=3, n_null=1)
+    conv0 = pool.conv_view().clone()
+    if kind == "hcl":
+        st0 = pool.ssm_view().clone()
+        inner, lp, st = prm["residues"], prm["log_poles"][..., 0], pool.ssm_view()
+    else:
+        K = prm["conv"].shape[-1]
+        st0 = pool.inner_view().clone()
+        inner, lp, st = prm["conv"].view(H, K), None, pool.inner_view(K - 1)
+    raw0 = pool.raw.clone()
+    out = oracle.hyena_decode_emulated(z, prm["short_filter"].view(3 * H, 3), pool.conv_view(),
+                                       slots, inner, st, prm.get("D"), lp)
+    for b in range(B):
+        blk = int(slots[b])
+        if blk == 0:
+            assert (out[b].float() == 0).all()
+            continue
+        ref, conv_new, st_new = _decode_f64(kind, prm, z[b], conv0[blk], st0[blk], H)
+        assert max_rel_err(out[b], ref) <= 1e-2, b
+        assert torch.equal(pool.conv_view()[blk].float(), conv_new)
+        if kind == "hcl":
+            assert max_rel_err(pool.ssm_view()[blk], st_new) <= 1e-6
+        else:
+            K = prm["conv"].shape[-1]
+            assert torch.equal(pool.inner_view()[blk, :, :K - 1], st_new.float())
+    # the null block's page and every block no row maps to are untouched
+    used = {int(s) for s in slots} - {0}
+    for blk in range(nblk):
+        if blk not in used:
+            assert torch.equal(pool.raw[blk], raw0[blk]), blk
+
+
+@pytest.mark.parametrize("kind", ["hcs", "hcm", "hcl"])
+def test_decode_emulated_vs_unfused(kind):
+    """The rounding-point emulation and the unfused fp32 path agree to 1e-2
+    and write the same windows."""
+    H, B, nblk = 128, 8, 12
+    prm, z, slots, pool = decode_case(kind, H, B, nblk, seed=9)
+    p2 = HyenaStatePool(nblk, H, "cpu")
+    p2.raw.copy_(pool.raw)
+    sw = prm["short_filter"].view(3 * H, 3)
+    if kind == "hcl":
+        args = (prm["residues"], pool.ssm_view(), prm["D"], prm["log_poles"][..., 0])
+        args2 = (prm["residues"], p2.ssm_view(), prm["D"], prm["log_poles"][..., 0])
+    else:
+        K = prm["conv"].shape[-1]
+        args = (prm["conv"].view(H, K), pool.inner_view(K - 1), prm.get("D"), None)
+        args2 = (prm["conv"].view(H, K), p2.inner_view(), prm.get("D"), None)
+    o1 = oracle.hyena_decode_emulated(z, sw, pool.conv_view(), slots, *args)
+    o2 = oracle.mixer_decode_unfused(z, sw, p2.conv_view(), slots, *args2)
+    assert max_rel_err(o1, o2) <= 1e-2
+    assert torch.equal(pool.kv_cache[0], p2.kv_cache[0])
+    if kind == "hcl":
+        assert max_rel_err(pool.kv_cache[2], p2.kv_cache[2]) <= 1e-6
+    else:
+        assert torch.equal(pool.kv_cache[1], p2.kv_cache[1])
+
+
+@pytest.mark.parametrize("kind", ["hcs", "hcm", "hcl"])
+def test_decode_after_prefill_matches_longer_prefill(kind):
+    """prefill(L) then one decode token == the last row of prefill(L + 1)."""
+    H, L = 32, 140
+    prm = mixer_params(kind, H, seed=6, in_proj_fp8=False)
+    z = (torch.randn(L + 1, 3 * H, generator=torch.Generator().manual_seed(1)) * 1.3
+         ).to(torch.bfloat16)
+    sw = prm["short_filter"].view(3 * H, 3)
+    D = prm.get("D")
+    outs, pools = [], []
+    for n in (L + 1, L):
+        pool = HyenaStatePool(3, H, "cpu")
+        if kind == "hcl":
+            o = oracle.iir_mixer_prefill(z[:n], sw, pool.conv_view(), prm["residues"],
+                                         prm["log_poles"][..., 0], pool.ssm_view(), D,
+                                         [0, n], [1], [0])
+        else:
+            K = prm["conv"].shape[-1]
+            o = oracle.fir_mixer_prefill(z[:n], sw, pool.conv_view(), prm["conv"].view(H, K),
+                                         pool.inner_view(K - 1), D, [0, n], [1], [0])
+        outs.append(o)
+        pools.append(pool)
+    pool = pools[1]
+    if kind == "hcl":
+        last = oracle.mixer_decode_unfused(z[L:], sw, pool.conv_view(), [1], prm["residues"],
+                                           pool.ssm_view(), D, prm["log_poles"][..., 0])
+    else:
+        K = prm["conv"].shape[-1]
+        last = oracle.mixer_decode_unfused(z[L:], sw, pool.conv_view(), [1],
+                                           prm["conv"].view(H, K), pool.inner_view(), D)
+    assert max_rel_err(last, outs[0][L:]) <= 1e-2
+    assert torch.equal(pool.kv_cache[0], pools[0].kv_cache[0])
+
+
+# ---------------------------------------------------------------- norm
+def test_rms_norm_known_answer():
+    """x = 2 everywhere, H = 4: ||x|| = 4, * H^-1/2 = 2, + eps -> x / 2 = 1."""
+    x = torch.full((1, 4), 2.0, dtype=torch.bfloat16)
+    w = torch.tensor([1.0, -0.5, 3.0, 0.25], dtype=torch.bfloat16)
+    y = oracle.rms_norm(x, w, 0.0)
+    assert torch.equal(y.float(), w.float().view(1, 4))
+
+
+def test_rms_norm_eps_outside_sqrt():
+    """y = w x / (||x|| H^-1/2 + eps) -- with a large eps, eps inside the
+    sqrt would give a clearly different value."""
+    H, eps = 64, 0.5
+    g = torch.Generator().manual_seed(0)
+    x = (torch.randn(3, H, generator=g) * 0.1).to(torch.bfloat16)
+    w = torch.randn(H, generator=g).to(torch.bfloat16)
+    y = oracle.rms_norm(x, w, eps)
+    xd = x.double()
+    den = xd.norm(dim=-1, keepdim=True) * H ** -0.5 + eps
+    ref = w.double() * xd / den
+    assert max_rel_err(y, ref) <= 1e-2
+    wrong = w.double() * xd / torch.sqrt((xd * xd).mean(-1, keepdim=True) + eps)
+    assert max_rel_err(y, wrong) > 0.1
+
+
+def test_rms_norm_residual():
+    H = 32
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(2, H, generator=g).to(torch.bfloat16)
+    r = torch.randn(2, H, generator=g).to(torch.bfloat16)
+    w = torch.ones(H, dtype=torch.bfloat16)
+    y, s = oracle.rms_norm(x, w, 1e-6, r)
+    assert torch.equal(s, (x.float() + r.float()).to(torch.bfloat16))
+    assert torch.equal(y, oracle.rms_norm(s, w, 1e-6))
+
+
+# ---------------------------------------------------------------- fp8
+def _e4m3_values():
+    """All finite non-negative OCP e4m3fn values from the format definition:
+    1 sign, 4 exponent (bias 7), 3 mantissa bits; exponent field 15 with
+    mantissa 7 is NaN, so the largest finite value is 448."""
+    vals = []
+    for code in range(0x7F):
+        e, m = code >> 3, code & 7
+        vals.append((m / 8.0) * 2.0 ** -6 if e == 0 else (1 + m / 8.0) * 2.0 ** (e - 7))
+    return vals
+
+
+def _e4m3_encode(x):
+    """Round-to-nearest-even onto e4m3fn codes (ties to the even code), with
+    saturation at 448 as the clamp in quantize_input makes it."""
+    vals = _e4m3_values()
+    mag = min(abs(x), 448.0)
+    best = min(range(len(vals)), key=lambda c: (abs(vals[c] - mag), c & 1))
+    return (0x80 if (x < 0 or (x == 0 and math.copysign(1, x) < 0)) else 0) | best
+
+
+def test_quantize_input_matches_format_definition():
+    g = torch.Generator().manual_seed(3)
+    x = torch.cat([torch.randn(500, generator=g) * 4,
+                   torch.tensor([0.0, -0.0, 448.0, 449.0, -1e4, 1e4, 0.0087890625, 2 ** -10,
+                                 2 ** -9 * 1.5, 240.0, 248.0, 256.0, 464.0, -17.0])])
+    x = x.to(torch.bfloat16)
+    scale = torch.tensor([0.75])
+    q = oracle.quantize_input(x, scale).view(torch.uint8)
+    for xi, qi in zip(x.float().tolist(), q.tolist()):
+        v = xi / 0.75
+        assert qi == _e4m3_encode(float(np.float32(v))), (xi, qi)
+
+
+def test_fp8_linear_known_answer():
+    """Small-integer e4m3 operands: every product and sum is exact in fp32."""
+    g = torch.Generator().manual_seed(4)
+    x = torch.randint(-4, 5, (5, 32), generator=g).float().to(torch.bfloat16)
+    w8 = torch.randint(-3, 4, (7, 32), generator=g).float().to(torch.float8_e4m3fn)
+    out = oracle.fp8_linear_dequant(x, w8, torch.tensor([1.0]), torch.tensor([0.5]))
+    want = (x.double() @ w8.double().t() * 0.5).float().to(torch.bfloat16)
+    assert torch.equal(out, want)
+
+
+# ---------------------------------------------------------------- tables, metadata, state
+def test_prefill_tables_known():
+    seq, tiles = oracle.prefill_tables([0, 100, 100, 164, 165], [0, 1, 1, 0], 64)
+    assert seq.tolist() == [[0, 100, 0], [100, 100, 1], [100, 164, 1], [164, 165, 0]]
+    assert tiles.tolist() == [[0, 0], [0, 64], [2, 100], [3, 164]]
+    s2, t2, ts = host_tables([0, 100, 100, 164, 165], [0, 1, 1, 0], 64, with_tile_start=True)
+    assert s2 == [tuple(r) for r in seq.tolist()]
+    assert t2 == [tuple(r) for r in tiles.tolist()]
+    assert ts == [0, 2, 2, 3, 4]
+
+
+def test_host_tables_reject_negative_segment():
+    with pytest.raises(ValueError):
+        host_tables([0, 5, 3], [0, 0], 64)
+
+
+def test_metadata_decode_indices_column0():
+    m = build_metadata(decode_slots=[4, 7], device="cpu")
+    from evo2_flash_amd.metadata import decode_state_indices
+    assert decode_state_indices(m).tolist() == [4, 7]
+    m.state_indices_tensor_d = torch.tensor([[4, 9], [7, 8]], dtype=torch.int32)
+    assert decode_state_indices(m).tolist() == [4, 7]
+
+
+def test_state_pool_layout_7b():
+    """The unified spec at H=4096: 2,392,064 bytes of payload per block; the
+    three slices alias one page, conv and FIR slices stored state-major."""
+    H = 4096
+    assert page_bytes(H, align=1) == 2 * 3 * H * 2 + 127 * H * 4 + H * 16 * 4 == 2392064
+    pool = HyenaStatePool(3, H, "cpu")
+    conv, inner, ssm = pool.kv_cache
+    assert conv.shape == (3, 2, 3 * H) and inner.shape == (3, 127, H) and ssm.shape == (3, H, 16)
+    page = pool.page
+    assert conv.stride(0) * 2 == page and inner.stride(0) * 4 == page and ssm.stride(0) * 4 == page
+    assert pool.conv_view().shape == (3, 3 * H, 2) and pool.conv_view().stride(1) == 1
+    assert pool.inner_view(6).shape == (3, H, 6) and pool.inner_view().stride(1) == 1
+    pool.inner_view()[1, 5, 0] = 7.0   # (block 1, channel 5, oldest column)
+    flat = pool.raw[1].view(torch.float32)
+    assert flat[(2 * 3 * H * 2) // 4 + 5].item() == 7.0
+
+
+def test_random_slot_table_is_permutation_without_null():
+    s = random_slot_table(64, 65, seed=3)
+    assert sorted(s.tolist()) == list(range(1, 65))
+    assert not torch.equal(s, torch.arange(1, 65, dtype=torch.int32))
+    with pytest.raises(ValueError):
+        random_slot_table(65, 65, seed=3)
