@@ -65,25 +65,42 @@ def prefill_bytes(T, H):
     return T * 3 * H * 2 + T * H * 2
 
 
-def _timed(fn, reps, stream):
-    """Average and median duration (us) of fn() over reps launches, each
-    bracketed by HIP events on `stream` (the stream the kernels run on)."""
+def _timed(fn, reps, stream, batches=4):
+    """Average duration (us) of one fn() call on `stream` (the stream the
+    kernels run on): `batches` batches of reps/batches back-to-back calls,
+    each batch bracketed by HIP events, so event overhead is amortised and
+    the figure includes the launch gaps a real step has.  Returns (mean over
+    all calls, median of the per-batch means)."""
+    per = max(1, reps // batches)
     evs = []
-    for _ in range(reps):
+    for _ in range(batches):
         a = torch.cuda.Event(enable_timing=True)
         b = torch.cuda.Event(enable_timing=True)
         a.record(stream)
-        fn()
+        for _ in range(per):
+            fn()
         b.record(stream)
         evs.append((a, b))
     torch.cuda.synchronize()
-    d = [a.elapsed_time(b) * 1e3 for a, b in evs]
+    d = [a.elapsed_time(b) * 1e3 / per for a, b in evs]
     return statistics.mean(d), statistics.median(d)
+
+
+def bench_copy(dev, nbytes=1 << 30, reps=8):
+    """Plain device-to-device copy of nbytes (read + write): the achievable
+    HBM bandwidth next to the 8 TB/s vendor peak."""
+    src = torch.ones(nbytes // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    avg, _ = _timed(lambda: dst.copy_(src), reps, torch.cuda.current_stream())
+    return {"bytes": 2 * nbytes, "avg_us": round(avg, 2),
+            "GBs": round(2 * nbytes / (avg * 1e-6) / 1e9, 1)}
 
 
 # ---------------------------------------------------------------- decode
 class DecodeLayer:
     def __init__(self, kind, idx, H, B, dev, seed):
+        from evo2_flash_amd.decode import channel_major_taps
         from evo2_flash_amd.state import HyenaStatePool
         from evo2_flash_amd.synthetic import mixer_params, random_slot_table
 
@@ -96,7 +113,8 @@ class DecodeLayer:
             self.lp = prm["log_poles"][..., 0]
         else:
             K = prm["conv"].shape[-1]
-            self.inner = prm["conv"].view(H, K)
+            # the decode taps as the mixers keep them: channel-contiguous
+            self.inner = channel_major_taps(prm["conv"].view(H, K))
             self.lp = None
         self.pool = HyenaStatePool(B + 1, H, dev)
         g = torch.Generator(device=dev).manual_seed(seed + 1000 + idx)
@@ -114,31 +132,57 @@ class DecodeLayer:
                             self.inner, self.state, self.D, self.lp)
 
 
+def _graph(fn, n):
+    """A HIP graph of n back-to-back calls of fn (captured on a side stream,
+    as torch requires); the decode step is replayed this way in serving."""
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()  # warm-up on the capture stream
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=s):
+            for _ in range(n):
+                fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    return g
+
+
 def bench_decode(steps, warmup, dev, seed=1234):
+    """27 fused decode launches per step, replayed from one HIP graph; per-kind
+    launch durations from graphs of 36 launches of one kind (event-timed on
+    the replay stream, so launch gaps are included)."""
     H, B = H_7B, B_DECODE
     order = sorted((i, k) for k, idxs in LAYER_MAP_7B.items() for i in idxs)
     layers = [DecodeLayer(k, i, H, B, dev, seed) for i, k in order]
-    for _ in range(warmup):
+
+    def step():
         for L in layers:
             L.step()
+
+    for _ in range(warmup):
+        step()
     torch.cuda.synchronize()
+    g_step = _graph(step, 1)
     stream = torch.cuda.current_stream()
-    # whole-step wall clock: every layer back to back, no per-launch events
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
+    g_step.replay()
     t0.record(stream)
     for _ in range(steps):
-        for L in layers:
-            L.step()
+        g_step.replay()
     t1.record(stream)
     torch.cuda.synchronize()
     ms_per_step = t0.elapsed_time(t1) / steps
-    # per-kind kernel durations, each launch bracketed by events
     per_kind = {}
+    reps = 4
     for kind in LAYER_MAP_7B:
         Ls = [L for L in layers if L.kind == kind]
-        it = iter(range(10 ** 9))
-        avg, med = _timed(lambda: Ls[next(it) % len(Ls)].step(), steps * len(Ls), stream)
+        g = _graph(lambda: [L.step() for L in Ls], reps)
+        n = reps * len(Ls)
+        avg, med = _timed(g.replay, max(4, steps // 4), stream)
+        avg, med = avg / n, med / n
         nbytes = decode_bytes_per_launch(kind, B, H)
         per_kind[kind] = {"avg_us": round(avg, 3), "median_us": round(med, 3),
                           "bytes_per_launch": nbytes,
@@ -295,11 +339,7 @@ def main(argv=None):
         return 2
     dev = "cuda:0"
     if args.only == "copy":
-        src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
-        dst = torch.empty_like(src)
-        avg, _ = _timed(lambda: dst.copy_(src), max(3, args.steps), torch.cuda.current_stream())
-        print(json.dumps({"copy_bytes": 2 * src.numel() * 4, "avg_us": round(avg, 2),
-                          "GBs": round(2 * src.numel() * 4 / (avg * 1e-6) / 1e9, 1)}), flush=True)
+        print(json.dumps(bench_copy(dev, reps=max(3, args.steps))), flush=True)
         return 0
     run = lambda leg, flag: (args.only == leg) or (args.only is None and not flag)  # noqa: E731
     dec = bench_decode(args.steps, args.warmup, dev) if run("decode", False) else None
@@ -322,7 +362,8 @@ def main(argv=None):
         "config": {"workload": "7B-shape Hyena decode: 27 mixer cores (9 hcs, 9 hcm, 9 hcl), "
                                "H=4096, B=64, paged state (page per block, random slot table), "
                                "one fused decode kernel per layer",
-                   "global_batch": B_DECODE, "H": H_7B, "layers": 27},
+                   "global_batch": B_DECODE, "H": H_7B, "layers": 27,
+                   "replay": "one HIP graph per step"},
     }
     if dec:
         hcm = dec["per_kind"]["hcm"]
@@ -334,6 +375,8 @@ def main(argv=None):
         line["prefill"] = pre
     if gem:
         line["fp8_gemm"] = gem
+    if not args.only:
+        line["hbm_copy"] = bench_copy(dev)
     line["cpu_baseline"] = cpu
     print(json.dumps(line), flush=True)
     return 0

@@ -82,6 +82,12 @@ SIGNATURES = {
         _c_i64, _c_i64, _c_i64, _c_p,                 # D, S, L, stream
     ],
     "evo2_fp8_quantize": [_c_p, _c_i64, _c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_p],
+    "evo2_rms_norm": [
+        _c_p, _c_i64, _c_p, _c_i64,               # x, sx, residual, sr
+        _c_p, _c_f, _c_p, _c_i64,                 # weight, eps, y, sy
+        _c_p, _c_i64, _c_p, _c_p, _c_i64,         # s_out, ss, q_scale, q, sq
+        _c_i64, _c_i64, _c_p,                     # T, H, stream
+    ],
     "evo2_fp8_gemm": [
         _c_p, _c_i64, _c_p, _c_i64,               # x8, sx, w8, sw
         _c_p, _c_p, _c_p,                         # x_scale, w_scale, bias

@@ -428,6 +428,255 @@ static void launch_pair(const DecodeArgs &a, int64_t B, hipStream_t stream) {
   hipLaunchKernelGGL((hyena_decode_pair_kernel<KIND, HAS_D, WT>), grid, dim3(BT), 0, stream, a);
 }
 
+// ---------------------------------------------------------------------------
+// hcm with the window split over four waves.  A workgroup owns one row and 64
+// channel pairs; wave m holds window columns k = 16j + 4m + l (j < 8, l < 4),
+// so its four accumulators are exactly the reference's acc[m][0..3] summed
+// over j in order.  Waves 1-3 hand theirs to wave 0 through LDS, which
+// combines them in the reference's order.  Every wave issues all its column
+// loads at once (32 x 512 B in flight per wave, four times the pair kernel's
+// per-channel share), and the shifted stores wait for a barrier: a wave
+// writes column 16j + 4m - 1, which another wave loads.
+
+template <bool HAS_D, bool WT>
+__global__ __launch_bounds__(256) void hcm_decode_split_kernel(DecodeArgs a) {
+  __shared__ float2 part[3][4][64];
+  const int lane = threadIdx.x & 63;
+  const int m = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int h0 = 2 * (blockIdx.x * 64 + lane);
+  const bool active = h0 < a.H;
+  const int hc = active ? h0 : 0;
+  const int64_t b = blockIdx.y;
+  const int64_t blk = a.slots[b * a.ssl];
+  if (blk == a.null_block || blk < 0 || blk >= a.num_blocks) {  // uniform
+    if (m == 0 && active) *reinterpret_cast<uint32_t *>(a.out + b * a.so + h0) = 0u;
+    return;
+  }
+  float *s = a.st + blk * a.is0 + hc;  // is1 == 1: the pair is one float2
+  const bf16_t *w = static_cast<const bf16_t *>(a.inner);
+
+  // Taps stay packed as loaded (bf16 pairs) and are widened at use, which
+  // keeps the kernel at four waves per SIMD.  WT: tw[j][l] = (h0, h0+1) of
+  // tap k; otherwise tw[j][2c], tw[j][2c+1] = taps (4m..4m+3) of channel h0+c.
+  float2 v[8][4];
+  uint32_t tw[8][4];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+#pragma unroll
+    for (int l = 0; l < 4; ++l) {
+      const int k = 16 * j + 4 * m + l;
+      v[j][l] = k < 127 ? *reinterpret_cast<const float2 *>(s + (int64_t)k * a.is2)
+                        : make_float2(0.f, 0.f);
+    }
+    if constexpr (WT) {
+#pragma unroll
+      for (int l = 0; l < 4; ++l) {
+        const int k = 16 * j + 4 * m + l;
+        tw[j][l] = k < 127 ? *reinterpret_cast<const uint32_t *>(w + (int64_t)k * a.wi1 + hc) : 0u;
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const uint2 t = *reinterpret_cast<const uint2 *>(w + (int64_t)(hc + c) * a.wi0 + 16 * j + 4 * m);
+        tw[j][2 * c] = t.x;
+        tw[j][2 * c + 1] = (16 * j + 4 * m + 3 < 127) ? t.y : (t.y & 0xffffu);
+      }
+    }
+  }
+  // bf16 tap l of channel c (0 = h0, 1 = h0 + 1) for column group j
+  auto tap = [&](int j, int l, int c) -> float {
+    if constexpr (WT) return c ? hi_bf(tw[j][l]) : lo_bf(tw[j][l]);
+    const uint32_t t = tw[j][2 * c + (l >> 1)];
+    return (l & 1) ? hi_bf(t) : lo_bf(t);
+  };
+
+  // Wave 0: the short filter on the 6 sub-channels of the pair and the gate.
+  uint32_t zraw[3], c1raw[3];
+  float x2[2] = {0.f, 0.f}, u[2] = {0.f, 0.f};
+  uint32_t *c0p = nullptr, *c1p = nullptr;
+  if (m == 0) {
+    const uint32_t *zr = reinterpret_cast<const uint32_t *>(a.z + b * a.sz + 3 * (int64_t)hc);
+    bf16_t *cbase = a.cs + blk * a.cs0 + 3 * (int64_t)hc;
+    c0p = reinterpret_cast<uint32_t *>(cbase);
+    c1p = reinterpret_cast<uint32_t *>(cbase + a.cs2);
+    uint32_t c0raw[3];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      zraw[i] = zr[i];
+      c0raw[i] = c0p[i];
+      c1raw[i] = c1p[i];
+    }
+    float xf[6], c0f[6], c1f[6], wsf[18];
+    unpack3(zraw, xf);
+    unpack3(c0raw, c0f);
+    unpack3(c1raw, c1f);
+    const uint32_t *wsp = reinterpret_cast<const uint32_t *>(a.ws + 9 * (int64_t)hc);
+#pragma unroll
+    for (int i = 0; i < 9; ++i) {
+      const uint32_t t = wsp[i];
+      wsf[2 * i] = lo_bf(t);
+      wsf[2 * i + 1] = hi_bf(t);
+    }
+    float y6[6];
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+      float acc = 0.0f + rbf(c0f[i] * wsf[3 * i]);
+      acc = acc + rbf(c1f[i] * wsf[3 * i + 1]);
+      acc = acc + rbf(xf[i] * wsf[3 * i + 2]);
+      y6[i] = rbf(acc);
+    }
+    x2[0] = y6[0];
+    x2[1] = y6[3];
+    u[0] = rbf(y6[1] * y6[2]);
+    u[1] = rbf(y6[4] * y6[5]);
+  }
+
+  float acc[2][4];
+#pragma unroll
+  for (int c = 0; c < 2; ++c)
+#pragma unroll
+    for (int l = 0; l < 4; ++l) acc[c][l] = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+#pragma unroll
+    for (int l = 0; l < 4; ++l) {
+      acc[0][l] = acc[0][l] + v[j][l].x * tap(j, l, 0);
+      acc[1][l] = acc[1][l] + v[j][l].y * tap(j, l, 1);
+    }
+  if (m > 0) {
+#pragma unroll
+    for (int l = 0; l < 4; ++l) part[m - 1][l][lane] = make_float2(acc[0][l], acc[1][l]);
+  }
+  __syncthreads();  // all window loads consumed; partial sums visible
+
+  if (active) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int l = 0; l < 4; ++l) {
+        const int k = 16 * j + 4 * m + l;
+        if (k >= 1 && k < 127) *reinterpret_cast<float2 *>(s + (int64_t)(k - 1) * a.is2) = v[j][l];
+      }
+  }
+  if (m != 0 || !active) return;
+  float last[2];
+  if constexpr (WT) {
+    const uint32_t t = *reinterpret_cast<const uint32_t *>(w + (int64_t)127 * a.wi1 + h0);
+    last[0] = lo_bf(t);
+    last[1] = hi_bf(t);
+  } else {
+    last[0] = bf2f(w[(int64_t)h0 * a.wi0 + 127]);
+    last[1] = bf2f(w[(int64_t)(h0 + 1) * a.wi0 + 127]);
+  }
+  float y[2];
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    float p[4];
+#pragma unroll
+    for (int l = 0; l < 4; ++l) {
+      const float2 p1 = part[0][l][lane], p2 = part[1][l][lane], p3 = part[2][l][lane];
+      p[l] = ((acc[c][l] + (c ? p1.y : p1.x)) + (c ? p2.y : p2.x)) + (c ? p3.y : p3.x);
+    }
+    y[c] = rbf(((p[0] + p[2]) + (p[1] + p[3])) + last[c] * u[c]);
+  }
+  *reinterpret_cast<float2 *>(s + 126 * a.is2) = make_float2(u[0], u[1]);
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    c0p[i] = c1raw[i];
+    c1p[i] = zraw[i];
+  }
+  if constexpr (HAS_D) {
+    const uint32_t dv = *reinterpret_cast<const uint32_t *>(a.D + h0);
+    y[0] = rbf(y[0] + rbf(lo_bf(dv) * u[0]));
+    y[1] = rbf(y[1] + rbf(hi_bf(dv) * u[1]));
+  }
+  *reinterpret_cast<uint32_t *>(a.out + b * a.so + h0) = pack_bf(x2[0] * y[0], x2[1] * y[1]);
+}
+
+template <bool HAS_D, bool WT>
+static void launch_hcm_split(const DecodeArgs &a, int64_t B, hipStream_t stream) {
+  dim3 grid(static_cast<unsigned>(cdiv(a.H / 2, 64)), static_cast<unsigned>(B));
+  hipLaunchKernelGGL((hcm_decode_split_kernel<HAS_D, WT>), grid, dim3(256), 0, stream, a);
+}
+
+// ---------------------------------------------------------------------------
+// hcl with four lanes per channel: lane q of a quad owns states 4q..4q+3, so
+// the state, residue and log-pole rows move as one float4 per lane with the
+// 64 lanes of a wave covering 1 KB contiguously.  Lanes 0-2 of the quad run
+// the short filter for sub-channels x2, x1, v; the values are shared with
+// quad DPP moves.  The readout keeps the reference's halving tree:
+// r[i] += r[i+8] (lane q takes lane q+2), r[i] += r[i+4] (lane 0 takes lane
+// 1), r[i] += r[i+2] in lane 0, y = r0 + r1 (triton_decode.py:81-96).
+template <int CTRL>
+__device__ __forceinline__ float quad_perm(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+template <bool HAS_D>
+__global__ __launch_bounds__(256) void hcl_decode_quad_kernel(DecodeArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int q = lane & 3;
+  const int h = blockIdx.x * 64 + (threadIdx.x >> 2);
+  const bool active = h < a.H;
+  const int hc = active ? h : a.H - 1;
+  const int64_t b = blockIdx.y;
+  const int64_t blk = a.slots[b * a.ssl];
+  bf16_t *o = a.out + b * a.so + h;
+  if (blk == a.null_block || blk < 0 || blk >= a.num_blocks) {  // uniform
+    if (q == 0 && active) *o = 0;
+    return;
+  }
+  const float4 s4 = *reinterpret_cast<const float4 *>(a.st + blk * a.is0 + (int64_t)hc * a.is1 + 4 * q);
+  const float4 r4 = *reinterpret_cast<const float4 *>(static_cast<const float *>(a.inner) +
+                                                      (int64_t)hc * a.wi0 + 4 * q);
+  const float4 l4 = *reinterpret_cast<const float4 *>(a.lp + (int64_t)hc * a.lp0 + 4 * q);
+  // short filter, sub-channel i = q (lane 3 mirrors lane 2 and stores nothing)
+  const int i = q < 3 ? q : 2;
+  const int64_t ch = 3 * (int64_t)hc + i;
+  bf16_t *cw = a.cs + blk * a.cs0 + ch * a.cs1;
+  const bf16_t xb = a.z[b * a.sz + ch];
+  const bf16_t c0b = cw[0], c1b = cw[a.cs2];
+  const float yi = short_tap(bf2f(xb), bf2f(c0b), bf2f(c1b), a.ws + ch * 3);
+  const float x2 = quad_perm<0x00>(yi);
+  const float x1 = quad_perm<0x55>(yi);
+  const float vv = quad_perm<0xAA>(yi);
+  const float u = rbf(x1 * vv);
+
+  float sv[4] = {s4.x, s4.y, s4.z, s4.w};
+  const float rv[4] = {r4.x, r4.y, r4.z, r4.w};
+  const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
+  float r[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    sv[e] = sv[e] * expf(lv[e]) + u;
+    r[e] = sv[e] * rv[e];
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) r[e] = r[e] + quad_perm<0xEE>(r[e]);  // lane q += lane q+2
+#pragma unroll
+  for (int e = 0; e < 4; ++e) r[e] = r[e] + quad_perm<0xF5>(r[e]);  // lane 0 += lane 1
+  r[0] = r[0] + r[2];
+  r[1] = r[1] + r[3];
+  float y = rbf((r[0] + r[1]) + 0.0f);
+
+  if (active) {
+    *reinterpret_cast<float4 *>(a.st + blk * a.is0 + (int64_t)h * a.is1 + 4 * q) =
+        make_float4(sv[0], sv[1], sv[2], sv[3]);
+    if (q < 3) {
+      cw[0] = c1b;
+      cw[a.cs2] = xb;
+    }
+  }
+  if constexpr (HAS_D) y = rbf(y + rbf(bf2f(a.D[hc]) * u));
+  if (q == 0 && active) *o = f2bf(x2 * y);
+}
+
+template <bool HAS_D>
+static void launch_hcl_quad(const DecodeArgs &a, int64_t B, hipStream_t stream) {
+  dim3 grid(static_cast<unsigned>(cdiv(a.H, 64)), static_cast<unsigned>(B));
+  hipLaunchKernelGGL((hcl_decode_quad_kernel<HAS_D>), grid, dim3(256), 0, stream, a);
+}
+
 static bool aligned(const void *p, uintptr_t n) {
   return p == nullptr || (reinterpret_cast<uintptr_t>(p) % n) == 0;
 }
@@ -497,10 +746,10 @@ extern "C" int evo2_hyena_decode(const void *z, int64_t sz, const void *short_w,
   const int pv = pair_variant(a, kind);
   if (pv >= 0) {
     if (kind == KIND_HCL) {
-      hasD ? launch_pair<KIND_HCL, true, false>(a, B, st) : launch_pair<KIND_HCL, false, false>(a, B, st);
+      hasD ? launch_hcl_quad<true>(a, B, st) : launch_hcl_quad<false>(a, B, st);
     } else if (kind == KIND_HCM) {
-      if (pv) hasD ? launch_pair<KIND_HCM, true, true>(a, B, st) : launch_pair<KIND_HCM, false, true>(a, B, st);
-      else hasD ? launch_pair<KIND_HCM, true, false>(a, B, st) : launch_pair<KIND_HCM, false, false>(a, B, st);
+      if (pv) hasD ? launch_hcm_split<true, true>(a, B, st) : launch_hcm_split<false, true>(a, B, st);
+      else hasD ? launch_hcm_split<true, false>(a, B, st) : launch_hcm_split<false, false>(a, B, st);
     } else {
       if (pv) hasD ? launch_pair<KIND_HCS, true, true>(a, B, st) : launch_pair<KIND_HCS, false, true>(a, B, st);
       else hasD ? launch_pair<KIND_HCS, true, false>(a, B, st) : launch_pair<KIND_HCS, false, false>(a, B, st);

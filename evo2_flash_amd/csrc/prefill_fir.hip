@@ -420,10 +420,14 @@ __global__ __launch_bounds__(256) void fir_prefill_kernel(FirArgs p) {
 // ---------------------------------------------------------------------------
 // Window update after a prefill launch: per segment and channel, the new
 // windows are the last inputs of cat(old window, segment) (mixers.py:380-382),
-// written oldest first.  Destination column q reads source column q + (e-a)
-// when it falls in the old window, so increasing q is safe in place.  The
-// inner window is written before the conv window because recomputing u near
-// the segment start reads the old conv window.
+// oldest first.  The update is in place, and for a segment shorter than the
+// window destination column q reads old column q + (e - a), so every value is
+// gathered into registers first and written after a workgroup barrier.  A
+// workgroup owns 64 channels of one segment: with W = 127 its four waves take
+// 32 columns each, with W = 6 each wave owns its own 64 channels.  The conv
+// window (2 columns of the 3 sub-channels) rides along with the first wave of
+// each channel block.  u near the segment start is recomputed through the
+// short filter from z and the old conv window (FUSED), or read from u rows.
 struct WinArgs {
   const bf16_t *x; int64_t sx;              // z (FUSED) or u rows
   const bf16_t *ws;
@@ -432,66 +436,97 @@ struct WinArgs {
   const int32_t *seq;
   const int32_t *blocks; int64_t sblk;
   int H;
-  int K;          // inner window K-1 columns; 0 for none
   bool fused;     // u from z through the short filter, else u = x
   bool conv;      // rewrite the conv window too
   int64_t num_blocks;
 };
 
-__global__ __launch_bounds__(64) void window_update_kernel(WinArgs p) {
+template <int W>
+__global__ __launch_bounds__(256) void window_update_kernel(WinArgs p) {
+  constexpr int NW = W > 32 ? 4 : 1;          // waves per channel block
+  constexpr int CPW = (W + NW - 1) / NW;      // window columns per wave
+  constexpr int CB = 4 / NW;                  // channel blocks per workgroup
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int part = wave % NW;
+  const int c = (blockIdx.y * CB + wave / NW) * 64 + lane;
+  const bool active = c < p.H;
+  const int cl = active ? c : p.H - 1;
   const int seg = blockIdx.x;
-  const int c = blockIdx.y * 64 + threadIdx.x;
-  if (c >= p.H) return;
   const int64_t a = p.seq[3 * seg], e = p.seq[3 * seg + 1];
-  if (e <= a) return;
   const int64_t blk = p.blocks[seg * p.sblk];
-  if (blk < 0 || blk >= p.num_blocks) return;
+  if (e <= a || blk < 0 || blk >= p.num_blocks) return;  // uniform over the block
   const bool init = p.seq[3 * seg + 2] != 0;
-  ShortCtx ctx{p.x, p.sx, init ? p.cs + blk * p.cs0 : nullptr, p.cs1, p.cs2, a, init};
-  if (p.K > 1) {
-    float *st = p.st + blk * p.st0 + (int64_t)c * p.st1;
-    const int W = p.K - 1;
-    float wsf[3][3];
-    float zm2[3] = {0.f, 0.f, 0.f}, zm1[3] = {0.f, 0.f, 0.f};
-    const int64_t src0 = e - W;
-    if (p.fused) {
-      for (int i = 0; i < 3; ++i) {
-        for (int j = 0; j < 3; ++j) wsf[i][j] = bf2f(p.ws[(3 * (int64_t)c + i) * 3 + j]);
-        zm2[i] = z_at(ctx, src0 - 2, 3 * (int64_t)c + i);
-        zm1[i] = z_at(ctx, src0 - 1, 3 * (int64_t)c + i);
-      }
+  const bf16_t *conv_old = init ? p.cs + blk * p.cs0 : nullptr;
+  ShortCtx ctx{p.x, p.sx, conv_old, p.cs1, p.cs2, a, init};
+  float *st = p.st + blk * p.st0 + (int64_t)cl * p.st1;
+
+  // ---- gather
+  const int q0 = part * CPW;
+  const int64_t src0 = e - W + q0;
+  float v[CPW];
+  if (p.fused) {
+    float wsf[2][3], zm2[2], zm1[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+      for (int j = 0; j < 3; ++j) wsf[i][j] = bf2f(p.ws[(3 * (int64_t)cl + 1 + i) * 3 + j]);
+      zm2[i] = z_at(ctx, src0 - 2, 3 * (int64_t)cl + 1 + i);
+      zm1[i] = z_at(ctx, src0 - 1, 3 * (int64_t)cl + 1 + i);
     }
-    for (int q = 0; q < W; ++q) {
+#pragma unroll
+    for (int q = 0; q < CPW; ++q) {
       const int64_t src = src0 + q;
-      float v;
-      if (p.fused) {
-        float z0[3], y3[3];
-        for (int i = 0; i < 3; ++i) {
-          z0[i] = z_at(ctx, src, 3 * (int64_t)c + i);
-          y3[i] = short_out(zm2[i], zm1[i], z0[i], wsf[i]);
-          zm2[i] = zm1[i];
-          zm1[i] = z0[i];
-        }
-        v = rbf(y3[1] * y3[2]);
-      } else {
-        v = (src >= a) ? bf2f(p.x[src * p.sx + c]) : 0.0f;
+      float y[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        // columns past the window (the last wave's padding) would read row e
+        const float z0 = (q0 + q < W) ? z_at(ctx, src, 3 * (int64_t)cl + 1 + i) : 0.0f;
+        y[i] = short_out(zm2[i], zm1[i], z0, wsf[i]);
+        zm2[i] = zm1[i];
+        zm1[i] = z0;
       }
-      if (src < a) v = init ? st[(q + (e - a)) * p.st2] : 0.0f;
-      st[q * p.st2] = v;
+      v[q] = rbf(y[0] * y[1]);
+    }
+  } else {
+#pragma unroll
+    for (int q = 0; q < CPW; ++q) {
+      const int64_t src = src0 + q;
+      v[q] = (src >= a && q0 + q < W) ? bf2f(p.x[src * p.sx + cl]) : 0.0f;
     }
   }
-  if (p.conv) {
-    bf16_t *cw = p.cs + blk * p.cs0;
+#pragma unroll
+  for (int q = 0; q < CPW; ++q) {
+    const int64_t src = src0 + q;
+    if (src < a) v[q] = (init && q0 + q < W) ? st[(q0 + q + (e - a)) * p.st2] : 0.0f;
+  }
+  bf16_t cv[2][3];
+  const bool do_conv = p.conv && part == 0;
+  bf16_t *cw = p.cs + blk * p.cs0;
+  if (do_conv) {
+#pragma unroll
     for (int q = 0; q < 2; ++q) {
       const int64_t src = e - 2 + q;
+#pragma unroll
       for (int i = 0; i < 3; ++i) {
-        const int64_t ch = 3 * (int64_t)c + i;
-        bf16_t v;
-        if (src >= a) v = p.x[src * p.sx + ch];
-        else v = init ? cw[ch * p.cs1 + (q + (e - a)) * p.cs2] : bf16_t(0);
-        cw[ch * p.cs1 + q * p.cs2] = v;
+        const int64_t ch = 3 * (int64_t)cl + i;
+        cv[q][i] = src >= a ? p.x[src * p.sx + ch]
+                            : (init ? cw[ch * p.cs1 + (q + (e - a)) * p.cs2] : bf16_t(0));
       }
     }
+  }
+  __syncthreads();  // every old value is in registers before any write
+
+  // ---- write
+  if (!active) return;
+#pragma unroll
+  for (int q = 0; q < CPW; ++q)
+    if (q0 + q < W) st[(q0 + q) * p.st2] = v[q];
+  if (do_conv) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+#pragma unroll
+      for (int i = 0; i < 3; ++i) cw[(3 * (int64_t)c + i) * p.cs1 + q * p.cs2] = cv[q][i];
   }
 }
 
@@ -501,10 +536,15 @@ static void launch_fir(const FirArgs &a, int64_t ntiles, hipStream_t st) {
   hipLaunchKernelGGL((fir_prefill_kernel<K, HAS_D, FUSED>), grid, dim3(256), 0, st, a);
 }
 
-static int launch_window(const WinArgs &w, int64_t nseq, hipStream_t st) {
+static int launch_window(const WinArgs &w, int K, int64_t nseq, hipStream_t st) {
   if (nseq == 0) return EVO2_OK;
-  dim3 grid(static_cast<unsigned>(nseq), static_cast<unsigned>(cdiv(w.H, 64)));
-  hipLaunchKernelGGL(window_update_kernel, grid, dim3(64), 0, st, w);
+  if (K == 128) {
+    dim3 grid(static_cast<unsigned>(nseq), static_cast<unsigned>(cdiv(w.H, 64)));
+    hipLaunchKernelGGL(window_update_kernel<127>, grid, dim3(256), 0, st, w);
+  } else {
+    dim3 grid(static_cast<unsigned>(nseq), static_cast<unsigned>(cdiv(w.H, 256)));
+    hipLaunchKernelGGL(window_update_kernel<6>, grid, dim3(256), 0, st, w);
+  }
   return check_launch("prefill window update");
 }
 
@@ -553,8 +593,8 @@ extern "C" int evo2_fir_prefill(const void *u, int64_t su, const void *w, int64_
     if (rc) return rc;
   }
   WinArgs wa{static_cast<const bf16_t *>(u), su, nullptr, nullptr, 0, 0, 0, state, st0, st1, st2,
-             seq_table, blocks, sblk, static_cast<int>(H), K, false, false, num_blocks};
-  return launch_window(wa, nseq, st);
+             seq_table, blocks, sblk, static_cast<int>(H), false, false, num_blocks};
+  return launch_window(wa, K, nseq, st);
 }
 
 extern "C" int evo2_hyena_fir_prefill(const void *z, int64_t sz, const void *short_w,
@@ -590,6 +630,6 @@ extern "C" int evo2_hyena_fir_prefill(const void *z, int64_t sz, const void *sho
   }
   WinArgs wa{static_cast<const bf16_t *>(z), sz, static_cast<const bf16_t *>(short_w),
              static_cast<bf16_t *>(conv_state), cs0, cs1, cs2, inner_state, st0, st1, st2,
-             seq_table, blocks, sblk, static_cast<int>(H), K, true, true, num_blocks};
-  return launch_window(wa, nseq, st);
+             seq_table, blocks, sblk, static_cast<int>(H), true, true, num_blocks};
+  return launch_window(wa, K, nseq, st);
 }

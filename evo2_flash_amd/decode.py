@@ -52,6 +52,17 @@ def decode_supported(z, short_w, conv_state, inner, inner_state, D=None, log_pol
     return True
 
 
+def channel_major_taps(w):
+    """The FIR taps (H, K) as a view over channel-contiguous (K, H) storage.
+
+    Same values and shape as `w`; only the memory order changes, so tap k of
+    neighbouring channels is contiguous and the decode kernel reads each tap
+    column as one coalesced sweep.  The mixers keep their decode taps in this
+    layout (made once when the weights are loaded).
+    """
+    return w.t().contiguous().t()
+
+
 def hyena_decode(z, short_w, conv_state, slots, inner, inner_state, D=None,
                  log_poles=None, null_block=0):
     """x2 * (inner(x1*v) + D*(x1*v)) for one decode token per row; states in place.

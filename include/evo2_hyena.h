@@ -203,6 +203,26 @@ int evo2_fp8_gemm(const void *x8, int64_t sx, const void *w8, int64_t sw,
                   const float *x_scale, const float *w_scale, const void *bias,
                   void *out, int64_t so, int64_t M, int64_t N, int64_t K, void *stream);
 
+/*
+ * Evo2RMSNorm, optionally with the residual add and an fp8 epilogue:
+ *   s = bf16(x + residual)                     (when residual != NULL; written to s_out)
+ *   y = bf16(w * bf16(s / bf16(bf16(bf16(||s||_2) * H^-1/2) + eps)))
+ *   q = e4m3fn(clamp(y / q_scale[0], -448, 448))   (when q != NULL)
+ * eps sits outside the sqrt.  y may be NULL when q is given (the row only
+ * feeds the fp8 in_proj).  Rows have unit element stride.
+ *
+ *   x, residual, y, s_out  (T, H) bf16, row strides sx, sr, sy, ss
+ *   weight (H,) bf16;  q (T, H) e4m3 bytes, row stride sq (bytes)
+ *
+ * Replaces triton_norm.rms_norm / _norm_kernel (evo2_flash/triton_norm.py:70-156)
+ * behind Evo2RMSNorm.forward (evo2_flash/model.py:58-74), plus the activation
+ * quantisation of the static fp8 in_proj (evo2_flash/fp8_emul.py:76-78).
+ */
+int evo2_rms_norm(const void *x, int64_t sx, const void *residual, int64_t sr,
+                  const void *weight, float eps, void *y, int64_t sy,
+                  void *s_out, int64_t ss, const float *q_scale, void *q, int64_t sq,
+                  int64_t T, int64_t H, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,103 @@
+"""GPU parity of the operator-level mixers (HyenaFIRMixer / HyenaIIRMixer,
+mixers.py:1238-1423) against the oracle's composition of the reference path:
+fp8 in_proj (dequantised matmul), the mixer core, bf16 out_proj with bias.
+
+One mixed step per mixer kind: decode rows first (one on the null block),
+then two prefill segments (one continuing a cached state), then graph-padding
+rows that must come out zero.  Outputs within 1e-2 max relative error; the
+paged state pool after the step within tolerance.
+"""
+
+import itertools
+
+import pytest
+import torch
+
+import oracle
+from evo2_flash_amd.config import HyenaConfig
+from evo2_flash_amd.metadata import build_metadata
+from evo2_flash_amd.mixers import load_mixer_params, make_mixer, set_forward_context
+from evo2_flash_amd.synthetic import mixer_params
+
+from _cases import clone_pool, max_rel_err, random_pool
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+_ids = itertools.count()
+
+
+def _oracle_step(kind, prm, hs, pool, dec_slots, pre_lens, pre_slots, pre_init, H):
+    nd, npt = len(dec_slots), sum(pre_lens)
+    z = oracle.fp8_linear_dequant(hs[:nd + npt], prm["in_proj.weight"], prm["in_proj.input_scale"],
+                                  prm["in_proj.weight_scale"])
+    sw = prm["short_filter"].view(3 * H, 3)
+    D = prm.get("D")
+    qsl = [0]
+    for n in pre_lens:
+        qsl.append(qsl[-1] + n)
+    if kind == "hcl":
+        res, lp = prm["residues"], prm["log_poles"][..., 0]
+        gd = oracle.hyena_decode_emulated(z[:nd], sw, pool.conv_view(), dec_slots, res,
+                                          pool.ssm_view(), D, lp)
+        gp = oracle.iir_mixer_prefill(z[nd:], sw, pool.conv_view(), res, lp, pool.ssm_view(), D,
+                                      qsl, pre_slots, pre_init)
+    else:
+        K = prm["conv"].shape[-1]
+        w = prm["conv"].view(H, K)
+        gd = oracle.hyena_decode_emulated(z[:nd], sw, pool.conv_view(), dec_slots, w,
+                                          pool.inner_view(K - 1), D)
+        gp = oracle.fir_mixer_prefill(z[nd:], sw, pool.conv_view(), w, pool.inner_view(K - 1), D,
+                                      qsl, pre_slots, pre_init)
+    g = torch.cat([gd, gp]).float()
+    out = (g @ prm["out_proj.weight"].float().t() + prm["out_proj.bias"].float()).to(torch.bfloat16)
+    full = torch.zeros(hs.shape, dtype=torch.bfloat16)
+    full[:nd + npt] = out
+    return full
+
+
+@pytest.mark.parametrize("kind", ["hcs", "hcm", "hcl"])
+def test_mixer_mixed_step_vs_oracle(kind):
+    H, nblk = 256, 10
+    cfg = HyenaConfig(hidden_size=H, num_hidden_layers=3, hcs_layer_idxs=[0], hcm_layer_idxs=[1],
+                      hcl_layer_idxs=[2], use_fp8_input_projections=True)
+    layer = {"hcs": 0, "hcm": 1, "hcl": 2}[kind]
+    mixer = make_mixer(cfg, layer, prefix=f"t{next(_ids)}.mixer", device=DEV)
+    prm = mixer_params(kind, H, seed=40 + layer, in_proj_fp8=True)
+    load_mixer_params(mixer, prm)
+    pool = random_pool(nblk, H, seed=41)
+    gp = clone_pool(pool, DEV)
+    mixer.kv_cache = gp.kv_cache
+    dec_slots, pre_lens, pre_slots, pre_init = [3, 0, 7], [37, 70], [5, 2], [1, 0]
+    nd, npt, pad = len(dec_slots), sum(pre_lens), 5
+    g = torch.Generator().manual_seed(layer)
+    hs = torch.randn(nd + npt + pad, H, generator=g).to(torch.bfloat16)
+    m = build_metadata(decode_slots=dec_slots, prefill_lens=pre_lens, prefill_slots=pre_slots,
+                       has_init=pre_init, device=DEV)
+    print(f"mixer {kind} nd={nd} prefill={pre_lens}", flush=True)
+    with set_forward_context(m):
+        out = mixer(hs.to(DEV)).cpu()
+    ref = _oracle_step(kind, prm, hs, pool, dec_slots, pre_lens, pre_slots, pre_init, H)
+    assert (out[nd + npt:].float() == 0).all()
+    assert max_rel_err(out, ref) <= 1e-2
+    # conv windows hold raw in_proj rows, which the GPU's fp8 GEMM and the
+    # oracle's dequantised matmul round independently
+    assert max_rel_err(gp.kv_cache[0].cpu(), pool.kv_cache[0]) <= 1e-2
+    assert max_rel_err(gp.kv_cache[1].cpu(), pool.kv_cache[1]) <= 1e-2
+    assert max_rel_err(gp.kv_cache[2].cpu(), pool.kv_cache[2]) <= 1e-3
+
+
+def test_mixer_profile_run_without_metadata():
+    """No metadata (the engine's profiling pass): out_proj(x2 * x1 * v)."""
+    H = 256
+    cfg = HyenaConfig(hidden_size=H, num_hidden_layers=1, hcm_layer_idxs=[0],
+                      use_fp8_input_projections=True)
+    mixer = make_mixer(cfg, 0, prefix=f"t{next(_ids)}.mixer", device=DEV)
+    prm = mixer_params("hcm", H, seed=3, in_proj_fp8=True)
+    load_mixer_params(mixer, prm)
+    hs = torch.randn(9, H, generator=torch.Generator().manual_seed(0)).to(torch.bfloat16)
+    out = mixer(hs.to(DEV)).cpu()
+    z = oracle.fp8_linear_dequant(hs, prm["in_proj.weight"], prm["in_proj.input_scale"],
+                                  prm["in_proj.weight_scale"])
+    y = (z[:, 0::3] * z[:, 1::3] * z[:, 2::3]).float()
+    ref = (y @ prm["out_proj.weight"].float().t() + prm["out_proj.bias"].float())
+    assert max_rel_err(out, ref) <= 2e-2
