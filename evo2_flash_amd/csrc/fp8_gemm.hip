@@ -7,25 +7,35 @@
 // (mixers.py:741-757, 1076-1092; scales in the dequantisation convention,
 // convert.py:195-201), and the same GEMM for out_proj when it is quantised.
 //
-// Kernel: a 256 x 256 output tile per workgroup (W rows x X rows), K in steps
-// of 128 bytes.  Four waves each own a 128 x 128 quadrant as 4 x 4 tiles of
+// Kernel: a 256 x 256 output tile per workgroup (W rows x X rows).  Four
+// waves each own a 128 x 128 quadrant as 4 x 4 tiles of
 // v_mfma_f32_32x32x64_f8f6f4 (the weight is MFMA operand A, so each lane
 // ends up with four consecutive output columns of one row, stored as one
-// 8-byte write).  Tiles of W and X move HBM -> LDS with direct-to-LDS loads
-// into a double buffer, the next K step in flight while the current one
-// computes.  LDS rows are 128 bytes; the 16-byte chunk c of row r sits at
-// c ^ (r & 7), so the b128 fragment reads of 8 consecutive rows hit 8
-// different bank groups.
+// 8-byte write).  K moves through a ring of five LDS stages of 64 bytes
+// each (16 KB of W and 16 KB of X per stage), filled HBM -> LDS by
+// direct-to-LDS loads four steps ahead of the MFMAs that consume them, so
+// about three steps of MFMA work (~1.5 us) cover the load latency even when
+// a load misses L2.  Each
+// stage is its own __shared__ variable and the step loop is unrolled over
+// the ring, so the compiler can see that reading one stage does not wait on
+// the loads still landing in the others.  LDS rows are 64 bytes; the 16-byte
+// chunk c of row r sits at c ^ ((r >> 2) & 3): a b128 read is served 16
+// lanes (16 consecutive rows) at a time over 64 banks, and the swizzle puts
+// those 16 rows' chunks in 16 different bank groups.
+#include <type_traits>
+
 #include "common.h"
 
 namespace evo2 {
 
 typedef __attribute__((ext_vector_type(8))) int i32x8;
 typedef __attribute__((ext_vector_type(16))) float f32x16;
+typedef __attribute__((address_space(3))) void lds_void;
 
-constexpr int G_BM = 256;   // X rows per workgroup
-constexpr int G_BN = 256;   // W rows per workgroup
-constexpr int G_BK = 128;   // bytes of K per step
+constexpr int G_BM = 256;       // X rows per workgroup
+constexpr int G_BN = 256;       // W rows per workgroup
+constexpr int G_BK = 64;        // bytes of K per stage (one MFMA k-step)
+constexpr int G_STAGE = G_BN * G_BK;  // bytes per operand per stage
 
 struct GemmArgs {
   const uint8_t *x; int64_t sx;   // (M, K) e4m3, row stride (bytes)
@@ -37,14 +47,17 @@ struct GemmArgs {
   int M, N, K;
 };
 
-__device__ __forceinline__ void vmcnt_wait_16() {
-  // s_waitcnt vmcnt(16): vmcnt bits [3:0] and [15:14], expcnt/lgkmcnt maxed.
-  __builtin_amdgcn_s_waitcnt((16 & 0xF) | ((16 >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+// s_waitcnt vmcnt(n) alone (expcnt and lgkmcnt left at their maxima), without
+// the workgroup memory fence __syncthreads adds.
+template <int N>
+__device__ __forceinline__ void vmcnt_wait() {
+  static_assert(N >= 0 && N < 64, "vmcnt field is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
 __global__ __launch_bounds__(256) void fp8_gemm_kernel(GemmArgs p) {
-  __shared__ __align__(16) uint8_t lw[2][G_BN * G_BK];
-  __shared__ __align__(16) uint8_t lx[2][G_BM * G_BK];
+  __shared__ __align__(16) uint8_t w0[G_STAGE], w1[G_STAGE], w2[G_STAGE], w3[G_STAGE], w4[G_STAGE];
+  __shared__ __align__(16) uint8_t x0[G_STAGE], x1[G_STAGE], x2[G_STAGE], x3[G_STAGE], x4[G_STAGE];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -54,23 +67,27 @@ __global__ __launch_bounds__(256) void fp8_gemm_kernel(GemmArgs p) {
   const int wn = (wave & 1) * 128;   // wave quadrant in W rows
   const int wm = (wave >> 1) * 128;  // wave quadrant in X rows
 
-  // DMA: each wave instruction fills 1 KB = 8 rows of 128 bytes; lane i
-  // writes LDS chunk i of that block, i.e. row i/8, physical chunk i%8,
-  // which holds logical chunk (i%8) ^ (row & 7).
-  auto issue = [&](int buf, int k0) {
+  // DMA: one wave instruction fills 1 KB = 16 rows of 64 bytes; lane i
+  // writes row i/4, physical chunk i%4, which holds logical chunk
+  // (i%4) ^ ((row >> 2) & 3).  Each wave moves 4 such blocks of W and 4 of X
+  // per stage; rows past M or N re-read the last row (never stored).
+  const uint8_t *gw[4], *gx[4];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int blk = wave * 8 + j;         // 32 blocks of 8 rows per tile
-      const int row = blk * 8 + lane / 8;
-      const int lchunk = (lane & 7) ^ (row & 7);
-      const int wr = min(n0 + row, p.N - 1);
-      const int xr = min(m0 + row, p.M - 1);
-      __builtin_amdgcn_global_load_lds(p.w + (int64_t)wr * p.sw + k0 + lchunk * 16,
-                                       (__attribute__((address_space(3))) void *)(&lw[buf][blk * 1024]),
-                                       16, 0, 0);
-      __builtin_amdgcn_global_load_lds(p.x + (int64_t)xr * p.sx + k0 + lchunk * 16,
-                                       (__attribute__((address_space(3))) void *)(&lx[buf][blk * 1024]),
-                                       16, 0, 0);
+  for (int j = 0; j < 4; ++j) {
+    const int row = (wave * 4 + j) * 16 + lane / 4;
+    const int lchunk = (lane & 3) ^ ((row >> 2) & 3);
+    gw[j] = p.w + (int64_t)min(n0 + row, p.N - 1) * p.sw + lchunk * 16;
+    gx[j] = p.x + (int64_t)min(m0 + row, p.M - 1) * p.sx + lchunk * 16;
+  }
+  auto issue = [&](auto stage, int k0) __attribute__((always_inline)) {
+    constexpr int S = decltype(stage)::value;
+    uint8_t *lw = S == 0 ? w0 : S == 1 ? w1 : S == 2 ? w2 : S == 3 ? w3 : w4;
+    uint8_t *lx = S == 0 ? x0 : S == 1 ? x1 : S == 2 ? x2 : S == 3 ? x3 : x4;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int blk = wave * 4 + j;
+      __builtin_amdgcn_global_load_lds(gw[j] + k0, (lds_void *)(lw + blk * 1024), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(gx[j] + k0, (lds_void *)(lx + blk * 1024), 16, 0, 0);
     }
   };
 
@@ -82,69 +99,126 @@ __global__ __launch_bounds__(256) void fp8_gemm_kernel(GemmArgs p) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-  const int KT = p.K / G_BK;
-  issue(0, 0);
-  const int g = lane >> 5;   // lane group: k bytes [32g, 32g + 32) of a 64-k step
+  const int g = lane >> 5;   // lane group: k bytes [32g, 32g + 32) of the step
   const int lr = lane & 31;  // row within a 32-row MFMA tile
-  for (int kt = 0; kt < KT; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < KT) {
-      issue(buf ^ 1, (kt + 1) * G_BK);
-      vmcnt_wait_16();  // this step's 16 loads have landed; the next 16 fly
-    } else {
-      __builtin_amdgcn_s_waitcnt(0);
+  // Byte offset of this lane's two 16-byte chunks in row r of a stage.
+  auto frag_off = [&](int r) __attribute__((always_inline)) {
+    const int sw = (r >> 2) & 3;
+    return r * G_BK + (((2 * g) ^ sw) << 4);
+  };
+  auto frag_off1 = [&](int r) __attribute__((always_inline)) {
+    const int sw = (r >> 2) & 3;
+    return r * G_BK + (((2 * g + 1) ^ sw) << 4);
+  };
+
+  const int KT = p.K / G_BK;
+  auto read_frags = [&](auto stage, i32x8 fa[4], i32x8 fb[4]) __attribute__((always_inline)) {
+    constexpr int S = decltype(stage)::value;
+    const uint8_t *lw = S == 0 ? w0 : S == 1 ? w1 : S == 2 ? w2 : S == 3 ? w3 : w4;
+    const uint8_t *lx = S == 0 ? x0 : S == 1 ? x1 : S == 2 ? x2 : S == 3 ? x3 : x4;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int rw = wn + 32 * t + lr;
+      const int rx = wm + 32 * t + lr;
+      const uint4 a0 = *reinterpret_cast<const uint4 *>(lw + frag_off(rw));
+      const uint4 a1 = *reinterpret_cast<const uint4 *>(lw + frag_off1(rw));
+      const uint4 b0 = *reinterpret_cast<const uint4 *>(lx + frag_off(rx));
+      const uint4 b1 = *reinterpret_cast<const uint4 *>(lx + frag_off1(rx));
+      fa[t] = i32x8{(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w, (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
+      fb[t] = i32x8{(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w, (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
     }
-    __syncthreads();
+  };
+  auto mma = [&](const i32x8 fa[4], const i32x8 fb[4]) __attribute__((always_inline)) {
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      i32x8 fa[4], fb[4];
-      const int c0 = ks * 4 + 2 * g;  // logical chunks c0, c0+1
+    for (int tn = 0; tn < 4; ++tn)
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const int rw = wn + 32 * t + lr;
-        const int rx = wm + 32 * t + lr;
-        const uint4 a0 = *reinterpret_cast<const uint4 *>(&lw[buf][rw * G_BK + ((c0 ^ (rw & 7)) << 4)]);
-        const uint4 a1 = *reinterpret_cast<const uint4 *>(&lw[buf][rw * G_BK + (((c0 + 1) ^ (rw & 7)) << 4)]);
-        const uint4 b0 = *reinterpret_cast<const uint4 *>(&lx[buf][rx * G_BK + ((c0 ^ (rx & 7)) << 4)]);
-        const uint4 b1 = *reinterpret_cast<const uint4 *>(&lx[buf][rx * G_BK + (((c0 + 1) ^ (rx & 7)) << 4)]);
-        fa[t] = i32x8{(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w, (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
-        fb[t] = i32x8{(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w, (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
-      }
+      for (int tm = 0; tm < 4; ++tm)
+        acc[tn][tm] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa[tn], fb[tm], acc[tn][tm],
+                                                                       0, 0, 0, 0, 0, 0);
+  };
+
+  // Step k runs the MFMAs of stage k from fragments read during step k - 1,
+  // and meanwhile reads stage k + 1's fragments: it first waits for stage
+  // k + 1's loads (stages k + 2 and k + 3 stay in flight) and a barrier
+  // (every wave's loads for k + 1 have landed; every wave has consumed stage
+  // k - 1, which is refilled with stage k + 4 right after).  Refills past the
+  // end of K re-read the last slice, and the fragments read for the step
+  // after the last are never used, so every step has the same shape.
+  i32x8 fa[2][4], fb[2][4];
+  auto step = [&](auto stage, auto fbuf, int k) __attribute__((always_inline)) {
+    constexpr int S = decltype(stage)::value;
+    constexpr int B = decltype(fbuf)::value;  // fragment buffer holding stage k
+    vmcnt_wait<16>();
+    __builtin_amdgcn_s_barrier();
+    issue(std::integral_constant<int, (S + 4) % 5>{}, min(k + 4, KT - 1) * G_BK);
+    read_frags(std::integral_constant<int, (S + 1) % 5>{}, fa[B ^ 1], fb[B ^ 1]);
+    mma(fa[B], fb[B]);
+    // Interleave: each MFMA is followed by one fragment read for the next
+    // stage and (for the first eight) one refill load, so the LDS and memory
+    // traffic hides under the matrix pipe instead of bunching up.
 #pragma unroll
-      for (int tn = 0; tn < 4; ++tn)
-#pragma unroll
-        for (int tm = 0; tm < 4; ++tm)
-          acc[tn][tm] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa[tn], fb[tm], acc[tn][tm],
-                                                                         0, 0, 0, 0, 0, 0);
+    for (int i = 0; i < 16; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      if (i < 8) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
     }
-    __syncthreads();  // everyone is done with `buf` before it is refilled
-  }
+  };
+  // Ten steps cover every (stage, fragment buffer) pair once.
+  auto ten_steps = [&](int k, bool guard) __attribute__((always_inline)) {
+    using std::integral_constant;
+    using I0 = integral_constant<int, 0>;
+    using I1 = integral_constant<int, 1>;
+    step(I0{}, I0{}, k);
+    if (!guard || k + 1 < KT) step(I1{}, I1{}, k + 1);
+    if (!guard || k + 2 < KT) step(integral_constant<int, 2>{}, I0{}, k + 2);
+    if (!guard || k + 3 < KT) step(integral_constant<int, 3>{}, I1{}, k + 3);
+    if (!guard || k + 4 < KT) step(integral_constant<int, 4>{}, I0{}, k + 4);
+    if (!guard || k + 5 < KT) step(I0{}, I1{}, k + 5);
+    if (!guard || k + 6 < KT) step(I1{}, I0{}, k + 6);
+    if (!guard || k + 7 < KT) step(integral_constant<int, 2>{}, I1{}, k + 7);
+    if (!guard || k + 8 < KT) step(integral_constant<int, 3>{}, I0{}, k + 8);
+    if (!guard || k + 9 < KT) step(integral_constant<int, 4>{}, I1{}, k + 9);
+  };
+
+  using S0 = std::integral_constant<int, 0>;
+  issue(S0{}, 0);
+  issue(std::integral_constant<int, 1>{}, min(1, KT - 1) * G_BK);
+  issue(std::integral_constant<int, 2>{}, min(2, KT - 1) * G_BK);
+  issue(std::integral_constant<int, 3>{}, min(3, KT - 1) * G_BK);
+  vmcnt_wait<24>();  // stage 0 (stages 1-3 in flight)
+  __builtin_amdgcn_s_barrier();
+  read_frags(S0{}, fa[0], fb[0]);
+  int k = 0;
+  for (; k + 10 <= KT; k += 10) ten_steps(k, false);
+  if (k < KT) ten_steps(k, true);
+  // No direct-to-LDS write may still be landing when the workgroup's LDS is
+  // handed to the next one.
+  vmcnt_wait<0>();
 
   // Epilogue: lane holds, for X row m = m0 + wm + 32 tm + lr, the W rows
   // n = n0 + wn + 32 tn + 8 q + 4 g + i (i < 4) in acc[tn][tm][4 q + i].
   const float scale = p.sx_scale[0] * p.sw_scale[0];
+  const bool full = m0 + G_BM <= p.M && n0 + G_BN <= p.N && (p.so % 4) == 0 &&
+                    (reinterpret_cast<uintptr_t>(p.out) & 7) == 0;
 #pragma unroll
   for (int tm = 0; tm < 4; ++tm) {
     const int m = m0 + wm + 32 * tm + lr;
-    if (m >= p.M) continue;
+    if (!full && m >= p.M) continue;
     bf16_t *orow = p.out + (int64_t)m * p.so;
 #pragma unroll
     for (int tn = 0; tn < 4; ++tn) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int n = n0 + wn + 32 * tn + 8 * q + 4 * g;
-        if (n >= p.N) continue;
         float v[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          v[i] = acc[tn][tm][4 * q + i] * scale;
-          if (p.bias) v[i] += bf2f(p.bias[min(n + i, p.N - 1)]);
+        for (int i = 0; i < 4; ++i) v[i] = acc[tn][tm][4 * q + i] * scale;
+        if (p.bias) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) v[i] += bf2f(p.bias[min(n + i, p.N - 1)]);
         }
-        if (n + 4 <= p.N && ((reinterpret_cast<uintptr_t>(orow + n) & 7) == 0)) {
-          uint2 st;
-          st.x = pack_bf(v[0], v[1]);
-          st.y = pack_bf(v[2], v[3]);
-          *reinterpret_cast<uint2 *>(orow + n) = st;
+        if (full || (n + 4 <= p.N && ((reinterpret_cast<uintptr_t>(orow + n) & 7) == 0))) {
+          *reinterpret_cast<uint2 *>(orow + n) = make_uint2(pack_bf(v[0], v[1]), pack_bf(v[2], v[3]));
         } else {
 #pragma unroll
           for (int i = 0; i < 4; ++i)

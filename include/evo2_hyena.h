@@ -193,7 +193,7 @@ int evo2_fp8_quantize(const void *x, int64_t sx, void *q, int64_t sq,
  * out[m, n] = bf16((sum_k x8[m, k] w8[n, k]) * x_scale[0] * w_scale[0] [+ bias[n]]).
  *   x8 (M, K), w8 (N, K) e4m3 bytes with 16-byte aligned rows (strides in
  *   bytes); bias (N,) bf16 or NULL; out (M, N) bf16, row stride so.
- *   K must be a multiple of 128.
+ *   K must be a multiple of 64.
  *
  * Replaces the in_proj GEMM of vLLM's static W8A8 ReplicatedLinear
  * (evo2_flash/mixers.py:741-757, 1076-1092) and, when quantised, out_proj
