@@ -107,6 +107,11 @@ __global__ __launch_bounds__(256) void fir_prefill_kernel(FirArgs p) {
   const int c = c0 + lane;
   const bool active = c < p.H;
   const int cl = active ? c : p.H - 1;  // clamped channel for loads
+  // Output rows go out as channel pairs: even lanes store row r of (c, c+1),
+  // odd lanes row r + 1 of (c - 1, c).
+  const bool odd = lane & 1;
+  const int cpair = c & ~1;
+  bf16_t *const obase = p.out + (odd ? p.so : 0) + cpair;
   const SegInfo S = seg_of_tile(p);
   if (S.t0 >= S.t_end) return;  // uniform across the block
 
@@ -144,7 +149,8 @@ __global__ __launch_bounds__(256) void fir_prefill_kernel(FirArgs p) {
   }
   const float *stc = S.init ? p.st + S.blk * p.st0 + (int64_t)cl * p.st1 : nullptr;
   const bool vec_z = FUSED && (c0 + 64 <= p.H) && (p.sx % 8 == 0) &&
-                     ((reinterpret_cast<uintptr_t>(p.x) & 15) == 0);
+                     ((reinterpret_cast<uintptr_t>(p.x) & 15) == 0) &&
+                     p.sx * G::ZROWS < (int64_t(1) << 31);  // 32-bit lane offsets
 
   // ---- stage z rows [rs, rs + ZROWS) of this block's 192 sub-channels into
   // LDS with direct-to-LDS loads: chunk i = row*24 + col (16 bytes), and one
@@ -157,18 +163,34 @@ __global__ __launch_bounds__(256) void fir_prefill_kernel(FirArgs p) {
   // past the tile end keep stale (finite) values; only discarded rows read them.
   constexpr int ZCH = G::ZROWS * 24;             // 16-byte chunks per tile
   constexpr int ZW = (ZCH + 63) / 64;            // wave instructions per tile
+  // Lane offsets of the staged chunks are fixed for the kernel: wave
+  // instruction j moves chunks i = (wave + 4j) * 64 + lane, i.e. row i / 24,
+  // column i % 24 of the (ZROWS x 192) tile.  zoff[j] is that chunk's element
+  // offset from the tile's first row (-1 past the tile); interior sub-tiles
+  // (no row before the segment or past the tile end) skip the row checks.
+  constexpr int NJ = (ZW + 3) / 4;
+  int zoff[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int i = (wave + 4 * j) * 64 + lane;
+    zoff[j] = i < ZCH ? (i / 24) * static_cast<int>(p.sx) + 3 * c0 + 8 * (i % 24) : -1;
+  }
   auto prefetch = [&](int rs) {
     if (!vec_z) return;
+    const bf16_t *base = p.x + (int64_t)rs * p.sx;
+    const bool interior = rs >= S.a && rs + G::ZROWS <= S.t_end;  // uniform
 #pragma unroll
-    for (int j = 0; j < (ZW + 3) / 4; ++j) {
+    for (int j = 0; j < NJ; ++j) {
       const int cw = wave + 4 * j;  // wave-uniform
       if (cw >= ZW) break;
-      const int i = cw * 64 + lane;
-      const int row = i / 24, col = i - 24 * (i / 24);
-      const int t = rs + row;
-      if (i < ZCH && t >= S.a && t < S.t_end)
+      bool ok = zoff[j] >= 0;
+      if (!interior) {
+        const int t = rs + ((cw * 64 + lane) / 24);
+        ok = ok && t >= S.a && t < S.t_end;
+      }
+      if (ok)
         __builtin_amdgcn_global_load_lds(
-            reinterpret_cast<const uint4 *>(p.x + (int64_t)t * p.sx + 3 * c0) + col,
+            reinterpret_cast<const uint4 *>(base + zoff[j]),
             (__attribute__((address_space(3))) void *)(&zst[0][0] + cw * 512), 16, 0, 0);
     }
   };
@@ -383,12 +405,11 @@ __global__ __launch_bounds__(256) void fir_prefill_kernel(FirArgs p) {
     }
     float dval = 0.0f;
     if constexpr (HAS_D) dval = bf2f(p.D[cl]);
-    const bool odd = lane & 1;
-    const int cpair = c & ~1;
     const int trow = s0 + wave * G::RW;
-    bf16_t *orow = p.out + (int64_t)trow * p.so + cpair;
+    const bool full = trow + G::RW <= S.t_end && c0 + 64 <= p.H;  // uniform
+    bf16_t *orow = obase + (int64_t)trow * p.so;
 #pragma unroll
-    for (int r = 0; r < G::RW; r += 2) {
+    for (int r = 0; r < G::RW; r += 2, orow += 2 * p.so) {
       uint32_t py = cvt_pk(acc[r], acc[r + 1]);
       if constexpr (FUSED) {
         if constexpr (HAS_D) {
@@ -399,13 +420,11 @@ __global__ __launch_bounds__(256) void fir_prefill_kernel(FirArgs p) {
         const uint32_t px = xq[r / 2];
         py = cvt_pk(lo_bf(px) * lo_bf(py), hi_bf(px) * hi_bf(py));
       }
-      // py = (row r, row r+1) of channel c.  Even lanes store row r of the
-      // channel pair (c, c+1), odd lanes row r+1 of (c-1, c).
+      // py = (row r, row r+1) of channel c
       const uint32_t nb = __shfl_xor(py, 1);
       const uint32_t dw = odd ? ((nb >> 16) | (py & 0xffff0000u)) : ((py & 0xffffu) | (nb << 16));
-      const int rr = r + (odd ? 1 : 0);
-      if (trow + rr < S.t_end && cpair < p.H)
-        *reinterpret_cast<uint32_t *>(orow + (int64_t)rr * p.so) = dw;
+      if (full || (trow + r + (odd ? 1 : 0) < S.t_end && cpair < p.H))
+        *reinterpret_cast<uint32_t *>(orow) = dw;
     }
     if constexpr (FUSED) {
       if (more) {

@@ -14,15 +14,17 @@
 //   phase 1  per tile, the end state of a scan started from zero;
 //   phase 2  per segment and channel, the carry into every tile
 //            C_j = p^(L_{j-1}) C_{j-1} + E_{j-1}, C_0 = the cached state
-//            (continuation) or 0; the segment's final state goes to the
-//            cache (mixers.py:1391-1394);
+//            (continuation) or 0, as a scan over tiles with wavefront
+//            shuffles; the segment's final state goes to the cache
+//            (mixers.py:1391-1394);
 //   phase 3  per tile, the scan again from its carry, the readout and the
 //            mixer tail g = bf16(bf16(bf16(y) + bf16(u D)) x2) (mixers.py:1397).
 // No workgroup waits on another, so the launch shape can never deadlock.
 //
 // Lanes run along channels (coalesced rows); a workgroup owns 256 channels
 // (4 waves) and sweeps its tile in 16-row sub-tiles staged into LDS with
-// direct-to-LDS loads, like the FIR prefill.
+// direct-to-LDS loads, double-buffered so the next sub-tile lands while the
+// current one computes.
 #include <type_traits>
 
 #include "featurize.h"
@@ -55,7 +57,11 @@ constexpr int HCL_ZPITCH = 3 * HCL_CH;  // bf16 per staged row, unpadded
 
 template <int PHASE>
 __global__ __launch_bounds__(256) void hcl_scan_kernel(HclArgs p) {
-  __shared__ __align__(16) bf16_t zst[HCL_ZROWS][HCL_ZPITCH];
+  // Two staging buffers (distinct variables, so reading one never waits on
+  // the direct-to-LDS loads still landing in the other): sub-tile i + 1 is
+  // loaded while sub-tile i computes.
+  __shared__ __align__(16) bf16_t zs0[HCL_ZROWS][HCL_ZPITCH];
+  __shared__ __align__(16) bf16_t zs1[HCL_ZROWS][HCL_ZPITCH];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -91,49 +97,53 @@ __global__ __launch_bounds__(256) void hcl_scan_kernel(HclArgs p) {
   constexpr int ZCH = HCL_ZROWS * (HCL_ZPITCH / 8);  // 16-byte chunks per stage
   constexpr int ZW = (ZCH + 63) / 64;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  // stage rows [rs, rs + HCL_ZROWS): direct-to-LDS for interior rows, then
-  // element-wise left context / zeros (see the FIR prefill for the scheme).
-  auto stage = [&](int rs) {
-    if (vec_z) {
+  // Rows [rs, rs + HCL_ZROWS) of the tile: `prefetch` issues direct-to-LDS
+  // loads for the interior rows; `fix` (after they land) writes the rows the
+  // loads skip element by element: the short filter's left context (conv
+  // window when continuing, else zero) and every row when z is not 16-byte
+  // addressable.  Rows past the tile end are never read.
+  auto prefetch = [&](auto buf, int rs) {
+    bf16_t(*zst)[HCL_ZPITCH] = decltype(buf)::value ? zs1 : zs0;
+    if (!vec_z) return;
 #pragma unroll
-      for (int j = 0; j < (ZW + 3) / 4; ++j) {
-        const int cw = wave + 4 * j;
-        if (cw >= ZW) break;
-        const int i = cw * 64 + lane;
-        const int row = i / (HCL_ZPITCH / 8), col = i - (HCL_ZPITCH / 8) * row;
-        const int t = rs + row;
-        if (i < ZCH && t >= a && t < t_end)
-          __builtin_amdgcn_global_load_lds(
-              reinterpret_cast<const uint4 *>(p.z + (int64_t)t * p.sz + 3 * c0) + col,
-              (__attribute__((address_space(3))) void *)(&zst[0][0] + cw * 512), 16, 0, 0);
-      }
-      __builtin_amdgcn_s_waitcnt(0);
+    for (int j = 0; j < (ZW + 3) / 4; ++j) {
+      const int cw = wave + 4 * j;
+      if (cw >= ZW) break;
+      const int i = cw * 64 + lane;
+      const int row = i / (HCL_ZPITCH / 8), col = i - (HCL_ZPITCH / 8) * row;
+      const int t = rs + row;
+      if (i < ZCH && t >= a && t < t_end)
+        __builtin_amdgcn_global_load_lds(
+            reinterpret_cast<const uint4 *>(p.z + (int64_t)t * p.sz + 3 * c0) + col,
+            (__attribute__((address_space(3))) void *)(&zst[0][0] + cw * 512), 16, 0, 0);
     }
-    if (!vec_z || rs < a || rs + HCL_ZROWS > t_end) {
+  };
+  auto fix = [&](auto buf, int rs) {
+    bf16_t(*zst)[HCL_ZPITCH] = decltype(buf)::value ? zs1 : zs0;
+    if (vec_z && rs >= a) return;  // uniform: nothing to patch
 #pragma unroll 1
-      for (int i = tid; i < ZCH; i += 256) {
-        const int row = i / (HCL_ZPITCH / 8), col = i - (HCL_ZPITCH / 8) * row;
-        const int t = rs + row;
-        const bool inside = t >= a && t < t_end;
-        if (vec_z && inside) continue;
+    for (int i = tid; i < ZCH; i += 256) {
+      const int row = i / (HCL_ZPITCH / 8), col = i - (HCL_ZPITCH / 8) * row;
+      const int t = rs + row;
+      const bool inside = t >= a && t < t_end;
+      if (vec_z && inside) continue;
 #pragma unroll 1
-        for (int q = 0; q < 8; ++q) {
-          const int ch = 3 * c0 + 8 * col + q;
-          bf16_t b = 0;
-          if (ch < 3 * p.H) {
-            if (inside) b = p.z[(int64_t)t * p.sz + ch];
-            else if (conv && t < a && t >= a - 2) b = conv[ch * p.cs1 + (t - a + 2) * p.cs2];
-          }
-          zst[row][8 * col + q] = b;
+      for (int q = 0; q < 8; ++q) {
+        const int ch = 3 * c0 + 8 * col + q;
+        bf16_t b = 0;
+        if (ch < 3 * p.H) {
+          if (inside) b = p.z[(int64_t)t * p.sz + ch];
+          else if (conv && t < a && t >= a - 2) b = conv[ch * p.cs1 + (t - a + 2) * p.cs2];
         }
+        zst[row][8 * col + q] = b;
       }
     }
   };
 
-  for (int s0 = t0; s0 < t_end; s0 += HCL_RS) {
-    __syncthreads();  // previous sub-tile's readers are done
-    stage(s0 - 2);
-    __syncthreads();
+  // One 16-row sub-tile from a staged buffer: short filter, gate, the scan
+  // (and in phase 3 the readout and the mixer tail, stored as bf16 rows).
+  auto compute = [&](auto buf, int s0) {
+    const bf16_t(*zst)[HCL_ZPITCH] = decltype(buf)::value ? zs1 : zs0;
     const int nr = min(HCL_RS, t_end - s0);
     float zm2[3], zm1[3];
 #pragma unroll
@@ -207,6 +217,25 @@ __global__ __launch_bounds__(256) void hcl_scan_kernel(HclArgs p) {
         if (rr < nr && cpair < p.H) *reinterpret_cast<uint32_t *>(orow + (int64_t)rr * p.so) = dw;
       }
     }
+  };
+
+  // Sub-tile i lives in buffer i & 1.  Per sub-tile: wait for its loads,
+  // patch its boundary rows, barrier (all waves' data visible; everyone is
+  // done with the other buffer), issue the next sub-tile into the other
+  // buffer, compute.
+  using B0 = std::integral_constant<int, 0>;
+  using B1 = std::integral_constant<int, 1>;
+  auto sub = [&](auto buf, auto nbuf, int s0) {
+    __builtin_amdgcn_s_waitcnt(0);
+    fix(buf, s0 - 2);
+    __syncthreads();
+    if (s0 + HCL_RS < t_end) prefetch(nbuf, s0 + HCL_RS - 2);
+    compute(buf, s0);
+  };
+  prefetch(B0{}, t0 - 2);
+  for (int s0 = t0; s0 < t_end; s0 += 2 * HCL_RS) {
+    sub(B0{}, B1{}, s0);
+    if (s0 + HCL_RS < t_end) sub(B1{}, B0{}, s0 + HCL_RS);
   }
   if constexpr (PHASE == 1) {
     if (active) {
@@ -217,12 +246,68 @@ __global__ __launch_bounds__(256) void hcl_scan_kernel(HclArgs p) {
   }
 }
 
-// Phase 2: walk each segment's tiles in order, turning tile end states into
-// carries in place, and write the segment's final state to the cache.
-__global__ __launch_bounds__(64) void hcl_carry_kernel(HclArgs p) {
+// Phase 2: the carry across tiles as a wavefront scan.  Tile i of a segment
+// maps its entering state s to p^len_i (.) s + E_i (E_i: its end state from
+// a zero start), so the state entering tile i is the composition of the maps
+// of tiles 0..i-1 applied to the segment's initial state.  One wavefront per
+// channel: lane l holds tile l of a window of 64 tiles and the 64 prefix
+// compositions come out of an inclusive scan over lanes in log2(64) = 6
+// shuffle steps, (A, B) <- (A A', A B' + B) with (A', B') from lane l - d.
+// Windows of 64 tiles chain serially through the last lane's composition.
+// The carries replace the tile end states in `work`; the state after the
+// last tile is returned in S.
+__device__ __forceinline__ void carry_scan(float *work, int64_t H, int c, int j0, int n,
+                                           int first_t0, int block_t, int e, const float lpv[16],
+                                           float S[16]) {
+  const int lane = threadIdx.x & 63;
+  for (int w0 = 0; w0 < n; w0 += 64) {
+    const int l = w0 + lane;
+    const bool valid = l < n;
+    const int len = valid ? min(first_t0 + (l + 1) * block_t, e) - (first_t0 + l * block_t) : 0;
+    float A[16], B[16];
+    const float4 *wp = reinterpret_cast<const float4 *>(work + ((int64_t)(j0 + (valid ? l : 0)) * H + c) * 16);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float4 v = valid ? wp[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+      B[4 * q] = v.x; B[4 * q + 1] = v.y; B[4 * q + 2] = v.z; B[4 * q + 3] = v.w;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) A[i] = valid ? expf(lpv[i] * static_cast<float>(len)) : 1.0f;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const float Ap = __shfl_up(A[i], d), Bp = __shfl_up(B[i], d);
+        if (lane >= d) {
+          B[i] = fmaf(A[i], Bp, B[i]);
+          A[i] = A[i] * Ap;
+        }
+      }
+    }
+    // carry into tile l: the composition of tiles < l applied to S
+    float C[16], Sn[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float Ap = __shfl_up(A[i], 1), Bp = __shfl_up(B[i], 1);
+      C[i] = lane == 0 ? S[i] : fmaf(Ap, S[i], Bp);
+      Sn[i] = fmaf(__shfl(A[i], 63), S[i], __shfl(B[i], 63));
+    }
+    if (valid) {
+      float4 *wq = reinterpret_cast<float4 *>(work + ((int64_t)(j0 + l) * H + c) * 16);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) wq[q] = make_float4(C[4 * q], C[4 * q + 1], C[4 * q + 2], C[4 * q + 3]);
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) S[i] = Sn[i];
+  }
+}
+
+// One wavefront per (segment, channel); writes the segment's final state to
+// the cache (mixers.py:1391-1394).
+__global__ __launch_bounds__(256) void hcl_carry_kernel(HclArgs p) {
   const int seg = blockIdx.x;
-  const int c = blockIdx.y * 64 + threadIdx.x;
-  if (c >= p.H) return;
+  const int c = blockIdx.y * 4 + (threadIdx.x >> 6);
+  if (c >= p.H) return;  // wave-uniform
   const int a = p.seq[3 * seg], e = p.seq[3 * seg + 1];
   if (e <= a) return;
   const int64_t blk = p.blocks[seg * p.sblk];
@@ -235,24 +320,12 @@ __global__ __launch_bounds__(64) void hcl_carry_kernel(HclArgs p) {
     S[i] = init ? st[i * p.m2] : 0.0f;
     lpv[i] = p.lp[(int64_t)c * p.l0 + i * p.l1];
   }
-  const int j0 = p.tile_start[seg], j1 = p.tile_start[seg + 1];
-  for (int j = j0; j < j1; ++j) {
-    const int tt0 = p.tiles[2 * j + 1];
-    const int len = min(tt0 + p.block_t, e) - tt0;
-    float4 *w = reinterpret_cast<float4 *>(p.work + ((int64_t)j * p.H + c) * 16);
-    float E[16];
+  const int j0 = p.tile_start[seg], n = p.tile_start[seg + 1] - j0;
+  if (n > 0) carry_scan(p.work, p.H, c, j0, n, p.tiles[2 * j0 + 1], p.block_t, e, lpv, S);
+  if ((threadIdx.x & 63) == 0) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const float4 v = w[q];
-      E[4 * q] = v.x; E[4 * q + 1] = v.y; E[4 * q + 2] = v.z; E[4 * q + 3] = v.w;
-    }
-#pragma unroll
-    for (int q = 0; q < 4; ++q) w[q] = make_float4(S[4 * q], S[4 * q + 1], S[4 * q + 2], S[4 * q + 3]);
-#pragma unroll
-    for (int i = 0; i < 16; ++i) S[i] = fmaf(expf(lpv[i] * static_cast<float>(len)), S[i], E[i]);
+    for (int i = 0; i < 16; ++i) st[i * p.m2] = S[i];
   }
-#pragma unroll
-  for (int i = 0; i < 16; ++i) st[i * p.m2] = S[i];
 }
 
 // Conv window update for the LI prefill: same contract as the FIR window
@@ -327,8 +400,9 @@ extern "C" int evo2_hyena_hcl_prefill(const void *z, int64_t sz, const void *sho
     int rc = check_launch("hcl phase 1");
     if (rc) return rc;
   }
+  dim3 cgrid(static_cast<unsigned>(nseq), static_cast<unsigned>(cdiv(H, 4)));
+  hipLaunchKernelGGL(hcl_carry_kernel, cgrid, dim3(256), 0, st, a);
   dim3 sgrid(static_cast<unsigned>(nseq), static_cast<unsigned>(cdiv(H, 64)));
-  hipLaunchKernelGGL(hcl_carry_kernel, sgrid, dim3(64), 0, st, a);
   int rc = check_launch("hcl phase 2");
   if (rc) return rc;
   if (ntiles) {
@@ -395,27 +469,20 @@ __global__ __launch_bounds__(256) void iir_scan_kernel(IirArgs p) {
   }
 }
 
-__global__ __launch_bounds__(64) void iir_carry_kernel(IirArgs p) {
-  const int c = blockIdx.x * 64 + threadIdx.x;
-  if (c >= p.H) return;
+__global__ __launch_bounds__(256) void iir_carry_kernel(IirArgs p) {
+  const int c = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (c >= p.H) return;  // wave-uniform
   float S[16], lpv[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     S[i] = p.sp ? p.sp[(int64_t)c * p.sp0 + i * p.sp1] : 0.0f;
     lpv[i] = p.lp[(int64_t)c * p.l0 + i * p.l1];
   }
-  for (int j = 0; j < p.ntiles; ++j) {
-    const int len = min((j + 1) * p.block_t, p.L) - j * p.block_t;
-    float *w = p.work + ((int64_t)j * p.H + c) * 16;
+  if (p.ntiles > 0) carry_scan(p.work, p.H, c, 0, p.ntiles, 0, p.block_t, p.L, lpv, S);
+  if ((threadIdx.x & 63) == 0) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const float E = w[i];
-      w[i] = S[i];
-      S[i] = fmaf(expf(lpv[i] * static_cast<float>(len)), S[i], E);
-    }
+    for (int i = 0; i < 16; ++i) p.st[(int64_t)c * 16 + i] = S[i];
   }
-#pragma unroll
-  for (int i = 0; i < 16; ++i) p.st[(int64_t)c * 16 + i] = S[i];
 }
 
 // h[d, l] = sum_s residues[d, s] * exp(log_poles[d, s] * t[l])  (triton_hcl.py:46-74)
@@ -464,7 +531,7 @@ extern "C" int evo2_iir_segment(const float *seq, int64_t xh, int64_t xl,
     int rc = check_launch("iir_segment phase 1");
     if (rc) return rc;
   }
-  hipLaunchKernelGGL(iir_carry_kernel, dim3(static_cast<unsigned>(cdiv(H, 64))), dim3(64), 0, strm, a);
+  hipLaunchKernelGGL(iir_carry_kernel, dim3(static_cast<unsigned>(cdiv(H, 4))), dim3(256), 0, strm, a);
   int rc = check_launch("iir_segment phase 2");
   if (rc) return rc;
   if (ntiles) {
