@@ -22,6 +22,7 @@ Also measured in the same run and reported in the same JSON line:
 import argparse
 import json
 import os
+import re
 import statistics
 import sys
 import time
@@ -42,6 +43,26 @@ LAYER_MAP_7B = {  # evo2_configs/evo2-7b-1m.yml:7-9
 HBM_PEAK_GBS = 8000.0
 FP8_PEAK_TFLOPS = 5000.0
 METRIC = "decode tok/s (7B-shape, bs=64) + prefill tok/s at 32k; % HBM/MFMA roofline"
+
+
+DECODE_ROOFLINE_KERNEL = "hcm_decode_split_kernel"
+DECODE_PROFILE = os.path.join(ROOT, "profiles", "decode_7b_b64_kernels.md")
+
+
+def profiled_traffic(kernel, path=DECODE_PROFILE):
+    """HBM bytes per launch of `kernel` as measured by the FETCH_SIZE and
+    WRITE_SIZE counter passes summarised in `path` (a line
+    `traffic_bytes <kernel> <int>`, already scaled by the copy-kernel
+    calibration); None when no such measurement is recorded."""
+    try:
+        with open(path) as f:
+            for ln in f:
+                m = re.match(r"\s*traffic_bytes\s+(\S+)\s+(\d+)", ln)
+                if m and m.group(1) == kernel:
+                    return int(m.group(2))
+    except OSError:
+        pass
+    return None
 
 
 def decode_bytes_per_launch(kind, B, H):
@@ -367,9 +388,10 @@ def main(argv=None):
     }
     if dec:
         hcm = dec["per_kind"]["hcm"]
-        line["roofline"] = {"bound": "hbm", "kernel": "hyena_decode_pair_kernel<hcm>",
+        line["roofline"] = {"bound": "hbm", "kernel": DECODE_ROOFLINE_KERNEL,
                             "achieved": hcm["achieved_GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                            "frac": hcm["frac"], "traffic": None}
+                            "frac": hcm["frac"],
+                            "traffic": profiled_traffic(DECODE_ROOFLINE_KERNEL)}
         line["decode"] = dec
     if pre:
         line["prefill"] = pre
