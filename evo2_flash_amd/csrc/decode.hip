@@ -33,6 +33,7 @@ struct DecodeArgs {
   int H;
   int null_block;
   int64_t num_blocks;
+  int rows;  // B
 };
 
 // vLLM's K=3 conv update for one channel (triton_decode.py:44-53):
@@ -187,13 +188,16 @@ static void launch(const DecodeArgs &a, int64_t B, hipStream_t stream) {
 }
 
 // ---------------------------------------------------------------------------
-// Fast path for the engine's native layouts: each lane owns a channel pair
+// Fast paths for the engine's native layouts.  A lane owns a channel pair
 // (h0, h0+1), so every operand moves as 4/8/16-byte vectors: the z triple
 // pair and both conv-state columns as three dwords each, FIR window columns
-// as float2 (channel-contiguous native storage), LI states, residues and
-// log-poles as float4.  The hcm window is streamed in 16-column chunks with
-// the next chunk's loads issued before the current chunk's arithmetic and
-// shifted stores.  Arithmetic and rounding are exactly the generic kernel's.
+// as float2 (channel-contiguous native storage).  Arithmetic and rounding are
+// exactly the generic kernel's.
+//
+// The fast kernels never return early on a null row: its loads go to block
+// 0 (which always exists), its results are dropped and it writes a zero
+// output.  With no branch in front of them, the loads that do not depend on
+// the slot (z, taps, D) are issued while the slot lookup is in flight.
 //
 // WT: FIR taps in channel-contiguous (K, H) storage (wi0 == 1), one dword
 // per tap for the pair; otherwise tap-contiguous (H, K) rows (wi1 == 1).
@@ -207,41 +211,39 @@ __device__ __forceinline__ void unpack3(const uint32_t *p, float f[6]) {
   }
 }
 
-template <int KIND, bool HAS_D, bool WT>
-__global__ __launch_bounds__(128) void hyena_decode_pair_kernel(DecodeArgs a) {
-  const int pair = blockIdx.x * blockDim.x + threadIdx.x;
-  const int h0 = 2 * pair;
-  const int64_t b = blockIdx.y;
-  if (h0 >= a.H) return;
-  const int64_t blk = a.slots[b * a.ssl];
-  uint32_t *o = reinterpret_cast<uint32_t *>(a.out + b * a.so + h0);
-  if (blk == a.null_block || blk < 0 || blk >= a.num_blocks) {
-    *o = 0u;
-    return;
-  }
+// Slot of decode row b: `blk` is the block to read (0 for a null row),
+// the return value whether the row is live.
+__device__ __forceinline__ bool row_slot(const DecodeArgs &a, int64_t b, int64_t &blk) {
+  const int64_t sl = a.slots[b * a.ssl];
+  // bitwise, not short-circuit: no branch may split the load sequence
+  const bool live = (sl != a.null_block) & (sl >= 0) & (sl < a.num_blocks);
+  blk = live ? sl : 0;
+  return live;
+}
 
-  // ---- short filter: z triples and both window columns for 6 sub-channels
-  const uint32_t *zr = reinterpret_cast<const uint32_t *>(a.z + b * a.sz + 3 * (int64_t)h0);
-  bf16_t *cbase = a.cs + blk * a.cs0 + 3 * (int64_t)h0;
-  uint32_t *c0p = reinterpret_cast<uint32_t *>(cbase);
-  uint32_t *c1p = reinterpret_cast<uint32_t *>(cbase + a.cs2);
-  uint32_t zraw[3], c0raw[3], c1raw[3];
-#pragma unroll
-  for (int i = 0; i < 3; ++i) {
-    zraw[i] = zr[i];
-    c0raw[i] = c0p[i];
-    c1raw[i] = c1p[i];
-  }
+// All ones for a live row, zero for a null one, as a value the optimizer
+// cannot see through: the output is `result & mask`, so the row's loads and
+// arithmetic are needed on both paths and stay in front of the slot lookup
+// instead of being moved behind a branch on it.
+__device__ __forceinline__ uint32_t live_mask(bool live) {
+  uint32_t m = live ? 0xffffffffu : 0u;
+  asm volatile("" : "+v"(m));
+  return m;
+}
+
+// Short filter and gate for the six sub-channels of the pair h0, h0+1:
+// x2 and u per channel (triton_decode.py:44-53, 72-78).
+__device__ __forceinline__ void pair_featurize(const uint32_t zraw[3], const uint32_t c0raw[3],
+                                               const uint32_t c1raw[3], const uint32_t wsraw[9],
+                                               float x2[2], float u[2]) {
   float xf[6], c0f[6], c1f[6], wsf[18];
   unpack3(zraw, xf);
   unpack3(c0raw, c0f);
   unpack3(c1raw, c1f);
-  const uint32_t *wsp = reinterpret_cast<const uint32_t *>(a.ws + 9 * (int64_t)h0);
 #pragma unroll
   for (int i = 0; i < 9; ++i) {
-    const uint32_t v = wsp[i];
-    wsf[2 * i] = lo_bf(v);
-    wsf[2 * i + 1] = hi_bf(v);
+    wsf[2 * i] = lo_bf(wsraw[i]);
+    wsf[2 * i + 1] = hi_bf(wsraw[i]);
   }
   float y6[6];
 #pragma unroll
@@ -251,181 +253,109 @@ __global__ __launch_bounds__(128) void hyena_decode_pair_kernel(DecodeArgs a) {
     acc = acc + rbf(xf[i] * wsf[3 * i + 2]);
     y6[i] = rbf(acc);
   }
-  const float x2[2] = {y6[0], y6[3]};
-  const float u[2] = {rbf(y6[1] * y6[2]), rbf(y6[4] * y6[5])};
-  float y[2];
+  x2[0] = y6[0];
+  x2[1] = y6[3];
+  u[0] = rbf(y6[1] * y6[2]);
+  u[1] = rbf(y6[4] * y6[5]);
+}
 
-  if constexpr (KIND == KIND_HCL) {
-    float sv[2][16], res[2][16], lpv[2][16];
+// hcs (K=7): the 6-column window of the pair moves as six float2.
+template <bool HAS_D, bool WT>
+__global__ __launch_bounds__(128) void hcs_decode_pair_kernel(DecodeArgs a) {
+  const int pair = blockIdx.x * blockDim.x + threadIdx.x;
+  const bool active = 2 * pair < a.H;
+  const int h0 = active ? 2 * pair : 0;  // inactive lanes load channel pair 0, store nothing
+  const int64_t b = blockIdx.y;
+
+  const uint32_t *zr = reinterpret_cast<const uint32_t *>(a.z + b * a.sz + 3 * (int64_t)h0);
+  const uint32_t *wsp = reinterpret_cast<const uint32_t *>(a.ws + 9 * (int64_t)h0);
+  const bf16_t *w = static_cast<const bf16_t *>(a.inner);
+  uint32_t zraw[3], wsraw[9];
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      const float4 *sp = reinterpret_cast<const float4 *>(a.st + blk * a.is0 + (int64_t)(h0 + c) * a.is1);
-      const float4 *rp = reinterpret_cast<const float4 *>(static_cast<const float *>(a.inner) + (int64_t)(h0 + c) * a.wi0);
-      const float4 *lq = reinterpret_cast<const float4 *>(a.lp + (int64_t)(h0 + c) * a.lp0);
+  for (int i = 0; i < 3; ++i) zraw[i] = zr[i];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const float4 s4 = sp[q], r4 = rp[q], l4 = lq[q];
-        sv[c][4 * q] = s4.x; sv[c][4 * q + 1] = s4.y; sv[c][4 * q + 2] = s4.z; sv[c][4 * q + 3] = s4.w;
-        res[c][4 * q] = r4.x; res[c][4 * q + 1] = r4.y; res[c][4 * q + 2] = r4.z; res[c][4 * q + 3] = r4.w;
-        lpv[c][4 * q] = l4.x; lpv[c][4 * q + 1] = l4.y; lpv[c][4 * q + 2] = l4.z; lpv[c][4 * q + 3] = l4.w;
-      }
+  for (int i = 0; i < 9; ++i) wsraw[i] = wsp[i];
+  // taps kept as loaded (bf16 bits, tap k of channel h0+c) until after the
+  // slot lookup has been issued
+  bf16_t wb[2][7];
+  if constexpr (WT) {
+#pragma unroll
+    for (int k = 0; k < 7; ++k) {
+      const uint32_t v = *reinterpret_cast<const uint32_t *>(w + (int64_t)k * a.wi1 + h0);
+      wb[0][k] = static_cast<bf16_t>(v);
+      wb[1][k] = static_cast<bf16_t>(v >> 16);
     }
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      float r[16];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        sv[c][i] = sv[c][i] * expf(lpv[c][i]) + u[c];
-        r[i] = sv[c][i] * res[c][i];
-      }
-#pragma unroll
-      for (int i = 0; i < 8; ++i) r[i] = r[i] + r[i + 8];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) r[i] = r[i] + r[i + 4];
-#pragma unroll
-      for (int i = 0; i < 2; ++i) r[i] = r[i] + r[i + 2];
-      y[c] = rbf((r[0] + r[1]) + 0.0f);
-      float4 *sp = reinterpret_cast<float4 *>(a.st + blk * a.is0 + (int64_t)(h0 + c) * a.is1);
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        sp[q] = make_float4(sv[c][4 * q], sv[c][4 * q + 1], sv[c][4 * q + 2], sv[c][4 * q + 3]);
-    }
-  } else if constexpr (KIND == KIND_HCM) {
-    float *s = a.st + blk * a.is0 + h0;  // is1 == 1: the pair is one float2
-    const bf16_t *w = static_cast<const bf16_t *>(a.inner);
-    float acc[2][16];
+  } else {
 #pragma unroll
     for (int c = 0; c < 2; ++c)
 #pragma unroll
-      for (int q = 0; q < 16; ++q) acc[c][q] = 0.0f;
-    float2 cur[16], nxt[16];
-#pragma unroll
-    for (int q = 0; q < 16; ++q) cur[q] = *reinterpret_cast<const float2 *>(s + q * a.is2);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      if (j < 7) {
-#pragma unroll
-        for (int q = 0; q < 16; ++q) {
-          const int k = 16 * (j + 1) + q;
-          nxt[q] = (k < 127) ? *reinterpret_cast<const float2 *>(s + k * a.is2) : make_float2(0.f, 0.f);
-        }
-      }
-      float wf[2][16];
-      if constexpr (WT) {
-#pragma unroll
-        for (int q = 0; q < 16; ++q) {
-          const int k = 16 * j + q;
-          const uint32_t v = *reinterpret_cast<const uint32_t *>(w + (int64_t)k * a.wi1 + h0);
-          wf[0][q] = lo_bf(v);
-          wf[1][q] = hi_bf(v);
-        }
-      } else {
-#pragma unroll
-        for (int c = 0; c < 2; ++c) {
-          const uint4 *wp = reinterpret_cast<const uint4 *>(w + (int64_t)(h0 + c) * a.wi0 + 16 * j);
-#pragma unroll
-          for (int v4 = 0; v4 < 2; ++v4) {
-            const uint4 v = wp[v4];
-            const uint32_t d[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              wf[c][8 * v4 + 2 * e] = lo_bf(d[e]);
-              wf[c][8 * v4 + 2 * e + 1] = hi_bf(d[e]);
-            }
-          }
-        }
-      }
-#pragma unroll
-      for (int q = 0; q < 16; ++q) {
-        const int k = 16 * j + q;
-        const float w0 = (k < 127) ? wf[0][q] : 0.0f;
-        const float w1 = (k < 127) ? wf[1][q] : 0.0f;
-        acc[0][q] = acc[0][q] + cur[q].x * w0;
-        acc[1][q] = acc[1][q] + cur[q].y * w1;
-      }
-#pragma unroll
-      for (int q = 0; q < 16; ++q) {
-        const int k = 16 * j + q;
-        if (k >= 1 && k < 127) *reinterpret_cast<float2 *>(s + (k - 1) * a.is2) = cur[q];
-      }
-      if (j < 7) {
-#pragma unroll
-        for (int q = 0; q < 16; ++q) cur[q] = nxt[q];
-      }
-    }
-    float last[2];
-    if constexpr (WT) {
-      const uint32_t v = *reinterpret_cast<const uint32_t *>(w + (int64_t)127 * a.wi1 + h0);
-      last[0] = lo_bf(v);
-      last[1] = hi_bf(v);
-    } else {
-      last[0] = bf2f(w[(int64_t)h0 * a.wi0 + 127]);
-      last[1] = bf2f(w[(int64_t)(h0 + 1) * a.wi0 + 127]);
-    }
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      float p[4];
-#pragma unroll
-      for (int l = 0; l < 4; ++l)
-        p[l] = ((acc[c][l] + acc[c][4 + l]) + acc[c][8 + l]) + acc[c][12 + l];
-      y[c] = rbf(((p[0] + p[2]) + (p[1] + p[3])) + last[c] * u[c]);
-    }
-    *reinterpret_cast<float2 *>(s + 126 * a.is2) = make_float2(u[0], u[1]);
-  } else {
-    float *s = a.st + blk * a.is0 + h0;
-    const bf16_t *w = static_cast<const bf16_t *>(a.inner);
-    float2 sv[6];
-#pragma unroll
-    for (int k = 0; k < 6; ++k) sv[k] = *reinterpret_cast<const float2 *>(s + k * a.is2);
-    float wf[2][7];
-    if constexpr (WT) {
-#pragma unroll
-      for (int k = 0; k < 7; ++k) {
-        const uint32_t v = *reinterpret_cast<const uint32_t *>(w + (int64_t)k * a.wi1 + h0);
-        wf[0][k] = lo_bf(v);
-        wf[1][k] = hi_bf(v);
-      }
-    } else {
-#pragma unroll
-      for (int c = 0; c < 2; ++c)
-#pragma unroll
-        for (int k = 0; k < 7; ++k) wf[c][k] = bf2f(w[(int64_t)(h0 + c) * a.wi0 + k]);
-    }
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      float s6[6];
-#pragma unroll
-      for (int k = 0; k < 6; ++k) s6[k] = c ? sv[k].y : sv[k].x;
-      const float aa = (s6[0] * wf[c][0] + 0.0f) + s6[4] * wf[c][4];
-      const float bb = (s6[1] * wf[c][1] + 0.0f) + s6[5] * wf[c][5];
-      const float cc = s6[2] * wf[c][2] + 0.0f;
-      const float dd = s6[3] * wf[c][3] + 0.0f;
-      y[c] = rbf((((aa + bb) + cc) + dd) + wf[c][6] * u[c]);
-    }
-#pragma unroll
-    for (int k = 0; k < 5; ++k) *reinterpret_cast<float2 *>(s + k * a.is2) = sv[k + 1];
-    *reinterpret_cast<float2 *>(s + 5 * a.is2) = make_float2(u[0], u[1]);
+      for (int k = 0; k < 7; ++k) wb[c][k] = w[(int64_t)(h0 + c) * a.wi0 + k];
   }
+  uint32_t dv = 0;
+  if constexpr (HAS_D) dv = *reinterpret_cast<const uint32_t *>(a.D + h0);
 
-  // Short-filter windows (c0, c1) <- (c1, x) for the 6 sub-channels.
+  // the loads above go out before the slot lookup below is waited on
+  __builtin_amdgcn_sched_barrier(0);
+  int64_t blk;
+  const bool live = row_slot(a, b, blk);  // uniform
+  bf16_t *cbase = a.cs + blk * a.cs0 + 3 * (int64_t)h0;
+  uint32_t *c0p = reinterpret_cast<uint32_t *>(cbase);
+  uint32_t *c1p = reinterpret_cast<uint32_t *>(cbase + a.cs2);
+  float *s = a.st + blk * a.is0 + h0;
+  uint32_t c0raw[3], c1raw[3];
 #pragma unroll
   for (int i = 0; i < 3; ++i) {
-    c0p[i] = c1raw[i];
-    c1p[i] = zraw[i];
+    c0raw[i] = c0p[i];
+    c1raw[i] = c1p[i];
+  }
+  float2 sv[6];
+#pragma unroll
+  for (int k = 0; k < 6; ++k) sv[k] = *reinterpret_cast<const float2 *>(s + k * a.is2);
+
+  float x2[2], u[2], y[2];
+  pair_featurize(zraw, c0raw, c1raw, wsraw, x2, u);
+  float wf[2][7];
+#pragma unroll
+  for (int c = 0; c < 2; ++c)
+#pragma unroll
+    for (int k = 0; k < 7; ++k) wf[c][k] = bf2f(wb[c][k]);
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    float s6[6];
+#pragma unroll
+    for (int k = 0; k < 6; ++k) s6[k] = c ? sv[k].y : sv[k].x;
+    // triton_decode.py:126-143: ((((s0w0+s4w4)+(s1w1+s5w5))+s2w2)+s3w3)+w6u
+    const float aa = (s6[0] * wf[c][0] + 0.0f) + s6[4] * wf[c][4];
+    const float bb = (s6[1] * wf[c][1] + 0.0f) + s6[5] * wf[c][5];
+    const float cc = s6[2] * wf[c][2] + 0.0f;
+    const float dd = s6[3] * wf[c][3] + 0.0f;
+    y[c] = rbf((((aa + bb) + cc) + dd) + wf[c][6] * u[c]);
   }
   if constexpr (HAS_D) {
-    const uint32_t dv = *reinterpret_cast<const uint32_t *>(a.D + h0);
     y[0] = rbf(y[0] + rbf(lo_bf(dv) * u[0]));
     y[1] = rbf(y[1] + rbf(hi_bf(dv) * u[1]));
   }
-  *o = pack_bf(x2[0] * y[0], x2[1] * y[1]);
+  if (!active) return;
+  if (live) {
+#pragma unroll
+    for (int k = 0; k < 5; ++k) *reinterpret_cast<float2 *>(s + k * a.is2) = sv[k + 1];
+    *reinterpret_cast<float2 *>(s + 5 * a.is2) = make_float2(u[0], u[1]);
+    // Short-filter windows (c0, c1) <- (c1, x) for the 6 sub-channels.
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      c0p[i] = c1raw[i];
+      c1p[i] = zraw[i];
+    }
+  }
+  *reinterpret_cast<uint32_t *>(a.out + b * a.so + h0) =
+      pack_bf(x2[0] * y[0], x2[1] * y[1]) & live_mask(live);
 }
 
-template <int KIND, bool HAS_D, bool WT>
-static void launch_pair(const DecodeArgs &a, int64_t B, hipStream_t stream) {
+template <bool HAS_D, bool WT>
+static void launch_hcs_pair(const DecodeArgs &a, int64_t B, hipStream_t stream) {
   constexpr int BT = 128;  // 256 channels per block
   dim3 grid(static_cast<unsigned>(cdiv(a.H / 2, BT)), static_cast<unsigned>(B));
-  hipLaunchKernelGGL((hyena_decode_pair_kernel<KIND, HAS_D, WT>), grid, dim3(BT), 0, stream, a);
+  hipLaunchKernelGGL((hcs_decode_pair_kernel<HAS_D, WT>), grid, dim3(BT), 0, stream, a);
 }
 
 // ---------------------------------------------------------------------------
@@ -442,32 +372,20 @@ template <bool HAS_D, bool WT>
 __global__ __launch_bounds__(256) void hcm_decode_split_kernel(DecodeArgs a) {
   __shared__ float2 part[3][4][64];
   const int lane = threadIdx.x & 63;
-  const int m = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int m = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) & 3;  // 256 threads
   const int h0 = 2 * (blockIdx.x * 64 + lane);
   const bool active = h0 < a.H;
   const int hc = active ? h0 : 0;
   const int64_t b = blockIdx.y;
-  const int64_t blk = a.slots[b * a.ssl];
-  if (blk == a.null_block || blk < 0 || blk >= a.num_blocks) {  // uniform
-    if (m == 0 && active) *reinterpret_cast<uint32_t *>(a.out + b * a.so + h0) = 0u;
-    return;
-  }
-  float *s = a.st + blk * a.is0 + hc;  // is1 == 1: the pair is one float2
   const bf16_t *w = static_cast<const bf16_t *>(a.inner);
 
   // Taps stay packed as loaded (bf16 pairs) and are widened at use, which
   // keeps the kernel at four waves per SIMD.  WT: tw[j][l] = (h0, h0+1) of
   // tap k; otherwise tw[j][2c], tw[j][2c+1] = taps (4m..4m+3) of channel h0+c.
-  float2 v[8][4];
+  // They go out before the slot lookup, the window columns after it.
   uint32_t tw[8][4];
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-#pragma unroll
-    for (int l = 0; l < 4; ++l) {
-      const int k = 16 * j + 4 * m + l;
-      v[j][l] = k < 127 ? *reinterpret_cast<const float2 *>(s + (int64_t)k * a.is2)
-                        : make_float2(0.f, 0.f);
-    }
     if constexpr (WT) {
 #pragma unroll
       for (int l = 0; l < 4; ++l) {
@@ -483,6 +401,19 @@ __global__ __launch_bounds__(256) void hcm_decode_split_kernel(DecodeArgs a) {
       }
     }
   }
+  __builtin_amdgcn_sched_barrier(0);
+  int64_t blk;
+  const bool live = row_slot(a, b, blk);  // uniform
+  float *s = a.st + blk * a.is0 + hc;  // is1 == 1: the pair is one float2
+  float2 v[8][4];
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+#pragma unroll
+    for (int l = 0; l < 4; ++l) {
+      const int k = 16 * j + 4 * m + l;
+      v[j][l] = k < 127 ? *reinterpret_cast<const float2 *>(s + (int64_t)k * a.is2)
+                        : make_float2(0.f, 0.f);
+    }
   // bf16 tap l of channel c (0 = h0, 1 = h0 + 1) for column group j
   auto tap = [&](int j, int l, int c) -> float {
     if constexpr (WT) return c ? hi_bf(tw[j][l]) : lo_bf(tw[j][l]);
@@ -496,39 +427,20 @@ __global__ __launch_bounds__(256) void hcm_decode_split_kernel(DecodeArgs a) {
   uint32_t *c0p = nullptr, *c1p = nullptr;
   if (m == 0) {
     const uint32_t *zr = reinterpret_cast<const uint32_t *>(a.z + b * a.sz + 3 * (int64_t)hc);
+    const uint32_t *wsp = reinterpret_cast<const uint32_t *>(a.ws + 9 * (int64_t)hc);
     bf16_t *cbase = a.cs + blk * a.cs0 + 3 * (int64_t)hc;
     c0p = reinterpret_cast<uint32_t *>(cbase);
     c1p = reinterpret_cast<uint32_t *>(cbase + a.cs2);
-    uint32_t c0raw[3];
+    uint32_t c0raw[3], wsraw[9];
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
       zraw[i] = zr[i];
       c0raw[i] = c0p[i];
       c1raw[i] = c1p[i];
     }
-    float xf[6], c0f[6], c1f[6], wsf[18];
-    unpack3(zraw, xf);
-    unpack3(c0raw, c0f);
-    unpack3(c1raw, c1f);
-    const uint32_t *wsp = reinterpret_cast<const uint32_t *>(a.ws + 9 * (int64_t)hc);
 #pragma unroll
-    for (int i = 0; i < 9; ++i) {
-      const uint32_t t = wsp[i];
-      wsf[2 * i] = lo_bf(t);
-      wsf[2 * i + 1] = hi_bf(t);
-    }
-    float y6[6];
-#pragma unroll
-    for (int i = 0; i < 6; ++i) {
-      float acc = 0.0f + rbf(c0f[i] * wsf[3 * i]);
-      acc = acc + rbf(c1f[i] * wsf[3 * i + 1]);
-      acc = acc + rbf(xf[i] * wsf[3 * i + 2]);
-      y6[i] = rbf(acc);
-    }
-    x2[0] = y6[0];
-    x2[1] = y6[3];
-    u[0] = rbf(y6[1] * y6[2]);
-    u[1] = rbf(y6[4] * y6[5]);
+    for (int i = 0; i < 9; ++i) wsraw[i] = wsp[i];
+    pair_featurize(zraw, c0raw, c1raw, wsraw, x2, u);
   }
 
   float acc[2][4];
@@ -549,7 +461,7 @@ __global__ __launch_bounds__(256) void hcm_decode_split_kernel(DecodeArgs a) {
   }
   __syncthreads();  // all window loads consumed; partial sums visible
 
-  if (active) {
+  if (active && live) {
 #pragma unroll
     for (int j = 0; j < 8; ++j)
 #pragma unroll
@@ -579,18 +491,21 @@ __global__ __launch_bounds__(256) void hcm_decode_split_kernel(DecodeArgs a) {
     }
     y[c] = rbf(((p[0] + p[2]) + (p[1] + p[3])) + last[c] * u[c]);
   }
-  *reinterpret_cast<float2 *>(s + 126 * a.is2) = make_float2(u[0], u[1]);
+  if (live) {
+    *reinterpret_cast<float2 *>(s + 126 * a.is2) = make_float2(u[0], u[1]);
 #pragma unroll
-  for (int i = 0; i < 3; ++i) {
-    c0p[i] = c1raw[i];
-    c1p[i] = zraw[i];
+    for (int i = 0; i < 3; ++i) {
+      c0p[i] = c1raw[i];
+      c1p[i] = zraw[i];
+    }
   }
   if constexpr (HAS_D) {
     const uint32_t dv = *reinterpret_cast<const uint32_t *>(a.D + h0);
     y[0] = rbf(y[0] + rbf(lo_bf(dv) * u[0]));
     y[1] = rbf(y[1] + rbf(hi_bf(dv) * u[1]));
   }
-  *reinterpret_cast<uint32_t *>(a.out + b * a.so + h0) = pack_bf(x2[0] * y[0], x2[1] * y[1]);
+  *reinterpret_cast<uint32_t *>(a.out + b * a.so + h0) =
+      pack_bf(x2[0] * y[0], x2[1] * y[1]) & live_mask(live);
 }
 
 template <bool HAS_D, bool WT>
@@ -607,6 +522,15 @@ static void launch_hcm_split(const DecodeArgs &a, int64_t B, hipStream_t stream)
 // quad DPP moves.  The readout keeps the reference's halving tree:
 // r[i] += r[i+8] (lane q takes lane q+2), r[i] += r[i+4] (lane 0 takes lane
 // 1), r[i] += r[i+2] in lane 0, y = r0 + r1 (triton_decode.py:81-96).
+//
+// A workgroup owns 64 channels of HCL_RB rows: the residues, log-poles and
+// exp(log-poles) are fetched and computed once for those rows, and every
+// row's slot, state, window and z loads are issued before any of them is
+// used, so one memory round trip (after the slot lookup) covers all rows.
+// Rows on the null block (or past the batch) read block 0, which always
+// exists, and write nothing but a zero output.
+constexpr int HCL_RB = 4;
+
 template <int CTRL>
 __device__ __forceinline__ float quad_perm(float v) {
   return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
@@ -619,61 +543,86 @@ __global__ __launch_bounds__(256) void hcl_decode_quad_kernel(DecodeArgs a) {
   const int h = blockIdx.x * 64 + (threadIdx.x >> 2);
   const bool active = h < a.H;
   const int hc = active ? h : a.H - 1;
-  const int64_t b = blockIdx.y;
-  const int64_t blk = a.slots[b * a.ssl];
-  bf16_t *o = a.out + b * a.so + h;
-  if (blk == a.null_block || blk < 0 || blk >= a.num_blocks) {  // uniform
-    if (q == 0 && active) *o = 0;
-    return;
-  }
-  const float4 s4 = *reinterpret_cast<const float4 *>(a.st + blk * a.is0 + (int64_t)hc * a.is1 + 4 * q);
+  const int b0 = blockIdx.y * HCL_RB;
+  const int i = q < 3 ? q : 2;  // short-filter sub-channel (lane 3 mirrors lane 2)
+  const int64_t ch = 3 * (int64_t)hc + i;
+
   const float4 r4 = *reinterpret_cast<const float4 *>(static_cast<const float *>(a.inner) +
                                                       (int64_t)hc * a.wi0 + 4 * q);
   const float4 l4 = *reinterpret_cast<const float4 *>(a.lp + (int64_t)hc * a.lp0 + 4 * q);
-  // short filter, sub-channel i = q (lane 3 mirrors lane 2 and stores nothing)
-  const int i = q < 3 ? q : 2;
-  const int64_t ch = 3 * (int64_t)hc + i;
-  bf16_t *cw = a.cs + blk * a.cs0 + ch * a.cs1;
-  const bf16_t xb = a.z[b * a.sz + ch];
-  const bf16_t c0b = cw[0], c1b = cw[a.cs2];
-  const float yi = short_tap(bf2f(xb), bf2f(c0b), bf2f(c1b), a.ws + ch * 3);
-  const float x2 = quad_perm<0x00>(yi);
-  const float x1 = quad_perm<0x55>(yi);
-  const float vv = quad_perm<0xAA>(yi);
-  const float u = rbf(x1 * vv);
-
-  float sv[4] = {s4.x, s4.y, s4.z, s4.w};
+  const bf16_t w0b = a.ws[ch * 3], w1b = a.ws[ch * 3 + 1], w2b = a.ws[ch * 3 + 2];
+  const bf16_t db = HAS_D ? a.D[hc] : bf16_t(0);
+  bf16_t xb[HCL_RB];
+#pragma unroll
+  for (int r = 0; r < HCL_RB; ++r) xb[r] = a.z[(int64_t)min(b0 + r, a.rows - 1) * a.sz + ch];
+  __builtin_amdgcn_sched_barrier(0);  // the loads above go out before the slot lookups
+  int64_t blk[HCL_RB];
+  bool live[HCL_RB];
+  int32_t sl[HCL_RB];
+#pragma unroll
+  for (int r = 0; r < HCL_RB; ++r) sl[r] = a.slots[(int64_t)min(b0 + r, a.rows - 1) * a.ssl];
+#pragma unroll
+  for (int r = 0; r < HCL_RB; ++r) {
+    live[r] = (b0 + r < a.rows) & (sl[r] != a.null_block) & (sl[r] >= 0) & (sl[r] < a.num_blocks);
+    blk[r] = live[r] ? sl[r] : 0;
+  }
+  float4 s4[HCL_RB];
+  bf16_t c0b[HCL_RB], c1b[HCL_RB];
+#pragma unroll
+  for (int r = 0; r < HCL_RB; ++r) {
+    s4[r] = *reinterpret_cast<const float4 *>(a.st + blk[r] * a.is0 + (int64_t)hc * a.is1 + 4 * q);
+    const bf16_t *cw = a.cs + blk[r] * a.cs0 + ch * a.cs1;
+    c0b[r] = cw[0];
+    c1b[r] = cw[a.cs2];
+  }
   const float rv[4] = {r4.x, r4.y, r4.z, r4.w};
-  const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
-  float r[4];
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    sv[e] = sv[e] * expf(lv[e]) + u;
-    r[e] = sv[e] * rv[e];
-  }
-#pragma unroll
-  for (int e = 0; e < 4; ++e) r[e] = r[e] + quad_perm<0xEE>(r[e]);  // lane q += lane q+2
-#pragma unroll
-  for (int e = 0; e < 4; ++e) r[e] = r[e] + quad_perm<0xF5>(r[e]);  // lane 0 += lane 1
-  r[0] = r[0] + r[2];
-  r[1] = r[1] + r[3];
-  float y = rbf((r[0] + r[1]) + 0.0f);
+  const float pe[4] = {expf(l4.x), expf(l4.y), expf(l4.z), expf(l4.w)};
+  const float w0 = bf2f(w0b), w1 = bf2f(w1b), w2 = bf2f(w2b), dval = bf2f(db);
 
-  if (active) {
-    *reinterpret_cast<float4 *>(a.st + blk * a.is0 + (int64_t)h * a.is1 + 4 * q) =
-        make_float4(sv[0], sv[1], sv[2], sv[3]);
-    if (q < 3) {
-      cw[0] = c1b;
-      cw[a.cs2] = xb;
+#pragma unroll
+  for (int r = 0; r < HCL_RB; ++r) {
+    // bf16(((0 + bf16(c0 w0)) + bf16(c1 w1)) + bf16(x w2)) (triton_decode.py:44-53)
+    float acc = 0.0f + rbf(bf2f(c0b[r]) * w0);
+    acc = acc + rbf(bf2f(c1b[r]) * w1);
+    acc = acc + rbf(bf2f(xb[r]) * w2);
+    const float yi = rbf(acc);
+    const float x2 = quad_perm<0x00>(yi);
+    const float x1 = quad_perm<0x55>(yi);
+    const float vv = quad_perm<0xAA>(yi);
+    const float u = rbf(x1 * vv);
+    float sv[4] = {s4[r].x, s4[r].y, s4[r].z, s4[r].w};
+    float rr[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      sv[e] = sv[e] * pe[e] + u;
+      rr[e] = sv[e] * rv[e];
     }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) rr[e] = rr[e] + quad_perm<0xEE>(rr[e]);  // lane q += lane q+2
+#pragma unroll
+    for (int e = 0; e < 4; ++e) rr[e] = rr[e] + quad_perm<0xF5>(rr[e]);  // lane 0 += lane 1
+    rr[0] = rr[0] + rr[2];
+    rr[1] = rr[1] + rr[3];
+    float y = rbf((rr[0] + rr[1]) + 0.0f);
+    if constexpr (HAS_D) y = rbf(y + rbf(dval * u));
+
+    if (live[r] && active) {  // live is uniform
+      *reinterpret_cast<float4 *>(a.st + blk[r] * a.is0 + (int64_t)h * a.is1 + 4 * q) =
+          make_float4(sv[0], sv[1], sv[2], sv[3]);
+      if (q < 3) {
+        bf16_t *cw = a.cs + blk[r] * a.cs0 + ch * a.cs1;
+        cw[0] = c1b[r];
+        cw[a.cs2] = xb[r];
+      }
+    }
+    if (q == 0 && active && b0 + r < a.rows)
+      a.out[(int64_t)(b0 + r) * a.so + h] = f2bf(x2 * y) & static_cast<bf16_t>(live_mask(live[r]));
   }
-  if constexpr (HAS_D) y = rbf(y + rbf(bf2f(a.D[hc]) * u));
-  if (q == 0 && active) *o = f2bf(x2 * y);
 }
 
 template <bool HAS_D>
 static void launch_hcl_quad(const DecodeArgs &a, int64_t B, hipStream_t stream) {
-  dim3 grid(static_cast<unsigned>(cdiv(a.H, 64)), static_cast<unsigned>(B));
+  dim3 grid(static_cast<unsigned>(cdiv(a.H, 64)), static_cast<unsigned>(cdiv(B, HCL_RB)));
   hipLaunchKernelGGL((hcl_decode_quad_kernel<HAS_D>), grid, dim3(256), 0, stream, a);
 }
 
@@ -740,7 +689,7 @@ extern "C" int evo2_hyena_decode(const void *z, int64_t sz, const void *short_w,
                static_cast<bf16_t *>(conv_state), cs0, cs1, cs2, slots, ssl,
                inner, wi0, wi1, log_poles, lp0, lp1, inner_state, is0, is1, is2,
                static_cast<const bf16_t *>(D), static_cast<bf16_t *>(out), so,
-               static_cast<int>(H), null_block, num_blocks};
+               static_cast<int>(H), null_block, num_blocks, static_cast<int>(B)};
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool hasD = D != nullptr;
   const int pv = pair_variant(a, kind);
@@ -751,8 +700,8 @@ extern "C" int evo2_hyena_decode(const void *z, int64_t sz, const void *short_w,
       if (pv) hasD ? launch_hcm_split<true, true>(a, B, st) : launch_hcm_split<false, true>(a, B, st);
       else hasD ? launch_hcm_split<true, false>(a, B, st) : launch_hcm_split<false, false>(a, B, st);
     } else {
-      if (pv) hasD ? launch_pair<KIND_HCS, true, true>(a, B, st) : launch_pair<KIND_HCS, false, true>(a, B, st);
-      else hasD ? launch_pair<KIND_HCS, true, false>(a, B, st) : launch_pair<KIND_HCS, false, false>(a, B, st);
+      if (pv) hasD ? launch_hcs_pair<true, true>(a, B, st) : launch_hcs_pair<false, true>(a, B, st);
+      else hasD ? launch_hcs_pair<true, false>(a, B, st) : launch_hcs_pair<false, false>(a, B, st);
     }
     return check_launch("hyena_decode");
   }
