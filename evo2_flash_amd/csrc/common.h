@@ -31,8 +31,12 @@ __device__ __forceinline__ float lo_bf(uint32_t packed) {
 __device__ __forceinline__ float hi_bf(uint32_t packed) {
   return __uint_as_float(packed & 0xffff0000u);
 }
+// (bf16(lo), bf16(hi)) in one dword: a single v_cvt_pk_bf16_f32, the same
+// rounding as two f2bf calls.
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16v2_t;
 __device__ __forceinline__ uint32_t pack_bf(float lo, float hi) {
-  return static_cast<uint32_t>(f2bf(lo)) | (static_cast<uint32_t>(f2bf(hi)) << 16);
+  bf16v2_t v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+  return __builtin_bit_cast(uint32_t, v);
 }
 
 // ---------------------------------------------------------------- host side

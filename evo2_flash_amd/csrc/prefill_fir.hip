@@ -87,12 +87,7 @@ __device__ __forceinline__ SegInfo seg_of_tile(const FirArgs &p) {
   return s;
 }
 
-// bf16 pair (lo, hi) from two fp32 values, one v_cvt_pk_bf16_f32.
-typedef __attribute__((ext_vector_type(2))) __bf16 bf16v2_t;
-__device__ __forceinline__ uint32_t cvt_pk(float lo, float hi) {
-  bf16v2_t v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
-  return __builtin_bit_cast(uint32_t, v);
-}
+
 
 template <int K, bool HAS_D, bool FUSED>
 __global__ __launch_bounds__(256) void fir_prefill_kernel(FirArgs p) {
@@ -278,10 +273,10 @@ __global__ __launch_bounds__(256) void fir_prefill_kernel(FirArgs p) {
             zm1[i] = z0;
           }
         }
-        const uint32_t px1 = cvt_pk(y[0][1], y[1][1]);
-        const uint32_t pv = cvt_pk(y[0][2], y[1][2]);
-        upk[r / 2] = cvt_pk(lo_bf(px1) * lo_bf(pv), hi_bf(px1) * hi_bf(pv));
-        xpk[r / 2] = cvt_pk(y[0][0], y[1][0]);
+        const uint32_t px1 = pack_bf(y[0][1], y[1][1]);
+        const uint32_t pv = pack_bf(y[0][2], y[1][2]);
+        upk[r / 2] = pack_bf(lo_bf(px1) * lo_bf(pv), hi_bf(px1) * hi_bf(pv));
+        xpk[r / 2] = pack_bf(y[0][0], y[1][0]);
       }
     } else {
       const bf16_t *xp = p.x + (int64_t)r0 * p.sx + cl;
@@ -410,15 +405,15 @@ __global__ __launch_bounds__(256) void fir_prefill_kernel(FirArgs p) {
     bf16_t *orow = obase + (int64_t)trow * p.so;
 #pragma unroll
     for (int r = 0; r < G::RW; r += 2, orow += 2 * p.so) {
-      uint32_t py = cvt_pk(acc[r], acc[r + 1]);
+      uint32_t py = pack_bf(acc[r], acc[r + 1]);
       if constexpr (FUSED) {
         if constexpr (HAS_D) {
           const uint32_t pu = uq[r / 2];
-          const uint32_t pd = cvt_pk(dval * lo_bf(pu), dval * hi_bf(pu));
-          py = cvt_pk(lo_bf(py) + lo_bf(pd), hi_bf(py) + hi_bf(pd));
+          const uint32_t pd = pack_bf(dval * lo_bf(pu), dval * hi_bf(pu));
+          py = pack_bf(lo_bf(py) + lo_bf(pd), hi_bf(py) + hi_bf(pd));
         }
         const uint32_t px = xq[r / 2];
-        py = cvt_pk(lo_bf(px) * lo_bf(py), hi_bf(px) * hi_bf(py));
+        py = pack_bf(lo_bf(px) * lo_bf(py), hi_bf(px) * hi_bf(py));
       }
       // py = (row r, row r+1) of channel c
       const uint32_t nb = __shfl_xor(py, 1);

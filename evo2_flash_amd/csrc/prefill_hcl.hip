@@ -22,7 +22,7 @@
 // No workgroup waits on another, so the launch shape can never deadlock.
 //
 // Lanes run along channels (coalesced rows); a workgroup owns 256 channels
-// (4 waves) and sweeps its tile in 16-row sub-tiles staged into LDS with
+// (4 waves) and sweeps its tile in 8-row sub-tiles staged into LDS with
 // direct-to-LDS loads, double-buffered so the next sub-tile lands while the
 // current one computes.
 #include <type_traits>
@@ -51,7 +51,7 @@ struct HclArgs {
 };
 
 constexpr int HCL_CH = 256;    // channels per workgroup (4 waves x 64 lanes)
-constexpr int HCL_RS = 16;     // rows per sub-tile
+constexpr int HCL_RS = 8;      // rows per sub-tile (8: three waves per SIMD in phase 3)
 constexpr int HCL_ZROWS = HCL_RS + 2;
 constexpr int HCL_ZPITCH = 3 * HCL_CH;  // bf16 per staged row, unpadded
 
@@ -140,11 +140,14 @@ __global__ __launch_bounds__(256) void hcl_scan_kernel(HclArgs p) {
     }
   };
 
-  // One 16-row sub-tile from a staged buffer: short filter, gate, the scan
+  // One sub-tile from a staged buffer: short filter, gate, the scan
   // (and in phase 3 the readout and the mixer tail, stored as bf16 rows).
-  auto compute = [&](auto buf, int s0) {
+  // FULL: all HCL_RS rows are inside the tile, so no row is checked (a
+  // per-row condition would make the compiler copy the 16 states around it).
+  auto compute = [&](auto buf, auto full, int s0) {
     const bf16_t(*zst)[HCL_ZPITCH] = decltype(buf)::value ? zs1 : zs0;
-    const int nr = min(HCL_RS, t_end - s0);
+    constexpr bool FULL = decltype(full)::value;
+    const int nr = FULL ? HCL_RS : min(HCL_RS, t_end - s0);
     float zm2[3], zm1[3];
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
@@ -168,38 +171,36 @@ __global__ __launch_bounds__(256) void hcl_scan_kernel(HclArgs p) {
           zm1[i] = z0;
         }
       }
+      // bf16 roundings two rows at a time: one packed conversion per pair
       const uint32_t px1 = pack_bf(yv[0][1], yv[1][1]);
       const uint32_t pv = pack_bf(yv[0][2], yv[1][2]);
-      upair[0] = rbf(lo_bf(px1) * lo_bf(pv));
-      upair[1] = rbf(hi_bf(px1) * hi_bf(pv));
-      x2pair[0] = rbf(yv[0][0]);
-      x2pair[1] = rbf(yv[1][0]);
+      const uint32_t pu = pack_bf(lo_bf(px1) * lo_bf(pv), hi_bf(px1) * hi_bf(pv));
+      const uint32_t px2 = pack_bf(yv[0][0], yv[1][0]);
+      upair[0] = lo_bf(pu);
+      upair[1] = hi_bf(pu);
+      x2pair[0] = lo_bf(px2);
+      x2pair[1] = hi_bf(px2);
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
-        if (r + q < nr) {  // uniform
-          float ya = 0.f, yb = 0.f, yc = 0.f, yd = 0.f;
+        if (FULL || r + q < nr) {  // uniform
+          float ya = 0.f, yb = 0.f;
 #pragma unroll
           for (int i = 0; i < 16; ++i) {
             s[i] = fmaf(pole[i], s[i], upair[q]);
             if constexpr (PHASE == 3) {
-              if ((i & 3) == 0) ya = fmaf(res[i], s[i], ya);
-              if ((i & 3) == 1) yb = fmaf(res[i], s[i], yb);
-              if ((i & 3) == 2) yc = fmaf(res[i], s[i], yc);
-              if ((i & 3) == 3) yd = fmaf(res[i], s[i], yd);
+              if ((i & 1) == 0) ya = fmaf(res[i], s[i], ya);
+              else yb = fmaf(res[i], s[i], yb);
             }
           }
-          ypair[q] = (ya + yb) + (yc + yd);
+          ypair[q] = ya + yb;
         }
       }
       if constexpr (PHASE == 3) {
-        float g[2];
-#pragma unroll
-        for (int q = 0; q < 2; ++q) {
-          float y = rbf(ypair[q]);
-          y = rbf(y + rbf(upair[q] * dval));
-          g[q] = x2pair[q] * y;
-        }
-        gpk[r / 2] = pack_bf(g[0], g[1]);
+        // g = bf16(bf16(bf16(y) + bf16(u D)) x2) for both rows
+        const uint32_t py = pack_bf(ypair[0], ypair[1]);
+        const uint32_t pd = pack_bf(upair[0] * dval, upair[1] * dval);
+        const uint32_t ps = pack_bf(lo_bf(py) + lo_bf(pd), hi_bf(py) + hi_bf(pd));
+        gpk[r / 2] = pack_bf(x2pair[0] * lo_bf(ps), x2pair[1] * hi_bf(ps));
       }
     }
     if constexpr (PHASE == 3) {
@@ -214,7 +215,7 @@ __global__ __launch_bounds__(256) void hcl_scan_kernel(HclArgs p) {
         const uint32_t nb = __shfl_xor(py, 1);
         const uint32_t dw = odd ? ((nb >> 16) | (py & 0xffff0000u)) : ((py & 0xffffu) | (nb << 16));
         const int rr = r + (odd ? 1 : 0);
-        if (rr < nr && cpair < p.H) *reinterpret_cast<uint32_t *>(orow + (int64_t)rr * p.so) = dw;
+        if ((FULL || rr < nr) && cpair < p.H) *reinterpret_cast<uint32_t *>(orow + (int64_t)rr * p.so) = dw;
       }
     }
   };
@@ -230,7 +231,10 @@ __global__ __launch_bounds__(256) void hcl_scan_kernel(HclArgs p) {
     fix(buf, s0 - 2);
     __syncthreads();
     if (s0 + HCL_RS < t_end) prefetch(nbuf, s0 + HCL_RS - 2);
-    compute(buf, s0);
+    if (s0 + HCL_RS <= t_end)  // uniform
+      compute(buf, std::true_type{}, s0);
+    else
+      compute(buf, std::false_type{}, s0);
   };
   prefetch(B0{}, t0 - 2);
   for (int s0 = t0; s0 < t_end; s0 += 2 * HCL_RS) {
