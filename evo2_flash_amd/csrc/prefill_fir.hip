@@ -56,12 +56,14 @@ template <int K>
 struct FirGeom {
   static constexpr int KP = (K + 1) & ~1;  // taps padded to even (zero tap first)
   static constexpr int NP = KP / 2;        // tap pairs
-  static constexpr int RS = 64;            // rows per sub-tile
-  static constexpr int RW = 16;            // rows per wave per sub-tile
+  // rows per sub-tile: 64 for hcm; 32 for hcs, whose smaller staging lets
+  // more workgroups share a CU (its time goes to memory, not arithmetic)
+  static constexpr int RS = K > 8 ? 64 : 32;
+  static constexpr int RW = RS / 4;        // rows per wave per sub-tile
   static constexpr int NE = NP + RW / 2;   // pairs in one wave's window
-  static constexpr int RING = (KP + RS <= 128) ? 128 : 256;
-  // Row pitches are 4 dwords mod 32 banks, so the b128 accesses of 8 lanes
-  // (one LDS cycle) cover all banks once.
+  static constexpr int RING = (KP + RS <= 64) ? 64 : (KP + RS <= 128) ? 128 : 256;
+  // Row pitches are 4 or 36 dwords mod 64 banks, so the 16 lanes a b128
+  // access serves per cycle cover all banks once.
   static constexpr int PITCH = RING + 8;   // bf16 per channel row of the u ring
   static constexpr int XPITCH = RS + 8;    // bf16 per channel row of x2
   static constexpr int ZROWS = RS + 2;     // staged z rows: sub-tile + 2-row short halo
@@ -297,14 +299,14 @@ __global__ __launch_bounds__(256) void fir_prefill_kernel(FirArgs p) {
             make_uint4(xpk[4 * g], xpk[4 * g + 1], xpk[4 * g + 2], xpk[4 * g + 3]);
     }
   };
-  using R16 = std::integral_constant<int, 16>;
+  using RWC = std::integral_constant<int, G::RW>;
   using R8 = std::integral_constant<int, 8>;
 
   // ---- halo: rows t0-KP .. t0-1
   if constexpr (G::KP == 128) {
 #pragma unroll 1
-    for (int h = 0; h < 2; ++h) {
-      const int rbase = S.t0 - G::KP + 64 * h;
+    for (int h = 0; h < G::KP / G::RS; ++h) {
+      const int rbase = S.t0 - G::KP + G::RS * h;
       if constexpr (FUSED) {
         __syncthreads();
         prefetch(rbase - 2);
@@ -312,7 +314,7 @@ __global__ __launch_bounds__(256) void fir_prefill_kernel(FirArgs p) {
         fix(rbase - 2);
         __syncthreads();
       }
-      produce(rbase + 16 * wave, rbase - 2, R16{}, false);
+      produce(rbase + G::RW * wave, rbase - 2, RWC{}, false);
     }
   } else {
     static_assert(G::KP == 8, "halo split assumes KP = 8 or 128");
@@ -334,7 +336,7 @@ __global__ __launch_bounds__(256) void fir_prefill_kernel(FirArgs p) {
   }
 
   for (int s0 = S.t0; s0 < S.t_end; s0 += G::RS) {
-    produce(s0 + wave * G::RW, s0 - 2, R16{}, FUSED);
+    produce(s0 + wave * G::RW, s0 - 2, RWC{}, FUSED);
     __syncthreads();  // ring / x2s complete; zst free
     const bool more = s0 + G::RS < S.t_end;
     if constexpr (FUSED) {
@@ -387,16 +389,16 @@ __global__ __launch_bounds__(256) void fir_prefill_kernel(FirArgs p) {
     }
 
     // ---- epilogue on row pairs: bf16(y) [+ D*u] then * x2.
-    uint32_t xq[8], uq[8];
+    uint32_t xq[G::RW / 2], uq[G::RW / 2];
     if constexpr (FUSED) {
-      const uint4 c4 = *reinterpret_cast<const uint4 *>(&ring[lane][(pbase + G::KP) & (G::RING - 1)]);
-      const uint4 d4 = *reinterpret_cast<const uint4 *>(&ring[lane][(pbase + G::KP + 8) & (G::RING - 1)]);
-      uq[0] = c4.x; uq[1] = c4.y; uq[2] = c4.z; uq[3] = c4.w;
-      uq[4] = d4.x; uq[5] = d4.y; uq[6] = d4.z; uq[7] = d4.w;
-      const uint4 a4 = *reinterpret_cast<const uint4 *>(&x2s[lane][wave * G::RW]);
-      const uint4 b4 = *reinterpret_cast<const uint4 *>(&x2s[lane][wave * G::RW + 8]);
-      xq[0] = a4.x; xq[1] = a4.y; xq[2] = a4.z; xq[3] = a4.w;
-      xq[4] = b4.x; xq[5] = b4.y; xq[6] = b4.z; xq[7] = b4.w;
+#pragma unroll
+      for (int q = 0; q < G::RW / 8; ++q) {
+        const uint4 c4 =
+            *reinterpret_cast<const uint4 *>(&ring[lane][(pbase + G::KP + 8 * q) & (G::RING - 1)]);
+        uq[4 * q] = c4.x; uq[4 * q + 1] = c4.y; uq[4 * q + 2] = c4.z; uq[4 * q + 3] = c4.w;
+        const uint4 a4 = *reinterpret_cast<const uint4 *>(&x2s[lane][wave * G::RW + 8 * q]);
+        xq[4 * q] = a4.x; xq[4 * q + 1] = a4.y; xq[4 * q + 2] = a4.z; xq[4 * q + 3] = a4.w;
+      }
     }
     float dval = 0.0f;
     if constexpr (HAS_D) dval = bf2f(p.D[cl]);

@@ -52,6 +52,8 @@ struct HclArgs {
 
 constexpr int HCL_CH = 256;    // channels per workgroup (4 waves x 64 lanes)
 constexpr int HCL_RS = 8;      // rows per sub-tile (8: three waves per SIMD in phase 3)
+constexpr int HCL_TILE_ALIGN = 16;  // the documented block_t granularity
+static_assert(HCL_TILE_ALIGN % HCL_RS == 0, "tiles are whole sub-tiles");
 constexpr int HCL_ZROWS = HCL_RS + 2;
 constexpr int HCL_ZPITCH = 3 * HCL_CH;  // bf16 per staged row, unpadded
 
@@ -380,9 +382,9 @@ extern "C" int evo2_hyena_hcl_prefill(const void *z, int64_t sz, const void *sho
   if (T < 0 || H <= 0 || nseq < 0 || ntiles < 0 || num_blocks <= 0)
     return fail(EVO2_ERR_INVALID, "hyena_hcl_prefill: bad sizes");
   if (H % 2) return fail(EVO2_ERR_UNSUPPORTED, "hyena_hcl_prefill: H must be even");
-  if (block_t <= 0 || block_t % HCL_RS)
+  if (block_t <= 0 || block_t % HCL_TILE_ALIGN)
     return fail(EVO2_ERR_INVALID, "hyena_hcl_prefill: block_t=%d must be a multiple of %d",
-                block_t, HCL_RS);
+                block_t, HCL_TILE_ALIGN);
   if (T == 0 || nseq == 0) return EVO2_OK;
   if (!z || !short_w || !conv_state || !residues || !log_poles || !ssm || !D || !seq_table ||
       !blocks || !out || !tile_start || (ntiles && (!tile_table || !workspace)))

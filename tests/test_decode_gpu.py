@@ -53,7 +53,7 @@ def _run_gpu(kind, prm, z, slots, pool, H):
 
 
 @pytest.mark.parametrize("kind", KINDS)
-@pytest.mark.parametrize("H,B,nblk,n_null", [(256, 5, 9, 1), (4096, 64, 80, 3)])
+@pytest.mark.parametrize("H,B,nblk,n_null", [(256, 5, 9, 1), (4096, 64, 80, 3), (8192, 32, 40, 2)])
 def test_decode_bitwise_vs_emulation(kind, H, B, nblk, n_null):
     prm, z, slots, pool = decode_case(kind, H, B, nblk, seed=11 + H, n_null=n_null)
     print(f"decode bitwise kind={kind} H={H} B={B}", flush=True)
