@@ -229,6 +229,175 @@ __global__ __launch_bounds__(256) void fp8_gemm_kernel(GemmArgs p) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Decode-sized GEMMs (M <= 64 rows, e.g. the in_proj of a 64-sequence decode
+// step): the weight stream is the whole cost (N x K bytes against 64 x K of
+// activations), so the kernel is built to keep HBM busy rather than the
+// matrix pipe.  A workgroup owns 16 W rows per wave (four waves, or two
+// when N is below 8192) and all M rows;
+// v_mfma_f32_16x16x128_f8f6f4 with the weight as operand A.  Each wave
+// streams its 16 W rows straight into VGPRs, S_DEPTH K steps (128 bytes)
+// ahead; the activation slice of every step (64 rows x 128 bytes) goes
+// through a ring of S_DEPTH LDS stages filled by direct-to-LDS loads and is
+// shared by the waves.  Steps past the end of K re-read the last slice with
+// a zero weight fragment, so every step issues the same loads and the wait
+// counts stay exact.  LDS rows are 128 bytes; 16-byte chunk c of row r sits
+// at c ^ ((r >> 1) & 7), which spreads the 16 rows a b128 read serves per
+// cycle over all 64 banks.
+constexpr int S_BK = 128;                 // bytes of K per step
+constexpr int S_ROWS = 64;                // activation rows (max M)
+constexpr int S_DEPTH = 8;                // steps in flight
+constexpr int S_STAGE = S_ROWS * S_BK;    // 8 KB of activations per step
+constexpr int SMALL_WIDE_MIN_GROUPS = 128;  // 64-row groups from N = 64 * this (measured)
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+
+template <int WPG>  // waves per workgroup (2 or 4): 16 W rows each
+__global__ __launch_bounds__(256) void fp8_gemm_small_kernel(GemmArgs p) {
+  // one variable per stage: the compiler then sees which stage each
+  // direct-to-LDS load writes and waits only for that stage's loads
+  __shared__ __align__(16) uint8_t s0[S_STAGE], s1[S_STAGE], s2[S_STAGE], s3[S_STAGE];
+  __shared__ __align__(16) uint8_t s4[S_STAGE], s5[S_STAGE], s6[S_STAGE], s7[S_STAGE];
+  auto stage_of = [&](auto slot) __attribute__((always_inline)) -> uint8_t * {
+    constexpr int J = decltype(slot)::value;
+    static_assert(S_DEPTH == 8, "eight stage variables");
+    return J == 0 ? s0 : J == 1 ? s1 : J == 2 ? s2 : J == 3 ? s3
+         : J == 4 ? s4 : J == 5 ? s5 : J == 6 ? s6 : s7;
+  };
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6) & (WPG - 1);
+  const int n0 = blockIdx.x * 16 * WPG;
+  const int g = lane >> 4;   // K bytes [32g, 32g + 32) of a step
+  const int lr = lane & 15;  // row within a 16-row tile
+  const int KT = p.K / S_BK;
+
+  // activation DMA: the 8 blocks of a stage (1 KB = 8 rows each) are split
+  // over the waves, block XB * wave + j for j < XB
+  constexpr int XB = 8 / WPG;
+  int xoff[XB];
+#pragma unroll
+  for (int j = 0; j < XB; ++j) {
+    const int row = (XB * wave + j) * 8 + lane / 8;
+    const int lchunk = (lane & 7) ^ ((row >> 1) & 7);
+    xoff[j] = min(row, p.M - 1) * (int)p.sx + 16 * lchunk;
+  }
+  // weight rows of this wave, straight into registers
+  const uint8_t *wrow = p.w + (int64_t)min(n0 + 16 * wave + lr, p.N - 1) * p.sw + 32 * g;
+  i32x8 wf[S_DEPTH];
+  auto issue = [&](auto slot, int k) __attribute__((always_inline)) {
+    constexpr int J = decltype(slot)::value;
+    const int k0 = min(k, KT - 1) * S_BK;
+    // (a uint4 source pointer: given a byte pointer inside this kernel
+    // template, the host pass drops the template's launch stub)
+#pragma unroll
+    for (int j = 0; j < XB; ++j)
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint4 *>(p.x + k0 + xoff[j]),
+                                       (lds_void *)(stage_of(slot) + (XB * wave + j) * 1024), 16,
+                                       0, 0);
+    const uint4 a0 = *reinterpret_cast<const uint4 *>(wrow + k0);
+    const uint4 a1 = *reinterpret_cast<const uint4 *>(wrow + k0 + 16);
+    wf[J] = i32x8{(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w, (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
+  };
+  f32x4 acc[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // activation fragments of step k from its stage (rows 16 t + lr)
+  auto read_x = [&](auto slot, i32x8 (&xf)[4]) __attribute__((always_inline)) {
+    const uint8_t *xst = stage_of(slot);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int r = 16 * t + lr;
+      const int sw = (r >> 1) & 7;
+      const uint4 b0 = *reinterpret_cast<const uint4 *>(xst + r * S_BK + (((2 * g) ^ sw) << 4));
+      const uint4 b1 = *reinterpret_cast<const uint4 *>(xst + r * S_BK + (((2 * g + 1) ^ sw) << 4));
+      xf[t] = i32x8{(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w,
+                    (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
+    }
+  };
+  // Step k runs its MFMAs on fragments read during step k - 1 and meanwhile
+  // reads step k + 1's: it first waits until this wave's loads for steps k
+  // and k + 1 have landed (the XB + 2 loads of each of the S_DEPTH - 3 later
+  // steps may still fly), then a barrier makes every wave's share of stage
+  // k + 1 visible.  Stage k - 1, refilled with step k + S_DEPTH - 1, was last
+  // read during step k - 2, before the previous barrier.
+  i32x8 xa[4], xb[4];
+  auto step = [&](auto slot, i32x8 (&cur)[4], i32x8 (&nxt)[4], int k) __attribute__((always_inline)) {
+    constexpr int J = decltype(slot)::value;
+    vmcnt_wait<(XB + 2) * (S_DEPTH - 3)>();
+    __builtin_amdgcn_s_barrier();
+    // a step past the end of K multiplies a zero weight fragment (its loads
+    // re-read the last slice), so every step has the same straight-line shape
+    const bool live = k < KT;  // uniform
+    i32x8 w = wf[J];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) w[e] = live ? w[e] : 0;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      acc[t] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(w, cur[t], acc[t], 0, 0, 0, 0, 0,
+                                                                 0);
+      // the accumulators stay in fixed AGPRs (otherwise the unrolled loop
+      // renames them at every step and copies them around)
+      asm volatile("" : "+a"(acc[t]));
+    }
+    issue(std::integral_constant<int, (J + S_DEPTH - 1) % S_DEPTH>{}, k + S_DEPTH - 1);
+    read_x(std::integral_constant<int, (J + 1) % S_DEPTH>{}, nxt);
+  };
+  using std::integral_constant;
+  issue(integral_constant<int, 0>{}, 0);
+  issue(integral_constant<int, 1>{}, 1);
+  issue(integral_constant<int, 2>{}, 2);
+  issue(integral_constant<int, 3>{}, 3);
+  issue(integral_constant<int, 4>{}, 4);
+  issue(integral_constant<int, 5>{}, 5);
+  issue(integral_constant<int, 6>{}, 6);
+  vmcnt_wait<(XB + 2) * (S_DEPTH - 2)>();  // step 0 landed
+  __builtin_amdgcn_s_barrier();
+  read_x(integral_constant<int, 0>{}, xa);
+  for (int k = 0; k < KT; k += S_DEPTH) {
+    step(integral_constant<int, 0>{}, xa, xb, k);
+    step(integral_constant<int, 1>{}, xb, xa, k + 1);
+    step(integral_constant<int, 2>{}, xa, xb, k + 2);
+    step(integral_constant<int, 3>{}, xb, xa, k + 3);
+    step(integral_constant<int, 4>{}, xa, xb, k + 4);
+    step(integral_constant<int, 5>{}, xb, xa, k + 5);
+    step(integral_constant<int, 6>{}, xa, xb, k + 6);
+    step(integral_constant<int, 7>{}, xb, xa, k + 7);
+  }
+  vmcnt_wait<0>();  // no DMA may still target this workgroup's LDS
+
+  // lane holds out[m = 16 t + lr][n = n0 + 16 wave + 4 g + i] in acc[t][i]
+  const float scale = p.sx_scale[0] * p.sw_scale[0];
+  const int n = n0 + 16 * wave + 4 * g;  // (n0 + 16 * wave: this wave's W rows)
+  float bias[4] = {0.f, 0.f, 0.f, 0.f};
+  if (p.bias) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) bias[i] = bf2f(p.bias[min(n + i, p.N - 1)]);
+  }
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int m = 16 * t + lr;
+    if (m >= p.M) continue;
+    bf16_t *o = p.out + (int64_t)m * p.so + n;
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = acc[t][i] * scale + bias[i];
+    if (n + 4 <= p.N && (reinterpret_cast<uintptr_t>(o) & 7) == 0) {
+      *reinterpret_cast<uint2 *>(o) = make_uint2(pack_bf(v[0], v[1]), pack_bf(v[2], v[3]));
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (n + i < p.N) o[i] = f2bf(v[i]);
+    }
+  }
+}
+
+template <int WPG>
+static void launch_small(const GemmArgs &a, hipStream_t stream) {
+  dim3 grid(static_cast<unsigned>(cdiv(a.N, 16 * WPG)));
+  hipLaunchKernelGGL((fp8_gemm_small_kernel<WPG>), grid, dim3(64 * WPG), 0, stream, a);
+}
+
 // x (rows, K) bf16 -> e4m3fn(clamp(x / s, -448, 448)) (fp8_emul.py:76-78),
 // two values per v_cvt_pk_fp8_f32 (round to nearest even).
 __global__ __launch_bounds__(256) void fp8_quantize_kernel(const bf16_t *x, int64_t sx, uint8_t *q,
@@ -303,6 +472,15 @@ extern "C" int evo2_fp8_gemm(const void *x8, int64_t sx, const void *w8, int64_t
   GemmArgs a{static_cast<const uint8_t *>(x8), sx, static_cast<const uint8_t *>(w8), sw, x_scale,
              w_scale, static_cast<const bf16_t *>(bias), static_cast<bf16_t *>(out), so,
              static_cast<int>(M), static_cast<int>(N), static_cast<int>(K)};
+  if (M <= S_ROWS && K % S_BK == 0 && sx * S_ROWS < (int64_t(1) << 31)) {
+    // 64 W rows per workgroup from N = 8192 (the 7B in_proj: 192 groups), else 32
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (N >= 64 * SMALL_WIDE_MIN_GROUPS)
+      launch_small<4>(a, st);
+    else
+      launch_small<2>(a, st);
+    return check_launch("fp8_gemm");
+  }
   dim3 grid(static_cast<unsigned>(cdiv(N, G_BN)), static_cast<unsigned>(cdiv(M, G_BM)));
   hipLaunchKernelGGL(fp8_gemm_kernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream), a);
   return check_launch("fp8_gemm");

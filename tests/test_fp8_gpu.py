@@ -5,8 +5,9 @@
 * GEMM known answers: small-integer e4m3 operands whose fp32 sums are exact,
   so the bf16 output must equal the oracle bit for bit;
 * GEMM within 2e-2 max relative error of the dequantised bf16 reference on
-  random operands, at ragged shapes and at both config-3 shapes
-  (M=8192, K=4096 -> N=12288 and N=4096).
+  random operands, at ragged shapes, at decode sizes (M <= 64, the 7B and
+  40B in_proj) and at both config-3 shapes (M=8192, K=4096 -> N=12288 and
+  N=4096).
 """
 
 import pytest
@@ -39,7 +40,10 @@ def _small_int_e4m3(shape, g):
     return (torch.randint(-6, 7, shape, generator=g).float()).to(E4M3)
 
 
-@pytest.mark.parametrize("M,N,K", [(256, 256, 128), (64, 384, 256), (300, 512, 1920)])
+# M <= 64 with K a multiple of 128 runs the decode-sized kernel (weights
+# streamed into registers, 16x16x128 MFMA); the others the 256x256-tile one.
+@pytest.mark.parametrize("M,N,K", [(256, 256, 128), (64, 384, 256), (300, 512, 1920),
+                                   (1, 64, 128), (5, 130, 1920), (64, 4096, 4096)])
 def test_gemm_known_answer(M, N, K):
     g = torch.Generator().manual_seed(M + N)
     x8 = _small_int_e4m3((M, K), g)
@@ -51,7 +55,9 @@ def test_gemm_known_answer(M, N, K):
     assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
 
 
-@pytest.mark.parametrize("M,N,K", [(64, 12288, 4096), (333, 4096, 4096), (1000, 640, 1920)])
+@pytest.mark.parametrize("M,N,K", [(64, 12288, 4096), (333, 4096, 4096), (1000, 640, 1920),
+                                   (1, 12288, 4096), (37, 200, 1920), (64, 16384, 8192),
+                                   (48, 256, 192)])
 def test_static_linear_vs_dequant(M, N, K):
     g = torch.Generator().manual_seed(K)
     x = torch.randn(M, K, generator=g).to(torch.bfloat16)
