@@ -94,6 +94,27 @@ SIGNATURES = {
         _c_p, _c_i64, _c_i64, _c_i64, _c_i64,     # out, so, M, N, K
         _c_p,                                     # stream
     ],
+    "evo2_fir_verify": [
+        _c_p, _c_i64, _c_i64, _c_i32,             # x, xs0, xs1, x_f32
+        _c_p, _c_i64, _c_i64, _c_i32,             # w, w0, w1, K
+        _c_p, _c_i64, _c_i64, _c_i64,             # state + strides
+        _c_p, _c_i64, _c_i64,                     # ins + strides
+        _c_p, _c_i64, _c_i64, _c_i32,             # outs + strides, Q
+        _c_p, _c_p, _c_p,                         # starts, ends, accepted
+        _c_p, _c_i64, _c_i64, _c_i64, _c_i64,     # y, ys0, nreq, T, H
+        _c_i32, _c_i64, _c_p,                     # null_block, num_blocks, stream
+    ],
+    "evo2_iir_verify": [
+        _c_p, _c_i64, _c_i64, _c_i32,             # x, xs0, xs1, x_f32
+        _c_p, _c_i64, _c_i64,                     # poles + strides
+        _c_p, _c_i64, _c_i64,                     # residues + strides
+        _c_p, _c_i64, _c_i64, _c_i64,             # state + strides
+        _c_p, _c_i64, _c_i64,                     # ins + strides
+        _c_p, _c_i64, _c_i64, _c_i32,             # outs + strides, Q
+        _c_p, _c_p, _c_p,                         # starts, ends, accepted
+        _c_p, _c_i64, _c_i64, _c_i64, _c_i64,     # y, ys0, nreq, T, H
+        _c_i32, _c_i64, _c_p,                     # null_block, num_blocks, stream
+    ],
 }
 
 RESTYPES = {"evo2_last_error": ctypes.c_char_p, "evo2_hcl_workspace_bytes": ctypes.c_int64}

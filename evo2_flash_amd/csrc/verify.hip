@@ -1,0 +1,324 @@
+// Speculative verification of the inner Hyena operators on gfx950: one
+// request carries up to Q = 1 + num_spec tokens (packed rows
+// [starts[r], ends[r])), starts from the snapshot its previous step
+// accepted (ins[r][accepted[r] - 1]) and writes a complete state snapshot
+// after every token (outs[r][pos]), so that the next step can resume from
+// whichever prefix the sampler accepts.  Replaces triton_verifier.py
+// (_fir_kernel / _iir_kernel, lines 46-137) and its wrappers fir_snapshots,
+// iir_snapshots, fir_one, iir_one (lines 125-178); the plain torch form is
+// mixers.py:578-660.
+//
+// Arithmetic follows the reference kernels exactly: separate multiply and
+// add (no FMA in this file), the FIR sum over k = 16 j + 4 m + l kept as 16
+// accumulators (m, l) over j in order, then ((m0 + m1) + m2) + m3 per l, then
+// (l0 + l2) + (l1 + l3), plus last * x (triton_verifier.py:17-43, 73); the
+// width-7 sum ((p0 + p4) + (p1 + p5) + p2) + p3; the LI readout as the
+// halving tree r[s] += r[s + 8], r[s + 4], r[s + 2], r[s + 1] (lines 128-131).
+// Outputs keep the input's dtype (bf16 or fp32); rows outside every
+// request's range are not written (the wrappers zero them first).
+//
+// Layout: FIR windows are channel-contiguous native storage (blocks, K-1, H)
+// seen as a (blocks, H, K-1) view with unit channel stride, so each column
+// moves as one coalesced row per wave; LI states are (blocks, H, 16) with
+// unit state stride.  A destination equal to the null block, or outside the
+// pool, is not written (the reference skips block 0, line 80); a source
+// outside the pool reads as a zero state.
+#include "common.h"
+
+#pragma clang fp contract(off)
+
+namespace evo2 {
+
+struct VerifyArgs {
+  const void *x; int64_t xs0, xs1;        // (T, H) bf16 or fp32 token inputs u
+  int x_f32;
+  const bf16_t *w; int64_t w0, w1;        // FIR taps (H, K) bf16
+  const float *poles; int64_t p0, p1;     // LI poles exp(log_poles) (H, 16)
+  const float *res; int64_t r0, r1;       // LI residues (H, 16)
+  float *st; int64_t ss0, ss1, ss2;       // state view (blocks, H, K-1 | 16)
+  const int32_t *ins; int64_t is0, is1;   // (nreq, Q) source snapshots
+  const int32_t *outs; int64_t os0, os1;  // (nreq, Q) destination snapshots
+  const int64_t *starts, *ends, *accepted;  // (nreq,) each; null: one token per request
+  void *y; int64_t ys0;                   // (T, H) output, x's dtype
+  int Q, H, null_block;
+  int64_t num_blocks, T;
+};
+
+// Request r's token range, source block and whether it reads a real block.
+struct Req {
+  int64_t first, end, src;
+  bool src_ok;
+};
+
+__device__ __forceinline__ Req request_of(const VerifyArgs &a, int64_t r) {
+  Req q;
+  int64_t col = 0;
+  if (a.starts) {
+    q.first = a.starts[r];
+    q.end = a.ends[r];
+    col = a.accepted[r] - 1;
+  } else {
+    q.first = r;
+    q.end = r + 1;
+  }
+  // rows outside x are never touched, whatever the tables say
+  q.end = min(q.end, a.T);
+  if (q.first < 0) q.end = q.first;
+  const bool col_ok = col >= 0 && col < a.Q;
+  const int64_t s = col_ok ? a.ins[r * a.is0 + col * a.is1] : -1;
+  q.src_ok = s >= 0 && s < a.num_blocks;
+  q.src = q.src_ok ? s : 0;
+  return q;
+}
+
+__device__ __forceinline__ int64_t dest_of(const VerifyArgs &a, int64_t r, int pos) {
+  const int64_t d = a.outs[r * a.os0 + (int64_t)pos * a.os1];
+  return (d == a.null_block || d < 0 || d >= a.num_blocks) ? -1 : d;
+}
+
+__device__ __forceinline__ float load_x(const VerifyArgs &a, int64_t t, int c) {
+  const int64_t off = t * a.xs0 + (int64_t)c * a.xs1;
+  return a.x_f32 ? static_cast<const float *>(a.x)[off] : bf2f(static_cast<const bf16_t *>(a.x)[off]);
+}
+
+__device__ __forceinline__ void store_y(const VerifyArgs &a, int64_t t, int c, float v) {
+  const int64_t off = t * a.ys0 + c;
+  if (a.x_f32) static_cast<float *>(a.y)[off] = v;
+  else static_cast<bf16_t *>(a.y)[off] = f2bf(v);
+}
+
+// ---------------------------------------------------------------------------
+// K = 128.  A workgroup owns one request and 64 channels (lane = channel).
+// The 127-column window lives in an LDS ring of 128 columns: at position p
+// column k of the window is ring slot (p + k) mod 128, so appending the token
+// overwrites the slot of the dropped column and nothing moves.  Wave m sums
+// the columns k = 16 j + 4 m + l (its accumulators (m, l)); waves 1-3 hand
+// their four partials to wave 0 through LDS, which combines them in the
+// reference's order.  After each token every wave writes a quarter of the
+// new window to the destination snapshot.
+__global__ __launch_bounds__(256) void fir128_verify_kernel(VerifyArgs a) {
+  __shared__ float ring[128][64];
+  __shared__ float part[3][4][64];
+  const int lane = threadIdx.x & 63;
+  const int m = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) & 3;
+  const int64_t r = blockIdx.x;
+  const int c = blockIdx.y * 64 + lane;
+  const bool active = c < a.H;
+  const int cc = active ? c : 0;
+  const Req q = request_of(a, r);
+
+  // taps of this wave's columns, and the window from the source snapshot
+  float wk[8][4];
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+#pragma unroll
+    for (int l = 0; l < 4; ++l) {
+      const int k = 16 * j + 4 * m + l;
+      wk[j][l] = k < 127 ? bf2f(a.w[(int64_t)cc * a.w0 + (int64_t)k * a.w1]) : 0.0f;
+    }
+  const float last = bf2f(a.w[(int64_t)cc * a.w0 + 127 * a.w1]);
+  const float *src = a.st + q.src * a.ss0 + (int64_t)cc * a.ss1;
+  for (int k = m; k < 127; k += 4) ring[k][lane] = (q.src_ok && active) ? src[(int64_t)k * a.ss2] : 0.0f;
+  __syncthreads();
+
+  for (int pos = 0; pos < a.Q; ++pos) {
+    if (q.first + pos >= q.end) break;  // uniform; positions are consecutive
+    const int64_t t = q.first + pos;
+    const float x = active ? load_x(a, t, c) : 0.0f;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int l = 0; l < 4; ++l) {
+        const int k = 16 * j + 4 * m + l;
+        const float s = k < 127 ? ring[(pos + k) & 127][lane] : 0.0f;
+        acc[l] = acc[l] + s * wk[j][l];
+      }
+    if (m > 0) {
+#pragma unroll
+      for (int l = 0; l < 4; ++l) part[m - 1][l][lane] = acc[l];
+    }
+    __syncthreads();  // partials visible; every wave done reading this window
+    if (m == 0) {
+      float p[4];
+#pragma unroll
+      for (int l = 0; l < 4; ++l)
+        p[l] = ((acc[l] + part[0][l][lane]) + part[1][l][lane]) + part[2][l][lane];
+      const float yv = ((p[0] + p[2]) + (p[1] + p[3])) + last * x;
+      if (active) store_y(a, t, c, yv);
+      ring[(pos + 127) & 127][lane] = x;  // the dropped column's slot
+    }
+    __syncthreads();  // appended token visible; partials consumed
+    const int64_t d = dest_of(a, r, pos);
+    if (d >= 0 && active) {
+      float *dst = a.st + d * a.ss0 + (int64_t)c * a.ss1;
+      for (int k = m; k < 127; k += 4) dst[(int64_t)k * a.ss2] = ring[(pos + 1 + k) & 127][lane];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// K = 7: one channel per thread, the 6-column window in registers.
+__global__ __launch_bounds__(256) void fir7_verify_kernel(VerifyArgs a) {
+  const int64_t r = blockIdx.x;
+  const int c = blockIdx.y * 256 + threadIdx.x;
+  if (c >= a.H) return;
+  const Req q = request_of(a, r);
+  float w[7], s[6];
+#pragma unroll
+  for (int k = 0; k < 7; ++k) w[k] = bf2f(a.w[(int64_t)c * a.w0 + (int64_t)k * a.w1]);
+  const float *src = a.st + q.src * a.ss0 + (int64_t)c * a.ss1;
+#pragma unroll
+  for (int k = 0; k < 6; ++k) s[k] = q.src_ok ? src[(int64_t)k * a.ss2] : 0.0f;
+  for (int pos = 0; pos < a.Q; ++pos) {
+    if (q.first + pos >= q.end) break;
+    const int64_t t = q.first + pos;
+    const float x = load_x(a, t, c);
+    // ((p0 + p4) + (p1 + p5) + p2) + p3 (triton_verifier.py:35-43)
+    float pa = s[0] * w[0], pb = s[1] * w[1];
+    const float pc = s[2] * w[2], pd = s[3] * w[3];
+    pa = pa + s[4] * w[4];
+    pb = pb + s[5] * w[5];
+    const float yv = (((pa + pb) + pc) + pd) + w[6] * x;
+    store_y(a, t, c, yv);
+#pragma unroll
+    for (int k = 0; k < 5; ++k) s[k] = s[k + 1];
+    s[5] = x;
+    const int64_t d = dest_of(a, r, pos);
+    if (d >= 0) {
+      float *dst = a.st + d * a.ss0 + (int64_t)c * a.ss1;
+#pragma unroll
+      for (int k = 0; k < 6; ++k) dst[(int64_t)k * a.ss2] = s[k];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// LI: four lanes per channel, lane q of a quad owns states 4q..4q+3 (one
+// float4 of the state, residue and pole rows); the readout tree runs over
+// quad DPP moves as in the fused decode step.
+template <int CTRL>
+__device__ __forceinline__ float quad_move(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+__global__ __launch_bounds__(256) void iir_verify_kernel(VerifyArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int qd = lane & 3;
+  const int64_t r = blockIdx.x;
+  const int c = blockIdx.y * 64 + (threadIdx.x >> 2);
+  const bool active = c < a.H;
+  const int cc = active ? c : a.H - 1;
+  const Req q = request_of(a, r);
+  const float4 p4 = *reinterpret_cast<const float4 *>(a.poles + (int64_t)cc * a.p0 + 4 * qd);
+  const float4 r4 = *reinterpret_cast<const float4 *>(a.res + (int64_t)cc * a.r0 + 4 * qd);
+  float4 s4 = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (q.src_ok) s4 = *reinterpret_cast<const float4 *>(a.st + q.src * a.ss0 + (int64_t)cc * a.ss1 + 4 * qd);
+  const float pv[4] = {p4.x, p4.y, p4.z, p4.w};
+  const float rv[4] = {r4.x, r4.y, r4.z, r4.w};
+  float sv[4] = {s4.x, s4.y, s4.z, s4.w};
+  for (int pos = 0; pos < a.Q; ++pos) {
+    if (q.first + pos >= q.end) break;  // uniform
+    const int64_t t = q.first + pos;
+    const float x = load_x(a, t, cc);
+    float rr[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      sv[e] = sv[e] * pv[e] + x;
+      rr[e] = sv[e] * rv[e];
+    }
+    const int64_t d = dest_of(a, r, pos);
+    if (d >= 0 && active)
+      *reinterpret_cast<float4 *>(a.st + d * a.ss0 + (int64_t)c * a.ss1 + 4 * qd) =
+          make_float4(sv[0], sv[1], sv[2], sv[3]);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) rr[e] = rr[e] + quad_move<0xEE>(rr[e]);  // += state + 8
+#pragma unroll
+    for (int e = 0; e < 4; ++e) rr[e] = rr[e] + quad_move<0xF5>(rr[e]);  // += state + 4
+    rr[0] = rr[0] + rr[2];                                                   // += state + 2
+    rr[1] = rr[1] + rr[3];
+    const float yv = rr[0] + rr[1];                                          // += state + 1
+    if (qd == 0 && active) store_y(a, t, c, yv);
+  }
+}
+
+}  // namespace evo2
+
+using namespace evo2;
+
+static int verify_common(const char *who, const void *x, int64_t nreq, int64_t T, int64_t H,
+                         int32_t Q,
+                         const int32_t *ins, const int32_t *outs, const int64_t *starts,
+                         const int64_t *ends, const int64_t *accepted, const void *y,
+                         const float *state, int64_t num_blocks) {
+  if (nreq < 0 || T < 0 || H <= 0 || H > (1 << 30) || Q <= 0 || num_blocks <= 0)
+    return fail(EVO2_ERR_INVALID, "%s: bad sizes nreq=%lld H=%lld Q=%d blocks=%lld", who,
+                (long long)nreq, (long long)H, Q, (long long)num_blocks);
+  if (nreq > 65535) return fail(EVO2_ERR_UNSUPPORTED, "%s: %lld requests exceed 65535", who,
+                                (long long)nreq);
+  if (!x || !ins || !outs || !y || !state)
+    return fail(EVO2_ERR_INVALID, "%s: null pointer argument", who);
+  if ((starts == nullptr) != (ends == nullptr) || (starts == nullptr) != (accepted == nullptr))
+    return fail(EVO2_ERR_INVALID, "%s: starts, ends and accepted go together", who);
+  if (!starts && Q != 1) return fail(EVO2_ERR_INVALID, "%s: one-token form needs Q=1", who);
+  return EVO2_OK;
+}
+
+extern "C" int evo2_fir_verify(const void *x, int64_t xs0, int64_t xs1, int32_t x_f32,
+                               const void *w, int64_t w0, int64_t w1, int32_t K,
+                               float *state, int64_t ss0, int64_t ss1, int64_t ss2,
+                               const int32_t *ins, int64_t is0, int64_t is1,
+                               const int32_t *outs, int64_t os0, int64_t os1, int32_t Q,
+                               const int64_t *starts, const int64_t *ends,
+                               const int64_t *accepted, void *y, int64_t ys0, int64_t nreq,
+                               int64_t T, int64_t H, int32_t null_block, int64_t num_blocks,
+                               void *stream) {
+  int rc = verify_common("fir_verify", x, nreq, T, H, Q, ins, outs, starts, ends, accepted, y, state,
+                         num_blocks);
+  if (rc) return rc;
+  if (K != 7 && K != 128)
+    return fail(EVO2_ERR_UNSUPPORTED, "fir_verify: filter length %d (7 or 128 only)", K);
+  if (!w) return fail(EVO2_ERR_INVALID, "fir_verify: null pointer argument");
+  if (nreq == 0) return EVO2_OK;
+  VerifyArgs a{x, xs0, xs1, x_f32, static_cast<const bf16_t *>(w), w0, w1, nullptr, 0, 0,
+               nullptr, 0, 0, state, ss0, ss1, ss2, ins, is0, is1, outs, os0, os1,
+               starts, ends, accepted, y, ys0, Q, static_cast<int>(H), null_block, num_blocks, T};
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (K == 128) {
+    dim3 grid(static_cast<unsigned>(nreq), static_cast<unsigned>(cdiv(H, 64)));
+    hipLaunchKernelGGL(fir128_verify_kernel, grid, dim3(256), 0, st, a);
+  } else {
+    dim3 grid(static_cast<unsigned>(nreq), static_cast<unsigned>(cdiv(H, 256)));
+    hipLaunchKernelGGL(fir7_verify_kernel, grid, dim3(256), 0, st, a);
+  }
+  return check_launch("fir_verify");
+}
+
+extern "C" int evo2_iir_verify(const void *x, int64_t xs0, int64_t xs1, int32_t x_f32,
+                               const float *poles, int64_t p0, int64_t p1,
+                               const float *residues, int64_t r0, int64_t r1,
+                               float *state, int64_t ss0, int64_t ss1, int64_t ss2,
+                               const int32_t *ins, int64_t is0, int64_t is1,
+                               const int32_t *outs, int64_t os0, int64_t os1, int32_t Q,
+                               const int64_t *starts, const int64_t *ends,
+                               const int64_t *accepted, void *y, int64_t ys0, int64_t nreq,
+                               int64_t T, int64_t H, int32_t null_block, int64_t num_blocks,
+                               void *stream) {
+  int rc = verify_common("iir_verify", x, nreq, T, H, Q, ins, outs, starts, ends, accepted, y, state,
+                         num_blocks);
+  if (rc) return rc;
+  if (!poles || !residues) return fail(EVO2_ERR_INVALID, "iir_verify: null pointer argument");
+  if (p1 != 1 || r1 != 1 || ss2 != 1 || p0 % 4 || r0 % 4 || ss1 % 4 || ss0 % 4 ||
+      reinterpret_cast<uintptr_t>(poles) % 16 || reinterpret_cast<uintptr_t>(residues) % 16 ||
+      reinterpret_cast<uintptr_t>(state) % 16)
+    return fail(EVO2_ERR_UNSUPPORTED,
+                "iir_verify: poles, residues and states need 16 contiguous, 16-byte aligned "
+                "fp32 per channel");
+  if (nreq == 0) return EVO2_OK;
+  VerifyArgs a{x, xs0, xs1, x_f32, nullptr, 0, 0, poles, p0, p1, residues, r0, r1,
+               state, ss0, ss1, ss2, ins, is0, is1, outs, os0, os1,
+               starts, ends, accepted, y, ys0, Q, static_cast<int>(H), null_block, num_blocks, T};
+  dim3 grid(static_cast<unsigned>(nreq), static_cast<unsigned>(cdiv(H, 64)));
+  hipLaunchKernelGGL(iir_verify_kernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream), a);
+  return check_launch("iir_verify");
+}

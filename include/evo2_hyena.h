@@ -223,6 +223,59 @@ int evo2_rms_norm(const void *x, int64_t sx, const void *residual, int64_t sr,
                   void *s_out, int64_t ss, const float *q_scale, void *q, int64_t sq,
                   int64_t T, int64_t H, void *stream);
 
+/*
+ * Speculative verification of the inner FIR (K = 7 or 128): each request r
+ * runs tokens [starts[r], ends[r]) of x (at most Q of them) from the snapshot
+ * ins[r][accepted[r] - 1], writes y for those rows (x's dtype) and, after
+ * each token pos, the whole window to block outs[r][pos] (skipped when that
+ * is the null block or outside the pool).  With starts = ends = accepted =
+ * NULL and Q = 1 it is the one-token step: request r is row r, reading
+ * ins[r] and writing outs[r].  Summation order, rounding and the absence of
+ * FMA follow the reference kernel.
+ *
+ * Replaces triton_verifier._fir_kernel, fir_snapshots and fir_one
+ * (evo2_flash/triton_verifier.py:46-80, 125-135, 157-167).
+ *
+ *   x          (T, H) bf16 (x_f32 = 0) or fp32, strides xs0, xs1
+ *   w          (H, K) bf16 taps, strides w0, w1
+ *   state      (blocks, H, K-1) fp32 view, strides ss0, ss1, ss2
+ *   ins, outs  (nreq, Q) int32 block ids, strides is0/is1, os0/os1 (the same
+ *              Q columns in both)
+ *   starts, ends, accepted  (nreq,) int64, or all NULL
+ *   y          (T, H) output, x's dtype, row stride ys0, unit column stride
+ *   Rows at or past T are never read or written, whatever the tables say.
+ */
+int evo2_fir_verify(const void *x, int64_t xs0, int64_t xs1, int32_t x_f32,
+                    const void *w, int64_t w0, int64_t w1, int32_t K,
+                    float *state, int64_t ss0, int64_t ss1, int64_t ss2,
+                    const int32_t *ins, int64_t is0, int64_t is1,
+                    const int32_t *outs, int64_t os0, int64_t os1, int32_t Q,
+                    const int64_t *starts, const int64_t *ends, const int64_t *accepted,
+                    void *y, int64_t ys0, int64_t nreq, int64_t T, int64_t H,
+                    int32_t null_block, int64_t num_blocks, void *stream);
+
+/*
+ * The same for the LI operator: s = s * poles + x (separate multiply and
+ * add), each token's 16-state snapshot written to outs[r][pos], y = the
+ * halving-tree readout of residues * s.  poles = exp(log_poles).
+ *
+ * Replaces triton_verifier._iir_kernel, iir_snapshots and iir_one
+ * (evo2_flash/triton_verifier.py:83-122, 146-155, 170-178).
+ *
+ *   poles, residues  (H, 16) fp32, strides p0/p1, r0/r1 (unit state stride)
+ *   state            (blocks, H, 16) fp32 view, strides ss0, ss1, ss2 = 1
+ *   other arguments as evo2_fir_verify.
+ */
+int evo2_iir_verify(const void *x, int64_t xs0, int64_t xs1, int32_t x_f32,
+                    const float *poles, int64_t p0, int64_t p1,
+                    const float *residues, int64_t r0, int64_t r1,
+                    float *state, int64_t ss0, int64_t ss1, int64_t ss2,
+                    const int32_t *ins, int64_t is0, int64_t is1,
+                    const int32_t *outs, int64_t os0, int64_t os1, int32_t Q,
+                    const int64_t *starts, const int64_t *ends, const int64_t *accepted,
+                    void *y, int64_t ys0, int64_t nreq, int64_t T, int64_t H,
+                    int32_t null_block, int64_t num_blocks, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -17,7 +17,8 @@ __all__ = [
     "fir_mixer_prefill", "iir_mixer_prefill", "fir_decode_one", "iir_decode_one",
     "short_conv_update", "hyena_decode_emulated", "mixer_decode_unfused",
     "rms_norm", "quantize_input", "fp8_linear_dequant", "prefill_tables",
-    "STATE_ACC_BUDGET",
+    "fir_decode_snapshots", "iir_decode_snapshots", "fir_verify_emulated",
+    "iir_verify_emulated", "STATE_ACC_BUDGET",
 ]
 
 # mixers.py:72-74: bound on the (H, blk, L) temporary of the LI final state.
@@ -294,6 +295,129 @@ def mixer_decode_unfused(z, short_w, conv_state, slots, inner, inner_state, D=No
     if D is not None:
         y = y + D.to(y.dtype) * u
     return x2 * y
+
+
+# ------------------------------------------------------------ speculative verify
+def _verify_rows(ins, outs, starts, ends, accepted, r):
+    """(source block, first row, end row, destinations) of request r."""
+    src = int(ins[r, int(accepted[r]) - 1])
+    return src, int(starts[r]), int(ends[r]), [int(d) for d in outs[r]]
+
+
+def fir_decode_snapshots(x, weight, state, ins, outs, starts, ends, accepted):
+    """The reference's torch verify path for the FIR (mixers.py:578-624):
+    each request starts from the snapshot ins[r, accepted-1], runs its tokens
+    [starts[r], ends[r]) and writes the window after token pos to outs[r, pos]
+    (block 0 is the null block: never written, as the fused kernel skips it).
+    fp32 torch sums; returns (T, H) in x's dtype, zero outside every range.
+    state: (blocks, H, K-1) fp32, modified in place."""
+    K = weight.shape[1]
+    wf = weight.float()
+    y = torch.zeros(x.shape, dtype=torch.float32)
+    for r in range(ins.shape[0]):
+        src, a, e, dst = _verify_rows(ins, outs, starts, ends, accepted, r)
+        st = state[src, :, : K - 1].float().clone()
+        for pos in range(outs.shape[1]):
+            if a + pos >= e:
+                break
+            xt = x[a + pos].float()
+            y[a + pos] = (st * wf[:, :-1]).sum(-1) + wf[:, -1] * xt
+            st = torch.cat([st[:, 1:], xt[:, None]], dim=1)
+            if dst[pos] != 0:
+                state[dst[pos], :, : K - 1] = st
+    return y.to(x.dtype)
+
+
+def iir_decode_snapshots(x, poles, residues, state, ins, outs, starts, ends, accepted):
+    """The reference's torch verify path for the LI operator (mixers.py:627-658),
+    with the same snapshot and null-block rules as `fir_decode_snapshots`."""
+    y = torch.zeros(x.shape, dtype=torch.float32)
+    for r in range(ins.shape[0]):
+        src, a, e, dst = _verify_rows(ins, outs, starts, ends, accepted, r)
+        st = state[src, :, :16].float().clone()
+        for pos in range(outs.shape[1]):
+            if a + pos >= e:
+                break
+            st = st * poles + x[a + pos].float()[:, None]
+            if dst[pos] != 0:
+                state[dst[pos], :, :16] = st
+            y[a + pos] = (residues * st).sum(-1)
+    return y.to(x.dtype)
+
+
+def _fir_dot_kernel_order(s, wf):
+    """sum_k s_k w_k, k < K-1, in the verify kernel's order
+    (triton_verifier.py:17-43): for K=128 sixteen accumulators (m, l) over
+    k = 16 j + 4 m + l, j in order, then ((m0 + m1) + m2) + m3, then
+    (l0 + l2) + (l1 + l3); for K=7 ((p0 + p4) + (p1 + p5) + p2) + p3."""
+    K = wf.shape[1]
+    if K == 7:
+        a = s[:, 0] * wf[:, 0] + s[:, 4] * wf[:, 4]
+        b = s[:, 1] * wf[:, 1] + s[:, 5] * wf[:, 5]
+        return ((a + b) + s[:, 2] * wf[:, 2]) + s[:, 3] * wf[:, 3]
+    H = s.shape[0]
+    acc = [[torch.zeros(H) for _ in range(4)] for _ in range(4)]
+    for j in range(8):
+        for m in range(4):
+            for l in range(4):
+                k = 16 * j + 4 * m + l
+                if k < 127:
+                    acc[m][l] = acc[m][l] + s[:, k] * wf[:, k]
+    p = [((acc[0][l] + acc[1][l]) + acc[2][l]) + acc[3][l] for l in range(4)]
+    return (p[0] + p[2]) + (p[1] + p[3])
+
+
+def fir_verify_emulated(x, weight, state, ins, outs, starts, ends, accepted, null_block=0):
+    """`fir_decode_snapshots` with the fused verify kernel's summation order
+    (no FMA on the CPU), for bitwise comparison with a GPU kernel that keeps
+    that order.  starts=None runs the one-token form (fir_one): row r reads
+    and writes ins[r, 0] / outs[r, 0]."""
+    K = weight.shape[1]
+    wf = weight.float()
+    y = torch.zeros(x.shape, dtype=torch.float32)
+    one = starts is None
+    for r in range(ins.shape[0]):
+        if one:
+            src, a, e, dst = int(ins[r, 0]), r, r + 1, [int(outs[r, 0])]
+        else:
+            src, a, e, dst = _verify_rows(ins, outs, starts, ends, accepted, r)
+        st = state[src, :, : K - 1].float().clone()
+        for pos in range(outs.shape[1]):
+            if a + pos >= e:
+                break
+            xt = x[a + pos].float()
+            y[a + pos] = _fir_dot_kernel_order(st, wf) + wf[:, K - 1] * xt
+            st = torch.cat([st[:, 1:], xt[:, None]], dim=1)
+            if dst[pos] != null_block:
+                state[dst[pos], :, : K - 1] = st
+    return y.to(x.dtype)
+
+
+def iir_verify_emulated(x, poles, residues, state, ins, outs, starts, ends, accepted,
+                        null_block=0):
+    """`iir_decode_snapshots` with the fused kernel's halving-tree readout
+    (triton_verifier.py:128-131): r[s] += r[s+8], += r[s+4], += r[s+2],
+    += r[s+1], y = r[0]."""
+    y = torch.zeros(x.shape, dtype=torch.float32)
+    one = starts is None
+    for r in range(ins.shape[0]):
+        if one:
+            src, a, e, dst = int(ins[r, 0]), r, r + 1, [int(outs[r, 0])]
+        else:
+            src, a, e, dst = _verify_rows(ins, outs, starts, ends, accepted, r)
+        st = state[src, :, :16].float().clone()
+        for pos in range(outs.shape[1]):
+            if a + pos >= e:
+                break
+            st = st * poles + x[a + pos].float()[:, None]
+            if dst[pos] != null_block:
+                state[dst[pos], :, :16] = st
+            q = st * residues
+            q = q[:, :8] + q[:, 8:]
+            q = q[:, :4] + q[:, 4:]
+            q = q[:, :2] + q[:, 2:]
+            y[a + pos] = q[:, 0] + q[:, 1]
+    return y.to(x.dtype)
 
 
 # ------------------------------------------------------------------ norm, fp8

@@ -59,3 +59,37 @@ def decode_case(kind, H, B, num_blocks, seed, n_null=0):
         slots[rows] = 0
     pool = random_pool(num_blocks, H, seed + 3)
     return prm, z, slots, pool
+
+
+def verify_case(kind, H, nreq, Q, num_blocks, seed, x_dtype=torch.bfloat16, n_null_out=2):
+    """CPU tensors for one speculative verify step of the inner operator.
+
+    Requests carry 1..Q tokens (ragged, at least one full), start from the
+    snapshot of their previous step's accepted count (1..Q) and write one
+    snapshot per token.  ins and outs use disjoint blocks (block 0 is the
+    null block); `n_null_out` destinations are the null block.
+    Returns (params, x, state, (ins, outs, starts, ends, accepted)); state is
+    (blocks, H, K-1 | 16) fp32.
+    """
+    g = torch.Generator().manual_seed(seed)
+    prm = mixer_params(kind, H, seed, in_proj_fp8=False)
+    lens = torch.randint(1, Q + 1, (nreq,), generator=g)
+    lens[0] = Q
+    T = int(lens.sum())
+    x = (torch.randn(T, H, generator=g) * 1.3).to(x_dtype)
+    ends = torch.cumsum(lens, 0)
+    starts = ends - lens
+    accepted = torch.randint(1, Q + 1, (nreq,), generator=g)
+    perm = torch.randperm(num_blocks - 1, generator=g)[: 2 * nreq * Q] + 1
+    if perm.numel() < 2 * nreq * Q:
+        raise ValueError("state pool too small for disjoint snapshot blocks")
+    ins = perm[: nreq * Q].view(nreq, Q).to(torch.int32)
+    outs = perm[nreq * Q:].view(nreq, Q).clone().to(torch.int32)
+    flat = outs.view(-1)
+    flat[torch.randperm(flat.numel(), generator=g)[:n_null_out]] = 0
+    if kind == "hcl":
+        state = torch.randn(num_blocks, H, 16, generator=g) * 10.0
+    else:
+        K = prm["conv"].shape[-1]
+        state = torch.randn(num_blocks, H, K - 1, generator=g).to(torch.bfloat16).float()
+    return prm, x, state, (ins, outs, starts, ends, accepted)

@@ -112,3 +112,38 @@ def test_decode_supported_false_on_cpu():
                                 torch.zeros(3 * H, 3, dtype=torch.bfloat16),
                                 torch.zeros(2, 3 * H, 2, dtype=torch.bfloat16),
                                 torch.zeros(H, 7, dtype=torch.bfloat16), torch.zeros(2, H, 6))
+
+
+def test_verify_validation_before_launch():
+    """The verify entry points reject bad sizes, a missing table and an
+    unsupported filter length before touching any pointer."""
+    lib = _lib.lib()
+    n = None
+    args = lambda Q, K, starts, nreq: (n, 0, 0, 0, n, 0, 0, K, n, 0, 0, 0, n, 0, 0, n, 0, 0,  # noqa: E731
+                                       Q, starts, n, n, n, 0, nreq, 4, 64, 0, 8, n)
+    assert lib.evo2_fir_verify(*args(0, 128, n, 2)) == EVO2_ERR_INVALID      # Q = 0
+    assert b"bad sizes" in lib.evo2_last_error()
+    assert lib.evo2_fir_verify(*args(2, 128, n, 2)) == EVO2_ERR_INVALID      # null pointers
+    ok = ctypes.c_void_p(8)  # never dereferenced: validation fails first
+    full = (ok, 0, 0, 0, ok, 0, 0, 64, ok, 0, 0, 0, ok, 0, 0, ok, 0, 0, 1, n, n, n, ok, 0, 2, 4,
+            64, 0, 8, n)
+    assert lib.evo2_fir_verify(*full) == EVO2_ERR_UNSUPPORTED               # K = 64
+    assert b"7 or 128" in lib.evo2_last_error()
+    two = list(full)
+    two[7], two[18] = 128, 2                                                # Q=2 without tables
+    assert lib.evo2_fir_verify(*two) == EVO2_ERR_INVALID
+    assert b"Q=1" in lib.evo2_last_error()
+    iir = (ok, 0, 0, 1, ok, 16, 1, ok, 16, 1, ok, 0, 16, 1, ok, 0, 0, ok, 0, 0, 1, ok, n, n, ok,
+           0, 2, 4, 64, 0, 8, n)
+    assert lib.evo2_iir_verify(*iir) == EVO2_ERR_INVALID                     # starts without ends
+    assert b"go together" in lib.evo2_last_error()
+
+
+def test_verify_wrappers_check_metadata():
+    from evo2_flash_amd.verify import fir_snapshots
+
+    x = torch.zeros(3, 8)
+    meta = (torch.zeros(2, 3, dtype=torch.int32), torch.zeros(2, 4, dtype=torch.int32),
+            torch.zeros(2), torch.zeros(2), torch.ones(2))
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        fir_snapshots(x, torch.zeros(8, 7, dtype=torch.bfloat16), torch.zeros(4, 8, 6), meta)

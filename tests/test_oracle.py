@@ -18,7 +18,7 @@ from evo2_flash_amd.metadata import build_metadata, host_tables
 from evo2_flash_amd.state import HyenaStatePool, page_bytes
 from evo2_flash_amd.synthetic import mixer_params, random_slot_table
 
-from _cases import bf16_ulp_diff, decode_case, max_rel_err
+from _cases import bf16_ulp_diff, decode_case, max_rel_err, verify_case
 
 
 def _qsl(lens):
@@ -483,3 +483,131 @@ def test_random_slot_table_is_permutation_without_null():
     assert not torch.equal(s, torch.arange(1, 65, dtype=torch.int32))
     with pytest.raises(ValueError):
         random_slot_table(65, 65, seed=3)
+
+
+# ---------------------------------------------------------------- speculative verify
+def _verify_float64(kind, prm, x, state, meta):
+    """Each request's tokens run one by one in float64 from its source
+    snapshot: y per row, and the window / state after every token."""
+    ins, outs, starts, ends, accepted = meta
+    y = torch.zeros(x.shape, dtype=torch.float64)
+    snaps = {}
+    for r in range(ins.shape[0]):
+        src = int(ins[r, int(accepted[r]) - 1])
+        st = state[src].double().clone()
+        for pos in range(int(ends[r] - starts[r])):
+            t = int(starts[r]) + pos
+            xt = x[t].double()
+            if kind == "hcl":
+                st = st * torch.exp(prm["log_poles"][..., 0].double()) + xt[:, None]
+                y[t] = (prm["residues"].double() * st).sum(-1)
+            else:
+                K = prm["conv"].shape[-1]
+                w = prm["conv"].view(-1, K).double()
+                y[t] = (st * w[:, :-1]).sum(-1) + w[:, -1] * xt
+                st = torch.cat([st[:, 1:], xt[:, None]], dim=1)
+            snaps[(r, pos)] = st.clone()
+    return y, snaps
+
+
+@pytest.mark.parametrize("kind", ["hcs", "hcm", "hcl"])
+def test_verify_emulated_vs_float64(kind):
+    """Snapshots after every token, outputs on every covered row, nothing
+    written to the null block, to positions past a request's tokens or to
+    the source blocks."""
+    H, nreq, Q, nblk = 48, 5, 4, 60
+    prm, x, state, meta = verify_case(kind, H, nreq, Q, nblk, seed=31, x_dtype=torch.float32)
+    ins, outs, starts, ends, accepted = meta
+    y64, snaps = _verify_float64(kind, prm, x, state, meta)
+    st = state.clone()
+    if kind == "hcl":
+        poles = torch.exp(prm["log_poles"][..., 0].float())
+        y = oracle.iir_verify_emulated(x, poles, prm["residues"], st, *meta)
+        y2 = oracle.iir_decode_snapshots(x, poles, prm["residues"], state.clone(), *meta)
+        tol = 1e-5
+    else:
+        K = prm["conv"].shape[-1]
+        w = prm["conv"].view(H, K)
+        y = oracle.fir_verify_emulated(x, w, st, *meta)
+        y2 = oracle.fir_decode_snapshots(x, w, state.clone(), *meta)
+        tol = 1e-5
+    assert ((y.double() - y64).abs().max() / y64.abs().max()).item() <= tol
+    assert max_rel_err(y, y2) <= tol
+    written = set()
+    for (r, pos), s64 in snaps.items():
+        d = int(outs[r, pos])
+        if d == 0:
+            continue
+        written.add(d)
+        if kind == "hcl":
+            assert ((st[d].double() - s64).abs().max() / s64.abs().max()).item() <= 1e-5
+        else:
+            assert torch.equal(st[d].double(), s64)  # windows are copies of inputs
+    for b in range(nblk):
+        if b not in written:
+            assert torch.equal(st[b], state[b]), b
+
+
+@pytest.mark.parametrize("kind", ["hcs", "hcm", "hcl"])
+def test_verify_one_token_matches_decode_order(kind):
+    """The one-token form rounds to the fused decode step's inner value bit
+    for bit: both keep the same summation tree (triton_verifier.py:17-43,
+    128-131 against triton_decode.py:81-143)."""
+    from oracle import hyena_ref
+    H, B, nblk = 64, 6, 20
+    prm, x, state, _ = verify_case(kind, H, B, 1, nblk, seed=7)
+    slots = torch.randperm(nblk - 1)[:B].to(torch.int32)[:, None] + 1
+    st = state.clone()
+    if kind == "hcl":
+        poles = torch.exp(prm["log_poles"][..., 0].float())
+        y = oracle.iir_verify_emulated(x, poles, prm["residues"], st, slots, slots, None, None,
+                                       None)
+        for b in range(B):
+            s = state[int(slots[b])] * poles + x[b].float()[:, None]
+            r = s * prm["residues"]
+            r = r[:, :8] + r[:, 8:]
+            r = r[:, :4] + r[:, 4:]
+            r = r[:, :2] + r[:, 2:]
+            assert torch.equal(y[b].float(), oracle.bf((r[:, 0] + r[:, 1]) + 0.0))
+    else:
+        K = prm["conv"].shape[-1]
+        w = prm["conv"].view(H, K)
+        y = oracle.fir_verify_emulated(x, w, st, slots, slots, None, None, None)
+        summ = hyena_ref._hcm_sum if K == 128 else hyena_ref._hcs_sum
+        for b in range(B):
+            ref = summ(state[int(slots[b])].float(), w.float(), x[b].float())
+            assert torch.equal(y[b].float(), ref)
+
+
+@pytest.mark.parametrize("kind", ["hcm", "hcl"])
+def test_verify_equals_sequential_one_token_steps(kind):
+    """Q draft tokens in one verify step == Q one-token steps chained through
+    the snapshots (outputs and every snapshot, bit for bit)."""
+    H, Q, nblk = 32, 4, 20
+    prm, x, state, _ = verify_case(kind, H, 1, Q, nblk, seed=5, x_dtype=torch.float32)
+    ins = torch.tensor([[3, 4, 5, 6]], dtype=torch.int32)
+    outs = torch.tensor([[10, 11, 12, 13]], dtype=torch.int32)
+    meta = (ins, outs, torch.tensor([0]), torch.tensor([Q]), torch.tensor([2]))
+    s1, s2 = state.clone(), state.clone()
+    s2[10] = s2[4]   # the one-token chain starts from the accepted snapshot in place
+    if kind == "hcl":
+        poles = torch.exp(prm["log_poles"][..., 0].float())
+        y1 = oracle.iir_verify_emulated(x[:Q], poles, prm["residues"], s1, *meta)
+        steps = [oracle.iir_verify_emulated(x[p:p + 1], poles, prm["residues"], s2,
+                                            torch.tensor([[10 + max(p - 1, 0)]], dtype=torch.int32),
+                                            torch.tensor([[10 + p]], dtype=torch.int32),
+                                            None, None, None) for p in range(Q)]
+    else:
+        K = prm["conv"].shape[-1]
+        w = prm["conv"].view(H, K)
+        y1 = oracle.fir_verify_emulated(x[:Q], w, s1, *meta)
+        steps = []
+        for p in range(Q):
+            if p:
+                s2[10 + p] = s2[10 + p - 1]
+            steps.append(oracle.fir_verify_emulated(
+                x[p:p + 1], w, s2, torch.tensor([[10 + p]], dtype=torch.int32),
+                torch.tensor([[10 + p]], dtype=torch.int32), None, None, None))
+    assert torch.equal(y1, torch.cat(steps))
+    for p in range(Q):
+        assert torch.equal(s1[10 + p], s2[10 + p]), p
