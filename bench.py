@@ -11,12 +11,16 @@ Also measured in the same run and reported in the same JSON line:
   * prefill: the 27 mixer cores over one 32768-token sequence (fused
     featurizer + FIR / modal scan + gate per layer), tokens/s;
   * fp8: the e4m3 projection GEMMs M=8192, K=4096 -> N=12288 and N=4096,
-    TFLOP/s against the dense fp8 MFMA peak;
+    TFLOP/s against the dense fp8 MFMA peak, and the decode-sized in_proj
+    (M=64) against HBM;
+  * verify: the inner operators of a speculative verify step (64 requests
+    of 4 tokens, a state snapshot per token) against HBM;
   * roofline of the dominant decode kernel (hcm) from HIP events on the
     stream it is launched on, and the CPU baseline: the oracle's restatement
     of the reference torch decode path timed on the host cores.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--no-prefill] [--no-gemm]
+                    [--no-verify] [--only decode|verify|prefill|gemm|copy]
 """
 
 import argparse
@@ -217,6 +221,50 @@ def bench_decode(steps, warmup, dev, seed=1234):
             "mixer_frac": round(ideal_us / kern_us, 4)}
 
 
+# ---------------------------------------------------------------- speculative verify
+def bench_verify(reps, dev, H=H_7B, B=B_DECODE, Q=4, seed=9):
+    """The inner operators of a speculative verify step, 7B shape: B requests
+    of Q = 4 tokens (3 drafts) each, every request reading its accepted
+    snapshot and writing a snapshot per token.  Bytes per launch: the source
+    state and the Q snapshots (fp32), the token rows in and out (bf16 for
+    the FIRs, fp32 for LI as the mixers pass them), the parameters once."""
+    from evo2_flash_amd.synthetic import mixer_params
+    from evo2_flash_amd.verify import fir_snapshots, iir_snapshots
+
+    g = torch.Generator(device=dev).manual_seed(seed)
+    nblk = 2 * B * Q + 1
+    ins = (torch.randperm(B * Q, device=dev, generator=g) + 1).to(torch.int32).view(B, Q)
+    outs = (torch.randperm(B * Q, device=dev, generator=g) + 1 + B * Q).to(torch.int32).view(B, Q)
+    starts = torch.arange(B, device=dev, dtype=torch.int64) * Q
+    meta = (ins, outs, starts, starts + Q, torch.full((B,), 2, device=dev, dtype=torch.int64))
+    stream = torch.cuda.current_stream()
+    res = {}
+    for kind in ("hcs", "hcm", "hcl"):
+        prm = mixer_params(kind, H, seed, in_proj_fp8=False)
+        if kind == "hcl":
+            x = torch.randn(B * Q, H, generator=g, device=dev)
+            st = torch.randn(nblk, H, 16, generator=g, device=dev)
+            poles = prm["log_poles"][..., 0].to(dev).exp()
+            r = prm["residues"].to(dev)
+            fn = lambda x=x, st=st, poles=poles, r=r: iir_snapshots(x, poles, r, st, meta)  # noqa: E731
+            cols, xb, pbytes = 16, 4, 2 * H * 16 * 4
+        else:
+            K = prm["conv"].shape[-1]
+            x = torch.randn(B * Q, H, generator=g, device=dev).to(torch.bfloat16)
+            st = torch.randn(nblk, K - 1, H, generator=g, device=dev).transpose(1, 2)
+            w = prm["conv"].view(H, K).to(dev)
+            fn = lambda x=x, st=st, w=w: fir_snapshots(x, w, st, meta)  # noqa: E731
+            cols, xb, pbytes = K - 1, 2, H * K * 2
+        fn()
+        torch.cuda.synchronize()
+        avg, med = _timed(fn, reps, stream)
+        nbytes = B * (1 + Q) * H * cols * 4 + 2 * B * Q * H * xb + pbytes
+        res[kind] = {"avg_us": round(avg, 2), "median_us": round(med, 2), "bytes": nbytes,
+                     "achieved_GBs": round(nbytes / (avg * 1e-6) / 1e9, 1),
+                     "frac": round(nbytes / (avg * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    return {"requests": B, "tokens_per_request": Q, "per_kind": res}
+
+
 # ---------------------------------------------------------------- prefill
 def bench_prefill(reps, dev, L=L_PREFILL, H=H_7B, seed=77):
     """One fresh L-token sequence through one mixer core of each kind; the
@@ -360,7 +408,8 @@ def main(argv=None):
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill leg")
     ap.add_argument("--no-gemm", action="store_true", help="skip the fp8 GEMM leg")
-    ap.add_argument("--only", choices=["decode", "prefill", "gemm", "copy"], default=None,
+    ap.add_argument("--no-verify", action="store_true", help="skip the speculative verify leg")
+    ap.add_argument("--only", choices=["decode", "verify", "prefill", "gemm", "copy"], default=None,
                     help="run one leg only (for profiling); `copy` runs a plain 1 GiB "
                          "device copy, the reference dispatch for scaling HBM counters")
     args = ap.parse_args(argv)
@@ -378,6 +427,7 @@ def main(argv=None):
         return 0
     run = lambda leg, flag: (args.only == leg) or (args.only is None and not flag)  # noqa: E731
     dec = bench_decode(args.steps, args.warmup, dev) if run("decode", False) else None
+    ver = bench_verify(max(8, args.steps // 2), dev) if run("verify", args.no_verify) else None
     pre = bench_prefill(max(3, args.steps // 8), dev) if run("prefill", args.no_prefill) else None
     gem = bench_gemm(max(5, args.steps // 4), dev) if run("gemm", args.no_gemm) else None
     cpu = None if (args.no_cpu or args.only) else _cpu_baseline_decode()
@@ -407,6 +457,8 @@ def main(argv=None):
                             "frac": hcm["frac"],
                             "traffic": profiled_traffic(DECODE_ROOFLINE_KERNEL)}
         line["decode"] = dec
+    if ver:
+        line["verify"] = ver
     if pre:
         line["prefill"] = pre
     if gem:
