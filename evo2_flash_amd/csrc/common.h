@@ -25,6 +25,18 @@ __device__ __forceinline__ bf16_t f2bf(float x) {
 // Round fp32 to bf16 and back: the value a bf16 torch tensor would hold.
 __device__ __forceinline__ float rbf(float x) { return bf2f(f2bf(x)); }
 
+// The same rounding in one instruction: v_cvt_pk_bf16_f32 with the value in
+// the high half and 0 in the low half is already that fp32 (the compiler's
+// form is a cvt plus a shift or permute).  Inline asm is invisible to the
+// compiler's hazard recognizer, so x must come from an ordinary VALU op (add,
+// mul, fma, cvt, logic): a DOT, MFMA or transcendental result needs wait states
+// before another instruction may read it, and none would be inserted here.
+__device__ __forceinline__ float rbf_valu(float x) {
+  float r;
+  asm("v_cvt_pk_bf16_f32 %0, 0, %1" : "=v"(r) : "v"(x));
+  return r;
+}
+
 __device__ __forceinline__ float lo_bf(uint32_t packed) {
   return __uint_as_float(packed << 16);
 }
@@ -37,6 +49,18 @@ typedef __attribute__((ext_vector_type(2))) __bf16 bf16v2_t;
 __device__ __forceinline__ uint32_t pack_bf(float lo, float hi) {
   bf16v2_t v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
   return __builtin_bit_cast(uint32_t, v);
+}
+
+// a.lo * b.lo + a.hi * b.hi + c over bf16 pairs (v_dot2_f32_bf16): both
+// products are exact in fp32.
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16v2_t, a),
+                                         __builtin_bit_cast(bf16v2_t, b), c, false);
+}
+
+// Two bf16 values (lo = older row) in one dword.
+__device__ __forceinline__ uint32_t pair_bf(bf16_t lo, bf16_t hi) {
+  return static_cast<uint32_t>(lo) | (static_cast<uint32_t>(hi) << 16);
 }
 
 // ---------------------------------------------------------------- host side

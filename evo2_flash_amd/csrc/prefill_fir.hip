@@ -10,12 +10,14 @@
 // rows of one segment (tile table [segment, first row], as
 // mixers.py:386-415 builds it).  It sweeps the tile in 64-row sub-tiles:
 //   produce: each wave turns 16 rows into u (and x2) for its 64 channels and
-//            writes them into an LDS ring, u[channel][row mod RING];
+//            writes them into an LDS ring, u[channel][row mod RING]; the
+//            short filter runs as v_dot2 over (z[t-1], z[t]) row pairs;
 //   FIR:     each lane computes 16 consecutive outputs of its channel from
 //            the ring as bf16 pairs with v_dot2c_f32_bf16 (u and the taps are
-//            bf16, so every product is exact in fp32).  Outputs at odd offsets
-//            use pairs re-aligned by one element (one alignbit per tap pair
-//            per 16 outputs); the channel's taps stay in VGPRs for the tile.
+//            bf16, so every product is exact in fp32).  The ring's pairs start
+//            at even rows; outputs whose window starts at an odd row use the
+//            taps paired the other way, so no pair is ever re-aligned; the
+//            channel's taps stay in VGPRs for the tile.
 // The ring holds the K-1 rows of history the next sub-tile needs, so each
 // z row is read from HBM once per tile plus a (K-1)-row halo per tile.
 //
@@ -28,13 +30,6 @@
 #include "featurize.h"
 
 namespace evo2 {
-
-typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
-
-__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
-                                         __builtin_bit_cast(bf16x2_t, b), c, false);
-}
 
 struct FirArgs {
   const bf16_t *x; int64_t sx;              // z (FUSED) or u rows
@@ -59,8 +54,10 @@ struct FirGeom {
   // rows per sub-tile: 64 for hcm; 32 for hcs, whose smaller staging lets
   // more workgroups share a CU (its time goes to memory, not arithmetic)
   static constexpr int RS = K > 8 ? 64 : 32;
-  static constexpr int RW = RS / 4;        // rows per wave per sub-tile
-  static constexpr int NE = NP + RW / 2;   // pairs in one wave's window
+  static constexpr int NWAVE = 4;          // waves per workgroup
+  static constexpr int NT = 64 * NWAVE;    // threads per workgroup
+  static constexpr int RW = RS / NWAVE;    // rows per wave per sub-tile
+  static_assert(RW % 8 == 0, "produce and the epilogue work in 8-row groups");
   static constexpr int RING = (KP + RS <= 64) ? 64 : (KP + RS <= 128) ? 128 : 256;
   // Row pitches are 4 or 36 dwords mod 64 banks, so the 16 lanes a b128
   // access serves per cycle cover all banks once.
@@ -92,7 +89,7 @@ __device__ __forceinline__ SegInfo seg_of_tile(const FirArgs &p) {
 
 
 template <int K, bool HAS_D, bool FUSED>
-__global__ __launch_bounds__(256) void fir_prefill_kernel(FirArgs p) {
+__global__ __launch_bounds__(FirGeom<K>::NT) void fir_prefill_kernel(FirArgs p) {
   using G = FirGeom<K>;
   __shared__ __align__(16) bf16_t ring[64][G::PITCH];
   __shared__ __align__(16) bf16_t x2s[FUSED ? 64 : 1][G::XPITCH];
@@ -137,12 +134,19 @@ __global__ __launch_bounds__(256) void fir_prefill_kernel(FirArgs p) {
       W[m] = lo | (hi << 16);
     }
   }
-  float wsf[3][3];
+  // Even rows read the window pairs shifted by one element against the odd
+  // rows, so they take the taps re-paired the other way,
+  // V[m] = (w'[2m-1], w'[2m]) with w'[-1] = w'[KP] = 0 (NP + 1 pairs), and
+  // no window pair is ever re-aligned.
+  uint32_t V[G::NP + 1];
+  V[0] = W[0] << 16;
+#pragma unroll
+  for (int m = 1; m < G::NP; ++m) V[m] = __builtin_amdgcn_alignbit(W[m], W[m - 1], 16);
+  V[G::NP] = W[G::NP - 1] >> 16;
+  ShortTaps wsp[3];
   if constexpr (FUSED) {
 #pragma unroll
-    for (int i = 0; i < 3; ++i)
-#pragma unroll
-      for (int j = 0; j < 3; ++j) wsf[i][j] = bf2f(p.ws[(3 * (int64_t)cl + i) * 3 + j]);
+    for (int i = 0; i < 3; ++i) wsp[i] = short_taps(p.ws, 3 * (int64_t)cl + i);
   }
   const float *stc = S.init ? p.st + S.blk * p.st0 + (int64_t)cl * p.st1 : nullptr;
   const bool vec_z = FUSED && (c0 + 64 <= p.H) && (p.sx % 8 == 0) &&
@@ -160,34 +164,29 @@ __global__ __launch_bounds__(256) void fir_prefill_kernel(FirArgs p) {
   // past the tile end keep stale (finite) values; only discarded rows read them.
   constexpr int ZCH = G::ZROWS * 24;             // 16-byte chunks per tile
   constexpr int ZW = (ZCH + 63) / 64;            // wave instructions per tile
-  // Lane offsets of the staged chunks are fixed for the kernel: wave
-  // instruction j moves chunks i = (wave + 4j) * 64 + lane, i.e. row i / 24,
-  // column i % 24 of the (ZROWS x 192) tile.  zoff[j] is that chunk's element
-  // offset from the tile's first row (-1 past the tile); interior sub-tiles
-  // (no row before the segment or past the tile end) skip the row checks.
-  constexpr int NJ = (ZW + 3) / 4;
-  int zoff[NJ];
-#pragma unroll
-  for (int j = 0; j < NJ; ++j) {
-    const int i = (wave + 4 * j) * 64 + lane;
-    zoff[j] = i < ZCH ? (i / 24) * static_cast<int>(p.sx) + 3 * c0 + 8 * (i % 24) : -1;
-  }
+  // Wave instruction j moves chunks i = (wave + NWAVE j) * 64 + lane, i.e.
+  // row i / 24, column i % 24 of the (ZROWS x 192) tile, at element offset
+  // (i / 24) * sx + 3 c0 + 8 (i % 24) from the tile's first row.  The offsets
+  // are recomputed per sub-tile (a few VALU) rather than held in registers.
+  // Interior sub-tiles (no row before the segment or past the tile end) skip
+  // the row checks.
+  constexpr int NJ = (ZW + G::NWAVE - 1) / G::NWAVE;
   auto prefetch = [&](int rs) {
     if (!vec_z) return;
     const bf16_t *base = p.x + (int64_t)rs * p.sx;
     const bool interior = rs >= S.a && rs + G::ZROWS <= S.t_end;  // uniform
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
-      const int cw = wave + 4 * j;  // wave-uniform
+      const int cw = wave + G::NWAVE * j;  // wave-uniform
       if (cw >= ZW) break;
-      bool ok = zoff[j] >= 0;
-      if (!interior) {
-        const int t = rs + ((cw * 64 + lane) / 24);
-        ok = ok && t >= S.a && t < S.t_end;
-      }
+      const int i = cw * 64 + lane;
+      const int row = i / 24;
+      bool ok = i < ZCH;
+      if (!interior) ok = ok && rs + row >= S.a && rs + row < S.t_end;
       if (ok)
         __builtin_amdgcn_global_load_lds(
-            reinterpret_cast<const uint4 *>(base + zoff[j]),
+            reinterpret_cast<const uint4 *>(base + row * static_cast<int>(p.sx) + 3 * c0 +
+                                            8 * (i - 24 * row)),
             (__attribute__((address_space(3))) void *)(&zst[0][0] + cw * 512), 16, 0, 0);
     }
   };
@@ -195,7 +194,7 @@ __global__ __launch_bounds__(256) void fir_prefill_kernel(FirArgs p) {
     const bf16_t *conv = S.init ? p.cs + S.blk * p.cs0 : nullptr;
     if (vec_z && rs >= S.a) return;  // uniform: nothing to patch
 #pragma unroll 1
-    for (int i = threadIdx.x; i < ZCH; i += 256) {
+    for (int i = threadIdx.x; i < ZCH; i += G::NT) {
       const int row = i / 24, col = i - 24 * (i / 24);
       const int t = rs + row;
       const bool inside = t >= S.a && t < S.t_end;
@@ -227,8 +226,9 @@ __global__ __launch_bounds__(256) void fir_prefill_kernel(FirArgs p) {
       if constexpr (FUSED) {
         float y3[3];
         for (int i = 0; i < 3; ++i)
-          y3[i] = short_out(bf2f(zst[t - 2 - rs][3 * lane + i]), bf2f(zst[t - 1 - rs][3 * lane + i]),
-                            bf2f(zst[t - rs][3 * lane + i]), wsf[i]);
+          y3[i] = short_dot_rbf(pair_bf(zst[t - 2 - rs][3 * lane + i], zst[t - 1 - rs][3 * lane + i]),
+                                pair_bf(zst[t - 1 - rs][3 * lane + i], zst[t - rs][3 * lane + i]),
+                                wsp[i]);
         x2 = y3[0];
         u = rbf(y3[1] * y3[2]);
       } else {
@@ -253,32 +253,24 @@ __global__ __launch_bounds__(256) void fir_prefill_kernel(FirArgs p) {
     }
     uint32_t upk[NR / 2], xpk[NR / 2];
     if constexpr (FUSED) {
+      // Eight rows at a time from the row pairs (z[k], z[k+1]) of each
+      // sub-channel: staged rows rb + 8g - 2 .. rb + 8g + 8.
       const int rb = r0 - rs;
-      float zm2[3], zm1[3];
 #pragma unroll
-      for (int i = 0; i < 3; ++i) {
-        zm2[i] = bf2f(zst[rb - 2][3 * lane + i]);
-        zm1[i] = bf2f(zst[rb - 1][3 * lane + i]);
-      }
+      for (int g = 0; g < NR / 8; ++g) {
+        uint32_t P[9][3];
 #pragma unroll
-      for (int r = 0; r < NR; r += 2) {
-        float y[2][3];
+        for (int k = 0; k < 9; ++k)
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
+          for (int i = 0; i < 3; ++i)
+            P[k][i] = pair_bf(zst[rb + 8 * g - 2 + k][3 * lane + i], zst[rb + 8 * g - 1 + k][3 * lane + i]);
 #pragma unroll
-          for (int i = 0; i < 3; ++i) {
-            const float z0 = bf2f(zst[rb + r + q][3 * lane + i]);
-            float acc = wsf[i][0] * zm2[i];
-            acc = fmaf(wsf[i][1], zm1[i], acc);
-            y[q][i] = fmaf(wsf[i][2], z0, acc);
-            zm2[i] = zm1[i];
-            zm1[i] = z0;
-          }
+        for (int r = 0; r < 8; r += 2) {
+          float y0[3], y1[3];  // (x2, x1, v) of rows r and r + 1, rounded
+          short_rows2(P[r], P[r + 1], P[r + 2], wsp, y0, y1);
+          upk[4 * g + r / 2] = pack_bf(y0[1] * y0[2], y1[1] * y1[2]);
+          xpk[4 * g + r / 2] = pack_bf(y0[0], y1[0]);
         }
-        const uint32_t px1 = pack_bf(y[0][1], y[1][1]);
-        const uint32_t pv = pack_bf(y[0][2], y[1][2]);
-        upk[r / 2] = pack_bf(lo_bf(px1) * lo_bf(pv), hi_bf(px1) * hi_bf(pv));
-        xpk[r / 2] = pack_bf(y[0][0], y[1][0]);
       }
     } else {
       const bf16_t *xp = p.x + (int64_t)r0 * p.sx + cl;
@@ -345,13 +337,13 @@ __global__ __launch_bounds__(256) void fir_prefill_kernel(FirArgs p) {
 
     // ---- FIR for rows s0 + 16*wave + r, r < 16
     const int pbase = (s0 - S.t0) + wave * G::RW;  // ring pos of row base
-    // Tap pairs are consumed in order m = 0..NP-1.  At step m, row r reads
-    // window pair E[m + r/2 + 1] (odd r) or the pair re-aligned by one,
-    // O[m + r/2] = alignbit(E[m + r/2 + 1], E[m + r/2]) (even r); the eight
-    // O values in use slide by one per step, so each costs one alignbit.  The
-    // window is loaded per 16-step quarter and the steps are fenced in order,
-    // which keeps the live set to one quarter (otherwise the compiler runs
-    // each accumulator's whole chain in turn and holds the whole window).
+    // Tap pairs are consumed in order m = 0..NP-1.  At step m, odd row
+    // r = 2j+1 reads window pair E[m + j + 1] against W[m], even row r = 2j
+    // reads E[m + j] against V[m], and the even rows take one more step,
+    // E[NP + j] against V[NP].  The window is loaded per 16-step quarter and
+    // the steps are fenced in order, which keeps the live set to one quarter
+    // (otherwise the compiler runs each accumulator's whole chain in turn and
+    // holds the whole window).
     constexpr int MQ = G::NP >= 16 ? 16 : G::NP;  // tap pairs per quarter
     constexpr int EQ = MQ + G::RW / 2;            // window pairs per quarter
     static_assert(EQ % 4 == 0, "window quarters are whole b128 loads");
@@ -367,24 +359,22 @@ __global__ __launch_bounds__(256) void fir_prefill_kernel(FirArgs p) {
             &ring[lane][(pbase + 2 * m0 + 8 * q) & (G::RING - 1)]);
         E[4 * q] = v.x; E[4 * q + 1] = v.y; E[4 * q + 2] = v.z; E[4 * q + 3] = v.w;
       }
-      uint32_t O[G::RW / 2];
-#pragma unroll
-      for (int j = 0; j < G::RW / 2 - 1; ++j) O[j] = __builtin_amdgcn_alignbit(E[j + 1], E[j], 16);
 #pragma unroll
       for (int m = 0; m < MQ; ++m) {
-        O[G::RW / 2 - 1] = __builtin_amdgcn_alignbit(E[m + G::RW / 2], E[m + G::RW / 2 - 1], 16);
-        const uint32_t wm = W[m0 + m];
+        const uint32_t wm = W[m0 + m], vm = V[m0 + m];
 #pragma unroll
         for (int j = 0; j < G::RW / 2; ++j) {
-          acc[2 * j] = dot2(O[j], wm, acc[2 * j]);
+          acc[2 * j] = dot2(E[m + j], vm, acc[2 * j]);
           acc[2 * j + 1] = dot2(E[m + j + 1], wm, acc[2 * j + 1]);
         }
-#pragma unroll
-        for (int j = 0; j < G::RW / 2 - 1; ++j) O[j] = O[j + 1];
         // Empty volatile asm on every accumulator: volatile statements keep
         // their order, so step m+1 cannot start before step m is done.
 #pragma unroll
         for (int r = 0; r < G::RW; ++r) asm volatile("" : "+v"(acc[r]));
+      }
+      if (m0 + MQ == G::NP) {
+#pragma unroll
+        for (int j = 0; j < G::RW / 2; ++j) acc[2 * j] = dot2(E[MQ + j], V[G::NP], acc[2 * j]);
       }
     }
 
@@ -407,15 +397,18 @@ __global__ __launch_bounds__(256) void fir_prefill_kernel(FirArgs p) {
     bf16_t *orow = obase + (int64_t)trow * p.so;
 #pragma unroll
     for (int r = 0; r < G::RW; r += 2, orow += 2 * p.so) {
-      uint32_t py = pack_bf(acc[r], acc[r + 1]);
+      uint32_t py;
       if constexpr (FUSED) {
+        float y0 = rbf(acc[r]), y1 = rbf(acc[r + 1]);
         if constexpr (HAS_D) {
           const uint32_t pu = uq[r / 2];
-          const uint32_t pd = pack_bf(dval * lo_bf(pu), dval * hi_bf(pu));
-          py = pack_bf(lo_bf(py) + lo_bf(pd), hi_bf(py) + hi_bf(pd));
+          y0 = rbf_valu(y0 + rbf_valu(dval * lo_bf(pu)));
+          y1 = rbf_valu(y1 + rbf_valu(dval * hi_bf(pu)));
         }
         const uint32_t px = xq[r / 2];
-        py = pack_bf(lo_bf(px) * lo_bf(py), hi_bf(px) * hi_bf(py));
+        py = pack_bf(lo_bf(px) * y0, hi_bf(px) * y1);
+      } else {
+        py = pack_bf(acc[r], acc[r + 1]);
       }
       // py = (row r, row r+1) of channel c
       const uint32_t nb = __shfl_xor(py, 1);
@@ -549,7 +542,7 @@ __global__ __launch_bounds__(256) void window_update_kernel(WinArgs p) {
 template <int K, bool HAS_D, bool FUSED>
 static void launch_fir(const FirArgs &a, int64_t ntiles, hipStream_t st) {
   dim3 grid(static_cast<unsigned>(ntiles), static_cast<unsigned>(cdiv(a.H, 64)));
-  hipLaunchKernelGGL((fir_prefill_kernel<K, HAS_D, FUSED>), grid, dim3(256), 0, st, a);
+  hipLaunchKernelGGL((fir_prefill_kernel<K, HAS_D, FUSED>), grid, dim3(FirGeom<K>::NT), 0, st, a);
 }
 
 static int launch_window(const WinArgs &w, int K, int64_t nseq, hipStream_t st) {

@@ -79,11 +79,9 @@ __global__ __launch_bounds__(256) void hcl_scan_kernel(HclArgs p) {
   const int t_end = min(t0 + p.block_t, e);
   if (t0 >= t_end) return;  // uniform
 
-  float wsf[3][3];
+  ShortTaps wsp[3];
 #pragma unroll
-  for (int i = 0; i < 3; ++i)
-#pragma unroll
-    for (int j = 0; j < 3; ++j) wsf[i][j] = bf2f(p.ws[(3 * (int64_t)cl + i) * 3 + j]);
+  for (int i = 0; i < 3; ++i) wsp[i] = short_taps(p.ws, 3 * (int64_t)cl + i);
   float pole[16], res[16], s[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
@@ -150,38 +148,35 @@ __global__ __launch_bounds__(256) void hcl_scan_kernel(HclArgs p) {
     const bf16_t(*zst)[HCL_ZPITCH] = decltype(buf)::value ? zs1 : zs0;
     constexpr bool FULL = decltype(full)::value;
     const int nr = FULL ? HCL_RS : min(HCL_RS, t_end - s0);
-    float zm2[3], zm1[3];
+    // Row pairs (z[k], z[k+1]) of each sub-channel over the staged rows; rows
+    // past the tile end hold stale values that only discarded rows read.
+    uint32_t P[HCL_RS + 1][3];
 #pragma unroll
-    for (int i = 0; i < 3; ++i) {
-      zm2[i] = bf2f(zst[0][3 * tid + i]);
-      zm1[i] = bf2f(zst[1][3 * tid + i]);
-    }
+    for (int k = 0; k <= HCL_RS; ++k)
+#pragma unroll
+      for (int i = PHASE == 3 ? 0 : 1; i < 3; ++i)
+        P[k][i] = pair_bf(zst[k][3 * tid + i], zst[k + 1][3 * tid + i]);
     uint32_t gpk[HCL_RS / 2];
 #pragma unroll
     for (int r = 0; r < HCL_RS; r += 2) {
       float ypair[2] = {0.f, 0.f}, upair[2], x2pair[2];
-      float yv[2][3];
-#pragma unroll
-      for (int q = 0; q < 2; ++q) {
-#pragma unroll
-        for (int i = 0; i < 3; ++i) {
-          const float z0 = bf2f(zst[r + q + 2][3 * tid + i]);
-          float acc = wsf[i][0] * zm2[i];
-          acc = fmaf(wsf[i][1], zm1[i], acc);
-          yv[q][i] = fmaf(wsf[i][2], z0, acc);
-          zm2[i] = zm1[i];
-          zm1[i] = z0;
-        }
+      if constexpr (PHASE == 3) {
+        float y0[3], y1[3];  // (x2, x1, v) of rows r and r + 1, rounded
+        short_rows2(P[r], P[r + 1], P[r + 2], wsp, y0, y1);
+        x2pair[0] = y0[0];
+        x2pair[1] = y1[0];
+        upair[0] = rbf_valu(y0[1] * y0[2]);
+        upair[1] = rbf_valu(y1[1] * y1[2]);
+      } else {  // the end states need only u
+        const uint32_t Pa[2] = {P[r][1], P[r][2]}, Pb[2] = {P[r + 1][1], P[r + 1][2]},
+                       Pc[2] = {P[r + 2][1], P[r + 2][2]};
+        const ShortTaps w12[2] = {wsp[1], wsp[2]};
+        float y0[2], y1[2];  // (x1, v) of rows r and r + 1, rounded
+        short_rows2(Pa, Pb, Pc, w12, y0, y1);
+        upair[0] = rbf_valu(y0[0] * y0[1]);
+        upair[1] = rbf_valu(y1[0] * y1[1]);
+        x2pair[0] = x2pair[1] = 0.0f;
       }
-      // bf16 roundings two rows at a time: one packed conversion per pair
-      const uint32_t px1 = pack_bf(yv[0][1], yv[1][1]);
-      const uint32_t pv = pack_bf(yv[0][2], yv[1][2]);
-      const uint32_t pu = pack_bf(lo_bf(px1) * lo_bf(pv), hi_bf(px1) * hi_bf(pv));
-      const uint32_t px2 = pack_bf(yv[0][0], yv[1][0]);
-      upair[0] = lo_bf(pu);
-      upair[1] = hi_bf(pu);
-      x2pair[0] = lo_bf(px2);
-      x2pair[1] = hi_bf(px2);
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
         if (FULL || r + q < nr) {  // uniform
@@ -199,10 +194,9 @@ __global__ __launch_bounds__(256) void hcl_scan_kernel(HclArgs p) {
       }
       if constexpr (PHASE == 3) {
         // g = bf16(bf16(bf16(y) + bf16(u D)) x2) for both rows
-        const uint32_t py = pack_bf(ypair[0], ypair[1]);
-        const uint32_t pd = pack_bf(upair[0] * dval, upair[1] * dval);
-        const uint32_t ps = pack_bf(lo_bf(py) + lo_bf(pd), hi_bf(py) + hi_bf(pd));
-        gpk[r / 2] = pack_bf(x2pair[0] * lo_bf(ps), x2pair[1] * hi_bf(ps));
+        const float s0r = rbf_valu(rbf_valu(ypair[0]) + rbf_valu(upair[0] * dval));
+        const float s1r = rbf_valu(rbf_valu(ypair[1]) + rbf_valu(upair[1] * dval));
+        gpk[r / 2] = pack_bf(x2pair[0] * s0r, x2pair[1] * s1r);
       }
     }
     if constexpr (PHASE == 3) {
