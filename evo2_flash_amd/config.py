@@ -1,8 +1,27 @@
 """The Hyena fields of StripedHyena2Config (evo2_flash/config.py:6-205) that
-the mixer path reads, and the layer maps of the released model sizes
-(evo2_flash/evo2_configs/evo2-{1b-8k,7b-1m,40b-1m}.yml)."""
+the mixer path reads, the validation the reference applies to them when a
+converted checkpoint's config.json is loaded (config.py:95-170), and the layer
+maps of the released model sizes (evo2_flash/evo2_configs/
+evo2-{1b-8k,7b-1m,40b-1m}.yml)."""
 
-from dataclasses import dataclass, field
+from dataclasses import dataclass, field, fields
+
+# The selective fp8 marker a converted checkpoint carries when its Hyena
+# in_proj weights are e4m3 (convert.py:631-642); config.py:137-147 accepts
+# exactly these values.
+FP8_RUNTIME = "vllm_fp8_static_w8a8_v1"
+FP8_META_FILENAME = "metadata/hyena_in_proj_fp8_meta.safetensors"
+FP8_MARKER = {
+    "required": True,
+    "runtime": FP8_RUNTIME,
+    "format": "e4m3fn",
+    "fp8_max": 448,
+    "scale_scheme": "per_tensor_static",
+    "scale_convention": "dequantization",
+    "input_scale_source": "scale_inv_fwd[0]",
+    "weight_scale_source": "scale_inv_fwd[1]",
+    "metadata_file": FP8_META_FILENAME,
+}
 
 
 @dataclass
@@ -22,6 +41,85 @@ class HyenaConfig:
     state_size: int = 16
     rms_norm_eps: float = 1e-6
     use_fp8_input_projections: bool = False
+    hyena_in_proj_fp8: dict = None
+    # FP8 surgery output (config.py:73-112): layer 0's in_proj as a (vocab, 3H)
+    # token table; the Hopper-emulated layers and channels are not built here.
+    hyena_token_table_layers: list = field(default_factory=list)
+    hyena_fp8_emulated_layers: list = field(default_factory=list)
+    hyena_fp8_emulated_channels: dict = field(default_factory=dict)
+    fp8_surgery: dict = None
+    # Layout conventions the converter records (convert.py:611-616); the mixer
+    # kernels implement the released values only.
+    conv_kernels_pre_flipped: bool = True
+    interleave: bool = True
+    column_split_hyena: bool = False
+    hyena_flip_x1x2: bool = False
+    tie_word_embeddings: bool = True
+
+    @classmethod
+    def from_dict(cls, d):
+        """A config from a converted checkpoint's config.json contents, with
+        the reference's checks (config.py:95-170) and this build's limits;
+        raises ValueError (bad or inconsistent metadata, as the reference) or
+        NotImplementedError (a valid layout this build does not run)."""
+        names = {f.name for f in fields(cls)}
+        kw = {k: v for k, v in d.items() if k in names}
+        for k in ("attn_layer_idxs", "hcs_layer_idxs", "hcm_layer_idxs", "hcl_layer_idxs",
+                  "hyena_token_table_layers", "hyena_fp8_emulated_layers"):
+            kw[k] = [int(i) for i in (kw.get(k) or [])]
+        kw["hyena_fp8_emulated_channels"] = {
+            int(k): int(v) for k, v in (kw.get("hyena_fp8_emulated_channels") or {}).items()}
+        cfg = cls(**kw)
+        cfg.validate(quantization_config=d.get("quantization_config"))
+        return cfg
+
+    def validate(self, quantization_config=None):
+        hyena = set(self.hcs_layer_idxs) | set(self.hcm_layer_idxs) | set(self.hcl_layer_idxs)
+        kinds = [set(self.attn_layer_idxs), set(self.hcs_layer_idxs), set(self.hcm_layer_idxs),
+                 set(self.hcl_layer_idxs)]
+        covered = set().union(*kinds)
+        if sum(len(k) for k in kinds) != len(covered) or covered != set(range(self.num_hidden_layers)):
+            raise ValueError("layer-type lists must partition range(num_hidden_layers)")
+        if self.use_fp8_input_projections:
+            marker = self.hyena_in_proj_fp8
+            if not isinstance(marker, dict):
+                raise ValueError("use_fp8_input_projections=True requires converter-exported "
+                                 "hyena_in_proj_fp8 metadata; reconvert the source checkpoint")
+            bad = {k: marker.get(k) for k, v in FP8_MARKER.items() if marker.get(k) != v}
+            if bad:
+                raise ValueError(f"unsupported or incomplete hyena_in_proj_fp8 metadata: {bad}")
+            if marker.get("num_layers") != len(hyena):
+                raise ValueError("hyena_in_proj_fp8 num_layers does not match the layer map: "
+                                 f"{marker.get('num_layers')} != {len(hyena)}")
+            if quantization_config is not None:
+                raise ValueError("FP8 Hyena projections use the selective static-W8A8 runtime; "
+                                 "an embedded global quantization_config is unsupported")
+        elif self.hyena_in_proj_fp8 is not None:
+            raise ValueError("hyena_in_proj_fp8 metadata is present while "
+                             "use_fp8_input_projections=False")
+        if self.hyena_token_table_layers:
+            if self.hyena_token_table_layers != [0]:
+                raise ValueError("hyena_token_table_layers may only be [0]: only layer 0's "
+                                 "projection input depends on the token alone, got "
+                                 f"{self.hyena_token_table_layers}")
+            if 0 in self.attn_layer_idxs:
+                raise ValueError("layer 0 is attention; a token table needs Hyena")
+            if self.use_fp8_input_projections:
+                raise ValueError("hyena_token_table_layers is the output of FP8 surgery and "
+                                 "cannot be combined with use_fp8_input_projections=True")
+            if not isinstance(self.fp8_surgery, dict):
+                raise ValueError("token-table checkpoints must carry fp8_surgery provenance")
+        if self.hyena_fp8_emulated_layers or self.hyena_fp8_emulated_channels:
+            raise NotImplementedError(
+                "hyena_fp8_emulated_layers / hyena_fp8_emulated_channels model Hopper's fp8 "
+                "fast accumulation in software; this build's fp8 GEMM accumulates in fp32")
+        if not self.conv_kernels_pre_flipped:
+            raise NotImplementedError("conv kernels must be in cross-correlation order "
+                                      "(conv_kernels_pre_flipped=True)")
+        if not self.interleave or self.column_split_hyena or self.hyena_flip_x1x2:
+            raise NotImplementedError("only the interleaved (x2, x1, v) in_proj layout of the "
+                                      "released checkpoints is supported")
+        return self
 
     def layer_kind(self, i):
         """"attn" | "hcs" | "hcm" | "hcl" (config.py:190-199)."""
@@ -43,30 +141,37 @@ class HyenaConfig:
         return [i for i in range(self.num_hidden_layers) if self.layer_kind(i) != "attn"]
 
 
+def _with_marker(cfg):
+    """Attach the fp8 marker the converter writes for an fp8 model (convert.py:631-642)."""
+    if cfg.use_fp8_input_projections:
+        cfg.hyena_in_proj_fp8 = dict(FP8_MARKER, num_layers=len(cfg.hyena_layers()))
+    return cfg.validate()
+
+
 def evo2_1b():
     """evo2-1b-8k.yml:4-17, 21, 30."""
-    return HyenaConfig(
+    return _with_marker(HyenaConfig(
         hidden_size=1920, num_hidden_layers=25, num_attention_heads=15, intermediate_size=5120,
         attn_layer_idxs=[3, 10, 17, 24], hcl_layer_idxs=[2, 6, 9, 13, 16, 20, 23],
         hcm_layer_idxs=[1, 5, 8, 12, 15, 19, 22], hcs_layer_idxs=[0, 4, 7, 11, 14, 18, 21],
-        use_fp8_input_projections=True)
+        use_fp8_input_projections=True))
 
 
 def evo2_7b():
     """evo2-7b-1m.yml:4-17, 21, 32."""
-    return HyenaConfig(
+    return _with_marker(HyenaConfig(
         hidden_size=4096, num_hidden_layers=32, num_attention_heads=32, intermediate_size=11264,
         attn_layer_idxs=[3, 10, 17, 24, 31], hcl_layer_idxs=[2, 6, 9, 13, 16, 20, 23, 27, 30],
         hcm_layer_idxs=[1, 5, 8, 12, 15, 19, 22, 26, 29],
-        hcs_layer_idxs=[0, 4, 7, 11, 14, 18, 21, 25, 28], use_fp8_input_projections=True)
+        hcs_layer_idxs=[0, 4, 7, 11, 14, 18, 21, 25, 28], use_fp8_input_projections=True))
 
 
 def evo2_40b():
     """evo2-40b-1m.yml:4-16, 20, 31 (attention at 3, 10, 17, 24, 31, 35, 42, 49)."""
-    return HyenaConfig(
+    return _with_marker(HyenaConfig(
         hidden_size=8192, num_hidden_layers=50, num_attention_heads=64, intermediate_size=22528,
         attn_layer_idxs=[3, 10, 17, 24, 31, 35, 42, 49],
         hcl_layer_idxs=[2, 6, 9, 13, 16, 20, 23, 27, 30, 34, 38, 41, 45, 48],
         hcm_layer_idxs=[1, 5, 8, 12, 15, 19, 22, 26, 29, 33, 37, 40, 44, 47],
         hcs_layer_idxs=[0, 4, 7, 11, 14, 18, 21, 25, 28, 32, 36, 39, 43, 46],
-        use_fp8_input_projections=True)
+        use_fp8_input_projections=True))

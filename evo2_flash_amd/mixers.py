@@ -82,6 +82,15 @@ class Linear(nn.Module):
         return torch.nn.functional.linear(x, self.weight, self.bias), None
 
 
+class ProjectionTap(nn.Module):
+    """Parameter-free stand-in for in_proj when the projection is a token
+    table (FP8-surgery layer 0, mixers.py:681-688): returns (z, None) like a
+    linear, so a hook on `in_proj` still sees the projection output."""
+
+    def forward(self, z):
+        return z, None
+
+
 # ---------------------------------------------------------------- mixers
 class HyenaMixerBase(nn.Module):
     """Shared front half: in_proj, the stateful short filter, the paged state
@@ -98,9 +107,18 @@ class HyenaMixerBase(nn.Module):
         self.k_short = config.short_filter_length
         # Only in_proj is fp8 in the released checkpoints (mixers.py:736-757);
         # out_proj follows the model-wide quantisation, bf16 by default.
-        self.in_proj = (Fp8StaticLinear(h, 3 * h, bias=False, device=device)
-                        if config.use_fp8_input_projections
-                        else Linear(h, 3 * h, bias=False, device=device))
+        self.in_proj_token_table = None
+        if layer_idx in getattr(config, "hyena_token_table_layers", ()):
+            # FP8-surgery layer 0: the projection of each token, looked up
+            # (mixers.py:761-767); its input depends on the token alone.
+            self.in_proj = ProjectionTap()
+            self.in_proj_token_table = nn.Parameter(
+                torch.empty(config.vocab_size, 3 * h, device=device, dtype=torch.bfloat16),
+                requires_grad=False)
+        elif config.use_fp8_input_projections:
+            self.in_proj = Fp8StaticLinear(h, 3 * h, bias=False, device=device)
+        else:
+            self.in_proj = Linear(h, 3 * h, bias=False, device=device)
         self.out_proj = (Fp8StaticLinear(h, h, bias=True, device=device)
                          if quant_config == "fp8" else Linear(h, h, bias=True, device=device))
         self.short_filter = nn.Parameter(torch.empty(3 * h, 1, self.k_short, device=device,
@@ -135,7 +153,15 @@ class HyenaMixerBase(nn.Module):
     def _short_w(self):
         return self.short_filter.view(3 * self.hidden, self.k_short)
 
-    def _project(self, hidden_states):
+    def _project(self, hidden_states, token_ids=None):
+        """in_proj, or for a token-table layer the table rows of the step's
+        tokens (mixers.py:1076-1092)."""
+        if self.in_proj_token_table is not None:
+            if token_ids is None:
+                raise ValueError(f"{self.prefix}: token-table projection needs input_ids "
+                                 "(inputs_embeds are unsupported for FP8-surgery checkpoints)")
+            z, _ = self.in_proj(self.in_proj_token_table[token_ids[: hidden_states.shape[0]]])
+            return z
         z, _ = self.in_proj(hidden_states)
         return z
 
@@ -158,8 +184,8 @@ class HyenaMixerBase(nn.Module):
         full[:n_actual] = out
         return full
 
-    def _profile_run(self, hidden_states):
-        z = self._project(hidden_states)
+    def _profile_run(self, hidden_states, token_ids=None):
+        z = self._project(hidden_states, token_ids)
         y = z[:, 0::3] * z[:, 1::3] * z[:, 2::3]
         out, _ = self.out_proj(y)
         return out
@@ -195,12 +221,12 @@ class HyenaFIRMixer(HyenaMixerBase):
     def _forward_impl(self, hidden_states, token_ids=None):
         m = self._meta()
         if m is None:
-            return self._profile_run(hidden_states)
+            return self._profile_run(hidden_states, token_ids)
         self._check_meta(m)
         if self._decode_taps is None or self._decode_taps.device != self.conv.device:
             self.process_weights_after_loading()
         nd, npt = int(m.num_decode_tokens), int(m.num_prefill_tokens)
-        z = self._project(hidden_states[:nd + npt])
+        z = self._project(hidden_states[:nd + npt], token_ids)
         sw = self._short_w()
         conv_state = self._conv_state(0)
         inner_state = self._conv_state(1, self.k_inner - 1)
@@ -240,10 +266,10 @@ class HyenaIIRMixer(HyenaMixerBase):
     def _forward_impl(self, hidden_states, token_ids=None):
         m = self._meta()
         if m is None:
-            return self._profile_run(hidden_states)
+            return self._profile_run(hidden_states, token_ids)
         self._check_meta(m)
         nd, npt = int(m.num_decode_tokens), int(m.num_prefill_tokens)
-        z = self._project(hidden_states[:nd + npt])
+        z = self._project(hidden_states[:nd + npt], token_ids)
         sw = self._short_w()
         conv_state = self._conv_state(0)
         ssm = self._ssm_state()

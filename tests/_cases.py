@@ -93,3 +93,37 @@ def verify_case(kind, H, nreq, Q, num_blocks, seed, x_dtype=torch.bfloat16, n_nu
         K = prm["conv"].shape[-1]
         state = torch.randn(num_blocks, H, K - 1, generator=g).to(torch.bfloat16).float()
     return prm, x, state, (ins, outs, starts, ends, accepted)
+
+
+def oracle_mixer_step(kind, prm, hs, pool, dec_slots, pre_lens, pre_slots, pre_init, H):
+    """The oracle's composition of one mixer step (decode rows, then prefill
+    segments, then zero padding rows): fp8 in_proj as the dequantised matmul,
+    the mixer core, bf16 out_proj with bias."""
+    import oracle
+
+    nd, npt = len(dec_slots), sum(pre_lens)
+    z = oracle.fp8_linear_dequant(hs[:nd + npt], prm["in_proj.weight"], prm["in_proj.input_scale"],
+                                  prm["in_proj.weight_scale"])
+    sw = prm["short_filter"].view(3 * H, 3)
+    D = prm.get("D")
+    qsl = [0]
+    for n in pre_lens:
+        qsl.append(qsl[-1] + n)
+    if kind == "hcl":
+        res, lp = prm["residues"], prm["log_poles"][..., 0]
+        gd = oracle.hyena_decode_emulated(z[:nd], sw, pool.conv_view(), dec_slots, res,
+                                          pool.ssm_view(), D, lp)
+        gp = oracle.iir_mixer_prefill(z[nd:], sw, pool.conv_view(), res, lp, pool.ssm_view(), D,
+                                      qsl, pre_slots, pre_init)
+    else:
+        K = prm["conv"].shape[-1]
+        w = prm["conv"].view(H, K)
+        gd = oracle.hyena_decode_emulated(z[:nd], sw, pool.conv_view(), dec_slots, w,
+                                          pool.inner_view(K - 1), D)
+        gp = oracle.fir_mixer_prefill(z[nd:], sw, pool.conv_view(), w, pool.inner_view(K - 1), D,
+                                      qsl, pre_slots, pre_init)
+    g = torch.cat([gd, gp]).float()
+    out = (g @ prm["out_proj.weight"].float().t() + prm["out_proj.bias"].float()).to(torch.bfloat16)
+    full = torch.zeros(hs.shape, dtype=torch.bfloat16)
+    full[:nd + npt] = out
+    return full

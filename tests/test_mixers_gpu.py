@@ -19,40 +19,11 @@ from evo2_flash_amd.metadata import build_metadata
 from evo2_flash_amd.mixers import load_mixer_params, make_mixer, set_forward_context
 from evo2_flash_amd.synthetic import mixer_params
 
-from _cases import clone_pool, max_rel_err, random_pool
+from _cases import clone_pool, max_rel_err, oracle_mixer_step, random_pool
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
 _ids = itertools.count()
-
-
-def _oracle_step(kind, prm, hs, pool, dec_slots, pre_lens, pre_slots, pre_init, H):
-    nd, npt = len(dec_slots), sum(pre_lens)
-    z = oracle.fp8_linear_dequant(hs[:nd + npt], prm["in_proj.weight"], prm["in_proj.input_scale"],
-                                  prm["in_proj.weight_scale"])
-    sw = prm["short_filter"].view(3 * H, 3)
-    D = prm.get("D")
-    qsl = [0]
-    for n in pre_lens:
-        qsl.append(qsl[-1] + n)
-    if kind == "hcl":
-        res, lp = prm["residues"], prm["log_poles"][..., 0]
-        gd = oracle.hyena_decode_emulated(z[:nd], sw, pool.conv_view(), dec_slots, res,
-                                          pool.ssm_view(), D, lp)
-        gp = oracle.iir_mixer_prefill(z[nd:], sw, pool.conv_view(), res, lp, pool.ssm_view(), D,
-                                      qsl, pre_slots, pre_init)
-    else:
-        K = prm["conv"].shape[-1]
-        w = prm["conv"].view(H, K)
-        gd = oracle.hyena_decode_emulated(z[:nd], sw, pool.conv_view(), dec_slots, w,
-                                          pool.inner_view(K - 1), D)
-        gp = oracle.fir_mixer_prefill(z[nd:], sw, pool.conv_view(), w, pool.inner_view(K - 1), D,
-                                      qsl, pre_slots, pre_init)
-    g = torch.cat([gd, gp]).float()
-    out = (g @ prm["out_proj.weight"].float().t() + prm["out_proj.bias"].float()).to(torch.bfloat16)
-    full = torch.zeros(hs.shape, dtype=torch.bfloat16)
-    full[:nd + npt] = out
-    return full
 
 
 @pytest.mark.parametrize("kind", ["hcs", "hcm", "hcl"])
@@ -76,7 +47,7 @@ def test_mixer_mixed_step_vs_oracle(kind):
     print(f"mixer {kind} nd={nd} prefill={pre_lens}", flush=True)
     with set_forward_context(m):
         out = mixer(hs.to(DEV)).cpu()
-    ref = _oracle_step(kind, prm, hs, pool, dec_slots, pre_lens, pre_slots, pre_init, H)
+    ref = oracle_mixer_step(kind, prm, hs, pool, dec_slots, pre_lens, pre_slots, pre_init, H)
     assert (out[nd + npt:].float() == 0).all()
     assert max_rel_err(out, ref) <= 1e-2
     # conv windows hold raw in_proj rows, which the GPU's fp8 GEMM and the
