@@ -20,7 +20,9 @@
 // Layout: FIR windows are channel-contiguous native storage (blocks, K-1, H)
 // seen as a (blocks, H, K-1) view with unit channel stride, so each column
 // moves as one coalesced row per wave; LI states are (blocks, H, 16) with
-// unit state stride.  A destination equal to the null block, or outside the
+// unit state stride.  The grid runs channel blocks fastest (blockIdx.x) and
+// requests on blockIdx.y, so workgroups dispatched together write adjacent
+// pieces of the same columns.  A destination equal to the null block, or outside the
 // pool, is not written (the reference skips block 0, line 80); a source
 // outside the pool reads as a zero state.
 #include "common.h"
@@ -88,7 +90,96 @@ __device__ __forceinline__ void store_y(const VerifyArgs &a, int64_t t, int c, f
 }
 
 // ---------------------------------------------------------------------------
-// K = 128.  A workgroup owns one request and 64 channels (lane = channel).
+// K = 128, requests of up to VQ tokens.  A workgroup owns one request and 64
+// channels (lane = channel).  Every output and snapshot of the step is a
+// function of the source window and the step's tokens alone: with
+// e = window ++ (x_0 .. x_{n-1}), snapshot p is e[p+1 .. p+127] and y_p sums
+// e[p .. p+126] against the taps plus last * x_p.  So e is staged in LDS once,
+// and then every wave issues its share of all snapshot stores back to back
+// (no barrier between tokens, so the memory system sees every store of the
+// step at once) and computes whole outputs for its positions.
+//  * stores: wave m writes the columns k = m (mod 4) of every snapshot, in
+//    position order, so a block named by two positions ends with the later
+//    one's contents, as the reference's sequential writes leave it;
+//  * sums: wave m computes y_p for p = m (mod 4) with the reference's 16
+//    accumulators (k = 16 j + 4 m' + l over j in order), combined as
+//    ((A0 + A1) + A2) + A3 per l, then (l0 + l2) + (l1 + l3), plus last * x.
+constexpr int VQ = 16;
+
+__global__ __launch_bounds__(256) void fir128_verify_kernel(VerifyArgs a) {
+  __shared__ float e[127 + VQ][64];
+  const int lane = threadIdx.x & 63;
+  const int m = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) & 3;
+  const int64_t r = blockIdx.y;
+  const int c = blockIdx.x * 64 + lane;
+  const bool active = c < a.H;
+  const int cc = active ? c : 0;
+  const Req q = request_of(a, r);
+  const int n = static_cast<int>(max<int64_t>(0, min<int64_t>(a.Q, q.end - q.first)));
+
+  const float *src = a.st + q.src * a.ss0 + (int64_t)cc * a.ss1;
+  for (int k = m; k < 127; k += 4) e[k][lane] = (q.src_ok && active) ? src[(int64_t)k * a.ss2] : 0.0f;
+  for (int p = m; p < n; p += 4) e[127 + p][lane] = active ? load_x(a, q.first + p, c) : 0.0f;
+  __syncthreads();
+
+  for (int p = 0; p < n; ++p) {
+    const int64_t d = dest_of(a, r, p);
+    if (d >= 0 && active) {
+      float *dst = a.st + d * a.ss0 + (int64_t)c * a.ss1;
+#pragma unroll 8
+      for (int k = m; k < 127; k += 4) dst[(int64_t)k * a.ss2] = e[p + 1 + k][lane];
+    }
+  }
+  if (m >= n) return;  // uniform: no position for this wave
+
+  // the channel's taps as bf16 pairs (tap k = half k & 1 of W[k / 2])
+  uint32_t W[64];
+  const bf16_t *wrow = a.w + (int64_t)cc * a.w0;
+  if (a.w1 == 1 && a.w0 % 8 == 0 && (reinterpret_cast<uintptr_t>(a.w) & 15) == 0) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const uint4 v = reinterpret_cast<const uint4 *>(wrow)[i];
+      W[4 * i] = v.x; W[4 * i + 1] = v.y; W[4 * i + 2] = v.z; W[4 * i + 3] = v.w;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 64; ++i) W[i] = pair_bf(wrow[(2 * i) * a.w1], wrow[(2 * i + 1) * a.w1]);
+  }
+  const float last = hi_bf(W[63]);
+  for (int p = m; p < n; p += 4) {
+    // the taps stay packed (64 VGPRs): an empty asm per position keeps the
+    // compiler from hoisting 127 converted fp32 taps out of this loop
+#pragma unroll
+    for (int i = 0; i < 64; ++i) asm volatile("" : "+v"(W[i]));
+    float acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int l = 0; l < 4; ++l) acc[i][l] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+          const int k = 16 * j + 4 * i + l;
+          if (k < 127) {
+            const float wk = (k & 1) ? hi_bf(W[k >> 1]) : lo_bf(W[k >> 1]);
+            acc[i][l] = acc[i][l] + e[p + k][lane] * wk;
+          }
+        }
+    }
+    float pl[4];
+#pragma unroll
+    for (int l = 0; l < 4; ++l) pl[l] = ((acc[0][l] + acc[1][l]) + acc[2][l]) + acc[3][l];
+    const float yv = ((pl[0] + pl[2]) + (pl[1] + pl[3])) + last * e[127 + p][lane];
+    if (active) store_y(a, q.first + p, c, yv);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// K = 128, requests of more than VQ tokens (one token at a time).  A
+// workgroup owns one request and 64 channels (lane = channel).
 // The 127-column window lives in an LDS ring of 128 columns: at position p
 // column k of the window is ring slot (p + k) mod 128, so appending the token
 // overwrites the slot of the dropped column and nothing moves.  Wave m sums
@@ -96,13 +187,13 @@ __device__ __forceinline__ void store_y(const VerifyArgs &a, int64_t t, int c, f
 // their four partials to wave 0 through LDS, which combines them in the
 // reference's order.  After each token every wave writes a quarter of the
 // new window to the destination snapshot.
-__global__ __launch_bounds__(256) void fir128_verify_kernel(VerifyArgs a) {
+__global__ __launch_bounds__(256) void fir128_verify_serial_kernel(VerifyArgs a) {
   __shared__ float ring[128][64];
   __shared__ float part[3][4][64];
   const int lane = threadIdx.x & 63;
   const int m = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) & 3;
-  const int64_t r = blockIdx.x;
-  const int c = blockIdx.y * 64 + lane;
+  const int64_t r = blockIdx.y;
+  const int c = blockIdx.x * 64 + lane;
   const bool active = c < a.H;
   const int cc = active ? c : 0;
   const Req q = request_of(a, r);
@@ -160,8 +251,8 @@ __global__ __launch_bounds__(256) void fir128_verify_kernel(VerifyArgs a) {
 // ---------------------------------------------------------------------------
 // K = 7: one channel per thread, the 6-column window in registers.
 __global__ __launch_bounds__(256) void fir7_verify_kernel(VerifyArgs a) {
-  const int64_t r = blockIdx.x;
-  const int c = blockIdx.y * 256 + threadIdx.x;
+  const int64_t r = blockIdx.y;
+  const int c = blockIdx.x * 256 + threadIdx.x;
   if (c >= a.H) return;
   const Req q = request_of(a, r);
   float w[7], s[6];
@@ -170,10 +261,18 @@ __global__ __launch_bounds__(256) void fir7_verify_kernel(VerifyArgs a) {
   const float *src = a.st + q.src * a.ss0 + (int64_t)c * a.ss1;
 #pragma unroll
   for (int k = 0; k < 6; ++k) s[k] = q.src_ok ? src[(int64_t)k * a.ss2] : 0.0f;
-  for (int pos = 0; pos < a.Q; ++pos) {
-    if (q.first + pos >= q.end) break;
+  // the request's token inputs are loaded up front (up to VQ of them), so
+  // their latencies overlap instead of one per token
+  const int n = static_cast<int>(max<int64_t>(0, min<int64_t>(a.Q, q.end - q.first)));
+  float xs[VQ];
+#pragma unroll
+  for (int i = 0; i < VQ; ++i) xs[i] = i < n ? load_x(a, q.first + i, c) : 0.0f;
+  for (int pos = 0; pos < n; ++pos) {
     const int64_t t = q.first + pos;
-    const float x = load_x(a, t, c);
+    float x = 0.0f;
+#pragma unroll
+    for (int i = 0; i < VQ; ++i) x = i == pos ? xs[i] : x;
+    if (pos >= VQ) x = load_x(a, t, c);
     // ((p0 + p4) + (p1 + p5) + p2) + p3 (triton_verifier.py:35-43)
     float pa = s[0] * w[0], pb = s[1] * w[1];
     const float pc = s[2] * w[2], pd = s[3] * w[3];
@@ -205,8 +304,8 @@ __device__ __forceinline__ float quad_move(float v) {
 __global__ __launch_bounds__(256) void iir_verify_kernel(VerifyArgs a) {
   const int lane = threadIdx.x & 63;
   const int qd = lane & 3;
-  const int64_t r = blockIdx.x;
-  const int c = blockIdx.y * 64 + (threadIdx.x >> 2);
+  const int64_t r = blockIdx.y;
+  const int c = blockIdx.x * 64 + (threadIdx.x >> 2);
   const bool active = c < a.H;
   const int cc = active ? c : a.H - 1;
   const Req q = request_of(a, r);
@@ -217,10 +316,17 @@ __global__ __launch_bounds__(256) void iir_verify_kernel(VerifyArgs a) {
   const float pv[4] = {p4.x, p4.y, p4.z, p4.w};
   const float rv[4] = {r4.x, r4.y, r4.z, r4.w};
   float sv[4] = {s4.x, s4.y, s4.z, s4.w};
-  for (int pos = 0; pos < a.Q; ++pos) {
-    if (q.first + pos >= q.end) break;  // uniform
+  // token inputs up front (up to VQ), so their latencies overlap
+  const int n = static_cast<int>(max<int64_t>(0, min<int64_t>(a.Q, q.end - q.first)));
+  float xs[VQ];
+#pragma unroll
+  for (int i = 0; i < VQ; ++i) xs[i] = i < n ? load_x(a, q.first + i, cc) : 0.0f;
+  for (int pos = 0; pos < n; ++pos) {  // uniform
     const int64_t t = q.first + pos;
-    const float x = load_x(a, t, cc);
+    float x = 0.0f;
+#pragma unroll
+    for (int i = 0; i < VQ; ++i) x = i == pos ? xs[i] : x;
+    if (pos >= VQ) x = load_x(a, t, cc);
     float rr[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -285,10 +391,13 @@ extern "C" int evo2_fir_verify(const void *x, int64_t xs0, int64_t xs1, int32_t 
                starts, ends, accepted, y, ys0, Q, static_cast<int>(H), null_block, num_blocks, T};
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (K == 128) {
-    dim3 grid(static_cast<unsigned>(nreq), static_cast<unsigned>(cdiv(H, 64)));
-    hipLaunchKernelGGL(fir128_verify_kernel, grid, dim3(256), 0, st, a);
+    dim3 grid(static_cast<unsigned>(cdiv(H, 64)), static_cast<unsigned>(nreq));
+    if (Q <= VQ)
+      hipLaunchKernelGGL(fir128_verify_kernel, grid, dim3(256), 0, st, a);
+    else
+      hipLaunchKernelGGL(fir128_verify_serial_kernel, grid, dim3(256), 0, st, a);
   } else {
-    dim3 grid(static_cast<unsigned>(nreq), static_cast<unsigned>(cdiv(H, 256)));
+    dim3 grid(static_cast<unsigned>(cdiv(H, 256)), static_cast<unsigned>(nreq));
     hipLaunchKernelGGL(fir7_verify_kernel, grid, dim3(256), 0, st, a);
   }
   return check_launch("fir_verify");
@@ -318,7 +427,7 @@ extern "C" int evo2_iir_verify(const void *x, int64_t xs0, int64_t xs1, int32_t 
   VerifyArgs a{x, xs0, xs1, x_f32, nullptr, 0, 0, poles, p0, p1, residues, r0, r1,
                state, ss0, ss1, ss2, ins, is0, is1, outs, os0, os1,
                starts, ends, accepted, y, ys0, Q, static_cast<int>(H), null_block, num_blocks, T};
-  dim3 grid(static_cast<unsigned>(nreq), static_cast<unsigned>(cdiv(H, 64)));
+  dim3 grid(static_cast<unsigned>(cdiv(H, 64)), static_cast<unsigned>(nreq));
   hipLaunchKernelGGL(iir_verify_kernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream), a);
   return check_launch("iir_verify");
 }
