@@ -111,3 +111,31 @@ def test_one_token_bitwise(kind):
                                          None)
         assert torch.equal(y.view(torch.int16), ref.view(torch.int16))
     assert torch.equal(gst.cpu(), st)
+
+
+@pytest.mark.parametrize("kind", ["hcs", "hcm", "hcl"])
+def test_long_requests_bitwise(kind):
+    """More tokens per request (Q = 19) than the kernels stage at once (16):
+    the one-token-at-a-time K=128 kernel and the per-token input loads past
+    the staged ones, bit for bit against the emulation."""
+    H, nreq, Q = 256, 3, 19
+    nblk = 2 * nreq * Q + 2
+    x_dtype = torch.float32 if kind == "hcl" else torch.bfloat16
+    prm, x, state, meta = verify_case(kind, H, nreq, Q, nblk, seed=77, x_dtype=x_dtype)
+    st = state.clone()
+    print(f"long verify {kind} Q={Q}", flush=True)
+    if kind == "hcl":
+        poles = torch.exp(prm["log_poles"][..., 0].float())
+        gst = state.to(DEV)
+        y = iir_snapshots(x.to(DEV), poles.to(DEV), prm["residues"].to(DEV), gst,
+                          _meta_dev(meta, False)).cpu()
+        ref = oracle.iir_verify_emulated(x, poles, prm["residues"], st, *meta)
+        assert torch.equal(y, ref)
+    else:
+        K = prm["conv"].shape[-1]
+        w = prm["conv"].view(H, K)
+        gst = _fir_state_dev(state)
+        y = fir_snapshots(x.to(DEV), w.to(DEV), gst, _meta_dev(meta, False)).cpu()
+        ref = oracle.fir_verify_emulated(x, w, st, *meta)
+        assert torch.equal(y.view(torch.int16), ref.view(torch.int16))
+    assert torch.equal(gst.cpu(), st)
