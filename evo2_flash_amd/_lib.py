@@ -94,6 +94,12 @@ SIGNATURES = {
         _c_p, _c_i64, _c_i64, _c_i64, _c_i64,     # out, so, M, N, K
         _c_p,                                     # stream
     ],
+    "evo2_fp8_fast_accum_gemm": [
+        _c_p, _c_i64, _c_p, _c_i64,               # a8, sa, b_t, sb
+        _c_p, _c_p,                               # input_scale, weight_scale
+        _c_p, _c_i64, _c_i32,                     # out, so, out_f32
+        _c_i64, _c_i64, _c_i64, _c_p,             # N, M, K, stream
+    ],
     "evo2_fir_verify": [
         _c_p, _c_i64, _c_i64, _c_i32,             # x, xs0, xs1, x_f32
         _c_p, _c_i64, _c_i64, _c_i32,             # w, w0, w1, K

@@ -16,6 +16,11 @@ The keys of one Hyena layer i (convert.py:465-494, 175-209), under
   in_proj.input_scale    (1,) fp32 dequantisation scale = TE scale_inv_fwd[0]
   in_proj_token_table    (vocab, 3H) bf16, layer 0 of FP8-surgery checkpoints only,
                          in place of in_proj (config.py:73-80, convert.py:712-780)
+  in_proj_emul_weight_t  (H, 3H) bf16 E4M3 values, K-major, in place of in_proj for
+                         `hyena_fp8_emulated_layers`; (H, n) beside a bf16 in_proj for
+                         `hyena_fp8_emulated_channels` {i: n} (mixers.py:768-800)
+  in_proj_emul_scales    (2,) fp32 [input_scale, weight_scale] of the emulated GEMM
+  in_proj_emul_cols      (n,) int64 output channels the emulated GEMM overwrites
   short_filter.weight    (3H, 1, 3) bf16
   conv.weight            (H, 1, K) bf16, hcs / hcm, cross-correlation order
   D                      (H,) bf16, hcm and hcl
@@ -71,8 +76,17 @@ def expected_params(cfg, i):
     H, S = cfg.hidden_size, cfg.state_size
     bf16, f32 = torch.bfloat16, torch.float32
     p = {}
+    n_emul = cfg.hyena_fp8_emulated_channels.get(i, 0)
     if i in cfg.hyena_token_table_layers:
         p[TOKEN_TABLE] = ((cfg.vocab_size, 3 * H), bf16)
+    elif i in cfg.hyena_fp8_emulated_layers:
+        p["in_proj_emul_weight_t"] = ((H, 3 * H), bf16)
+        p["in_proj_emul_scales"] = ((2,), f32)
+    elif n_emul:
+        p["in_proj.weight"] = ((3 * H, H), bf16)
+        p["in_proj_emul_weight_t"] = ((H, n_emul), bf16)
+        p["in_proj_emul_scales"] = ((2,), f32)
+        p["in_proj_emul_cols"] = ((n_emul,), torch.int64)
     elif cfg.use_fp8_input_projections:
         p["in_proj.weight"] = ((3 * H, H), E4M3)
         p["in_proj.weight_scale"] = ((1,), f32)

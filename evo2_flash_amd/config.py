@@ -43,7 +43,8 @@ class HyenaConfig:
     use_fp8_input_projections: bool = False
     hyena_in_proj_fp8: dict = None
     # FP8 surgery output (config.py:73-112): layer 0's in_proj as a (vocab, 3H)
-    # token table; the Hopper-emulated layers and channels are not built here.
+    # token table; layers whose whole in_proj, or a calibrated subset of its
+    # output channels, runs the Hopper fast-accumulation fp8 model.
     hyena_token_table_layers: list = field(default_factory=list)
     hyena_fp8_emulated_layers: list = field(default_factory=list)
     hyena_fp8_emulated_channels: dict = field(default_factory=dict)
@@ -109,10 +110,20 @@ class HyenaConfig:
                                  "cannot be combined with use_fp8_input_projections=True")
             if not isinstance(self.fp8_surgery, dict):
                 raise ValueError("token-table checkpoints must carry fp8_surgery provenance")
-        if self.hyena_fp8_emulated_layers or self.hyena_fp8_emulated_channels:
-            raise NotImplementedError(
-                "hyena_fp8_emulated_layers / hyena_fp8_emulated_channels model Hopper's fp8 "
-                "fast accumulation in software; this build's fp8 GEMM accumulates in fp32")
+        if self.hyena_fp8_emulated_layers:
+            bad = [i for i in self.hyena_fp8_emulated_layers if i not in hyena]
+            if bad or (0 in self.hyena_token_table_layers and 0 in self.hyena_fp8_emulated_layers):
+                raise ValueError(f"invalid hyena_fp8_emulated_layers {self.hyena_fp8_emulated_layers}")
+            if self.use_fp8_input_projections or not isinstance(self.fp8_surgery, dict):
+                raise ValueError("hyena_fp8_emulated_layers is FP8-surgery output: needs "
+                                 "use_fp8_input_projections=False and fp8_surgery provenance")
+        if self.hyena_fp8_emulated_channels:
+            bad = {i: n for i, n in self.hyena_fp8_emulated_channels.items()
+                   if i not in hyena or i in self.hyena_fp8_emulated_layers
+                   or i in self.hyena_token_table_layers or not 0 < n < 3 * self.hidden_size}
+            if bad or self.use_fp8_input_projections or not isinstance(self.fp8_surgery, dict):
+                raise ValueError(f"invalid hyena_fp8_emulated_channels {bad or ''}: needs "
+                                 "FP8-surgery provenance, Hyena layers, 0 < n < 3H")
         if not self.conv_kernels_pre_flipped:
             raise NotImplementedError("conv kernels must be in cross-correlation order "
                                       "(conv_kernels_pre_flipped=True)")

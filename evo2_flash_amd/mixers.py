@@ -30,6 +30,7 @@ from torch import nn
 
 from .decode import channel_major_taps, hyena_decode
 from .fp8 import Fp8StaticLinear
+from .fp8_emul import static_fp8_linear_emulated
 from .hcl import hcl_block_t, hyena_hcl_prefill
 from .metadata import decode_state_indices, prefill_tables
 from .prefill import fir_prefill_block_t, hyena_fir_prefill
@@ -115,10 +116,31 @@ class HyenaMixerBase(nn.Module):
             self.in_proj_token_table = nn.Parameter(
                 torch.empty(config.vocab_size, 3 * h, device=device, dtype=torch.bfloat16),
                 requires_grad=False)
+        elif layer_idx in getattr(config, "hyena_fp8_emulated_layers", ()):
+            # FP8 surgery: the whole projection through the Hopper
+            # fast-accumulation model on E4M3 operands held in bf16, K-major
+            # (mixers.py:768-777).
+            self.in_proj = ProjectionTap()
+            self.in_proj_emul_weight_t = nn.Parameter(
+                torch.empty(h, 3 * h, device=device, dtype=torch.bfloat16), requires_grad=False)
+            self.in_proj_emul_scales = nn.Parameter(
+                torch.empty(2, device=device, dtype=torch.float32), requires_grad=False)
         elif config.use_fp8_input_projections:
             self.in_proj = Fp8StaticLinear(h, 3 * h, bias=False, device=device)
         else:
             self.in_proj = Linear(h, 3 * h, bias=False, device=device)
+            n_emul = getattr(config, "hyena_fp8_emulated_channels", {}).get(layer_idx, 0)
+            if n_emul:
+                # FP8 surgery, hybrid: the calibrated worst output channels of
+                # this bf16 projection are recomputed by the emulated fp8 GEMM
+                # and written over the bf16 ones (mixers.py:691-702, 779-800).
+                self.in_proj_emul_weight_t = nn.Parameter(
+                    torch.empty(h, n_emul, device=device, dtype=torch.bfloat16),
+                    requires_grad=False)
+                self.in_proj_emul_scales = nn.Parameter(
+                    torch.empty(2, device=device, dtype=torch.float32), requires_grad=False)
+                self.in_proj_emul_cols = nn.Parameter(
+                    torch.empty(n_emul, device=device, dtype=torch.int64), requires_grad=False)
         self.out_proj = (Fp8StaticLinear(h, h, bias=True, device=device)
                          if quant_config == "fp8" else Linear(h, h, bias=True, device=device))
         self.short_filter = nn.Parameter(torch.empty(3 * h, 1, self.k_short, device=device,
@@ -162,7 +184,16 @@ class HyenaMixerBase(nn.Module):
                                  "(inputs_embeds are unsupported for FP8-surgery checkpoints)")
             z, _ = self.in_proj(self.in_proj_token_table[token_ids[: hidden_states.shape[0]]])
             return z
+        emul_w = getattr(self, "in_proj_emul_weight_t", None)
+        if isinstance(self.in_proj, ProjectionTap):  # fully emulated layer
+            sc = self.in_proj_emul_scales
+            z, _ = self.in_proj(static_fp8_linear_emulated(hidden_states, emul_w, sc[0], sc[1]))
+            return z
         z, _ = self.in_proj(hidden_states)
+        if emul_w is not None:  # hybrid: emulated channels over the bf16 ones
+            sc = self.in_proj_emul_scales
+            z = z.index_copy(-1, self.in_proj_emul_cols,
+                             static_fp8_linear_emulated(hidden_states, emul_w, sc[0], sc[1]))
         return z
 
     def _check_meta(self, m):

@@ -95,15 +95,16 @@ def verify_case(kind, H, nreq, Q, num_blocks, seed, x_dtype=torch.bfloat16, n_nu
     return prm, x, state, (ins, outs, starts, ends, accepted)
 
 
-def oracle_mixer_step(kind, prm, hs, pool, dec_slots, pre_lens, pre_slots, pre_init, H):
+def oracle_mixer_step(kind, prm, hs, pool, dec_slots, pre_lens, pre_slots, pre_init, H, z=None):
     """The oracle's composition of one mixer step (decode rows, then prefill
     segments, then zero padding rows): fp8 in_proj as the dequantised matmul,
     the mixer core, bf16 out_proj with bias."""
     import oracle
 
     nd, npt = len(dec_slots), sum(pre_lens)
-    z = oracle.fp8_linear_dequant(hs[:nd + npt], prm["in_proj.weight"], prm["in_proj.input_scale"],
-                                  prm["in_proj.weight_scale"])
+    if z is None:  # else the caller's projection of hs[:nd + npt]
+        z = oracle.fp8_linear_dequant(hs[:nd + npt], prm["in_proj.weight"],
+                                      prm["in_proj.input_scale"], prm["in_proj.weight_scale"])
     sw = prm["short_filter"].view(3 * H, 3)
     D = prm.get("D")
     qsl = [0]

@@ -222,7 +222,7 @@ _n = itertools.count()
     (lambda c: c.pop("hyena_in_proj_fp8"), ValueError),
     (lambda c: c.update(use_fp8_input_projections=False), ValueError),
     (lambda c: c.update(quantization_config={"quant_method": "fp8"}), ValueError),
-    (lambda c: c.update(hyena_fp8_emulated_layers=[1]), NotImplementedError),
+    (lambda c: c.update(hyena_fp8_emulated_layers=[1]), ValueError),  # needs bf16 + surgery
     (lambda c: c.update(hyena_flip_x1x2=True), NotImplementedError),
     (lambda c: c.update(conv_kernels_pre_flipped=False), NotImplementedError),
     (lambda c: c.update(hcs_layer_idxs=[0, 4, 1]), ValueError),
@@ -351,3 +351,50 @@ def test_mixers_from_checkpoint_vs_oracle(ckpt):
         ref = oracle_mixer_step(kind, prm, hs, pool, dec, lens, slots, init, H)
         assert max_rel_err(got, ref) <= 1e-2, (i, kind)
         assert max_rel_err(gp.kv_cache[2].cpu(), pool.kv_cache[2]) <= 1e-3
+
+
+def test_surgery_checkpoint_layers(tmp_path):
+    """An FP8-surgery directory (config.py:73-94): token table on layer 0, a
+    fully emulated layer and a hybrid layer load with their own tensors."""
+    Hs, V = 64, 512
+    cfg = {"hidden_size": Hs, "num_hidden_layers": 3, "vocab_size": V, "hcs_layer_idxs": [0],
+           "hcm_layer_idxs": [1], "hcl_layer_idxs": [2], "use_fp8_input_projections": False,
+           "hyena_token_table_layers": [0], "hyena_fp8_emulated_layers": [1],
+           "hyena_fp8_emulated_channels": {"2": 12}, "fp8_surgery": {"version": 1}}
+    g = torch.Generator().manual_seed(0)
+    bf = torch.bfloat16
+    t = {}
+    p = lambda i, n: f"model.layers.{i}.mixer.{n}"  # noqa: E731
+    t[p(0, "in_proj_token_table")] = torch.randn(V, 3 * Hs, generator=g).to(bf)
+    t[p(1, "in_proj_emul_weight_t")] = torch.randn(Hs, 3 * Hs, generator=g).to(bf)
+    t[p(1, "in_proj_emul_scales")] = torch.tensor([0.01, 0.002])
+    t[p(2, "in_proj.weight")] = torch.randn(3 * Hs, Hs, generator=g).to(bf)
+    t[p(2, "in_proj_emul_weight_t")] = torch.randn(Hs, 12, generator=g).to(bf)
+    t[p(2, "in_proj_emul_scales")] = torch.tensor([0.01, 0.002])
+    t[p(2, "in_proj_emul_cols")] = torch.arange(12, dtype=torch.int64) * 5
+    for i, K in ((0, 7), (1, 128)):
+        t[p(i, "conv.weight")] = torch.randn(Hs, 1, K, generator=g).to(bf)
+    t[p(1, "D")] = torch.randn(Hs).to(bf)
+    t[p(2, "D")] = torch.randn(Hs).to(bf)
+    t[p(2, "log_poles")] = -torch.rand(Hs, 16, 1)
+    t[p(2, "residues")] = torch.randn(Hs, 16)
+    for i in range(3):
+        t[p(i, "short_filter.weight")] = torch.randn(3 * Hs, 1, 3, generator=g).to(bf)
+        t[p(i, "out_proj.weight")] = torch.randn(Hs, Hs, generator=g).to(bf)
+        t[p(i, "out_proj.bias")] = torch.randn(Hs, generator=g).to(bf)
+    out = convert.write_checkpoint(str(tmp_path / "surgery"), t, cfg)
+    rc = checkpoint.read_config(out)
+    assert rc.hyena_fp8_emulated_channels == {2: 12}
+    mixers = checkpoint.load_hyena_mixers(out, device="cpu", name_prefix="surgery.")
+    assert mixers[0].in_proj_token_table is not None
+    torch.testing.assert_close(mixers[1].in_proj_emul_weight_t, t[p(1, "in_proj_emul_weight_t")])
+    assert torch.equal(mixers[2].in_proj_emul_cols, t[p(2, "in_proj_emul_cols")])
+    assert mixers[2].in_proj.weight.dtype == torch.bfloat16
+    bad = dict(t)
+    bad.pop(p(2, "in_proj_emul_cols"))
+    out2 = convert.write_checkpoint(str(tmp_path / "surgery2"), bad, cfg)
+    with pytest.raises(ValueError, match="missing"):
+        checkpoint.load_mixer_params(out2, 2)
+    cfg_bad = dict(cfg, hyena_fp8_emulated_channels={"2": 3 * Hs})
+    with pytest.raises(ValueError):
+        HyenaConfig.from_dict(cfg_bad)
