@@ -246,8 +246,16 @@ class HyenaFIRMixer(HyenaMixerBase):
         self._decode_taps = None
 
     def process_weights_after_loading(self):
-        """Keep a channel-contiguous copy of the taps for the decode kernel."""
-        self._decode_taps = channel_major_taps(self.conv.detach().view(self.hidden, self.k_inner))
+        """Keep a channel-contiguous copy of the taps for the decode kernel,
+        rewritten in place on a reload, so a HIP graph captured before it
+        still reads the current taps."""
+        taps = channel_major_taps(self.conv.detach().view(self.hidden, self.k_inner))
+        old = self._decode_taps
+        if (old is not None and old.shape == taps.shape and old.stride() == taps.stride()
+                and old.device == taps.device):
+            old.copy_(taps)
+        else:
+            self._decode_taps = taps
 
     def _forward_impl(self, hidden_states, token_ids=None):
         m = self._meta()

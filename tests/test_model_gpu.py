@@ -1,0 +1,141 @@
+"""The decoder harness (model.py:47-200 restated around this build's mixers)
+against a CPU composition of the same weights: the oracle for RMSNorm and the
+Hyena mixer step, plain fp32 torch for the MLP and attention, bf16 at the
+same op boundaries.  Three decode steps of three sequences through a
+five-layer model (hcs, hcm, hcl, attention, hcs); logits within 2e-2 and the
+Hyena state pools within the mixer tolerance after every step."""
+
+import pytest
+import torch
+
+import oracle
+from evo2_flash_amd.config import HyenaConfig
+from evo2_flash_amd.model import Evo2DecodeModel, rotary_neox
+from evo2_flash_amd.state import HyenaStatePool
+
+from _cases import max_rel_err, oracle_mixer_step
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+bf = torch.bfloat16
+
+
+def _lin(x, w, b=None):
+    y = x.float() @ w.float().t()
+    if b is not None:
+        y = y + b.float()
+    return y.to(bf)
+
+
+def _attn_ref(a, x, pos, kc, vc):
+    """fp32 decode attention of the harness's layer a, on CPU copies of its
+    cache (updated in place)."""
+    B, nh, hd = x.shape[0], a.heads, a.hd
+    q, k, v = _lin(x, a.qkv_proj.weight.cpu()).view(B, 3, nh, hd).unbind(1)
+    inv = a.inv_freq.cpu()
+    q = rotary_neox(q, pos, inv, a.rope_factor)
+    k = rotary_neox(k, pos, inv, a.rope_factor)
+    for b in range(B):
+        kc[b, :, pos[b]] = k[b]
+        vc[b, :, pos[b]] = v[b]
+    out = torch.empty(B, nh, hd)
+    for b in range(B):
+        L = int(pos[b]) + 1
+        s = (kc[b, :, :L].float() @ q[b].float().unsqueeze(-1)).squeeze(-1) * hd ** -0.5
+        p = torch.softmax(s, dim=-1).to(bf).float()
+        out[b] = p.unsqueeze(1).matmul(vc[b, :, :L].float()).squeeze(1)
+    return _lin(out.to(bf).view(B, nh * hd), a.o_proj.weight.cpu(), a.o_proj.bias.cpu())
+
+
+def test_decode_steps_vs_cpu_composition():
+    H, B = 256, 3
+    cfg = HyenaConfig(hidden_size=H, num_hidden_layers=5, num_attention_heads=4,
+                      intermediate_size=384, vocab_size=512, hcs_layer_idxs=[0, 4],
+                      hcm_layer_idxs=[1], hcl_layer_idxs=[2], attn_layer_idxs=[3],
+                      use_fp8_input_projections=True)
+    model = Evo2DecodeModel(cfg, max_batch=B, max_ctx=32, device=DEV, rope_theta=10000.0,
+                            rope_factor=4.0, name="harness_test")
+    model.init_random(seed=11, state_scale=0.5, kv_scale=0.5)
+    # CPU copies of every state the step touches
+    pools = {}
+    for i, p in model.pools.items():
+        c = HyenaStatePool(p.num_blocks, H, "cpu")
+        c.raw.copy_(p.raw.cpu())
+        pools[i] = c
+    attn = model.layers[3].mixer
+    kc, vc = attn.k_cache.cpu(), attn.v_cache.cpu()
+    emb = model.embed.detach().cpu()
+    g = torch.Generator().manual_seed(3)
+    pos = torch.tensor([10, 4, 17])
+    slots = model.slots.cpu().tolist()
+    for step in range(3):
+        tok = torch.randint(0, 512, (B,), generator=g)
+        print(f"harness decode step {step}", flush=True)
+        logits = model.decode_step(tok.to(DEV), pos.to(DEV)).cpu()
+        x = emb[tok]
+        for i, layer in enumerate(model.layers):
+            pre = oracle.rms_norm(x, layer.pre_norm.weight.cpu(), cfg.rms_norm_eps)
+            if layer.kind == "attn":
+                m = _attn_ref(attn, pre, pos, kc, vc)
+            else:
+                prm = {k: v.detach().cpu() for k, v in layer.mixer.named_parameters()}
+                m = oracle_mixer_step(layer.kind, prm, pre, pools[i], slots, [], [], [], H)
+            post, x = oracle.rms_norm(m, layer.post_norm.weight.cpu(), cfg.rms_norm_eps,
+                                      residual=x)
+            z1 = _lin(post, layer.mlp.l1.weight.cpu())
+            z2 = _lin(post, layer.mlp.l2.weight.cpu())
+            if layer.mlp.use_act:
+                z1 = torch.nn.functional.gelu(z1.float()).to(bf)
+            x = (_lin((z1.float() * z2.float()).to(bf), layer.mlp.l3.weight.cpu()).float()
+                 + x.float()).to(bf)
+        ref = _lin(oracle.rms_norm(x, model.norm.weight.cpu(), cfg.rms_norm_eps), emb)
+        assert max_rel_err(logits, ref) <= 2e-2, step
+        for i, p in model.pools.items():
+            assert max_rel_err(p.kv_cache[1].cpu(), pools[i].kv_cache[1]) <= 2e-2, (step, i)
+            assert max_rel_err(p.kv_cache[2].cpu(), pools[i].kv_cache[2]) <= 1e-3, (step, i)
+        pos = pos + 1
+
+
+def test_decode_step_graph_replays():
+    """The whole decode step captured once as a HIP graph: replays advance the
+    states exactly as eager steps from the same starting state."""
+    H, B = 256, 2
+    cfg = HyenaConfig(hidden_size=H, num_hidden_layers=4, num_attention_heads=4,
+                      intermediate_size=256, vocab_size=512, hcs_layer_idxs=[0],
+                      hcm_layer_idxs=[1], hcl_layer_idxs=[2], attn_layer_idxs=[3],
+                      use_fp8_input_projections=True)
+
+    def build(name):
+        m = Evo2DecodeModel(cfg, max_batch=B, max_ctx=16, device=DEV, name=name)
+        return m.init_random(seed=5, state_scale=0.5, kv_scale=0.5)
+
+    eager, graphed = build("harness_eager"), build("harness_graph")
+    tok = torch.tensor([65, 84], device=DEV)
+    pos = torch.tensor([3, 7], device=DEV)
+    static_pos = pos.clone()
+    graphed.decode_step(tok, static_pos)        # warm-up outside capture (builds metadata)
+    graphed.init_random(seed=5, state_scale=0.5, kv_scale=0.5)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(graph, stream=s):
+            out = graphed.decode_step(tok, static_pos)
+            static_pos.add_(1)
+    torch.cuda.current_stream().wait_stream(s)
+    # capture records without running: states and positions are still the
+    # freshly initialised ones; reloading the weights in place keeps the
+    # graph's buffers (the decode taps are rewritten, not reallocated)
+    graphed.init_random(seed=5, state_scale=0.5, kv_scale=0.5)
+    static_pos.copy_(pos)
+    torch.cuda.synchronize()
+    print("harness graph replays", flush=True)
+    for step in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        ref = eager.decode_step(tok, pos + step)
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), step
+        for i in graphed.pools:
+            assert torch.equal(graphed.pools[i].raw, eager.pools[i].raw), (step, i)
