@@ -15,12 +15,15 @@ Also measured in the same run and reported in the same JSON line:
     (M=64) against HBM;
   * verify: the inner operators of a speculative verify step (64 requests
     of 4 tokens, a state snapshot per token) against HBM;
+  * model_decode: the whole 7B-shaped model at decode (the mixers in their
+    decoder layers, attention and MLPs in torch), end-to-end tokens/s;
   * roofline of the dominant decode kernel (hcm) from HIP events on the
     stream it is launched on, and the CPU baseline: the oracle's restatement
     of the reference torch decode path timed on the host cores.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--no-prefill] [--no-gemm]
-                    [--no-verify] [--only decode|verify|prefill|gemm|copy]
+                    [--no-verify] [--no-model]
+                    [--only decode|verify|prefill|gemm|copy|model]
 """
 
 import argparse
@@ -221,6 +224,59 @@ def bench_decode(steps, warmup, dev, seed=1234):
             "mixer_frac": round(ideal_us / kern_us, 4)}
 
 
+# ---------------------------------------------------------------- whole model
+CTX_7B = 8192 + 512   # prompt plus the decode steps of the 7B workload
+
+
+def bench_model(steps, dev, B=B_DECODE, seed=21):
+    """The whole 7B-shaped model at decode (32 layers: 27 Hyena on this
+    build's kernels, 5 attention and every MLP in torch), 64 sequences at
+    positions from 8192 on, rotary base 1e4 with linear scaling 128
+    (evo2-7b-1m.yml:27-29; the checkpoint's base wins, convert.py:524-570).
+    States and KV stand in for the prefilled prompt.  One decode step is one
+    HIP graph replay; the positions advance inside the graph."""
+    from evo2_flash_amd.config import evo2_7b
+    from evo2_flash_amd.model import Evo2DecodeModel, decode_flops_bytes
+
+    cfg = evo2_7b()
+    model = Evo2DecodeModel(cfg, max_batch=B, max_ctx=CTX_7B, device=dev, rope_theta=10000.0,
+                            rope_factor=128.0, name="bench_model")
+    model.init_random(seed, state_scale=0.5, kv_scale=0.5)
+    g = torch.Generator(device=dev).manual_seed(seed)
+    tok = torch.tensor([65, 67, 71, 84], device=dev)[
+        torch.randint(0, 4, (B,), generator=g, device=dev)]
+    pos = torch.full((B,), 8192, dtype=torch.int64, device=dev)
+    model.decode_step(tok, pos)          # warm-up, builds the step's metadata
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(graph, stream=s):
+            model.decode_step(tok, pos)
+            pos.add_(1)
+    torch.cuda.current_stream().wait_stream(s)
+    n = min(steps, 500)
+    graph.replay()
+    stream = torch.cuda.current_stream()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for _ in range(n):
+        graph.replay()
+    t1.record(stream)
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / n
+    wbytes, kvbytes = decode_flops_bytes(cfg, B, 8192 + n)
+    del model, graph
+    torch.cuda.empty_cache()
+    return {"tok_s": round(B / (ms * 1e-3), 1), "ms_per_step": round(ms, 3), "batch": B,
+            "context": f"8192..{8192 + n}", "layers": 32,
+            "bytes_per_step": {"weights": wbytes, "kv_cache": kvbytes},
+            "achieved_GBs": round((wbytes + kvbytes) / (ms * 1e-3) / 1e9, 1),
+            "note": "Hyena mixers on this build's kernels; attention and MLP in torch"}
+
+
 # ---------------------------------------------------------------- speculative verify
 def bench_verify(reps, dev, H=H_7B, B=B_DECODE, Q=4, seed=9):
     """The inner operators of a speculative verify step, 7B shape: B requests
@@ -409,7 +465,9 @@ def main(argv=None):
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill leg")
     ap.add_argument("--no-gemm", action="store_true", help="skip the fp8 GEMM leg")
     ap.add_argument("--no-verify", action="store_true", help="skip the speculative verify leg")
-    ap.add_argument("--only", choices=["decode", "verify", "prefill", "gemm", "copy"], default=None,
+    ap.add_argument("--no-model", action="store_true", help="skip the whole-model decode leg")
+    ap.add_argument("--only", choices=["decode", "verify", "prefill", "gemm", "copy", "model"],
+                    default=None,
                     help="run one leg only (for profiling); `copy` runs a plain 1 GiB "
                          "device copy, the reference dispatch for scaling HBM counters")
     args = ap.parse_args(argv)
@@ -430,6 +488,7 @@ def main(argv=None):
     ver = bench_verify(max(8, args.steps // 2), dev) if run("verify", args.no_verify) else None
     pre = bench_prefill(max(3, args.steps // 8), dev) if run("prefill", args.no_prefill) else None
     gem = bench_gemm(max(5, args.steps // 4), dev) if run("gemm", args.no_gemm) else None
+    mod = bench_model(max(16, args.steps // 2), dev) if run("model", args.no_model) else None
     cpu = None if (args.no_cpu or args.only) else _cpu_baseline_decode()
     line = {
         "metric": METRIC,
@@ -463,6 +522,8 @@ def main(argv=None):
         line["prefill"] = pre
     if gem:
         line["fp8_gemm"] = gem
+    if mod:
+        line["model_decode"] = mod
     if not args.only:
         line["hbm_copy"] = bench_copy(dev)
     line["cpu_baseline"] = cpu

@@ -12,8 +12,8 @@ end-to-end decode (the reference's model.py:47-200, restated).
 The Hyena layers are this build's: RMSNorm kernel, fp8 in_proj on MFMA, the
 fused decode step over the paged state pool, out_proj.  Attention and the
 MLPs are plain torch on ROCm (they are outside the mixer hot path): the
-attention layer keeps a contiguous (batch, heads, context, head_dim) KV cache
-per layer rather than vLLM's paged cache, applies neox-style rotary with the
+attention layer keeps a contiguous KV cache per layer (keys head_dim-major)
+rather than vLLM's paged cache, applies neox-style rotary with the
 config's base and linear scaling (model.py:104-153), and attends over the
 whole cache with positions past each sequence's masked, so a decode step has
 fixed shapes and captures into one HIP graph.  Its products are batched
@@ -79,9 +79,13 @@ class Evo2Attention(nn.Module):
         self.rope_factor = float(rope_factor)
         self.register_buffer("inv_freq", 1.0 / rope_theta ** (
             torch.arange(0, self.hd, 2, device=device, dtype=torch.float32) / self.hd))
-        shape = (max_batch, self.heads, max_ctx, self.hd)
-        self.k_cache = torch.zeros(shape, dtype=torch.bfloat16, device=device)
-        self.v_cache = torch.zeros(shape, dtype=torch.bfloat16, device=device)
+        # keys head_dim-major (B, nh, hd, L), values (B, nh, L, hd): both
+        # products of a decode step then take a contiguous right operand,
+        # (1 x hd)(hd x L) for the scores and (1 x L)(L x hd) for the output
+        self.k_cache = torch.zeros(max_batch, self.heads, self.hd, max_ctx, dtype=torch.bfloat16,
+                                   device=device)
+        self.v_cache = torch.zeros(max_batch, self.heads, max_ctx, self.hd, dtype=torch.bfloat16,
+                                   device=device)
         self.register_buffer("ctx_idx", torch.arange(max_ctx, device=device))
 
     def forward_decode(self, x, positions):
@@ -91,15 +95,13 @@ class Evo2Attention(nn.Module):
         q = rotary_neox(q, positions, self.inv_freq, self.rope_factor)
         k = rotary_neox(k, positions, self.inv_freq, self.rope_factor)
         rows = torch.arange(B, device=x.device)
-        self.k_cache[rows, :, positions] = k
+        self.k_cache[rows, :, :, positions] = k
         self.v_cache[rows, :, positions] = v.contiguous()
-        K, V = self.k_cache[:B], self.v_cache[:B]                        # (B, nh, L, hd)
-        scores = torch.matmul(K, q.contiguous().view(B, self.heads, self.hd, 1))  # (B, nh, L, 1)
-        scores = scores.squeeze(-1).float() * self.hd ** -0.5
-        scores = scores.masked_fill(self.ctx_idx[None, None, :] > positions[:, None, None],
-                                    float("-inf"))
-        p = torch.softmax(scores, dim=-1).to(torch.bfloat16)
-        out = torch.matmul(p.view(B, self.heads, 1, -1), V)             # (B, nh, 1, hd)
+        q = (q.float() * self.hd ** -0.5).to(torch.bfloat16).contiguous()
+        scores = torch.matmul(q.view(B, self.heads, 1, self.hd), self.k_cache[:B])  # (B, nh, 1, L)
+        scores = scores.masked_fill(self.ctx_idx > positions[:, None, None, None], float("-inf"))
+        p = torch.softmax(scores, dim=-1, dtype=torch.float32).to(torch.bfloat16)
+        out = torch.matmul(p, self.v_cache[:B])                           # (B, nh, 1, hd)
         o, _ = self.o_proj(out.reshape(B, self.heads * self.hd))
         return o
 

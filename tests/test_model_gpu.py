@@ -36,12 +36,12 @@ def _attn_ref(a, x, pos, kc, vc):
     q = rotary_neox(q, pos, inv, a.rope_factor)
     k = rotary_neox(k, pos, inv, a.rope_factor)
     for b in range(B):
-        kc[b, :, pos[b]] = k[b]
-        vc[b, :, pos[b]] = v[b]
+        kc[b, :, :, pos[b]] = k[b]          # keys (B, nh, hd, L)
+        vc[b, :, pos[b]] = v[b]             # values (B, nh, L, hd)
     out = torch.empty(B, nh, hd)
     for b in range(B):
         L = int(pos[b]) + 1
-        s = (kc[b, :, :L].float() @ q[b].float().unsqueeze(-1)).squeeze(-1) * hd ** -0.5
+        s = (q[b].float().unsqueeze(1) @ kc[b, :, :, :L].float()).squeeze(1) * hd ** -0.5
         p = torch.softmax(s, dim=-1).to(bf).float()
         out[b] = p.unsqueeze(1).matmul(vc[b, :, :L].float()).squeeze(1)
     return _lin(out.to(bf).view(B, nh * hd), a.o_proj.weight.cpu(), a.o_proj.bias.cpu())
