@@ -31,8 +31,8 @@ def hipcc():
     raise RuntimeError("hipcc not found; the HIP kernels cannot be built")
 
 
-# Packed FP32 instructions are disabled for all device code; see DESIGN notes
-# in the kernels that rely on plain v_fma_f32 / v_dot2c_f32_bf16 instead.
+# Packed FP32 instructions are disabled for all device code: the kernels are
+# written for plain v_fma_f32 and v_dot2 bf16 arithmetic.
 DEVICE_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",

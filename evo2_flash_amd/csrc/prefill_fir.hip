@@ -9,15 +9,18 @@
 // Layout.  A workgroup owns 64 channels (lane = channel) and one tile of
 // rows of one segment (tile table [segment, first row], as
 // mixers.py:386-415 builds it).  It sweeps the tile in 64-row sub-tiles:
-//   produce: each wave turns 16 rows into u (and x2) for its 64 channels and
-//            writes them into an LDS ring, u[channel][row mod RING]; the
-//            short filter runs as v_dot2 over (z[t-1], z[t]) row pairs;
-//   FIR:     each lane computes 16 consecutive outputs of its channel from
+//   produce: each wave turns 16 rows into u and x2 for its 64 channels,
+//            writes u into an LDS ring, u[channel][row mod RING], and keeps
+//            x2 in registers for its own epilogue; the short filter runs as
+//            v_dot2 over (z[t-1], z[t]) row pairs;
+//   FIR:     each lane computes the same 16 outputs of its channel from
 //            the ring as bf16 pairs with v_dot2c_f32_bf16 (u and the taps are
 //            bf16, so every product is exact in fp32).  The ring's pairs start
 //            at even rows; outputs whose window starts at an odd row use the
 //            taps paired the other way, so no pair is ever re-aligned; the
 //            channel's taps stay in VGPRs for the tile.
+// For hcm this fits 168 VGPRs and 50 KB of LDS: three workgroups (three
+// waves per SIMD) share a CU.
 // The ring holds the K-1 rows of history the next sub-tile needs, so each
 // z row is read from HBM once per tile plus a (K-1)-row halo per tile.
 //
@@ -56,16 +59,26 @@ struct FirGeom {
   static constexpr int RS = K > 8 ? 64 : 32;
   static constexpr int NWAVE = 4;          // waves per workgroup
   static constexpr int NT = 64 * NWAVE;    // threads per workgroup
+  // hcm: three waves per SIMD (<= 168 VGPRs; 50 KB of LDS lets three
+  // workgroups share a CU)
+  static constexpr int MIN_WAVES = K > 8 ? 3 : 1;
   static constexpr int RW = RS / NWAVE;    // rows per wave per sub-tile
   static_assert(RW % 8 == 0, "produce and the epilogue work in 8-row groups");
-  static constexpr int RING = (KP + RS <= 64) ? 64 : (KP + RS <= 128) ? 128 : 256;
-  // Row pitches are 4 or 36 dwords mod 64 banks, so the 16 lanes a b128
-  // access serves per cycle cover all banks once.
+  // u ring rows per channel: exactly the KP + RS rows one sub-tile's FIR
+  // reads for hcm (192; every b128 access starts at a multiple of 8 rows, so
+  // none wraps), the next power of two for hcs.
+  static constexpr int RING = K > 8 ? KP + RS : 64;
+  // Row pitches are 36 dwords mod 64 banks, so the 16 lanes a b128 access
+  // serves per cycle cover all banks once.
   static constexpr int PITCH = RING + 8;   // bf16 per channel row of the u ring
-  static constexpr int XPITCH = RS + 8;    // bf16 per channel row of x2
   static constexpr int ZROWS = RS + 2;     // staged z rows: sub-tile + 2-row short halo
   static constexpr int ZPITCH = 192;       // bf16 per staged z row (3 x 64 sub-channels)
-  static_assert(KP + RS <= RING, "ring too small");
+  static_assert(KP + RS <= RING && RING % 8 == 0, "ring too small or misaligned");
+  static_assert((PITCH / 2) % 64 == 36, "ring pitch bank pattern");
+  // ring slot of a non-negative row offset
+  static __device__ __forceinline__ int at(int x) {
+    return (RING & (RING - 1)) == 0 ? (x & (RING - 1)) : static_cast<int>(static_cast<unsigned>(x) % RING);
+  }
 };
 
 struct SegInfo {
@@ -89,10 +102,9 @@ __device__ __forceinline__ SegInfo seg_of_tile(const FirArgs &p) {
 
 
 template <int K, bool HAS_D, bool FUSED>
-__global__ __launch_bounds__(FirGeom<K>::NT) void fir_prefill_kernel(FirArgs p) {
+__global__ __launch_bounds__(FirGeom<K>::NT, FirGeom<K>::MIN_WAVES) void fir_prefill_kernel(FirArgs p) {
   using G = FirGeom<K>;
   __shared__ __align__(16) bf16_t ring[64][G::PITCH];
-  __shared__ __align__(16) bf16_t x2s[FUSED ? 64 : 1][G::XPITCH];
   __shared__ __align__(16) bf16_t zst[FUSED ? G::ZROWS : 1][G::ZPITCH];
 
   const int lane = threadIdx.x & 63;
@@ -134,15 +146,6 @@ __global__ __launch_bounds__(FirGeom<K>::NT) void fir_prefill_kernel(FirArgs p) 
       W[m] = lo | (hi << 16);
     }
   }
-  // Even rows read the window pairs shifted by one element against the odd
-  // rows, so they take the taps re-paired the other way,
-  // V[m] = (w'[2m-1], w'[2m]) with w'[-1] = w'[KP] = 0 (NP + 1 pairs), and
-  // no window pair is ever re-aligned.
-  uint32_t V[G::NP + 1];
-  V[0] = W[0] << 16;
-#pragma unroll
-  for (int m = 1; m < G::NP; ++m) V[m] = __builtin_amdgcn_alignbit(W[m], W[m - 1], 16);
-  V[G::NP] = W[G::NP - 1] >> 16;
   ShortTaps wsp[3];
   if constexpr (FUSED) {
 #pragma unroll
@@ -173,7 +176,8 @@ __global__ __launch_bounds__(FirGeom<K>::NT) void fir_prefill_kernel(FirArgs p) 
   constexpr int NJ = (ZW + G::NWAVE - 1) / G::NWAVE;
   auto prefetch = [&](int rs) {
     if (!vec_z) return;
-    const bf16_t *base = p.x + (int64_t)rs * p.sx;
+    // uniform base plus a 32-bit per-lane byte offset (vec_z bounds it)
+    const char *base = reinterpret_cast<const char *>(p.x + (int64_t)rs * p.sx + 3 * c0);
     const bool interior = rs >= S.a && rs + G::ZROWS <= S.t_end;  // uniform
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
@@ -183,10 +187,10 @@ __global__ __launch_bounds__(FirGeom<K>::NT) void fir_prefill_kernel(FirArgs p) 
       const int row = i / 24;
       bool ok = i < ZCH;
       if (!interior) ok = ok && rs + row >= S.a && rs + row < S.t_end;
+      const uint32_t off = 2u * static_cast<uint32_t>(row * static_cast<int>(p.sx) + 8 * (i - 24 * row));
       if (ok)
         __builtin_amdgcn_global_load_lds(
-            reinterpret_cast<const uint4 *>(base + row * static_cast<int>(p.sx) + 3 * c0 +
-                                            8 * (i - 24 * row)),
+            reinterpret_cast<const uint4 *>(base + off),
             (__attribute__((address_space(3))) void *)(&zst[0][0] + cw * 512), 16, 0, 0);
     }
   };
@@ -214,10 +218,11 @@ __global__ __launch_bounds__(FirGeom<K>::NT) void fir_prefill_kernel(FirArgs p) 
   };
   auto land = [&]() { __builtin_amdgcn_s_waitcnt(0); };
 
-  // ---- one row of u (and x2) at a segment or tile boundary, lane = channel:
-  // rows before the segment start take u from the inner window
-  // (continuation) or zero; rows at or past the tile end give zeros.
-  auto produce_row = [&](int t, int rs, bool keep_x2) {
+  // ---- one row of u at a segment or tile boundary, lane = channel, written
+  // to the ring; returns x2 (FUSED; zero otherwise).  Rows before the segment
+  // start take u from the inner window (continuation) or zero; rows at or
+  // past the tile end give zeros.
+  auto produce_row = [&](int t, int rs) -> float {
     float u = 0.0f, x2 = 0.0f;
     if (t < S.a) {
       const int col = (K - 1) + (t - S.a);
@@ -235,20 +240,37 @@ __global__ __launch_bounds__(FirGeom<K>::NT) void fir_prefill_kernel(FirArgs p) 
         u = active ? bf2f(p.x[(int64_t)t * p.sx + cl]) : 0.0f;
       }
     }
-    ring[lane][(t - S.t0 + G::KP) & (G::RING - 1)] = f2bf(u);
-    if (keep_x2) x2s[lane][(t - S.t0) & (G::RS - 1)] = f2bf(x2);
+    ring[lane][G::at(t - S.t0 + G::KP)] = f2bf(u);
+    return x2;
   };
 
-  // ---- u (and x2) for NR consecutive rows [r0, r0 + NR) of this wave, lane =
-  // channel, written to the ring (and x2 buffer) as packed row pairs with
-  // b128 stores.  FUSED reads z from the staged rows (stage row of t is
-  // t - rs); U_IN loads u rows.  Groups touching a boundary go row by row.
-  auto produce = [&](int r0, int rs, auto nr_tag, bool keep_x2) {
+  // ---- u for NR consecutive rows [r0, r0 + NR) of this wave, lane =
+  // channel, written to the ring as packed row pairs with b128 stores; x2 of
+  // the rows goes to xout[NR / 2] as packed row pairs when xout is given (the
+  // wave that produces a row is the wave that finishes it, so x2 never
+  // leaves registers).  FUSED reads z from the staged rows (stage row of t
+  // is t - rs); U_IN loads u rows.  Groups touching a boundary go row by
+  // row, x2 entering a 16-bit shift register so the row loop stays rolled.
+  auto produce = [&](int r0, int rs, auto nr_tag, uint32_t *xout) {
     constexpr int NR = decltype(nr_tag)::value;
     static_assert(NR % 8 == 0, "rows are written as 8-row b128 groups");
     if (!(r0 >= S.a && r0 + NR <= S.t_end)) {  // wave-uniform
+      uint32_t xf[NR / 2];
+#pragma unroll
+      for (int i = 0; i < NR / 2; ++i) xf[i] = 0u;
 #pragma unroll 1
-      for (int r = 0; r < NR; ++r) produce_row(r0 + r, rs, keep_x2);
+      for (int r = 0; r < NR; ++r) {
+        const float x2 = produce_row(r0 + r, rs);
+        if (xout) {
+#pragma unroll
+          for (int i = 0; i + 1 < NR / 2; ++i) xf[i] = __builtin_amdgcn_alignbit(xf[i + 1], xf[i], 16);
+          xf[NR / 2 - 1] = (xf[NR / 2 - 1] >> 16) | (static_cast<uint32_t>(f2bf(x2)) << 16);
+        }
+      }
+      if (xout) {
+#pragma unroll
+        for (int i = 0; i < NR / 2; ++i) xout[i] = xf[i];
+      }
       return;
     }
     uint32_t upk[NR / 2], xpk[NR / 2];
@@ -281,14 +303,14 @@ __global__ __launch_bounds__(FirGeom<K>::NT) void fir_prefill_kernel(FirArgs p) 
         xpk[r / 2] = 0;
       }
     }
-    const int pos = (r0 - S.t0 + G::KP) & (G::RING - 1);
+    const int pos = r0 - S.t0 + G::KP;
 #pragma unroll
-    for (int g = 0; g < NR / 8; ++g) {
-      *reinterpret_cast<uint4 *>(&ring[lane][(pos + 8 * g) & (G::RING - 1)]) =
+    for (int g = 0; g < NR / 8; ++g)
+      *reinterpret_cast<uint4 *>(&ring[lane][G::at(pos + 8 * g)]) =
           make_uint4(upk[4 * g], upk[4 * g + 1], upk[4 * g + 2], upk[4 * g + 3]);
-      if (keep_x2)
-        *reinterpret_cast<uint4 *>(&x2s[lane][((r0 - S.t0) & (G::RS - 1)) + 8 * g]) =
-            make_uint4(xpk[4 * g], xpk[4 * g + 1], xpk[4 * g + 2], xpk[4 * g + 3]);
+    if (xout) {
+#pragma unroll
+      for (int i = 0; i < NR / 2; ++i) xout[i] = xpk[i];
     }
   };
   using RWC = std::integral_constant<int, G::RW>;
@@ -306,7 +328,7 @@ __global__ __launch_bounds__(FirGeom<K>::NT) void fir_prefill_kernel(FirArgs p) 
         fix(rbase - 2);
         __syncthreads();
       }
-      produce(rbase + G::RW * wave, rbase - 2, RWC{}, false);
+      produce(rbase + G::RW * wave, rbase - 2, RWC{}, nullptr);
     }
   } else {
     static_assert(G::KP == 8, "halo split assumes KP = 8 or 128");
@@ -317,7 +339,7 @@ __global__ __launch_bounds__(FirGeom<K>::NT) void fir_prefill_kernel(FirArgs p) 
       fix(rbase - 2);
       __syncthreads();
     }
-    if (wave == 0) produce(rbase, rbase - 2, R8{}, false);
+    if (wave == 0) produce(rbase, rbase - 2, R8{}, nullptr);
   }
   if constexpr (FUSED) {
     __syncthreads();
@@ -328,8 +350,9 @@ __global__ __launch_bounds__(FirGeom<K>::NT) void fir_prefill_kernel(FirArgs p) 
   }
 
   for (int s0 = S.t0; s0 < S.t_end; s0 += G::RS) {
-    produce(s0 + wave * G::RW, s0 - 2, RWC{}, FUSED);
-    __syncthreads();  // ring / x2s complete; zst free
+    uint32_t xq[G::RW / 2];  // x2 of this wave's rows, packed row pairs
+    produce(s0 + wave * G::RW, s0 - 2, RWC{}, FUSED ? xq : nullptr);
+    __syncthreads();  // ring complete; zst free
     const bool more = s0 + G::RS < S.t_end;
     if constexpr (FUSED) {
       if (more) prefetch(s0 + G::RS - 2);
@@ -340,10 +363,17 @@ __global__ __launch_bounds__(FirGeom<K>::NT) void fir_prefill_kernel(FirArgs p) 
     // Tap pairs are consumed in order m = 0..NP-1.  At step m, odd row
     // r = 2j+1 reads window pair E[m + j + 1] against W[m], even row r = 2j
     // reads E[m + j] against V[m], and the even rows take one more step,
-    // E[NP + j] against V[NP].  The window is loaded per 16-step quarter and
-    // the steps are fenced in order, which keeps the live set to one quarter
-    // (otherwise the compiler runs each accumulator's whole chain in turn and
-    // holds the whole window).
+    // E[NP + j] against V[NP].  Even rows read the window pairs shifted by
+    // one element against the odd rows, so they take the taps re-paired
+    // the other way, V[m] = (w'[2m-1], w'[2m]) with w'[-1] = w'[KP] = 0, and
+    // no window pair is ever re-aligned.  V[m] is formed at its step (one
+    // v_alignbit for RW dot2) rather than held for the tile, which keeps
+    // the tap registers to the NP pairs of W.
+    // The window is loaded per 16-step quarter and the steps are fenced in
+    // order, which keeps the live set to one quarter (otherwise the compiler
+    // runs each accumulator's whole chain in turn and holds the whole
+    // window).  Each fence also passes through the next step's tap pair, so
+    // that step's V cannot be formed early (or hoisted out of the sweep).
     constexpr int MQ = G::NP >= 16 ? 16 : G::NP;  // tap pairs per quarter
     constexpr int EQ = MQ + G::RW / 2;            // window pairs per quarter
     static_assert(EQ % 4 == 0, "window quarters are whole b128 loads");
@@ -355,13 +385,14 @@ __global__ __launch_bounds__(FirGeom<K>::NT) void fir_prefill_kernel(FirArgs p) 
       uint32_t E[EQ];
 #pragma unroll
       for (int q = 0; q < EQ / 4; ++q) {
-        const uint4 v = *reinterpret_cast<const uint4 *>(
-            &ring[lane][(pbase + 2 * m0 + 8 * q) & (G::RING - 1)]);
+        const uint4 v = *reinterpret_cast<const uint4 *>(&ring[lane][G::at(pbase + 2 * m0 + 8 * q)]);
         E[4 * q] = v.x; E[4 * q + 1] = v.y; E[4 * q + 2] = v.z; E[4 * q + 3] = v.w;
       }
 #pragma unroll
       for (int m = 0; m < MQ; ++m) {
-        const uint32_t wm = W[m0 + m], vm = V[m0 + m];
+        const int mm = m0 + m;
+        const uint32_t wm = W[mm];
+        const uint32_t vm = mm == 0 ? (W[0] << 16) : __builtin_amdgcn_alignbit(W[mm], W[mm - 1], 16);
 #pragma unroll
         for (int j = 0; j < G::RW / 2; ++j) {
           acc[2 * j] = dot2(E[m + j], vm, acc[2 * j]);
@@ -371,23 +402,35 @@ __global__ __launch_bounds__(FirGeom<K>::NT) void fir_prefill_kernel(FirArgs p) 
         // their order, so step m+1 cannot start before step m is done.
 #pragma unroll
         for (int r = 0; r < G::RW; ++r) asm volatile("" : "+v"(acc[r]));
+        if (mm + 1 < G::NP) asm volatile("" : "+v"(W[mm + 1]));
       }
       if (m0 + MQ == G::NP) {
+        const uint32_t vl = W[G::NP - 1] >> 16;
 #pragma unroll
-        for (int j = 0; j < G::RW / 2; ++j) acc[2 * j] = dot2(E[MQ + j], V[G::NP], acc[2 * j]);
+        for (int j = 0; j < G::RW / 2; ++j) acc[2 * j] = dot2(E[MQ + j], vl, acc[2 * j]);
+      }
+    }
+
+    // hcm waits for the next sub-tile's rows (issued before its long FIR)
+    // here, while no store is outstanding: stores count in vmcnt too, so a
+    // wait after the epilogue also waits for the output rows to be
+    // acknowledged.  hcs, whose FIR is short, measures faster waiting after
+    // its stores.
+    constexpr bool EARLY_LAND = K > 8;
+    if constexpr (FUSED && EARLY_LAND) {
+      if (more) {
+        land();
+        fix(s0 + G::RS - 2);
       }
     }
 
     // ---- epilogue on row pairs: bf16(y) [+ D*u] then * x2.
-    uint32_t xq[G::RW / 2], uq[G::RW / 2];
-    if constexpr (FUSED) {
+    uint32_t uq[G::RW / 2];
+    if constexpr (HAS_D) {
 #pragma unroll
       for (int q = 0; q < G::RW / 8; ++q) {
-        const uint4 c4 =
-            *reinterpret_cast<const uint4 *>(&ring[lane][(pbase + G::KP + 8 * q) & (G::RING - 1)]);
+        const uint4 c4 = *reinterpret_cast<const uint4 *>(&ring[lane][G::at(pbase + G::KP + 8 * q)]);
         uq[4 * q] = c4.x; uq[4 * q + 1] = c4.y; uq[4 * q + 2] = c4.z; uq[4 * q + 3] = c4.w;
-        const uint4 a4 = *reinterpret_cast<const uint4 *>(&x2s[lane][wave * G::RW + 8 * q]);
-        xq[4 * q] = a4.x; xq[4 * q + 1] = a4.y; xq[4 * q + 2] = a4.z; xq[4 * q + 3] = a4.w;
       }
     }
     float dval = 0.0f;
@@ -416,13 +459,13 @@ __global__ __launch_bounds__(FirGeom<K>::NT) void fir_prefill_kernel(FirArgs p) 
       if (full || (trow + r + (odd ? 1 : 0) < S.t_end && cpair < p.H))
         *reinterpret_cast<uint32_t *>(orow) = dw;
     }
-    if constexpr (FUSED) {
+    if constexpr (FUSED && !EARLY_LAND) {
       if (more) {
         land();
         fix(s0 + G::RS - 2);
       }
     }
-    __syncthreads();  // next produce may overwrite ring / x2s; zst committed
+    __syncthreads();  // next produce may overwrite the ring; zst committed
   }
 }
 
