@@ -24,7 +24,9 @@
 // Lanes run along channels (coalesced rows); a workgroup owns 256 channels
 // (4 waves) and sweeps its tile in 8-row sub-tiles staged into LDS with
 // direct-to-LDS loads, double-buffered so the next sub-tile lands while the
-// current one computes.
+// current one computes.  Each wave stages, patches and reads only its own 64
+// channels (a 384-byte slice of every z row), so the waves never wait for
+// each other: the sweep has no barrier.
 #include <type_traits>
 
 #include "featurize.h"
@@ -55,15 +57,20 @@ constexpr int HCL_RS = 8;      // rows per sub-tile (8: three waves per SIMD in 
 constexpr int HCL_TILE_ALIGN = 16;  // the documented block_t granularity
 static_assert(HCL_TILE_ALIGN % HCL_RS == 0, "tiles are whole sub-tiles");
 constexpr int HCL_ZROWS = HCL_RS + 2;
-constexpr int HCL_ZPITCH = 3 * HCL_CH;  // bf16 per staged row, unpadded
+constexpr int HCL_WROW = 3 * 64;        // bf16 per staged row of one wave, unpadded
+constexpr int HCL_WCH = HCL_ZROWS * HCL_WROW / 8;  // 16-byte chunks per wave stage (240)
+constexpr int HCL_WINS = (HCL_WCH + 63) / 64;      // wave instructions per stage (4)
+constexpr int HCL_WBUF = HCL_WINS * 512;           // bf16 per wave buffer (whole 1 KB loads)
 
 template <int PHASE>
-__global__ __launch_bounds__(256) void hcl_scan_kernel(HclArgs p) {
-  // Two staging buffers (distinct variables, so reading one never waits on
-  // the direct-to-LDS loads still landing in the other): sub-tile i + 1 is
-  // loaded while sub-tile i computes.
-  __shared__ __align__(16) bf16_t zs0[HCL_ZROWS][HCL_ZPITCH];
-  __shared__ __align__(16) bf16_t zs1[HCL_ZROWS][HCL_ZPITCH];
+__global__ __launch_bounds__(256, PHASE == 3 ? 4 : 5) void hcl_scan_kernel(HclArgs p) {
+  // Two staging buffers per wave (distinct variables, so reading one never
+  // waits on the direct-to-LDS loads still landing in the other): sub-tile
+  // i + 1 is loaded while sub-tile i computes.  Chunk i of a wave's stage
+  // (16 bytes: row i / 24, column i % 24 of its slice) sits at bf16 offset
+  // 8 i, so a staged row is 192 bf16 of (x2, x1, v) triples, lane-ordered.
+  __shared__ __align__(16) bf16_t zs0[4][HCL_WBUF];
+  __shared__ __align__(16) bf16_t zs1[4][HCL_WBUF];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -91,51 +98,57 @@ __global__ __launch_bounds__(256) void hcl_scan_kernel(HclArgs p) {
   }
   const float dval = PHASE == 3 ? bf2f(p.D[cl]) : 0.0f;
   const bool vec_z = (c0 + HCL_CH <= p.H) && (p.sz % 8 == 0) &&
-                     ((reinterpret_cast<uintptr_t>(p.z) & 15) == 0);
+                     ((reinterpret_cast<uintptr_t>(p.z) & 15) == 0) &&
+                     p.sz * HCL_ZROWS < (int64_t(1) << 30);  // 32-bit byte offsets
   const bf16_t *conv = init ? p.cs + blk * p.cs0 : nullptr;
-
-  constexpr int ZCH = HCL_ZROWS * (HCL_ZPITCH / 8);  // 16-byte chunks per stage
-  constexpr int ZW = (ZCH + 63) / 64;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  // Rows [rs, rs + HCL_ZROWS) of the tile: `prefetch` issues direct-to-LDS
-  // loads for the interior rows; `fix` (after they land) writes the rows the
-  // loads skip element by element: the short filter's left context (conv
-  // window when continuing, else zero) and every row when z is not 16-byte
-  // addressable.  Rows past the tile end are never read.
+  const int cw0 = 3 * (c0 + 64 * wave);  // first z column of this wave's slice
+  // Rows [rs, rs + HCL_ZROWS) of the tile, this wave's slice: `prefetch`
+  // issues direct-to-LDS loads for the interior rows; `fix` (after they land)
+  // writes the rows the loads skip element by element: the short filter's
+  // left context (conv window when continuing, else zero) and every row when
+  // z is not 16-byte addressable.  Rows past the tile end are never read.
+  // The per-lane offsets are recomputed at every prefetch from the lane id,
+  // passed through an empty asm so that the compiler cannot hoist them: held
+  // across the sweep they are the first values spilled, and reloading a
+  // spill waits for the loads already in flight.
   auto prefetch = [&](auto buf, int rs) {
-    bf16_t(*zst)[HCL_ZPITCH] = decltype(buf)::value ? zs1 : zs0;
+    bf16_t *zw = (decltype(buf)::value ? zs1 : zs0)[wave];
     if (!vec_z) return;
+    const char *base = reinterpret_cast<const char *>(p.z + (int64_t)rs * p.sz + cw0);
+    const bool interior = rs >= a && rs + HCL_ZROWS <= t_end;  // uniform
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
 #pragma unroll
-    for (int j = 0; j < (ZW + 3) / 4; ++j) {
-      const int cw = wave + 4 * j;
-      if (cw >= ZW) break;
-      const int i = cw * 64 + lane;
-      const int row = i / (HCL_ZPITCH / 8), col = i - (HCL_ZPITCH / 8) * row;
-      const int t = rs + row;
-      if (i < ZCH && t >= a && t < t_end)
+    for (int j = 0; j < HCL_WINS; ++j) {
+      const int i = 64 * j + ln, row = i / 24;
+      bool ok = i < HCL_WCH;
+      if (!interior) ok = ok && rs + row >= a && rs + row < t_end;
+      const uint32_t o = 2u * static_cast<uint32_t>(row * static_cast<int>(p.sz) + 8 * (i - 24 * row));
+      if (ok)
         __builtin_amdgcn_global_load_lds(
-            reinterpret_cast<const uint4 *>(p.z + (int64_t)t * p.sz + 3 * c0) + col,
-            (__attribute__((address_space(3))) void *)(&zst[0][0] + cw * 512), 16, 0, 0);
+            reinterpret_cast<const uint4 *>(base + o),
+            (__attribute__((address_space(3))) void *)(zw + 512 * j), 16, 0, 0);
     }
   };
   auto fix = [&](auto buf, int rs) {
-    bf16_t(*zst)[HCL_ZPITCH] = decltype(buf)::value ? zs1 : zs0;
+    bf16_t *zw = (decltype(buf)::value ? zs1 : zs0)[wave];
     if (vec_z && rs >= a) return;  // uniform: nothing to patch
 #pragma unroll 1
-    for (int i = tid; i < ZCH; i += 256) {
-      const int row = i / (HCL_ZPITCH / 8), col = i - (HCL_ZPITCH / 8) * row;
+    for (int i = lane; i < HCL_WCH; i += 64) {
+      const int row = i / 24, col = i - 24 * row;
       const int t = rs + row;
       const bool inside = t >= a && t < t_end;
       if (vec_z && inside) continue;
 #pragma unroll 1
       for (int q = 0; q < 8; ++q) {
-        const int ch = 3 * c0 + 8 * col + q;
+        const int ch = cw0 + 8 * col + q;
         bf16_t b = 0;
         if (ch < 3 * p.H) {
           if (inside) b = p.z[(int64_t)t * p.sz + ch];
           else if (conv && t < a && t >= a - 2) b = conv[ch * p.cs1 + (t - a + 2) * p.cs2];
         }
-        zst[row][8 * col + q] = b;
+        zw[8 * i + q] = b;
       }
     }
   };
@@ -145,7 +158,7 @@ __global__ __launch_bounds__(256) void hcl_scan_kernel(HclArgs p) {
   // FULL: all HCL_RS rows are inside the tile, so no row is checked (a
   // per-row condition would make the compiler copy the 16 states around it).
   auto compute = [&](auto buf, auto full, int s0) {
-    const bf16_t(*zst)[HCL_ZPITCH] = decltype(buf)::value ? zs1 : zs0;
+    const bf16_t *zw = (decltype(buf)::value ? zs1 : zs0)[wave];
     constexpr bool FULL = decltype(full)::value;
     const int nr = FULL ? HCL_RS : min(HCL_RS, t_end - s0);
     // Row pairs (z[k], z[k+1]) of each sub-channel over the staged rows; rows
@@ -155,7 +168,7 @@ __global__ __launch_bounds__(256) void hcl_scan_kernel(HclArgs p) {
     for (int k = 0; k <= HCL_RS; ++k)
 #pragma unroll
       for (int i = PHASE == 3 ? 0 : 1; i < 3; ++i)
-        P[k][i] = pair_bf(zst[k][3 * tid + i], zst[k + 1][3 * tid + i]);
+        P[k][i] = pair_bf(zw[HCL_WROW * k + 3 * lane + i], zw[HCL_WROW * (k + 1) + 3 * lane + i]);
     uint32_t gpk[HCL_RS / 2];
 #pragma unroll
     for (int r = 0; r < HCL_RS; r += 2) {
@@ -216,16 +229,15 @@ __global__ __launch_bounds__(256) void hcl_scan_kernel(HclArgs p) {
     }
   };
 
-  // Sub-tile i lives in buffer i & 1.  Per sub-tile: wait for its loads,
-  // patch its boundary rows, barrier (all waves' data visible; everyone is
-  // done with the other buffer), issue the next sub-tile into the other
-  // buffer, compute.
+  // Sub-tile i lives in buffer i & 1.  Per sub-tile: wait for its loads
+  // (and, by the same count, for this wave's reads of the other buffer),
+  // patch its boundary rows, issue the next sub-tile into the other buffer,
+  // compute.  Every step touches only this wave's buffers.
   using B0 = std::integral_constant<int, 0>;
   using B1 = std::integral_constant<int, 1>;
   auto sub = [&](auto buf, auto nbuf, int s0) {
     __builtin_amdgcn_s_waitcnt(0);
     fix(buf, s0 - 2);
-    __syncthreads();
     if (s0 + HCL_RS < t_end) prefetch(nbuf, s0 + HCL_RS - 2);
     if (s0 + HCL_RS <= t_end)  // uniform
       compute(buf, std::true_type{}, s0);
