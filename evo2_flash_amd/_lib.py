@@ -76,10 +76,36 @@ SIGNATURES = {
         _c_p, _c_i64,                             # workspace, bytes
         _c_i64, _c_i64, _c_i32, _c_p,             # H, L, block_t, stream
     ],
+    "evo2_iir_final_state": [
+        _c_p, _c_i64, _c_i64,                     # seq + strides
+        _c_p, _c_i64, _c_i64, _c_p,               # log_poles + strides, st
+        _c_p, _c_i64,                             # workspace, bytes
+        _c_i64, _c_i64, _c_i32, _c_p,             # H, L, block_t, stream
+    ],
     "evo2_hcl_compute_filter": [
         _c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_i64,  # residues, log_poles + strides
         _c_p, _c_i64, _c_p, _c_i64, _c_i64,           # t, st, h + strides
         _c_i64, _c_i64, _c_i64, _c_p,                 # D, S, L, stream
+    ],
+    "evo2_causal_conv1d_update": [
+        _c_p, _c_i64, _c_i64,                     # x + strides (row, channel)
+        _c_p, _c_i64, _c_i64, _c_i64,             # conv_state + strides
+        _c_p, _c_i64, _c_i64, _c_i32,             # w + strides, K
+        _c_p, _c_i32,                             # bias, activation
+        _c_p, _c_i64, _c_i32,                     # indices, stride, pad_slot_id
+        _c_p, _c_i64, _c_i64,                     # out + strides (row, channel)
+        _c_i64, _c_i64, _c_i64, _c_p,             # B, dim, num_blocks, stream
+    ],
+    "evo2_causal_conv1d_fn": [
+        _c_p, _c_i64, _c_i64,                     # x + strides (channel, row)
+        _c_p, _c_i64, _c_i64, _c_i32,             # w + strides, K
+        _c_p, _c_i32,                             # bias, activation
+        _c_p, _c_i64, _c_i64, _c_i64,             # conv_states + strides
+        _c_p,                                     # has_initial_state
+        _c_p, _c_i64, _c_i32,                     # cache_indices, stride, pad_slot_id
+        _c_p, _c_i64,                             # query_start_loc, nseq
+        _c_p, _c_i64, _c_i64,                     # out + strides (channel, row)
+        _c_i64, _c_i64, _c_i64, _c_p,             # T, dim, num_blocks, stream
     ],
     "evo2_fp8_quantize": [_c_p, _c_i64, _c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_p],
     "evo2_rms_norm": [

@@ -454,7 +454,7 @@ __global__ __launch_bounds__(256) void iir_scan_kernel(IirArgs p) {
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     pole[i] = expf(p.lp[(int64_t)c * p.l0 + i * p.l1]);
-    res[i] = p.res[(int64_t)c * p.r0 + i * p.r1];
+    res[i] = PHASE == 3 ? p.res[(int64_t)c * p.r0 + i * p.r1] : 0.0f;
     s[i] = PHASE == 3 ? p.work[((int64_t)j * p.H + c) * 16 + i] : 0.0f;
   }
   const float *xr = p.x + (int64_t)c * p.xh;
@@ -551,6 +551,37 @@ extern "C" int evo2_iir_segment(const float *seq, int64_t xh, int64_t xl,
     rc = check_launch("iir_segment phase 3");
   }
   return rc;
+}
+
+extern "C" int evo2_iir_final_state(const float *seq, int64_t xh, int64_t xl,
+                                    const float *log_poles, int64_t l0, int64_t l1, float *st,
+                                    float *workspace, int64_t workspace_bytes,
+                                    int64_t H, int64_t L, int32_t block_t, void *stream) {
+  if (H <= 0 || L < 0 || block_t <= 0)
+    return fail(EVO2_ERR_INVALID, "iir_final_state: bad sizes H=%lld L=%lld block_t=%d",
+                (long long)H, (long long)L, block_t);
+  const int64_t ntiles = cdiv(L, block_t);
+  if (!seq || !log_poles || !st || (ntiles && !workspace))
+    return fail(EVO2_ERR_INVALID, "iir_final_state: null pointer argument");
+  if (workspace_bytes < evo2_hcl_workspace_bytes(ntiles, H))
+    return fail(EVO2_ERR_INVALID, "iir_final_state: workspace too small");
+  if (ntiles > 65535 || L > 0x7fffffff)
+    return fail(EVO2_ERR_UNSUPPORTED, "iir_final_state: L=%lld too long for block_t=%d",
+                (long long)L, block_t);
+  hipStream_t strm = static_cast<hipStream_t>(stream);
+  // the scan's first two phases: tile end states, then the carry whose
+  // value after the last tile is the final state (no residues, no y)
+  IirArgs a{seq, xh, xl, nullptr, 0, 0, log_poles, l0, l1, nullptr, 0, 0, nullptr, 0, 0, st,
+            workspace, static_cast<int>(H), static_cast<int>(L), block_t,
+            static_cast<int>(ntiles)};
+  if (ntiles) {
+    dim3 grid(static_cast<unsigned>(ntiles), static_cast<unsigned>(cdiv(H, 256)));
+    hipLaunchKernelGGL(iir_scan_kernel<1>, grid, dim3(256), 0, strm, a);
+    int rc = check_launch("iir_final_state phase 1");
+    if (rc) return rc;
+  }
+  hipLaunchKernelGGL(iir_carry_kernel, dim3(static_cast<unsigned>(cdiv(H, 4))), dim3(256), 0, strm, a);
+  return check_launch("iir_final_state phase 2");
 }
 
 extern "C" int evo2_hcl_compute_filter(const float *residues, int64_t r0, int64_t r1,

@@ -92,6 +92,35 @@ def iir_segment(seq, res, lp, s_prev, force_torch=False, block_t=None):
     return y, st
 
 
+def iir_final_state(seq, lp, blk=None, block_t=None):
+    """s[h, s] = sum_t seq[h, t] * p[h, s]^(L-1-t), p = exp(lp): the final
+    state of one LI segment started from zero (triton_prefill.py:351-387).
+
+    seq: (H, L) fp32, any strides (the mixer passes a token-major view).
+    lp: (H, 16) log-poles.  `blk` (the reference's torch blocking of the state
+    channels, which fixes torch's summation order) is accepted and unused:
+    the state is the scan's, s_t = p*s_{t-1} + x_t in fp32, equal to the
+    closed form within fp32 rounding rather than bit for bit.  Returns (H, 16)
+    fp32, or None where the reference does too (a CPU or non-fp32 `seq`: the
+    caller's torch path).
+    """
+    if not (seq.is_cuda and seq.dtype == torch.float32):
+        return None
+    _lib.require_device(lp)
+    H, L = seq.shape
+    if lp.shape != (H, 16):
+        raise ValueError("the LI scan takes 16 poles per channel")
+    lp = lp.float()
+    bt = int(block_t or hcl_block_t(L, H))
+    ntiles = (L + bt - 1) // bt
+    st = torch.empty(H, 16, dtype=torch.float32, device=seq.device)
+    work, nbytes = _workspace(ntiles, H, seq.device)
+    _lib.call("evo2_iir_final_state",
+              _lib.ptr(seq), *seq.stride(), _lib.ptr(lp), *lp.stride(), _lib.ptr(st),
+              _lib.ptr(work), nbytes, H, L, bt, _lib.stream_of(seq))
+    return st
+
+
 def hyena_hcl_prefill(z, short_w, conv_state, residues, log_poles, ssm, D, seq_table, blocks,
                       tile_table, tile_start, block_t):
     """g = bf16(bf16(bf16(y) + bf16(u*D)) * x2) over packed prefill rows of z,

@@ -1,0 +1,165 @@
+"""vLLM's short causal depthwise convolution entry points on this build's kernels.
+
+The reference's mixers run the K=3 short filter through two vLLM kernels
+(evo2_flash/mixers.py:1121-1208):
+
+    causal_conv1d_fn(z_p.T, w, None, activation=None, conv_states=conv_state,
+                     has_initial_state=..., cache_indices=..., metadata=m,
+                     query_start_loc=...)                       # prefill rows
+    causal_conv1d_update(z_d, conv_state, w, None, activation=None,
+                         conv_state_indices=...)                # decode rows
+
+These functions take the same arguments and mutate the same window view
+(blocks, dim, K-1) (the mixers' dim-first view of the (blocks, 2, 3H)
+storage).  Outputs are rounded as the reference documents for vLLM's update
+kernel (triton_decode.py:10-11): each product rounded to bf16, an fp32 sum
+from the bias (or 0), oldest input first, bf16 out.  The mixers of this
+build fuse the short filter into their own kernels and do not call these;
+they are the drop-in for callers that bind the vLLM entry points.
+
+Not supported (NotImplementedError): the speculative form of the update
+(`num_accepted_tokens`, `query_start_loc`, ...) and prefix-caching block
+pointers, whose state conventions no reference file pins.
+"""
+
+import torch
+
+from . import _lib
+
+PAD_SLOT_ID = -1
+
+_UNSUPPORTED_UPDATE = ("num_accepted_tokens", "query_start_loc", "block_idx_last_scheduled_token",
+                       "initial_state_idx")
+_UNSUPPORTED_FN = ("block_idx_first_scheduled_token", "block_idx_last_scheduled_token",
+                   "initial_state_idx", "num_computed_tokens")
+
+
+def _activation_code(activation):
+    if activation in (None, False):
+        return 0
+    if activation in ("silu", "swish", True):
+        return 1
+    raise NotImplementedError(f"activation {activation!r} (None or 'silu' only)")
+
+
+def _check_common(fn, x, weight, bias, conv_state):
+    if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+        raise NotImplementedError(f"{fn}: bf16 inputs and weights only")
+    if weight.dim() != 2 or weight.shape[1] not in (2, 3, 4):
+        raise ValueError(f"{fn}: weight must be (dim, K) with K in 2..4, got {tuple(weight.shape)}")
+    dim, K = weight.shape
+    if bias is not None and (bias.shape != (dim,) or bias.dtype != torch.bfloat16):
+        raise ValueError(f"{fn}: bias must be ({dim},) bf16")
+    if conv_state is not None:
+        if conv_state.dtype != torch.bfloat16 or conv_state.dim() != 3:
+            raise ValueError(f"{fn}: conv state must be a (blocks, dim, K-1) bf16 view")
+        if conv_state.shape[1] != dim or conv_state.shape[2] < K - 1:
+            raise ValueError(f"{fn}: conv state {tuple(conv_state.shape)} does not fit dim={dim}, K={K}")
+    return dim, K
+
+
+def _index_table(idx, n, fn, name):
+    if idx is None:
+        return None, 0
+    if idx.dim() == 2:  # vLLM's (batch, max_query_len) slot matrix: column 0
+        idx = idx[:, 0]
+    if idx.dim() != 1 or idx.shape[0] < n:
+        raise ValueError(f"{fn}: {name} must hold one slot per sequence")
+    if idx.dtype != torch.int32:
+        idx = idx.to(torch.int32)
+    return idx, idx.stride(0)
+
+
+def causal_conv1d_update(x, conv_state, weight, bias=None, activation=None,
+                         conv_state_indices=None, pad_slot_id=PAD_SLOT_ID, **speculative):
+    """One new row per sequence: x (B, dim) bf16 -> out (B, dim) bf16.
+
+    conv_state (blocks, dim, >=K-1) bf16 view, updated in place for each row's
+    slot conv_state_indices[b] (slot b when None); rows whose slot is
+    pad_slot_id write no state and output zeros.  (B, dim, 1) inputs are
+    accepted and returned in that shape.
+    """
+    fn = "causal_conv1d_update"
+    act = _activation_code(activation)
+    for k in _UNSUPPORTED_UPDATE:
+        if speculative.pop(k, None) is not None:
+            raise NotImplementedError(f"{fn}: speculative argument {k!r} is not supported")
+    speculative.pop("max_query_len", None)
+    speculative.pop("validate_data", None)
+    if speculative:
+        raise TypeError(f"{fn}: unexpected arguments {sorted(speculative)}")
+    squeeze = x.dim() == 3
+    if squeeze:
+        if x.shape[2] != 1:
+            raise NotImplementedError(f"{fn}: one token per sequence only (got seqlen {x.shape[2]})")
+        x = x[..., 0]
+    _lib.require_device(x, conv_state, weight, bias, conv_state_indices)
+    dim, K = _check_common(fn, x, weight, bias, conv_state)
+    if x.dim() != 2 or x.shape[1] != dim:
+        raise ValueError(f"{fn}: x must be (B, {dim})")
+    B = x.shape[0]
+    idx, sidx = _index_table(conv_state_indices, B, fn, "conv_state_indices")
+    out = torch.empty(B, dim, dtype=torch.bfloat16, device=x.device)
+    _lib.call("evo2_causal_conv1d_update",
+              _lib.ptr(x), x.stride(0), x.stride(1),
+              _lib.ptr(conv_state), *conv_state.stride(),
+              _lib.ptr(weight), weight.stride(0), weight.stride(1), K,
+              _lib.ptr(bias), act,
+              _lib.ptr(idx), sidx, int(pad_slot_id),
+              _lib.ptr(out), out.stride(0), out.stride(1),
+              B, dim, conv_state.shape[0], _lib.stream_of(x))
+    return out.unsqueeze(-1) if squeeze else out
+
+
+def causal_conv1d_fn(x, weight, bias=None, conv_states=None, query_start_loc=None,
+                     cache_indices=None, has_initial_state=None, activation="silu",
+                     pad_slot_id=PAD_SLOT_ID, metadata=None, validate_data=False, **prefix):
+    """Packed prefill segments: x (dim, T) bf16 -> out (dim, T) bf16.
+
+    Segment j is columns query_start_loc[j] .. query_start_loc[j+1] - 1 of x;
+    its window is conv_states[cache_indices[j]] (slot j when None), read as
+    left context when has_initial_state[j] and rewritten with the segment's
+    last K-1 inputs.  `metadata` (vLLM's cached-buffer object) is accepted
+    and unused.  The output is a transposed view of a token-major (T, dim)
+    buffer, the orientation the mixers transpose back to.
+    """
+    fn = "causal_conv1d_fn"
+    act = _activation_code(activation)
+    for k in _UNSUPPORTED_FN:
+        if prefix.pop(k, None) is not None:
+            raise NotImplementedError(f"{fn}: prefix-caching argument {k!r} is not supported")
+    prefix.pop("block_size_to_align", None)
+    if prefix:
+        raise TypeError(f"{fn}: unexpected arguments {sorted(prefix)}")
+    if query_start_loc is None:
+        raise NotImplementedError(f"{fn}: query_start_loc is required (packed segments)")
+    _lib.require_device(x, weight, bias, conv_states, query_start_loc, cache_indices,
+                        has_initial_state)
+    dim, K = _check_common(fn, x, weight, bias, conv_states)
+    if x.dim() != 2 or x.shape[0] != dim:
+        raise ValueError(f"{fn}: x must be ({dim}, T)")
+    T = x.shape[1]
+    qsl = query_start_loc.to(torch.int32).contiguous()
+    nseq = qsl.shape[0] - 1
+    idx, sidx = _index_table(cache_indices, nseq, fn, "cache_indices")
+    init = None
+    if has_initial_state is not None:
+        if has_initial_state.shape[0] < nseq:
+            raise ValueError(f"{fn}: has_initial_state must hold one flag per sequence")
+        init = has_initial_state.to(torch.uint8).contiguous()
+    buf = torch.empty(T, dim, dtype=torch.bfloat16, device=x.device)
+    out = buf.t()
+    cs = conv_states
+    _lib.call("evo2_causal_conv1d_fn",
+              _lib.ptr(x), x.stride(0), x.stride(1),
+              _lib.ptr(weight), weight.stride(0), weight.stride(1), K,
+              _lib.ptr(bias), act,
+              _lib.ptr(cs), *(cs.stride() if cs is not None else (0, 0, 0)),
+              _lib.ptr(init), _lib.ptr(idx), sidx, int(pad_slot_id),
+              _lib.ptr(qsl), max(nseq, 0),
+              _lib.ptr(out), out.stride(0), out.stride(1),
+              T, dim, cs.shape[0] if cs is not None else 0, _lib.stream_of(x))
+    return out
+
+
+__all__ = ["causal_conv1d_fn", "causal_conv1d_update", "PAD_SLOT_ID"]

@@ -167,6 +167,20 @@ int evo2_iir_segment(const float *seq, int64_t xh, int64_t xl,
                      int64_t H, int64_t L, int32_t block_t, void *stream);
 
 /*
+ * Final state only of one LI prefill segment started from zero:
+ * st[h, s] = sum_t seq[h, t] p[h, s]^(L-1-t), p = exp(log_poles), evaluated
+ * as the recurrence s_t = p*s_{t-1} + x_t in fp32 (tile end states, then a
+ * carry scan).  seq (H, L) fp32 with any strides; st (H, 16) contiguous;
+ * workspace of evo2_hcl_workspace_bytes(cdiv(L, block_t), H) bytes.
+ *
+ * Replaces iir_final_state (evo2_flash/triton_prefill.py:351-387).
+ */
+int evo2_iir_final_state(const float *seq, int64_t xh, int64_t xl,
+                         const float *log_poles, int64_t l0, int64_t l1, float *st,
+                         float *workspace, int64_t workspace_bytes,
+                         int64_t H, int64_t L, int32_t block_t, void *stream);
+
+/*
  * Modal filter h[d, l] = sum_s residues[d, s] * exp(log_poles[d, s] * t[l]).
  *
  * Replaces hcl_compute_filter / _hcl_compute_filter_kernel
@@ -176,6 +190,53 @@ int evo2_hcl_compute_filter(const float *residues, int64_t r0, int64_t r1,
                             const float *log_poles, int64_t l0, int64_t l1,
                             const float *t, int64_t st, float *h, int64_t h0, int64_t h1,
                             int64_t D, int64_t S, int64_t L, void *stream);
+
+/*
+ * Short causal depthwise convolution, one new row per sequence (decode):
+ *   out[b, c] = bf16(act(((bias[c] + r(s0 w0)) + r(s1 w1)) + ... + r(x[b, c] w[K-1])))
+ * with r() rounding a product to bf16, (s0 .. s_{K-2}) the window of slot
+ * indices[b] (oldest first), which then becomes (s1 .. s_{K-2}, x[b, c]).
+ *   x (B, dim) bf16 (strides xb, xc); conv_state (blocks, dim, >= K-1) bf16
+ *   view; w (dim, K) bf16; bias (dim,) bf16 or NULL; activation 0 = none,
+ *   1 = SiLU; indices (B,) int32 (stride sidx) or NULL for slot b; a row whose
+ *   slot is pad_slot_id or outside [0, num_blocks) gets a zero output and
+ *   touches no state.  K in {2, 3, 4}.
+ *
+ * Replaces vLLM's causal_conv1d_update as the reference's mixers call it for
+ * the K=3 short filter (evo2_flash/mixers.py:1194-1204; rounding as
+ * triton_decode.py:10-11, 44-53 states it).
+ */
+int evo2_causal_conv1d_update(const void *x, int64_t xb, int64_t xc,
+                              void *conv_state, int64_t cs0, int64_t cs1, int64_t cs2,
+                              const void *w, int64_t w0, int64_t w1, int32_t K,
+                              const void *bias, int32_t activation,
+                              const int32_t *indices, int64_t sidx, int32_t pad_slot_id,
+                              void *out, int64_t ob, int64_t oc,
+                              int64_t B, int64_t dim, int64_t num_blocks, void *stream);
+
+/*
+ * Short causal depthwise convolution over packed prefill segments: segment j
+ * is rows [query_start_loc[j], query_start_loc[j + 1]) of x, with slot
+ * cache_indices[j] (or j when NULL).  Its left context is the slot's window
+ * when has_initial_state[j] (else zeros); after the launch the window holds
+ * the segment's last K-1 inputs of cat(window or zeros, segment).  Outputs
+ * are rounded as in evo2_causal_conv1d_update; rows outside every segment
+ * are zero.  x (dim, T) bf16 with strides (xc, xt); out likewise (oc, ot);
+ * conv_states NULL skips every window read and write.  Empty segments and
+ * padding slots touch no window.
+ *
+ * Replaces vLLM's causal_conv1d_fn as the reference's mixers call it for the
+ * K=3 short filter (evo2_flash/mixers.py:1138-1150).
+ */
+int evo2_causal_conv1d_fn(const void *x, int64_t xc, int64_t xt,
+                          const void *w, int64_t w0, int64_t w1, int32_t K,
+                          const void *bias, int32_t activation,
+                          void *conv_states, int64_t cs0, int64_t cs1, int64_t cs2,
+                          const uint8_t *has_initial_state,
+                          const int32_t *cache_indices, int64_t sidx, int32_t pad_slot_id,
+                          const int32_t *query_start_loc, int64_t nseq,
+                          void *out, int64_t oc, int64_t ot,
+                          int64_t T, int64_t dim, int64_t num_blocks, void *stream);
 
 /*
  * Static per-tensor activation quantisation for the fp8 projections:

@@ -19,6 +19,7 @@ __all__ = [
     "rms_norm", "quantize_input", "fp8_linear_dequant", "prefill_tables",
     "fir_decode_snapshots", "iir_decode_snapshots", "fir_verify_emulated",
     "iir_verify_emulated", "STATE_ACC_BUDGET", "fast_accum_mm", "fp8_linear_fast_accum",
+    "causal_conv1d_update_ref", "causal_conv1d_ref", "iir_final_state_recurrence",
 ]
 
 # mixers.py:72-74: bound on the (H, blk, L) temporary of the LI final state.
@@ -197,6 +198,94 @@ def short_conv_update(z, short_w, conv_state, slots):
         conv_state[blk, :, 0] = conv_state[blk, :, 1]
         conv_state[blk, :, 1] = z[b].to(conv_state.dtype)
     return out
+
+
+def _silu(acc):
+    return acc / (1.0 + torch.exp(-acc))
+
+
+def causal_conv1d_update_ref(x, conv_state, w, bias=None, activation=None, slots=None,
+                             pad_slot_id=-1):
+    """vLLM's causal_conv1d_update as the mixers call it (mixers.py:1194-1204),
+    with the rounding the reference states for it (triton_decode.py:10-11):
+    acc = bias (or 0), then + bf16(s_k w_k) over the window oldest first and
+    + bf16(x w_{K-1}); optional SiLU; bf16 out.  The slot's window shifts in
+    x.  A row whose slot is pad_slot_id (or outside the pool) outputs zeros
+    and touches no state.  x (B, dim); w (dim, K); conv_state (blocks, dim,
+    >=K-1) updated in place.  Returns (B, dim) fp32 holding bf16 values.
+    """
+    B, dim = x.shape
+    K = w.shape[1]
+    wf = w.float()
+    b0 = bias.float() if bias is not None else torch.zeros(dim)
+    out = torch.zeros(B, dim, dtype=torch.float32)
+    for b in range(B):
+        blk = int(slots[b]) if slots is not None else b
+        if blk == pad_slot_id or not 0 <= blk < conv_state.shape[0]:
+            continue
+        s = conv_state[blk, :, : K - 1].float()
+        xb = x[b].float()
+        acc = b0.clone()
+        for k in range(K - 1):
+            acc = acc + bf(s[:, k] * wf[:, k])
+        acc = acc + bf(xb * wf[:, K - 1])
+        if activation:
+            acc = _silu(acc)
+        out[b] = bf(acc)
+        new = torch.cat([s[:, 1:], xb.unsqueeze(1)], dim=1)
+        conv_state[blk, :, : K - 1] = new.to(conv_state.dtype)
+    return out
+
+
+def causal_conv1d_ref(x_p, w, bias, activation, qsl, slots, has_init, state, pad_slot_id=-1):
+    """vLLM's causal_conv1d_fn over packed prefill segments as the mixers call
+    it (mixers.py:1138-1150), with the update kernel's rounding (see
+    `causal_conv1d_update_ref`): each output sums bf16-rounded products of its
+    K inputs, oldest first, from the bias.  Segment j is rows qsl[j]..qsl[j+1]
+    of x_p (T, dim); its left context is its slot's window when has_init[j]
+    (zeros otherwise), and the window becomes the last K-1 inputs of
+    cat(window or zeros, segment).  Empty segments and padding slots touch no
+    state; rows outside every segment output zeros; state None skips every
+    window.  Returns (T, dim) fp32 holding bf16 values.
+    """
+    T, dim = x_p.shape
+    K = w.shape[1]
+    wf = w.float()
+    b0 = bias.float() if bias is not None else torch.zeros(dim)
+    out = torch.zeros(T, dim, dtype=torch.float32)
+    for j in range(len(qsl) - 1):
+        a, e = int(qsl[j]), int(qsl[j + 1])
+        if e <= a:
+            continue
+        blk = int(slots[j]) if slots is not None else j
+        valid = state is not None and blk != pad_slot_id and 0 <= blk < state.shape[0]
+        if valid and has_init is not None and bool(has_init[j]):
+            prev = state[blk, :, : K - 1].float()
+        else:
+            prev = torch.zeros(dim, K - 1, dtype=torch.float32)
+        seq = torch.cat([prev, x_p[a:e].transpose(0, 1).float()], dim=1)  # (dim, K-1+n)
+        n = e - a
+        acc = b0.unsqueeze(1).expand(dim, n).clone()
+        for k in range(K):
+            acc = acc + bf(seq[:, k:k + n] * wf[:, k:k + 1])
+        if activation:
+            acc = _silu(acc)
+        out[a:e] = bf(acc).transpose(0, 1)
+        if valid:
+            state[blk, :, : K - 1] = seq[:, -(K - 1):].to(state.dtype)
+    return out
+
+
+def iir_final_state_recurrence(seq, lp):
+    """Final state of s_t = exp(lp) * s_{t-1} + x_t from zero, in float64
+    (the recurrence form of triton_prefill.py:351-387's closed form
+    sum_t x_t p^(L-1-t)).  seq (H, L), lp (H, S).  Returns (H, S) float64."""
+    p = torch.exp(lp.double())
+    s = torch.zeros(lp.shape, dtype=torch.float64)
+    x = seq.double()
+    for t in range(x.shape[1]):
+        s = p * s + x[:, t:t + 1]
+    return s
 
 
 def _hcm_sum(s, wf, u):

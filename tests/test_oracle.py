@@ -660,3 +660,121 @@ def test_fast_accum_close_to_fp32_but_not_equal():
     assert not torch.equal(fa, (a @ b.t()).float())
     with pytest.raises(ValueError):
         oracle.fast_accum_mm(a[:, :40], b[:, :40])
+
+
+# ------------------------------------------------------- short conv entry points
+def test_conv1d_update_ref_known_answer():
+    """Hand-worked: window (1, 2) / (0.5, -1), x = (3, 4), taps and bias exact
+    in bf16, every product exact, so out = (7.5, 2.0); then a case where each
+    product rounds: a = 1 + 2^-7, b = 1 - 2^-8, a*b = 1 + 2^-8 - 2^-15 -> bf16
+    1.0, so three such products give 3.0 (exact products would give
+    bf16(3.0116...) = 3.015625)."""
+    st = torch.tensor([[[1.0, 2.0], [0.5, -1.0]]]).to(torch.bfloat16)
+    w = torch.tensor([[0.5, 0.25, 2.0], [1.5, -0.75, 0.125]]).to(torch.bfloat16)
+    x = torch.tensor([[3.0, 4.0]]).to(torch.bfloat16)
+    out = oracle.causal_conv1d_update_ref(x, st, w, torch.tensor([0.5, 0.0]).to(torch.bfloat16))
+    assert out.tolist() == [[7.5, 2.0]]
+    assert st[0].float().tolist() == [[2.0, 3.0], [-1.0, 4.0]]
+    a, b = 1 + 2 ** -7, 1 - 2 ** -8
+    st = torch.full((1, 1, 2), a).to(torch.bfloat16)
+    out = oracle.causal_conv1d_update_ref(torch.full((1, 1), a).to(torch.bfloat16), st,
+                                          torch.full((1, 3), b).to(torch.bfloat16))
+    assert out.item() == 3.0
+    exact = (torch.tensor(a, dtype=torch.float64) * b * 3).to(torch.bfloat16).item()
+    assert exact == 3.015625
+
+
+def test_conv1d_update_ref_matches_decode_short_filter():
+    """K=3 without bias is the fused decode's short filter, pinned by the
+    decode tests: bitwise equal outputs and windows."""
+    g = torch.Generator().manual_seed(3)
+    dim, B, nb = 96, 5, 8
+    w = (torch.randn(dim, 3, generator=g) * 0.3).to(torch.bfloat16)
+    x = torch.randn(B, dim, generator=g).to(torch.bfloat16)
+    st = torch.randn(nb, dim, 2, generator=g).to(torch.bfloat16)
+    slots = [3, 1, 7, 2, 5]
+    s1, s2 = st.clone(), st.clone()
+    ref = oracle.short_conv_update(x, w, s1, slots)
+    out = oracle.causal_conv1d_update_ref(x, s2, w, slots=slots)
+    assert torch.equal(out, ref) and torch.equal(s1, s2)
+
+
+def _conv_case(seed, lens, dim, K, nb=12):
+    g = torch.Generator().manual_seed(seed)
+    T = sum(lens)
+    x = torch.randn(T, dim, generator=g).to(torch.bfloat16)
+    w = (torch.randn(dim, K, generator=g) * 0.4).to(torch.bfloat16)
+    st = torch.randn(nb, dim, K - 1, generator=g).to(torch.bfloat16)
+    return x, w, st
+
+
+@pytest.mark.parametrize("K", [2, 3, 4])
+def test_conv1d_ref_vs_exact_products(K):
+    """Against the reference's own torch form of the prefill short filter
+    (`depthwise_prefill`, exact fp32 products): same outputs to bf16 rounding
+    of the products, identical windows."""
+    lens, has_init = [7, 0, 1, 40, 2], [1, 0, 1, 0, 1]
+    slots = [4, 9, 2, 6, 11]
+    x, w, st = _conv_case(5, lens, 64, K)
+    s1, s2 = st.clone(), st.clone()
+    q = _qsl(lens)
+    ref = oracle.depthwise_prefill(x, w, q, slots, has_init, s1, K).float()
+    out = oracle.causal_conv1d_ref(x, w, None, None, q, slots, has_init, s2)
+    assert max_rel_err(out, ref) <= 2e-2
+    assert torch.equal(s1, s2)
+
+
+def test_conv1d_ref_impulse_pins_tap_order():
+    K, L, t0 = 4, 12, 5
+    x = torch.zeros(L, 3).to(torch.bfloat16)
+    x[t0] = 1.0
+    g = torch.Generator().manual_seed(1)
+    w = torch.randn(3, K, generator=g).to(torch.bfloat16)
+    out = oracle.causal_conv1d_ref(x, w, None, None, [0, L], [0], [0], None)
+    for j in range(L - t0):
+        want = w[:, K - 1 - j].float() if j < K else torch.zeros(3)
+        assert torch.equal(out[t0 + j], want), j
+    assert torch.equal(out[:t0], torch.zeros(t0, 3))
+
+
+def test_conv1d_ref_one_row_continuation_equals_update():
+    x, w, st = _conv_case(7, [1, 1, 1], 48, 3)
+    bias = torch.linspace(-1, 1, 48).to(torch.bfloat16)
+    s1, s2 = st.clone(), st.clone()
+    slots = [2, 5, 8]
+    a = oracle.causal_conv1d_ref(x, w, bias, None, [0, 1, 2, 3], slots, [1, 1, 1], s1)
+    b = oracle.causal_conv1d_update_ref(x, s2, w, bias, None, slots)
+    assert torch.equal(a, b) and torch.equal(s1, s2)
+
+
+def test_conv1d_ref_split_invariance():
+    L, cut = 23, 9
+    x, w, st = _conv_case(9, [L], 32, 3)
+    s1, s2 = st.clone(), st.clone()
+    y = oracle.causal_conv1d_ref(x, w, None, None, [0, L], [3], [1], s1)
+    ya = oracle.causal_conv1d_ref(x[:cut], w, None, None, [0, cut], [3], [1], s2)
+    yb = oracle.causal_conv1d_ref(x[cut:], w, None, None, [0, L - cut], [3], [1], s2)
+    assert torch.equal(y, torch.cat([ya, yb])) and torch.equal(s1, s2)
+
+
+def test_conv1d_ref_silu_closed_form():
+    st = torch.tensor([[[1.0, 2.0], [0.5, -1.0]]]).to(torch.bfloat16)
+    w = torch.tensor([[0.5, 0.25, 2.0], [1.5, -0.75, 0.125]]).to(torch.bfloat16)
+    x = torch.tensor([[3.0, 4.0]]).to(torch.bfloat16)
+    out = oracle.causal_conv1d_update_ref(x, st, w, torch.tensor([0.5, 0.0]).to(torch.bfloat16),
+                                          "silu")
+    want = torch.nn.functional.silu(torch.tensor([7.5, 2.0])).to(torch.bfloat16).float()
+    assert torch.equal(out[0], want)
+
+
+def test_iir_final_state_recurrence_vs_closed_form():
+    """The float64 recurrence against the reference's closed form
+    sum_t x_t exp(lp (L-1-t)) (oracle.iir_segment, fp32)."""
+    g = torch.Generator().manual_seed(4)
+    H, L, S = 6, 57, 16
+    seq = torch.randn(H, L, generator=g)
+    lp = torch.log(torch.rand(H, S, generator=g) * 0.5 + 0.499)
+    res = torch.randn(H, S, generator=g)
+    _, st = oracle.iir_segment(seq, res, lp, None)
+    rec = oracle.iir_final_state_recurrence(seq, lp)
+    assert torch.allclose(st.double(), rec, rtol=1e-5, atol=1e-5)
