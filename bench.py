@@ -230,8 +230,8 @@ CTX_7B = 8192 + 512   # prompt plus the decode steps of the 7B workload
 
 def bench_model(steps, dev, B=B_DECODE, seed=21):
     """The whole 7B-shaped model at decode (32 layers: 27 Hyena on this
-    build's kernels, 5 attention and every MLP in torch), 64 sequences at
-    positions from 8192 on, rotary base 1e4 with linear scaling 128
+    build's kernels, 5 attention and every MLP in torch), B sequences (64 for
+    the 7B workload) at positions from 8192 on, rotary base 1e4 with linear scaling 128
     (evo2-7b-1m.yml:27-29; the checkpoint's base wins, convert.py:524-570).
     States and KV stand in for the prefilled prompt.  One decode step is one
     HIP graph replay; the positions advance inside the graph."""
@@ -240,7 +240,7 @@ def bench_model(steps, dev, B=B_DECODE, seed=21):
 
     cfg = evo2_7b()
     model = Evo2DecodeModel(cfg, max_batch=B, max_ctx=CTX_7B, device=dev, rope_theta=10000.0,
-                            rope_factor=128.0, name="bench_model")
+                            rope_factor=128.0, name=f"bench_model_b{B}")
     model.init_random(seed, state_scale=0.5, kv_scale=0.5)
     g = torch.Generator(device=dev).manual_seed(seed)
     tok = torch.tensor([65, 67, 71, 84], device=dev)[
@@ -489,6 +489,15 @@ def main(argv=None):
     pre = bench_prefill(max(3, args.steps // 8), dev) if run("prefill", args.no_prefill) else None
     gem = bench_gemm(max(5, args.steps // 4), dev) if run("gemm", args.no_gemm) else None
     mod = bench_model(max(16, args.steps // 2), dev) if run("model", args.no_model) else None
+    if mod:
+        # the reference's one published whole-step figure: a plain decode step
+        # of the 7B model at batch 8 under full CUDA graphs, 7.85 ms on
+        # H100/H200, context length not stated (api.py:384-385)
+        mod["batch8"] = bench_model(max(16, args.steps // 2), dev, B=8)
+        mod["batch8"]["reference"] = {"ms_per_step": 7.85, "hardware": "H100/H200",
+                                      "source": "api.py:384-385",
+                                      "note": "plain decode, whole 7B model, batch 8; "
+                                              "context length not stated"}
     cpu = None if (args.no_cpu or args.only) else _cpu_baseline_decode()
     line = {
         "metric": METRIC,
