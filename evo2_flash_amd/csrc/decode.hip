@@ -378,9 +378,17 @@ __global__ __launch_bounds__(256) void hcm_decode_split_kernel(DecodeArgs a) {
   const int hc = active ? h0 : 0;
   const int64_t b = blockIdx.y;
   const bf16_t *w = static_cast<const bf16_t *>(a.inner);
+  // Taps and window go through buffer descriptors: one lane offset in a
+  // VGPR, the column offset in an SGPR, instead of a live 64-bit address per
+  // access (which held the kernel at 192 VGPRs).  Record counts are the byte
+  // extents, checked on the host to fit 32 bits.
+  const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<bf16_t *>(w), 0,
+      static_cast<int>(WT ? (126 * a.wi1 + a.H) * 2 : ((int64_t)(a.H - 1) * a.wi0 + 128) * 2),
+      0x00020000);
 
-  // Taps stay packed as loaded (bf16 pairs) and are widened at use, which
-  // keeps the kernel at four waves per SIMD.  WT: tw[j][l] = (h0, h0+1) of
+  // Taps stay packed as loaded (bf16 pairs) and are widened at use (145
+  // VGPRs: three waves per SIMD).  WT: tw[j][l] = (h0, h0+1) of
   // tap k; otherwise tw[j][2c], tw[j][2c+1] = taps (4m..4m+3) of channel h0+c.
   // They go out before the slot lookup, the window columns after it.
   uint32_t tw[8][4];
@@ -390,14 +398,18 @@ __global__ __launch_bounds__(256) void hcm_decode_split_kernel(DecodeArgs a) {
 #pragma unroll
       for (int l = 0; l < 4; ++l) {
         const int k = 16 * j + 4 * m + l;
-        tw[j][l] = k < 127 ? *reinterpret_cast<const uint32_t *>(w + (int64_t)k * a.wi1 + hc) : 0u;
+        tw[j][l] = k < 127 ? static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(
+                                 wrs, 2 * hc, static_cast<int>(k * a.wi1 * 2), 0))
+                           : 0u;
       }
     } else {
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
-        const uint2 t = *reinterpret_cast<const uint2 *>(w + (int64_t)(hc + c) * a.wi0 + 16 * j + 4 * m);
-        tw[j][2 * c] = t.x;
-        tw[j][2 * c + 1] = (16 * j + 4 * m + 3 < 127) ? t.y : (t.y & 0xffffu);
+        const auto t = __builtin_amdgcn_raw_buffer_load_b64(
+            wrs, static_cast<int>((hc + c) * a.wi0 * 2), (16 * j + 4 * m) * 2, 0);
+        tw[j][2 * c] = static_cast<uint32_t>(t[0]);
+        tw[j][2 * c + 1] = (16 * j + 4 * m + 3 < 127) ? static_cast<uint32_t>(t[1])
+                                                       : (static_cast<uint32_t>(t[1]) & 0xffffu);
       }
     }
   }
@@ -405,14 +417,26 @@ __global__ __launch_bounds__(256) void hcm_decode_split_kernel(DecodeArgs a) {
   int64_t blk;
   const bool live = row_slot(a, b, blk);  // uniform
   float *s = a.st + blk * a.is0 + hc;  // is1 == 1: the pair is one float2
+  // The window moves through buffer loads and stores on a descriptor of this
+  // block's window (records = its byte extent, checked on the host to fit 32
+  // bits): one lane offset in a VGPR, the column offset in an SGPR, so no
+  // per-column 64-bit address has to stay live from the loads to the
+  // shifted stores after the barrier.
+  const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(
+      a.st + blk * a.is0, 0, static_cast<int>((126 * a.is2 + a.H) * 4), 0x00020000);
+  const int ls = 4 * hc;
   float2 v[8][4];
 #pragma unroll
   for (int j = 0; j < 8; ++j)
 #pragma unroll
     for (int l = 0; l < 4; ++l) {
       const int k = 16 * j + 4 * m + l;
-      v[j][l] = k < 127 ? *reinterpret_cast<const float2 *>(s + (int64_t)k * a.is2)
-                        : make_float2(0.f, 0.f);
+      if (k < 127) {
+        const auto t = __builtin_amdgcn_raw_buffer_load_b64(srs, ls, static_cast<int>(k * a.is2 * 4), 0);
+        v[j][l] = make_float2(__int_as_float(t[0]), __int_as_float(t[1]));
+      } else {
+        v[j][l] = make_float2(0.f, 0.f);
+      }
     }
   // bf16 tap l of channel c (0 = h0, 1 = h0 + 1) for column group j
   auto tap = [&](int j, int l, int c) -> float {
@@ -467,7 +491,11 @@ __global__ __launch_bounds__(256) void hcm_decode_split_kernel(DecodeArgs a) {
 #pragma unroll
       for (int l = 0; l < 4; ++l) {
         const int k = 16 * j + 4 * m + l;
-        if (k >= 1 && k < 127) *reinterpret_cast<float2 *>(s + (int64_t)(k - 1) * a.is2) = v[j][l];
+        if (k >= 1 && k < 127) {
+          typedef __attribute__((ext_vector_type(2))) int i32x2;
+          const i32x2 t = {__float_as_int(v[j][l].x), __float_as_int(v[j][l].y)};
+          __builtin_amdgcn_raw_buffer_store_b64(t, srs, ls, static_cast<int>((k - 1) * a.is2 * 4), 0);
+        }
       }
   }
   if (m != 0 || !active) return;
@@ -644,6 +672,13 @@ static int pair_variant(const DecodeArgs &a, int kind) {
     return ok ? 0 : -1;
   }
   if (a.is1 != 1 || a.is0 % 2 || a.is2 % 2 || !aligned(a.st, 8)) return -1;
+  // hcm addresses a block's window through a buffer descriptor: its byte
+  // extent must fit the 32-bit record count
+  if (kind == KIND_HCM && (a.is2 < 0 || (126 * a.is2 + a.H) * 4 >= (int64_t(1) << 31))) return -1;
+  // and so do its taps' (either layout)
+  if (kind == KIND_HCM && (a.wi0 < 0 || a.wi1 < 0 || (126 * a.wi1 + a.H) * 2 >= (int64_t(1) << 31) ||
+                           ((a.H - 1) * a.wi0 + 128) * 2 >= (int64_t(1) << 31)))
+    return -1;
   if (a.wi0 == 1 && a.wi1 % 2 == 0 && aligned(a.inner, 4)) return 1;
   if (a.wi1 == 1) {
     if (kind == KIND_HCS) return 0;
