@@ -230,7 +230,8 @@ CTX_7B = 8192 + 512   # prompt plus the decode steps of the 7B workload
 
 def bench_model(steps, dev, B=B_DECODE, seed=21):
     """The whole 7B-shaped model at decode (32 layers: 27 Hyena on this
-    build's kernels, 5 attention and every MLP in torch), B sequences (64 for
+    build's kernels, 5 attention layers on the decode-attention kernel, the
+    projections and MLPs in torch), B sequences (64 for
     the 7B workload) at positions from 8192 on, rotary base 1e4 with linear scaling 128
     (evo2-7b-1m.yml:27-29; the checkpoint's base wins, convert.py:524-570).
     States and KV stand in for the prefilled prompt.  One decode step is one
@@ -274,7 +275,8 @@ def bench_model(steps, dev, B=B_DECODE, seed=21):
             "context": f"8192..{8192 + n}", "layers": 32,
             "bytes_per_step": {"weights": wbytes, "kv_cache": kvbytes},
             "achieved_GBs": round((wbytes + kvbytes) / (ms * 1e-3) / 1e9, 1),
-            "note": "Hyena mixers on this build's kernels; attention and MLP in torch"}
+            "note": "Hyena mixers and decode attention on this build's kernels; "
+                    "projections and MLP in torch"}
 
 
 # ---------------------------------------------------------------- speculative verify

@@ -107,6 +107,15 @@ SIGNATURES = {
         _c_p, _c_i64, _c_i64,                     # out + strides (channel, row)
         _c_i64, _c_i64, _c_i64, _c_p,             # T, dim, num_blocks, stream
     ],
+    "evo2_decode_attention_workspace_bytes": [_c_i64, _c_i64, _c_i64, _c_i64],
+    "evo2_decode_attention": [
+        _c_p, _c_i64, _c_i64,                     # q + strides (b, h)
+        _c_p, _c_i64, _c_i64, _c_i64,             # k + strides (b, h, d)
+        _c_p, _c_i64, _c_i64, _c_i64,             # v + strides (b, h, l)
+        _c_p, _c_p, _c_i64,                       # positions, workspace, bytes
+        _c_p, _c_i64, _c_i64,                     # out + strides (b, h)
+        _c_i64, _c_i64, _c_i64, _c_i64, _c_f, _c_p,  # B, heads, head_dim, L, scale, stream
+    ],
     "evo2_fp8_quantize": [_c_p, _c_i64, _c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_p],
     "evo2_rms_norm": [
         _c_p, _c_i64, _c_p, _c_i64,               # x, sx, residual, sr
@@ -149,7 +158,8 @@ SIGNATURES = {
     ],
 }
 
-RESTYPES = {"evo2_last_error": ctypes.c_char_p, "evo2_hcl_workspace_bytes": ctypes.c_int64}
+RESTYPES = {"evo2_last_error": ctypes.c_char_p, "evo2_hcl_workspace_bytes": ctypes.c_int64,
+            "evo2_decode_attention_workspace_bytes": ctypes.c_int64}
 
 _lock = threading.Lock()
 _lib = None

@@ -1,0 +1,199 @@
+// Decode attention for the whole-model harness: one query token per
+// (sequence, head) against that head's contiguous KV cache, as
+// Evo2Attention computes it at decode (model.py:104-153) with the cache laid
+// out for one-pass streaming:
+//
+//   keys   (B, heads, head_dim, L)  head_dim-major: position is the unit stride
+//   values (B, heads, L, head_dim)  position-major: dim is the unit stride
+//   out[b, h] = sum_l softmax_l(scale * q . k_l) v_l  over l <= positions[b]
+//
+// Split over the context (flash decoding): workgroup (c, h, b) takes the
+// 2048 positions of chunk c, computes its scores with 16-byte loads of eight
+// consecutive positions per lane (q in LDS), the chunk's max and exp-sum with
+// a block reduction, then sum_l p_l v_l with lanes along head_dim, and writes
+// (o, max, sum) to a workspace; a second launch merges the chunks of each
+// (sequence, head).  Keys and values are each read once; everything is fp32
+// until the bf16 output.
+#include "common.h"
+
+namespace evo2 {
+
+constexpr int AT_T = 256;              // threads per workgroup
+constexpr int AT_CHUNK = 8 * AT_T;     // positions per chunk (eight per lane)
+
+struct AttnArgs {
+  const bf16_t *q; int64_t qb, qh;           // (B, heads, hd), dim stride 1
+  const bf16_t *k; int64_t kb, kh, kd;       // (B, heads, hd, L), position stride 1
+  const bf16_t *v; int64_t vb, vh, vl;       // (B, heads, L, hd), dim stride 1
+  const int64_t *pos;                        // (B,) this step's position; length pos + 1
+  float *part;                               // (B, heads, nchunk, hd + 2): o, max, sum
+  bf16_t *out; int64_t ob, oh;               // (B, heads, hd), dim stride 1
+  float scale;
+  int heads, L, nchunk;
+};
+
+__device__ __forceinline__ int valid_len(const AttnArgs &p, int b) {
+  const int64_t n = p.pos[b] + 1;
+  return static_cast<int>(n < 0 ? 0 : (n > p.L ? p.L : n));
+}
+
+template <int HD>
+__global__ __launch_bounds__(AT_T) void attn_chunk_kernel(AttnArgs p) {
+  __shared__ float qs[HD];
+  __shared__ float ps[AT_CHUNK];
+  __shared__ float red[AT_T / 64];
+  __shared__ float osum[AT_T / 64][HD];
+  const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int n = valid_len(p, b);
+  const int l0 = c * AT_CHUNK, l1 = min(l0 + AT_CHUNK, n);
+  float *part = p.part + (((int64_t)b * p.heads + h) * p.nchunk + c) * (HD + 2);
+  if (l0 >= l1) {  // uniform: an empty chunk contributes nothing
+    if (t < HD) part[t] = 0.0f;
+    if (t == 0) {
+      part[HD] = -INFINITY;
+      part[HD + 1] = 0.0f;
+    }
+    return;
+  }
+  if (t < HD) qs[t] = bf2f(p.q[(int64_t)b * p.qb + (int64_t)h * p.qh + t]);
+  __syncthreads();
+
+  // scores of positions l0 + 8t .. l0 + 8t + 7 (L % 8 == 0 keeps a group that
+  // starts below l1 inside the cache)
+  const int lb = l0 + 8 * t;
+  float s[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) s[e] = 0.0f;
+  if (lb < l1) {
+    const bf16_t *kr = p.k + (int64_t)b * p.kb + (int64_t)h * p.kh + lb;
+#pragma unroll 8
+    for (int d = 0; d < HD; ++d) {
+      const uint4 kv = *reinterpret_cast<const uint4 *>(kr + (int64_t)d * p.kd);
+      const float qd = qs[d];
+      s[0] += qd * lo_bf(kv.x); s[1] += qd * hi_bf(kv.x);
+      s[2] += qd * lo_bf(kv.y); s[3] += qd * hi_bf(kv.y);
+      s[4] += qd * lo_bf(kv.z); s[5] += qd * hi_bf(kv.z);
+      s[6] += qd * lo_bf(kv.w); s[7] += qd * hi_bf(kv.w);
+    }
+  }
+  float mx = -INFINITY;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    s[e] = lb + e < l1 ? s[e] * p.scale : -INFINITY;
+    mx = fmaxf(mx, s[e]);
+  }
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  if (lane == 0) red[wave] = mx;
+  __syncthreads();
+  mx = red[0];
+#pragma unroll
+  for (int w = 1; w < AT_T / 64; ++w) mx = fmaxf(mx, red[w]);  // finite: l0 < l1
+  float sum = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float pe = lb + e < l1 ? expf(s[e] - mx) : 0.0f;
+    ps[8 * t + e] = pe;
+    sum += pe;
+  }
+  for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
+  __syncthreads();  // ps complete; every wave has read red
+  if (lane == 0) red[wave] = sum;
+
+  // o[d] = sum_l p_l v[l][d]: lane owns dims (2 lane, 2 lane + 1), wave w
+  // positions l0 + w, l0 + w + 4, ...
+  float o0 = 0.0f, o1 = 0.0f;
+  if (2 * lane < HD) {
+    const bf16_t *vr = p.v + (int64_t)b * p.vb + (int64_t)h * p.vh + 2 * lane;
+    for (int l = l0 + wave; l < l1; l += AT_T / 64) {
+      const uint32_t vv = *reinterpret_cast<const uint32_t *>(vr + (int64_t)l * p.vl);
+      const float pl = ps[l - l0];
+      o0 += pl * lo_bf(vv);
+      o1 += pl * hi_bf(vv);
+    }
+    osum[wave][2 * lane] = o0;
+    osum[wave][2 * lane + 1] = o1;
+  }
+  __syncthreads();
+  if (t < HD) {
+    float o = osum[0][t];
+#pragma unroll
+    for (int w = 1; w < AT_T / 64; ++w) o += osum[w][t];
+    part[t] = o;
+  }
+  if (t == 0) {
+    float tot = red[0];
+#pragma unroll
+    for (int w = 1; w < AT_T / 64; ++w) tot += red[w];
+    part[HD] = mx;
+    part[HD + 1] = tot;
+  }
+}
+
+// Merge the chunks of (sequence b, head h): lane d of HD.
+template <int HD>
+__global__ __launch_bounds__(HD) void attn_merge_kernel(AttnArgs p) {
+  const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
+  const int n = valid_len(p, b);
+  const int nc = (n + AT_CHUNK - 1) / AT_CHUNK;
+  const float *part = p.part + ((int64_t)b * p.heads + h) * p.nchunk * (HD + 2);
+  float M = -INFINITY;
+  for (int c = 0; c < nc; ++c) M = fmaxf(M, part[c * (HD + 2) + HD]);
+  float tot = 0.0f, o = 0.0f;
+  for (int c = 0; c < nc; ++c) {
+    const float f = expf(part[c * (HD + 2) + HD] - M);
+    tot += f * part[c * (HD + 2) + HD + 1];
+    o += f * part[c * (HD + 2) + d];
+  }
+  p.out[(int64_t)b * p.ob + (int64_t)h * p.oh + d] = f2bf(nc > 0 ? o / tot : 0.0f);
+}
+
+template <int HD>
+static int launch_attn(const AttnArgs &a, int64_t B, hipStream_t st) {
+  hipLaunchKernelGGL(attn_chunk_kernel<HD>, dim3(a.nchunk, a.heads, static_cast<unsigned>(B)),
+                     dim3(AT_T), 0, st, a);
+  int rc = check_launch("decode_attention chunks");
+  if (rc) return rc;
+  hipLaunchKernelGGL(attn_merge_kernel<HD>, dim3(a.heads, static_cast<unsigned>(B)), dim3(HD), 0, st, a);
+  return check_launch("decode_attention merge");
+}
+
+}  // namespace evo2
+
+using namespace evo2;
+
+extern "C" int64_t evo2_decode_attention_workspace_bytes(int64_t B, int64_t heads, int64_t head_dim,
+                                                         int64_t L) {
+  if (B <= 0 || heads <= 0 || head_dim <= 0 || L <= 0) return 0;
+  return B * heads * cdiv(L, AT_CHUNK) * (head_dim + 2) * static_cast<int64_t>(sizeof(float));
+}
+
+extern "C" int evo2_decode_attention(const void *q, int64_t qb, int64_t qh,
+                                     const void *k, int64_t kb, int64_t kh, int64_t kd,
+                                     const void *v, int64_t vb, int64_t vh, int64_t vl,
+                                     const int64_t *positions, float *workspace,
+                                     int64_t workspace_bytes, void *out, int64_t ob, int64_t oh,
+                                     int64_t B, int64_t heads, int64_t head_dim, int64_t L,
+                                     float scale, void *stream) {
+  if (B < 0 || heads <= 0 || L <= 0 || B > 65535 || heads > 65535)
+    return fail(EVO2_ERR_INVALID, "decode_attention: bad sizes B=%lld heads=%lld L=%lld",
+                (long long)B, (long long)heads, (long long)L);
+  if (head_dim != 64 && head_dim != 128)
+    return fail(EVO2_ERR_UNSUPPORTED, "decode_attention: head_dim %lld (64 or 128)",
+                (long long)head_dim);
+  if (B == 0) return EVO2_OK;
+  if (!q || !k || !v || !positions || !out || !workspace)
+    return fail(EVO2_ERR_INVALID, "decode_attention: null pointer argument");
+  if (workspace_bytes < evo2_decode_attention_workspace_bytes(B, heads, head_dim, L))
+    return fail(EVO2_ERR_INVALID, "decode_attention: workspace too small");
+  // 16-byte key loads of eight positions, 4-byte value loads of two dims
+  if (L % 8 || kd % 8 || kh % 8 || kb % 8 || reinterpret_cast<uintptr_t>(k) % 16 ||
+      vl % 2 || vh % 2 || vb % 2 || reinterpret_cast<uintptr_t>(v) % 4 || L > 0x7fffffff)
+    return fail(EVO2_ERR_UNSUPPORTED, "decode_attention: cache strides or alignment not supported");
+  AttnArgs a{static_cast<const bf16_t *>(q), qb, qh, static_cast<const bf16_t *>(k), kb, kh, kd,
+             static_cast<const bf16_t *>(v), vb, vh, vl, positions, workspace,
+             static_cast<bf16_t *>(out), ob, oh, scale, static_cast<int>(heads),
+             static_cast<int>(L), static_cast<int>(cdiv(L, AT_CHUNK))};
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return head_dim == 64 ? launch_attn<64>(a, B, st) : launch_attn<128>(a, B, st);
+}

@@ -10,14 +10,14 @@ end-to-end decode (the reference's model.py:47-200, restated).
     logits = RMSNorm(x) @ embed^T                 tied head (model.py:343-348)
 
 The Hyena layers are this build's: RMSNorm kernel, fp8 in_proj on MFMA, the
-fused decode step over the paged state pool, out_proj.  Attention and the
-MLPs are plain torch on ROCm (they are outside the mixer hot path): the
-attention layer keeps a contiguous KV cache per layer (keys head_dim-major)
-rather than vLLM's paged cache, applies neox-style rotary with the
-config's base and linear scaling (model.py:104-153), and attends over the
-whole cache with positions past each sequence's masked, so a decode step has
-fixed shapes and captures into one HIP graph.  Its products are batched
-matmuls whose right operand is always a contiguous tensor.
+fused decode step over the paged state pool, out_proj.  The attention layer
+keeps a contiguous KV cache per layer (keys head_dim-major, values
+position-major) rather than vLLM's paged cache, applies neox-style rotary
+with the config's base and linear scaling (model.py:104-153), and attends
+with this build's split-context decode attention kernel (attention.py),
+which reads each cache once and masks positions past each sequence's; a
+decode step has fixed shapes and captures into one HIP graph.  The
+projections and MLPs are plain torch on ROCm (outside the mixer hot path).
 
 Weights are random, seeded, in the benchmark's distributions; the Hyena
 state pools and the KV cache are filled with random values that stand in for
@@ -27,6 +27,7 @@ a prefilled prompt.
 import torch
 from torch import nn
 
+from .attention import decode_attention, workspace as attention_workspace
 from .metadata import build_metadata
 from .mixers import Linear, load_mixer_params, make_mixer, set_forward_context
 from .norm import Evo2RMSNorm
@@ -86,7 +87,7 @@ class Evo2Attention(nn.Module):
                                    device=device)
         self.v_cache = torch.zeros(max_batch, self.heads, max_ctx, self.hd, dtype=torch.bfloat16,
                                    device=device)
-        self.register_buffer("ctx_idx", torch.arange(max_ctx, device=device))
+        self._attn_ws = attention_workspace(max_batch, self.heads, self.hd, max_ctx, device)
 
     def forward_decode(self, x, positions):
         B = x.shape[0]
@@ -97,11 +98,8 @@ class Evo2Attention(nn.Module):
         rows = torch.arange(B, device=x.device)
         self.k_cache[rows, :, :, positions] = k
         self.v_cache[rows, :, positions] = v.contiguous()
-        q = (q.float() * self.hd ** -0.5).to(torch.bfloat16).contiguous()
-        scores = torch.matmul(q.view(B, self.heads, 1, self.hd), self.k_cache[:B])  # (B, nh, 1, L)
-        scores = scores.masked_fill(self.ctx_idx > positions[:, None, None, None], float("-inf"))
-        p = torch.softmax(scores, dim=-1, dtype=torch.float32).to(torch.bfloat16)
-        out = torch.matmul(p, self.v_cache[:B])                           # (B, nh, 1, hd)
+        out = decode_attention(q.contiguous(), self.k_cache[:B], self.v_cache[:B], positions,
+                               self.hd ** -0.5, self._attn_ws)            # (B, nh, hd)
         o, _ = self.o_proj(out.reshape(B, self.heads * self.hd))
         return o
 

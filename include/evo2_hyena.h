@@ -239,6 +239,29 @@ int evo2_causal_conv1d_fn(const void *x, int64_t xc, int64_t xt,
                           int64_t T, int64_t dim, int64_t num_blocks, void *stream);
 
 /*
+ * Decode attention of the whole-model harness: for each sequence b and head
+ * h, out[b, h] = sum_l softmax_l(scale * q[b, h] . k[b, h, :, l]) v[b, h, l, :]
+ * over l <= positions[b] (int64).  k is (B, heads, head_dim, L) with unit
+ * position stride, v is (B, heads, L, head_dim) with unit dim stride, q and
+ * out are (B, heads, head_dim) bf16 with unit dim stride.  head_dim 64 or
+ * 128; L a multiple of 8; workspace of
+ * evo2_decode_attention_workspace_bytes(B, heads, head_dim, L) bytes.
+ *
+ * Serves the attention layers of Evo2Attention at decode
+ * (evo2_flash/model.py:104-153) over this build's contiguous KV cache (the
+ * reference runs vLLM's paged attention there, outside the mixer path).
+ */
+int64_t evo2_decode_attention_workspace_bytes(int64_t B, int64_t heads, int64_t head_dim,
+                                              int64_t L);
+int evo2_decode_attention(const void *q, int64_t qb, int64_t qh,
+                          const void *k, int64_t kb, int64_t kh, int64_t kd,
+                          const void *v, int64_t vb, int64_t vh, int64_t vl,
+                          const int64_t *positions, float *workspace, int64_t workspace_bytes,
+                          void *out, int64_t ob, int64_t oh,
+                          int64_t B, int64_t heads, int64_t head_dim, int64_t L,
+                          float scale, void *stream);
+
+/*
  * Static per-tensor activation quantisation for the fp8 projections:
  * q = e4m3fn(clamp(x / scale[0], -448, 448)), round to nearest even.
  *   x (rows, K) bf16, row stride sx; q (rows, K) e4m3 bytes, row stride sq.

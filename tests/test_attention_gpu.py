@@ -1,0 +1,64 @@
+"""Decode attention of the whole-model harness (attention.py, csrc/attention.hip)
+against plain fp32 attention on the CPU: out = softmax(scale q.k) v over cache
+positions 0..positions[b].  Bar: max |out - ref| / max |ref| <= 1e-2 per case
+(the kernel's output is bf16, ~4e-3 relative rounding).  Cases: head_dim 64 and
+128; contexts of one and several 2048-position chunks; lengths ending inside a
+chunk, at a chunk edge and at the cache end; a batch slice of a larger cache
+(the harness's k_cache[:B]); the 7B attention shape (32 heads of 128) at the
+benchmark's context.
+"""
+
+import pytest
+import torch
+
+from evo2_flash_amd.attention import decode_attention, workspace
+
+from _cases import max_rel_err
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+bf = torch.bfloat16
+
+
+def _ref(q, k, v, pos, scale):
+    B, nh, hd = q.shape
+    out = torch.empty(B, nh, hd)
+    for b in range(B):
+        n = int(pos[b]) + 1
+        s = torch.einsum("hd,hdl->hl", q[b].float(), k[b, :, :, :n].float()) * scale
+        p = torch.softmax(s, dim=-1)
+        out[b] = torch.einsum("hl,hld->hd", p, v[b, :, :n].float())
+    return out
+
+
+@pytest.mark.parametrize("hd,L,pos", [(64, 16, [15, 0, 7]), (128, 4104, [4103, 5, 2047, 2048]),
+                                      (64, 2056, [2055, 1000])])
+def test_decode_attention_vs_fp32(hd, L, pos):
+    g = torch.Generator().manual_seed(hd + L)
+    B, nh, maxb = len(pos), 4, len(pos) + 2
+    q = torch.randn(B, nh, hd, generator=g).to(bf)
+    kc = torch.randn(maxb, nh, hd, L, generator=g).to(bf)      # head_dim-major keys
+    vc = torch.randn(maxb, nh, L, hd, generator=g).to(bf)
+    positions = torch.tensor(pos, dtype=torch.int64)
+    scale = hd ** -0.5
+    ref = _ref(q, kc[:B], vc[:B], positions, scale)
+    kd, vd = kc.to(DEV), vc.to(DEV)
+    ws = workspace(maxb, nh, hd, L, DEV)
+    print(f"decode_attention hd={hd} L={L} pos={pos}", flush=True)
+    out = decode_attention(q.to(DEV), kd[:B], vd[:B], positions.to(DEV), scale, ws)
+    assert out.dtype == bf and out.shape == (B, nh, hd)
+    assert max_rel_err(out.cpu(), ref) <= 1e-2
+
+
+def test_decode_attention_7b_shape():
+    """32 heads of 128 at the 7B benchmark's context (8192 prompt + 512 steps)."""
+    g = torch.Generator().manual_seed(7)
+    B, nh, hd, L = 3, 32, 128, 8704
+    q = torch.randn(B, nh, hd, generator=g).to(bf)
+    kc = (torch.randn(B, nh, hd, L, generator=g) * 0.5).to(bf)
+    vc = (torch.randn(B, nh, L, hd, generator=g) * 0.5).to(bf)
+    positions = torch.tensor([8192, 8703, 3000], dtype=torch.int64)
+    ref = _ref(q, kc, vc, positions, hd ** -0.5)
+    print("decode_attention 7B shape", flush=True)
+    out = decode_attention(q.to(DEV), kc.to(DEV), vc.to(DEV), positions.to(DEV), hd ** -0.5)
+    assert max_rel_err(out.cpu(), ref) <= 1e-2
