@@ -63,6 +63,14 @@ __device__ __forceinline__ uint32_t pair_bf(bf16_t lo, bf16_t hi) {
   return static_cast<uint32_t>(lo) | (static_cast<uint32_t>(hi) << 16);
 }
 
+// s_waitcnt vmcnt(n) alone (expcnt and lgkmcnt left at their maxima), without
+// the workgroup memory fence __syncthreads adds.
+template <int N>
+__device__ __forceinline__ void vmcnt_wait() {
+  static_assert(N >= 0 && N < 64, "vmcnt field is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
 // ---------------------------------------------------------------- host side
 void set_error(const char *fmt, ...);
 int fail(int code, const char *fmt, ...);

@@ -47,14 +47,6 @@ struct GemmArgs {
   int M, N, K;
 };
 
-// s_waitcnt vmcnt(n) alone (expcnt and lgkmcnt left at their maxima), without
-// the workgroup memory fence __syncthreads adds.
-template <int N>
-__device__ __forceinline__ void vmcnt_wait() {
-  static_assert(N >= 0 && N < 64, "vmcnt field is 6 bits");
-  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
-}
-
 __global__ __launch_bounds__(256) void fp8_gemm_kernel(GemmArgs p) {
   __shared__ __align__(16) uint8_t w0[G_STAGE], w1[G_STAGE], w2[G_STAGE], w3[G_STAGE], w4[G_STAGE];
   __shared__ __align__(16) uint8_t x0[G_STAGE], x1[G_STAGE], x2[G_STAGE], x3[G_STAGE], x4[G_STAGE];
