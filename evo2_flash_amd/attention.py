@@ -32,8 +32,9 @@ def decode_attention(q, k_cache, v_cache, positions, scale, work=None):
                          f"match q {tuple(q.shape)}")
     if q.stride(2) != 1 or k_cache.stride(3) != 1 or v_cache.stride(3) != 1:
         raise ValueError("q rows, key positions and value dims must have unit stride")
-    if positions.dtype != torch.int64:
-        positions = positions.to(torch.int64)
+    if positions.shape != (B,):
+        raise ValueError(f"positions must be ({B},), got {tuple(positions.shape)}")
+    positions = positions.to(torch.int64).contiguous()
     if work is None:
         work = workspace(B, heads, hd, L, q.device)
     out = torch.empty(B, heads, hd, dtype=torch.bfloat16, device=q.device)

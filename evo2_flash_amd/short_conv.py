@@ -133,6 +133,8 @@ def causal_conv1d_fn(x, weight, bias=None, conv_states=None, query_start_loc=Non
         raise TypeError(f"{fn}: unexpected arguments {sorted(prefix)}")
     if query_start_loc is None:
         raise NotImplementedError(f"{fn}: query_start_loc is required (packed segments)")
+    if query_start_loc.dim() != 1 or query_start_loc.shape[0] < 1:
+        raise ValueError(f"{fn}: query_start_loc must be (nseq + 1,) with nseq >= 0")
     _lib.require_device(x, weight, bias, conv_states, query_start_loc, cache_indices,
                         has_initial_state)
     dim, K = _check_common(fn, x, weight, bias, conv_states)
@@ -156,7 +158,7 @@ def causal_conv1d_fn(x, weight, bias=None, conv_states=None, query_start_loc=Non
               _lib.ptr(bias), act,
               _lib.ptr(cs), *(cs.stride() if cs is not None else (0, 0, 0)),
               _lib.ptr(init), _lib.ptr(idx), sidx, int(pad_slot_id),
-              _lib.ptr(qsl), max(nseq, 0),
+              _lib.ptr(qsl), nseq,
               _lib.ptr(out), out.stride(0), out.stride(1),
               T, dim, cs.shape[0] if cs is not None else 0, _lib.stream_of(x))
     return out

@@ -44,3 +44,10 @@ def test_unsupported_forms_raise():
         causal_conv1d_update(x, st, w, None, activation="gelu")
     with pytest.raises(NotImplementedError, match="one token"):
         causal_conv1d_update(torch.zeros(2, 6, 3, dtype=bf), st, w)
+
+
+def test_fn_rejects_empty_segment_table():
+    x = torch.zeros(2, 6, dtype=bf)
+    w = torch.zeros(6, 3, dtype=bf)
+    with pytest.raises(ValueError, match="query_start_loc"):
+        causal_conv1d_fn(x.t(), w, None, query_start_loc=torch.zeros(0, dtype=torch.int32))
