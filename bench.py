@@ -17,13 +17,16 @@ Also measured in the same run and reported in the same JSON line:
     of 4 tokens, a state snapshot per token) against HBM;
   * model_decode: the whole 7B-shaped model at decode (the mixers in their
     decoder layers, attention and MLPs in torch), end-to-end tokens/s;
+  * config0_prefill: one mixer core of each kind at H=1920 over one fresh
+    2048-token sequence, tokens/s per block on the GPU and for the oracle's
+    restatement of the reference torch path on the host cores;
   * roofline of the dominant decode kernel (hcm) from HIP events on the
     stream it is launched on, and the CPU baseline: the oracle's restatement
     of the reference torch decode path timed on the host cores.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--no-prefill] [--no-gemm]
                     [--no-verify] [--no-model]
-                    [--only decode|verify|prefill|gemm|copy|model]
+                    [--only decode|verify|prefill|gemm|copy|model|config0]
 """
 
 import argparse
@@ -373,6 +376,94 @@ def bench_prefill(reps, dev, L=L_PREFILL, H=H_7B, seed=77):
             "L": L, "mixer_frac": round(ideal_us / step_us, 4), "per_kind": res}
 
 
+# ---------------------------------------------------------------- 1B-shaped blocks
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
+def bench_config0(reps, dev, H=1920, L=2048, seed=11, cpu=True):
+    """One block of each Hyena kind at the reference's CPU-runnable shape
+    (H=1920, one fresh 2048-token sequence): prefill tok/s per block of the
+    mixer core (z -> g) on this build's kernels, and, when `cpu`, of the
+    oracle's restatement of the reference torch path (the FIR mixer's prefill
+    rows, mixers.py:1277-1305; the IIR mixer's, mixers.py:1327-1401) on the
+    host cores, same inputs."""
+    from evo2_flash_amd.hcl import hcl_block_t, hyena_hcl_prefill
+    from evo2_flash_amd.metadata import build_metadata, prefill_tables
+    from evo2_flash_amd.prefill import fir_prefill_block_t, hyena_fir_prefill
+    from evo2_flash_amd.state import HyenaStatePool
+    from evo2_flash_amd.synthetic import mixer_params
+
+    g = torch.Generator().manual_seed(seed)
+    z_cpu = (torch.randn(L, 3 * H, generator=g) * 1.3).to(torch.bfloat16)
+    z = z_cpu.to(dev)
+    m = build_metadata(prefill_lens=[L], prefill_slots=[1], has_init=[0], device=dev)
+    pool = HyenaStatePool(2, H, dev)
+    stream = torch.cuda.current_stream()
+    n = len(os.sched_getaffinity(0))
+    res = {}
+    for kind in ("hcs", "hcm", "hcl"):
+        prm = mixer_params(kind, H, seed, in_proj_fp8=False)
+        pd = {k: v.to(dev) for k, v in prm.items()}
+        sw = pd["short_filter"].view(3 * H, 3)
+        if kind == "hcl":
+            bt = hcl_block_t(L, H)
+            seq_t, til_t, ts_t = prefill_tables(m, bt, dev)
+
+            def fn(pd=pd, sw=sw, bt=bt, seq_t=seq_t, til_t=til_t, ts_t=ts_t):
+                return hyena_hcl_prefill(z, sw, pool.conv_view(), pd["residues"],
+                                         pd["log_poles"][..., 0], pool.ssm_view(), pd["D"],
+                                         seq_t, m.state_indices_tensor_p, til_t, ts_t, bt)
+        else:
+            K = pd["conv"].shape[-1]
+            bt = fir_prefill_block_t(K, L, H)
+            seq_t, til_t, _ = prefill_tables(m, bt, dev)
+
+            def fn(pd=pd, sw=sw, bt=bt, seq_t=seq_t, til_t=til_t, K=K):
+                return hyena_fir_prefill(z, sw, pool.conv_view(), pd["conv"].view(H, K),
+                                         pool.inner_view(K - 1), pd.get("D"), seq_t,
+                                         m.state_indices_tensor_p, til_t, bt)
+        fn()
+        torch.cuda.synchronize()
+        avg, med = _timed(fn, reps, stream)
+        nbytes = prefill_bytes(L, H)
+        entry = {"gpu_us": round(avg, 2), "gpu_tok_s": round(L / (avg * 1e-6), 1),
+                 "bytes": nbytes, "achieved_GBs": round(nbytes / (avg * 1e-6) / 1e9, 1)}
+        if cpu:
+            import oracle
+            torch.set_num_threads(n)
+            cpool = HyenaStatePool(2, H, "cpu")
+            sw_c = prm["short_filter"].view(3 * H, 3)
+            times = []
+            with torch.inference_mode():
+                for _ in range(3):
+                    t = time.perf_counter()
+                    if kind == "hcl":
+                        oracle.iir_mixer_prefill(z_cpu, sw_c, cpool.conv_view(), prm["residues"],
+                                                 prm["log_poles"][..., 0], cpool.ssm_view(),
+                                                 prm["D"], [0, L], [1], [0])
+                    else:
+                        K = prm["conv"].shape[-1]
+                        oracle.fir_mixer_prefill(z_cpu, sw_c, cpool.conv_view(),
+                                                 prm["conv"].view(H, K), cpool.inner_view(K - 1),
+                                                 prm.get("D"), [0, L], [1], [0])
+                    times.append(time.perf_counter() - t)
+            cs = statistics.median(times[1:])
+            entry.update({"cpu_s": round(cs, 4), "cpu_tok_s": round(L / cs, 1)})
+        res[kind] = entry
+    del z
+    return {"H": H, "L": L, "cores": n if cpu else None, "cpu_model": _cpu_model() if cpu else None,
+            "cpu_kind": "oracle restatement of the reference torch path" if cpu else None,
+            "per_block": res}
+
+
 # ---------------------------------------------------------------- fp8 GEMMs
 def bench_gemm(reps, dev, M=8192, K=4096, seed=5):
     from evo2_flash_amd.fp8 import fp8_gemm, quantize_input
@@ -468,7 +559,8 @@ def main(argv=None):
     ap.add_argument("--no-gemm", action="store_true", help="skip the fp8 GEMM leg")
     ap.add_argument("--no-verify", action="store_true", help="skip the speculative verify leg")
     ap.add_argument("--no-model", action="store_true", help="skip the whole-model decode leg")
-    ap.add_argument("--only", choices=["decode", "verify", "prefill", "gemm", "copy", "model"],
+    ap.add_argument("--only", choices=["decode", "verify", "prefill", "gemm", "copy", "model",
+                                       "config0"],
                     default=None,
                     help="run one leg only (for profiling); `copy` runs a plain 1 GiB "
                          "device copy, the reference dispatch for scaling HBM counters")
@@ -490,6 +582,8 @@ def main(argv=None):
     ver = bench_verify(max(8, args.steps // 2), dev) if run("verify", args.no_verify) else None
     pre = bench_prefill(max(3, args.steps // 8), dev) if run("prefill", args.no_prefill) else None
     gem = bench_gemm(max(5, args.steps // 4), dev) if run("gemm", args.no_gemm) else None
+    cf0 = (bench_config0(max(5, args.steps // 4), dev, cpu=not (args.no_cpu or args.only))
+           if run("config0", False) else None)
     mod = bench_model(max(16, args.steps // 2), dev) if run("model", args.no_model) else None
     if mod:
         # the reference's one published whole-step figure: a plain decode step
@@ -535,6 +629,8 @@ def main(argv=None):
         line["fp8_gemm"] = gem
     if mod:
         line["model_decode"] = mod
+    if cf0:
+        line["config0_prefill"] = cf0
     if not args.only:
         line["hbm_copy"] = bench_copy(dev)
     line["cpu_baseline"] = cpu
