@@ -15,16 +15,30 @@ from . import _lib
 # parallelism when there are few tokens.
 _MAX_BLOCK_T = {7: 1024, 128: 2048}
 _TARGET_WORKGROUPS = 2048
+# Long filters: below 256 rows the 127-row halo is a third or more of a
+# tile's reads, and on one MI355X 256-row tiles beat 64-row ones by 10-22%
+# at 2048-8192 tokens (H = 1920 and 4096) once the launch has 128
+# workgroups; with fewer (a few hundred tokens) parallelism wins again.
+_LONG_FILTER_MIN_BLOCK_T = 256
+_LONG_FILTER_MIN_WORKGROUPS = 128
 
 
 def fir_prefill_block_t(k, num_tokens=None, hidden=None):
     """Rows per prefill tile for filter length k; the tile table is built for
     this value.  With `num_tokens` and `hidden` it shrinks (to a multiple of
-    64) until the launch has enough workgroups to fill the GPU."""
+    64) until the launch has enough workgroups to fill the GPU; for filters
+    longer than 8 taps it stops at 256 rows once the launch has 128
+    workgroups."""
     bt = _MAX_BLOCK_T.get(int(k), 1024)
     if num_tokens is not None and hidden is not None:
         cblocks = max(1, (int(hidden) + 63) // 64)
-        while bt > 64 and ((int(num_tokens) + bt - 1) // bt) * cblocks < _TARGET_WORKGROUPS:
+        while bt > 64:
+            nwg = ((int(num_tokens) + bt - 1) // bt) * cblocks
+            if nwg >= _TARGET_WORKGROUPS:
+                break
+            if (int(k) > 8 and bt <= _LONG_FILTER_MIN_BLOCK_T
+                    and nwg >= _LONG_FILTER_MIN_WORKGROUPS):
+                break
             bt //= 2
     return bt
 
