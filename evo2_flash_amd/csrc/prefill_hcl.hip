@@ -85,6 +85,10 @@ __global__ __launch_bounds__(256, PHASE == 3 ? 4 : 5) void hcl_scan_kernel(HclAr
   const bool init = p.seq[3 * seg + 2] != 0 && blk >= 0 && blk < p.num_blocks;
   const int t_end = min(t0 + p.block_t, e);
   if (t0 >= t_end) return;  // uniform
+  // Waves are independent (own staging buffers, no barrier): one whose 64
+  // channels all lie past H has nothing to do.
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  if (c0 + 64 * wave >= p.H) return;
 
   ShortTaps wsp[3];
 #pragma unroll
@@ -97,11 +101,12 @@ __global__ __launch_bounds__(256, PHASE == 3 ? 4 : 5) void hcl_scan_kernel(HclAr
     s[i] = PHASE == 3 ? p.work[((int64_t)blockIdx.x * p.H + cl) * 16 + i] : 0.0f;
   }
   const float dval = PHASE == 3 ? bf2f(p.D[cl]) : 0.0f;
-  const bool vec_z = (c0 + HCL_CH <= p.H) && (p.sz % 8 == 0) &&
+  // Per wave: the last group of an H that is not a multiple of 256 keeps its
+  // whole waves on 16-byte staging.
+  const bool vec_z = (c0 + 64 * wave + 64 <= p.H) && (p.sz % 8 == 0) &&
                      ((reinterpret_cast<uintptr_t>(p.z) & 15) == 0) &&
                      p.sz * HCL_ZROWS < (int64_t(1) << 30);  // 32-bit byte offsets
   const bf16_t *conv = init ? p.cs + blk * p.cs0 : nullptr;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int cw0 = 3 * (c0 + 64 * wave);  // first z column of this wave's slice
   // Rows [rs, rs + HCL_ZROWS) of the tile, this wave's slice: `prefetch`
   // issues direct-to-LDS loads for the interior rows; `fix` (after they land)

@@ -105,8 +105,21 @@ VARLEN = [([300, 5, 0, 130, 1, 77], [0, 1, 0, 1, 1, 0]), ([64, 200], [1, 1])]
 
 @pytest.mark.parametrize("lens,has_init", VARLEN)
 @pytest.mark.parametrize("block_t", [16, 64, None])
-def test_fused_hcl_prefill_vs_oracle(lens, has_init, block_t):
-    H, nblk = 256, 12
+def test_fused_hcl_prefill_vs_oracle(lens, has_init, block_t, H=256):
+    _check_fused_hcl(lens, has_init, block_t, H)
+
+
+@pytest.mark.parametrize("H", [1920, 1000, 200])
+@pytest.mark.parametrize("block_t", [16, None])
+def test_fused_hcl_prefill_partial_group(H, block_t):
+    """H not a multiple of the 256-channel group: at 1920 the last group has
+    two full waves (16-byte staging) and two with no channel; at 1000 and 200
+    the last wave is partial (element staging)."""
+    _check_fused_hcl(*VARLEN[0], block_t, H)
+
+
+def _check_fused_hcl(lens, has_init, block_t, H):
+    nblk = 12
     prm, _, _ = _poles(H, 11)
     g = torch.Generator().manual_seed(4)
     z = (torch.randn(sum(lens), 3 * H, generator=g) * 1.3).to(torch.bfloat16)
@@ -115,7 +128,7 @@ def test_fused_hcl_prefill_vs_oracle(lens, has_init, block_t):
     gp = clone_pool(pool, DEV)
     bt = block_t or hcl_block_t(sum(lens), H)
     qsl, seq_t, til_t, t0_t = _tables(lens, has_init, bt)
-    print(f"hcl fused lens={lens} block_t={bt}", flush=True)
+    print(f"hcl fused H={H} lens={lens} block_t={bt}", flush=True)
     out = _fused(prm, z, slots, gp, seq_t, til_t, t0_t, bt, H).cpu()
     ref = oracle.iir_mixer_prefill(z, prm["short_filter"].view(3 * H, 3), pool.conv_view(),
                                    prm["residues"], prm["log_poles"][..., 0], pool.ssm_view(),
