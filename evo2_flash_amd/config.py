@@ -75,61 +75,13 @@ class HyenaConfig:
         return cfg
 
     def validate(self, quantization_config=None):
-        hyena = set(self.hcs_layer_idxs) | set(self.hcm_layer_idxs) | set(self.hcl_layer_idxs)
-        kinds = [set(self.attn_layer_idxs), set(self.hcs_layer_idxs), set(self.hcm_layer_idxs),
-                 set(self.hcl_layer_idxs)]
-        covered = set().union(*kinds)
-        if sum(len(k) for k in kinds) != len(covered) or covered != set(range(self.num_hidden_layers)):
-            raise ValueError("layer-type lists must partition range(num_hidden_layers)")
-        if self.use_fp8_input_projections:
-            marker = self.hyena_in_proj_fp8
-            if not isinstance(marker, dict):
-                raise ValueError("use_fp8_input_projections=True requires converter-exported "
-                                 "hyena_in_proj_fp8 metadata; reconvert the source checkpoint")
-            bad = {k: marker.get(k) for k, v in FP8_MARKER.items() if marker.get(k) != v}
-            if bad:
-                raise ValueError(f"unsupported or incomplete hyena_in_proj_fp8 metadata: {bad}")
-            if marker.get("num_layers") != len(hyena):
-                raise ValueError("hyena_in_proj_fp8 num_layers does not match the layer map: "
-                                 f"{marker.get('num_layers')} != {len(hyena)}")
-            if quantization_config is not None:
-                raise ValueError("FP8 Hyena projections use the selective static-W8A8 runtime; "
-                                 "an embedded global quantization_config is unsupported")
-        elif self.hyena_in_proj_fp8 is not None:
-            raise ValueError("hyena_in_proj_fp8 metadata is present while "
-                             "use_fp8_input_projections=False")
-        if self.hyena_token_table_layers:
-            if self.hyena_token_table_layers != [0]:
-                raise ValueError("hyena_token_table_layers may only be [0]: only layer 0's "
-                                 "projection input depends on the token alone, got "
-                                 f"{self.hyena_token_table_layers}")
-            if 0 in self.attn_layer_idxs:
-                raise ValueError("layer 0 is attention; a token table needs Hyena")
-            if self.use_fp8_input_projections:
-                raise ValueError("hyena_token_table_layers is the output of FP8 surgery and "
-                                 "cannot be combined with use_fp8_input_projections=True")
-            if not isinstance(self.fp8_surgery, dict):
-                raise ValueError("token-table checkpoints must carry fp8_surgery provenance")
-        if self.hyena_fp8_emulated_layers:
-            bad = [i for i in self.hyena_fp8_emulated_layers if i not in hyena]
-            if bad or (0 in self.hyena_token_table_layers and 0 in self.hyena_fp8_emulated_layers):
-                raise ValueError(f"invalid hyena_fp8_emulated_layers {self.hyena_fp8_emulated_layers}")
-            if self.use_fp8_input_projections or not isinstance(self.fp8_surgery, dict):
-                raise ValueError("hyena_fp8_emulated_layers is FP8-surgery output: needs "
-                                 "use_fp8_input_projections=False and fp8_surgery provenance")
-        if self.hyena_fp8_emulated_channels:
-            bad = {i: n for i, n in self.hyena_fp8_emulated_channels.items()
-                   if i not in hyena or i in self.hyena_fp8_emulated_layers
-                   or i in self.hyena_token_table_layers or not 0 < n < 3 * self.hidden_size}
-            if bad or self.use_fp8_input_projections or not isinstance(self.fp8_surgery, dict):
-                raise ValueError(f"invalid hyena_fp8_emulated_channels {bad or ''}: needs "
-                                 "FP8-surgery provenance, Hyena layers, 0 < n < 3H")
-        if not self.conv_kernels_pre_flipped:
-            raise NotImplementedError("conv kernels must be in cross-correlation order "
-                                      "(conv_kernels_pre_flipped=True)")
-        if not self.interleave or self.column_split_hyena or self.hyena_flip_x1x2:
-            raise NotImplementedError("only the interleaved (x2, x1, v) in_proj layout of the "
-                                      "released checkpoints is supported")
+        """Apply the acceptance rules of a converted checkpoint's config
+        (config.py:73-170) in table order; the first rule a config breaks
+        raises its error.  Returns self."""
+        facts = _ConfigFacts(self, quantization_config)
+        for rule in _RULES:
+            if rule.applies(facts) and rule.broken(facts):
+                raise rule.error(rule.message(facts))
         return self
 
     def layer_kind(self, i):
@@ -150,6 +102,139 @@ class HyenaConfig:
 
     def hyena_layers(self):
         return [i for i in range(self.num_hidden_layers) if self.layer_kind(i) != "attn"]
+
+
+class _ConfigFacts:
+    """What the acceptance rules read from one config: the config itself,
+    the embedded quantization_config, and derived sets."""
+
+    def __init__(self, cfg, quantization_config):
+        self.cfg = cfg
+        self.quant = quantization_config
+        self.hyena = (set(cfg.hcs_layer_idxs) | set(cfg.hcm_layer_idxs)
+                      | set(cfg.hcl_layer_idxs))
+        self.kind_sets = [set(cfg.attn_layer_idxs), set(cfg.hcs_layer_idxs),
+                          set(cfg.hcm_layer_idxs), set(cfg.hcl_layer_idxs)]
+        marker = cfg.hyena_in_proj_fp8
+        self.marker = marker if isinstance(marker, dict) else None
+        self.surgery = isinstance(cfg.fp8_surgery, dict)
+
+    def marker_mismatch(self):
+        """Marker keys whose values differ from the converter's contract."""
+        return {k: self.marker.get(k) for k, want in FP8_MARKER.items()
+                if self.marker.get(k) != want}
+
+    def bad_emulated_channels(self):
+        c = self.cfg
+        return {i: n for i, n in c.hyena_fp8_emulated_channels.items()
+                if i not in self.hyena or i in c.hyena_fp8_emulated_layers
+                or i in c.hyena_token_table_layers or not 0 < n < 3 * c.hidden_size}
+
+
+@dataclass(frozen=True)
+class _Rule:
+    """One acceptance rule: where it applies, when it is broken, and the
+    error it raises then."""
+    applies: object
+    broken: object
+    error: type
+    message: object
+
+
+def _always(f):
+    return True
+
+
+def _partition_broken(f):
+    covered = set().union(*f.kind_sets)
+    return (sum(len(k) for k in f.kind_sets) != len(covered)
+            or covered != set(range(f.cfg.num_hidden_layers)))
+
+
+def _fp8(f):
+    return f.cfg.use_fp8_input_projections
+
+
+def _fp8_with_marker(f):
+    return f.cfg.use_fp8_input_projections and f.marker is not None
+
+
+def _token_table(f):
+    return bool(f.cfg.hyena_token_table_layers)
+
+
+def _emulated_layers(f):
+    return bool(f.cfg.hyena_fp8_emulated_layers)
+
+
+def _emulated_channels(f):
+    return bool(f.cfg.hyena_fp8_emulated_channels)
+
+
+def _surgery_needs_bf16(f):
+    return f.cfg.use_fp8_input_projections or not f.surgery
+
+
+# The checkpoint contract of config.py:73-170, plus the layouts this build's
+# kernels implement (the released ones).  Messages are the reference's, so a
+# user sees the same diagnosis from either implementation.
+_RULES = (
+    _Rule(_always, _partition_broken, ValueError,
+          lambda f: "layer-type lists must partition range(num_hidden_layers)"),
+    # fp8 in_proj: the converter's marker must be present, exact and consistent
+    _Rule(_fp8, lambda f: f.marker is None, ValueError,
+          lambda f: "use_fp8_input_projections=True requires converter-exported "
+                    "hyena_in_proj_fp8 metadata; reconvert the source checkpoint"),
+    _Rule(_fp8_with_marker, lambda f: f.marker_mismatch(), ValueError,
+          lambda f: f"unsupported or incomplete hyena_in_proj_fp8 metadata: "
+                    f"{f.marker_mismatch()}"),
+    _Rule(_fp8_with_marker, lambda f: f.marker.get("num_layers") != len(f.hyena), ValueError,
+          lambda f: "hyena_in_proj_fp8 num_layers does not match the layer map: "
+                    f"{f.marker.get('num_layers')} != {len(f.hyena)}"),
+    _Rule(_fp8, lambda f: f.quant is not None, ValueError,
+          lambda f: "FP8 Hyena projections use the selective static-W8A8 runtime; "
+                    "an embedded global quantization_config is unsupported"),
+    _Rule(lambda f: not f.cfg.use_fp8_input_projections,
+          lambda f: f.cfg.hyena_in_proj_fp8 is not None, ValueError,
+          lambda f: "hyena_in_proj_fp8 metadata is present while "
+                    "use_fp8_input_projections=False"),
+    # FP8 surgery, layer 0 token table
+    _Rule(_token_table, lambda f: f.cfg.hyena_token_table_layers != [0], ValueError,
+          lambda f: "hyena_token_table_layers may only be [0]: only layer 0's projection "
+                    f"input depends on the token alone, got {f.cfg.hyena_token_table_layers}"),
+    _Rule(_token_table, lambda f: 0 in f.cfg.attn_layer_idxs, ValueError,
+          lambda f: "layer 0 is attention; a token table needs Hyena"),
+    _Rule(_token_table, _fp8, ValueError,
+          lambda f: "hyena_token_table_layers is the output of FP8 surgery and cannot be "
+                    "combined with use_fp8_input_projections=True"),
+    _Rule(_token_table, lambda f: not f.surgery, ValueError,
+          lambda f: "token-table checkpoints must carry fp8_surgery provenance"),
+    # FP8 surgery, whole layers on the emulated GEMM
+    _Rule(_emulated_layers,
+          lambda f: (any(i not in f.hyena for i in f.cfg.hyena_fp8_emulated_layers)
+                     or (0 in f.cfg.hyena_token_table_layers
+                         and 0 in f.cfg.hyena_fp8_emulated_layers)),
+          ValueError,
+          lambda f: f"invalid hyena_fp8_emulated_layers {f.cfg.hyena_fp8_emulated_layers}"),
+    _Rule(_emulated_layers, _surgery_needs_bf16, ValueError,
+          lambda f: "hyena_fp8_emulated_layers is FP8-surgery output: needs "
+                    "use_fp8_input_projections=False and fp8_surgery provenance"),
+    # FP8 surgery, hybrid channels
+    _Rule(_emulated_channels,
+          lambda f: f.bad_emulated_channels() or _surgery_needs_bf16(f), ValueError,
+          lambda f: f"invalid hyena_fp8_emulated_channels {f.bad_emulated_channels() or ''}: "
+                    "needs FP8-surgery provenance, Hyena layers, 0 < n < 3H"),
+    # layouts the kernels implement
+    _Rule(_always, lambda f: not f.cfg.conv_kernels_pre_flipped, NotImplementedError,
+          lambda f: "conv kernels must be in cross-correlation order "
+                    "(conv_kernels_pre_flipped=True)"),
+    _Rule(_always,
+          lambda f: (not f.cfg.interleave or f.cfg.column_split_hyena
+                     or f.cfg.hyena_flip_x1x2),
+          NotImplementedError,
+          lambda f: "only the interleaved (x2, x1, v) in_proj layout of the released "
+                    "checkpoints is supported"),
+)
 
 
 def _with_marker(cfg):

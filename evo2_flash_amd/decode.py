@@ -73,8 +73,11 @@ def hyena_decode(z, short_w, conv_state, slots, inner, inner_state, D=None,
     `log_poles` (H, 16) is given.  inner_state: (blocks, H, K-1 | 16) fp32 view.
     D: (H,) or None.  Returns (B, H) bf16 (triton_decode.py:185-211).
     """
-    _lib.require_device(z, conv_state, inner, inner_state, slots)
     B, H = z.shape[0], inner.shape[0]
+    if slots.dim() != 1 or slots.shape[0] < B:
+        raise ValueError(f"hyena_decode needs one state block per row: slots has shape "
+                         f"{tuple(slots.shape)} for {B} rows")
+    _lib.require_device(z, conv_state, inner, inner_state, slots)
     out = torch.empty(B, H, dtype=z.dtype, device=z.device)
     if not B:
         return out

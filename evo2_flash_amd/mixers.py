@@ -3,10 +3,14 @@
 `HyenaFIRMixer` (hcs K=7, hcm K=128) and `HyenaIIRMixer` (hcl) keep the
 reference's constructor arguments, parameter names (which are the checkpoint
 keys, convert.py:465-499), `kv_cache` 3-tuple and `forward(hidden_states,
-token_ids=None)`.  A forward pass runs as the opaque operator
-`evo2_hyena_mixer(hidden_states, output, token_ids, layer_name)`, which
-looks the layer up by name and writes into a preallocated `output`
-(mixers.py:1404-1423), so a caller can treat one mixer as one graph node.
+token_ids=None)`.  A forward pass runs as the registered custom operator
+`torch.ops.vllm.evo2_hyena_mixer(hidden_states, output, token_ids,
+layer_name)` (schema `(Tensor hidden_states, Tensor(a!) output, Tensor?
+token_ids, str layer_name) -> ()`, with a fake implementation), which looks
+the layer up by name and writes into a preallocated `output`
+(mixers.py:1404-1423): a compiler treats one mixer as one opaque node and
+splits its graph there, so the metadata reads on the host stay out of traced
+code.
 
 Per step the metadata (a vLLM Mamba2 metadata object, or
 `metadata.Mamba2Metadata`) comes from the forward context.  Decode rows come
@@ -20,10 +24,12 @@ launch between in_proj and out_proj:
 With no metadata (the engine's profiling pass) the mixer returns
 out_proj(x2 * x1 * v) as the reference does (mixers.py:1230-1235).  There is
 no CPU path and no speculative-decode path: the kernels run on ROCm devices
-and a speculative step raises.
+and a step whose metadata is speculative by the reference's predicate
+(mixers.py:930-937) raises.
 """
 
 import contextlib
+from typing import Optional
 
 import torch
 from torch import nn
@@ -153,7 +159,7 @@ class HyenaMixerBase(nn.Module):
 
     def forward(self, hidden_states, token_ids=None):
         output = torch.empty_like(hidden_states)
-        evo2_hyena_mixer(hidden_states, output, token_ids, self.prefix)
+        torch.ops.vllm.evo2_hyena_mixer(hidden_states, output, token_ids, self.prefix)
         return output
 
     def _meta(self):
@@ -196,15 +202,29 @@ class HyenaMixerBase(nn.Module):
                              static_fp8_linear_emulated(hidden_states, emul_w, sc[0], sc[1]))
         return z
 
+    @staticmethod
+    def is_speculative_decode(m):
+        """Whether the decode half of a step carries speculative snapshots
+        (mixers.py:930-937): a slot matrix with more than one column, an
+        accepted-token count, or a decode token count that differs from the
+        number of decode requests.  A speculative-capable runner keeps the
+        slot matrix even on an ordinary one-token step, which is therefore
+        speculative too: the previous verify step may have accepted several
+        tokens."""
+        idx = m.state_indices_tensor_d
+        return ((idx is not None and idx.dim() > 1 and idx.shape[1] > 1)
+                or getattr(m, "num_accepted_tokens", None) is not None
+                or int(m.num_decode_tokens) != int(m.num_decodes))
+
     def _check_meta(self, m):
         if len(self.kv_cache) != 3:
             raise RuntimeError(f"{self.prefix}: kv_cache is not bound (the engine binds the "
                                "layer's three state slices before a step)")
-        if getattr(m, "num_accepted_tokens", None) is not None:
-            raise NotImplementedError("speculative decode steps are not supported")
-        idx = m.state_indices_tensor_d
-        if idx is not None and idx.dim() > 1 and idx.shape[1] > 1 and m.num_decode_tokens > m.num_decodes:
-            raise NotImplementedError("multi-token decode rows are not supported")
+        if int(m.num_decodes) and self.is_speculative_decode(m):
+            raise NotImplementedError(
+                f"{self.prefix}: speculative decode metadata (a multi-column "
+                "state_indices_tensor_d, num_accepted_tokens, or num_decode_tokens != "
+                "num_decodes) is not supported by these mixers")
 
     @staticmethod
     def _unpad(out, hidden_states, n_actual):
@@ -244,11 +264,21 @@ class HyenaFIRMixer(HyenaMixerBase):
         self.D = (nn.Parameter(torch.empty(h, device=device, dtype=torch.bfloat16),
                                requires_grad=False) if self.has_D else None)
         self._decode_taps = None
+        # The engine's loader calls `param.weight_loader(param, tensor)` when a
+        # parameter has one (model.py:374-377); loading `conv` through it also
+        # refreshes the decode copy of the taps.
+        self.conv.weight_loader = self._load_conv
+
+    def _load_conv(self, param, loaded_weight):
+        param.data.copy_(loaded_weight.to(param.dtype).view_as(param))
+        if self._decode_taps is not None:
+            self.process_weights_after_loading()
 
     def process_weights_after_loading(self):
         """Keep a channel-contiguous copy of the taps for the decode kernel,
         rewritten in place on a reload, so a HIP graph captured before it
-        still reads the current taps."""
+        still reads the current taps.  `conv`'s weight_loader calls this on
+        every load; code that writes `conv` by other means calls it after."""
         taps = channel_major_taps(self.conv.detach().view(self.hidden, self.k_inner))
         old = self._decode_taps
         if (old is not None and old.shape == taps.shape and old.stride() == taps.stride()
@@ -327,11 +357,38 @@ class HyenaIIRMixer(HyenaMixerBase):
 
 
 # ---------------------------------------------------------------- operator
-def evo2_hyena_mixer(hidden_states, output, token_ids, layer_name):
+HYENA_MIXER_OP = "vllm::evo2_hyena_mixer"
+
+
+def evo2_hyena_mixer(hidden_states: torch.Tensor, output: torch.Tensor,
+                     token_ids: Optional[torch.Tensor], layer_name: str) -> None:
     """The mixer as one opaque operator that writes `output` in place
     (mixers.py:1404-1410)."""
     layer = static_forward_context[layer_name]
     output.copy_(layer._forward_impl(hidden_states, token_ids))
+
+
+def evo2_hyena_mixer_fake(hidden_states: torch.Tensor, output: torch.Tensor,
+                          token_ids: Optional[torch.Tensor], layer_name: str) -> None:
+    """Shape propagation for tracing: the operator only mutates `output`
+    (mixers.py:1413-1415)."""
+    return None
+
+
+def _register_op():
+    """Register `vllm::evo2_hyena_mixer` with `output` as its one mutated
+    argument (mixers.py:1418-1423).  Registration is once per process; a
+    second import of this module finds the operator already there."""
+    try:
+        return getattr(torch.ops.vllm, "evo2_hyena_mixer")
+    except (AttributeError, RuntimeError):
+        pass
+    op = torch.library.custom_op(HYENA_MIXER_OP, evo2_hyena_mixer, mutates_args=("output",))
+    op.register_fake(evo2_hyena_mixer_fake)
+    return op
+
+
+_register_op()
 
 
 def make_mixer(config, layer_idx, prefix="", quant_config=None, device=None):
@@ -355,6 +412,11 @@ def load_mixer_params(mixer, params):
     for name, t in params.items():
         if name not in own:
             raise KeyError(f"{mixer.prefix}: unexpected parameter {name}")
-        own[name].data.copy_(t.to(own[name].dtype).view_as(own[name]))
+        p = own[name]
+        loader = getattr(p, "weight_loader", None)
+        if loader is not None:
+            loader(p, t)
+        else:
+            p.data.copy_(t.to(p.dtype).view_as(p))
     mixer.process_weights_after_loading()
     return mixer

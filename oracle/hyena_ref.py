@@ -375,12 +375,7 @@ def mixer_decode_unfused(z, short_w, conv_state, slots, inner, inner_state, D=No
         y = (y + u * D.to(y.dtype)) * x2
         return y
     K = inner.shape[1]
-    view = inner_state[..., : K - 1]
-    st = view[idx].float()
-    wf = inner.float()
-    yf = (st * wf[None, :, :-1]).sum(-1) + wf[None, :, -1] * u.float()
-    inner_state[idx, :, : K - 1] = torch.cat([st[..., 1:], u.float().unsqueeze(-1)], dim=-1)
-    y = yf.to(torch.bfloat16)
+    y = fir_decode_one(u, inner, idx, inner_state[..., : K - 1])
     if D is not None:
         y = y + D.to(y.dtype) * u
     return x2 * y

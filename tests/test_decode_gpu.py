@@ -53,7 +53,8 @@ def _run_gpu(kind, prm, z, slots, pool, H):
 
 
 @pytest.mark.parametrize("kind", KINDS)
-@pytest.mark.parametrize("H,B,nblk,n_null", [(256, 5, 9, 1), (4096, 64, 80, 3), (8192, 32, 40, 2)])
+@pytest.mark.parametrize("H,B,nblk,n_null", [(256, 5, 9, 1), (4096, 64, 80, 3), (8192, 32, 40, 2),
+                                             (1920, 24, 30, 2), (200, 7, 12, 1)])
 def test_decode_bitwise_vs_emulation(kind, H, B, nblk, n_null):
     prm, z, slots, pool = decode_case(kind, H, B, nblk, seed=11 + H, n_null=n_null)
     print(f"decode bitwise kind={kind} H={H} B={B}", flush=True)
@@ -79,8 +80,9 @@ def test_decode_bitwise_vs_emulation(kind, H, B, nblk, n_null):
 
 
 @pytest.mark.parametrize("kind", KINDS)
-def test_decode_vs_unfused_fp32(kind):
-    H, B, nblk = 4096, 64, 70
+@pytest.mark.parametrize("H,B", [(4096, 64), (1920, 13)])
+def test_decode_vs_unfused_fp32(kind, H, B):
+    nblk = B + 6
     prm, z, slots, pool = decode_case(kind, H, B, nblk, seed=5)
     out_g, _ = _run_gpu(kind, prm, z, slots, pool, H)
     inner, lp, state, D = _args(kind, prm, pool, H)

@@ -118,6 +118,12 @@ def test_fused_hcl_prefill_partial_group(H, block_t):
     _check_fused_hcl(*VARLEN[0], block_t, H)
 
 
+def test_fused_hcl_config0_shape():
+    """One 1B-shaped block (H=1920) over one fresh 2048-token sequence, the
+    CPU-benchmark shape, against the oracle's FFT form."""
+    _check_fused_hcl([2048], [0], None, 1920)
+
+
 def _check_fused_hcl(lens, has_init, block_t, H):
     nblk = 12
     prm, _, _ = _poles(H, 11)

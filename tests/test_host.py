@@ -88,3 +88,135 @@ def test_speculative_metadata_rejected():
     mixer.kv_cache = HyenaStatePool(2, 128, "cpu").kv_cache
     with pytest.raises(NotImplementedError):
         mixer._check_meta(m)
+
+
+def _spec_mixer(prefix):
+    cfg = HyenaConfig(hidden_size=128, num_hidden_layers=1, hcs_layer_idxs=[0])
+    mixer = make_mixer(cfg, 0, prefix=prefix)
+    mixer.kv_cache = HyenaStatePool(4, 128, "cpu").kv_cache
+    return mixer
+
+
+def test_speculative_predicate_is_the_reference_one():
+    """Each of the reference's three conditions alone marks a step
+    speculative (mixers.py:930-937); the mixers refuse such a step before any
+    state is touched."""
+    mixer = _spec_mixer("host.spec.pred")
+    plain = build_metadata(decode_slots=[1, 2], device="cpu")
+    assert not mixer.is_speculative_decode(plain)
+    mixer._check_meta(plain)
+    # a speculative-capable runner's ordinary step: (nd, 2) slots, one token per row
+    two_col = build_metadata(decode_slots=[1, 2], device="cpu")
+    two_col.state_indices_tensor_d = torch.tensor([[1, 3], [2, 0]], dtype=torch.int32)
+    assert two_col.num_decode_tokens == two_col.num_decodes
+    assert mixer.is_speculative_decode(two_col)
+    with pytest.raises(NotImplementedError, match="speculative"):
+        mixer._check_meta(two_col)
+    # more decode tokens than requests with a 1-D slot table
+    packed = build_metadata(decode_slots=[1, 2], device="cpu")
+    packed.num_decode_tokens = 4
+    assert mixer.is_speculative_decode(packed)
+    with pytest.raises(NotImplementedError, match="speculative"):
+        mixer._check_meta(packed)
+    # a (nd, 1) column is not speculative
+    one_col = build_metadata(decode_slots=[1, 2], device="cpu")
+    one_col.state_indices_tensor_d = torch.tensor([[1], [2]], dtype=torch.int32)
+    assert not mixer.is_speculative_decode(one_col)
+
+
+def test_hyena_decode_refuses_short_slot_table():
+    """Fewer slots than rows would make the kernel read past the slot table."""
+    from evo2_flash_amd.decode import hyena_decode
+
+    H = 128
+    prm = mixer_params("hcs", H, seed=3, in_proj_fp8=False)
+    pool = HyenaStatePool(4, H, "cpu")
+    z = torch.zeros(3, 3 * H, dtype=torch.bfloat16)
+    for slots in (torch.tensor([1, 2], dtype=torch.int32),
+                  torch.tensor([[1, 2, 3]], dtype=torch.int32)):
+        with pytest.raises(ValueError, match="one state block per row"):
+            hyena_decode(z, prm["short_filter"].view(3 * H, 3), pool.conv_view(), slots,
+                         prm["conv"].view(H, 7), pool.inner_view(6))
+
+
+class _SlottedMetadata:
+    """Metadata that refuses new attributes, like a class with __slots__."""
+    __slots__ = ("num_prefills", "num_prefill_tokens", "num_decodes", "num_decode_tokens",
+                 "query_start_loc_p", "has_initial_states_p", "state_indices_tensor_p",
+                 "state_indices_tensor_d", "seq_lens")
+
+
+def test_prefill_tables_on_engine_metadata_objects():
+    """The tables are built from any object with vLLM's field names: memoised
+    on it when it takes attributes, rebuilt per call when it does not
+    (mixers.py:95-123, 386-415)."""
+    import types
+
+    from evo2_flash_amd.metadata import prefill_segments, prefill_tables
+
+    qsl = torch.tensor([0, 5, 12], dtype=torch.int32)
+    flags = torch.tensor([True, False])
+    slots = torch.tensor([3, 1], dtype=torch.int32)
+    want_seq = [[0, 5, 1], [5, 12, 0]]
+    want_tiles = [[0, 0], [0, 4], [1, 5], [1, 9]]
+    ns = types.SimpleNamespace(num_prefills=2, num_prefill_tokens=12, num_decodes=0,
+                               num_decode_tokens=0, query_start_loc_p=qsl,
+                               has_initial_states_p=flags, state_indices_tensor_p=slots)
+    seq, tiles, ts = prefill_tables(ns, 4, "cpu")
+    assert seq.tolist() == want_seq and tiles.tolist() == want_tiles and ts.tolist() == [0, 2, 4]
+    assert prefill_tables(ns, 4, "cpu")[0] is seq  # memoised
+    assert prefill_segments(ns) == ([0, 5, 12], [True, False])
+    sl = _SlottedMetadata()
+    sl.num_prefills, sl.num_prefill_tokens = 2, 12
+    sl.query_start_loc_p, sl.has_initial_states_p, sl.state_indices_tensor_p = qsl, flags, slots
+    seq2, tiles2, _ = prefill_tables(sl, 4, "cpu")
+    assert seq2.tolist() == want_seq and tiles2.tolist() == want_tiles
+    assert not hasattr(sl, "_evo2_prefill_tables")
+    # no has_initial_states_p at all: every segment starts fresh
+    bare = types.SimpleNamespace(num_prefills=1, num_prefill_tokens=5,
+                                 query_start_loc_p=torch.tensor([0, 5]))
+    assert prefill_tables(bare, 8, "cpu")[0].tolist() == [[0, 5, 0]]
+
+
+def test_custom_op_registration_and_opcheck():
+    """`vllm::evo2_hyena_mixer` is registered with `output` as its only
+    mutated argument and a fake implementation; `forward` goes through it.
+    Checked with torch.library.opcheck on the profiling path (no metadata),
+    which runs on the CPU with bf16 projections."""
+    schema = str(torch.ops.vllm.evo2_hyena_mixer.default._schema)
+    assert schema == ("vllm::evo2_hyena_mixer(Tensor hidden_states, Tensor(a1!) output, "
+                      "Tensor? token_ids, str layer_name) -> ()")
+    H = 64
+    cfg = HyenaConfig(hidden_size=H, num_hidden_layers=1, hcm_layer_idxs=[0])
+    mixer = make_mixer(cfg, 0, prefix="host.op.0")
+    load_mixer_params(mixer, mixer_params("hcm", H, seed=5, in_proj_fp8=False))
+    hs = torch.randn(6, H, generator=torch.Generator().manual_seed(0)).to(torch.bfloat16)
+    out = torch.empty_like(hs)
+    torch.library.opcheck(torch.ops.vllm.evo2_hyena_mixer.default,
+                          (hs, out, None, "host.op.0"))
+    got = mixer(hs)
+    z = hs.float() @ mixer.in_proj.weight.float().t()
+    z = z.to(torch.bfloat16)
+    y = z[:, 0::3] * z[:, 1::3] * z[:, 2::3]
+    want = torch.nn.functional.linear(y, mixer.out_proj.weight, mixer.out_proj.bias)
+    assert torch.allclose(got.float(), want.float(), rtol=2e-2, atol=2e-2)
+    # traced, the operator stays one opaque node
+    gm = torch.fx.experimental.proxy_tensor.make_fx(
+        lambda h, o: torch.ops.vllm.evo2_hyena_mixer(h, o, None, "host.op.0"),
+        tracing_mode="fake")(hs, out)
+    assert any("evo2_hyena_mixer" in str(n.target) for n in gm.graph.nodes)
+
+
+def test_conv_reload_refreshes_decode_taps():
+    """Loading `conv` through its weight_loader (the engine's load path,
+    model.py:374-377) after the decode taps exist rewrites them in place."""
+    H = 128
+    cfg = HyenaConfig(hidden_size=H, num_hidden_layers=2, hcs_layer_idxs=[0], hcm_layer_idxs=[1])
+    mixer = make_mixer(cfg, 1, prefix="host.reload.1")
+    load_mixer_params(mixer, mixer_params("hcm", H, seed=6, in_proj_fp8=False))
+    taps = mixer._decode_taps
+    assert torch.equal(taps, mixer.conv.detach().view(H, 128))
+    new = mixer_params("hcm", H, seed=7, in_proj_fp8=False)["conv"]
+    mixer.conv.weight_loader(mixer.conv, new)
+    assert mixer._decode_taps is taps  # same storage: captured graphs stay valid
+    assert torch.equal(taps, new.view(H, 128))

@@ -72,3 +72,76 @@ def test_mixer_profile_run_without_metadata():
     y = (z[:, 0::3] * z[:, 1::3] * z[:, 2::3]).float()
     ref = (y @ prm["out_proj.weight"].float().t() + prm["out_proj.bias"].float())
     assert max_rel_err(out, ref) <= 2e-2
+
+
+class _EngineMetadata:
+    """Metadata shaped like vLLM's (its field names, no extra attributes
+    accepted), as the engine hands it to the mixers."""
+    __slots__ = ("num_prefills", "num_prefill_tokens", "num_decodes", "num_decode_tokens",
+                 "query_start_loc_p", "has_initial_states_p", "state_indices_tensor_p",
+                 "state_indices_tensor_d", "seq_lens")
+
+    def __init__(self, src):
+        for k in self.__slots__:
+            setattr(self, k, getattr(src, k))
+
+
+@pytest.mark.parametrize("kind", ["hcs", "hcm", "hcl"])
+def test_mixer_step_through_registered_op_with_engine_metadata(kind):
+    """A mixed decode + prefill step through torch.ops.vllm.evo2_hyena_mixer,
+    with a metadata object that takes no new attributes (so nothing can be
+    memoised on it), against the oracle."""
+    H, nblk = 256, 10
+    cfg = HyenaConfig(hidden_size=H, num_hidden_layers=3, hcs_layer_idxs=[0], hcm_layer_idxs=[1],
+                      hcl_layer_idxs=[2], use_fp8_input_projections=True)
+    layer = {"hcs": 0, "hcm": 1, "hcl": 2}[kind]
+    prefix = f"t{next(_ids)}.mixer"
+    mixer = make_mixer(cfg, layer, prefix=prefix, device=DEV)
+    prm = mixer_params(kind, H, seed=60 + layer, in_proj_fp8=True)
+    load_mixer_params(mixer, prm)
+    pool = random_pool(nblk, H, seed=61)
+    gp = clone_pool(pool, DEV)
+    mixer.kv_cache = gp.kv_cache
+    dec_slots, pre_lens, pre_slots, pre_init = [4, 8], [129, 3], [6, 1], [1, 1]
+    nd, npt = len(dec_slots), sum(pre_lens)
+    g = torch.Generator().manual_seed(70 + layer)
+    hs = torch.randn(nd + npt, H, generator=g).to(torch.bfloat16)
+    m = _EngineMetadata(build_metadata(decode_slots=dec_slots, prefill_lens=pre_lens,
+                                       prefill_slots=pre_slots, has_init=pre_init, device=DEV))
+    print(f"op {kind} nd={nd} prefill={pre_lens}", flush=True)
+    out = torch.empty(hs.shape, dtype=torch.bfloat16, device=DEV)
+    with set_forward_context({prefix: m}):
+        torch.ops.vllm.evo2_hyena_mixer(hs.to(DEV), out, None, prefix)
+    ref = oracle_mixer_step(kind, prm, hs, pool, dec_slots, pre_lens, pre_slots, pre_init, H)
+    assert max_rel_err(out.cpu(), ref) <= 1e-2
+    assert max_rel_err(gp.kv_cache[1].cpu(), pool.kv_cache[1]) <= 1e-2
+    assert max_rel_err(gp.kv_cache[2].cpu(), pool.kv_cache[2]) <= 1e-3
+
+
+def test_fir_decode_after_conv_reload():
+    """Reloading `conv` through its weight_loader after a decode step: the
+    next decode uses the new taps (checked against the oracle)."""
+    H, nblk = 256, 6
+    cfg = HyenaConfig(hidden_size=H, num_hidden_layers=2, hcs_layer_idxs=[0], hcm_layer_idxs=[1],
+                      use_fp8_input_projections=True)
+    prefix = f"t{next(_ids)}.mixer"
+    mixer = make_mixer(cfg, 1, prefix=prefix, device=DEV)
+    prm = mixer_params("hcm", H, seed=80, in_proj_fp8=True)
+    load_mixer_params(mixer, prm)
+    pool = random_pool(nblk, H, seed=81)
+    gp = clone_pool(pool, DEV)
+    mixer.kv_cache = gp.kv_cache
+    g = torch.Generator().manual_seed(82)
+    m = build_metadata(decode_slots=[2, 5], device=DEV)
+    with set_forward_context(m):
+        mixer(torch.randn(2, H, generator=g).to(torch.bfloat16).to(DEV))
+    # bring the CPU pool to the GPU pool's state, then reload and decode again
+    pool.raw.copy_(gp.raw.cpu())
+    new = mixer_params("hcm", H, seed=83, in_proj_fp8=True)
+    mixer.conv.weight_loader(mixer.conv, new["conv"].to(DEV))
+    prm2 = dict(prm, conv=new["conv"])
+    hs = torch.randn(2, H, generator=g).to(torch.bfloat16)
+    with set_forward_context(m):
+        out = mixer(hs.to(DEV)).cpu()
+    ref = oracle_mixer_step("hcm", prm2, hs, pool, [2, 5], [], [], [], H)
+    assert max_rel_err(out, ref) <= 1e-2

@@ -296,6 +296,37 @@ def test_decode_emulated_vs_float64(kind):
             assert torch.equal(pool.raw[blk], raw0[blk]), blk
 
 
+@pytest.mark.parametrize("K", [7, 128])
+def test_fir_decode_one_vs_float64(K):
+    """The reference's unfused FIR decode (mixers.py:555-565): the output is
+    the K-tap sum over the window and the new sample, taps in
+    cross-correlation order (w[:, -1] multiplies the new sample), and the
+    window shifts left by one with the sample appended; rows whose block is
+    not named are untouched."""
+    H, nblk = 16, 5
+    g = torch.Generator().manual_seed(K)
+    w = torch.randn(H, K, generator=g).to(torch.bfloat16)
+    state = torch.randn(nblk, H, K - 1, generator=g)
+    x = torch.randn(2, H, generator=g).to(torch.bfloat16)
+    idx = torch.tensor([3, 1])
+    st0 = state.clone()
+    y = oracle.fir_decode_one(x, w, idx, state)
+    for r, blk in enumerate(idx.tolist()):
+        win = st0[blk].double()
+        want = sum(win[:, k] * w[:, k].double() for k in range(K - 1)) \
+            + w[:, K - 1].double() * x[r].double()
+        assert max_rel_err(y[r], want) <= 1e-2
+        assert torch.equal(state[blk, :, :K - 2], st0[blk, :, 1:])
+        assert torch.equal(state[blk, :, K - 2], x[r].float())
+    for blk in (0, 2, 4):
+        assert torch.equal(state[blk], st0[blk])
+    # an impulse window picks out one tap
+    imp = torch.zeros(1, H, K - 1)
+    imp[0, :, 0] = 1.0
+    y1 = oracle.fir_decode_one(torch.zeros(1, H, dtype=torch.bfloat16), w, torch.tensor([0]), imp)
+    assert torch.equal(y1[0], w[:, 0])
+
+
 @pytest.mark.parametrize("kind", ["hcs", "hcm", "hcl"])
 def test_decode_emulated_vs_unfused(kind):
     """The rounding-point emulation and the unfused fp32 path agree to 1e-2
