@@ -109,6 +109,13 @@ def test_fused_hcl_prefill_vs_oracle(lens, has_init, block_t, H=256):
     _check_fused_hcl(lens, has_init, block_t, H)
 
 
+def test_fused_hcl_prefill_long_segments():
+    """Segments of many tiles, fresh and continued, between short ones: the
+    carry scan crosses up to 80 tiles per segment and segments end in short
+    tiles."""
+    _check_fused_hcl([5000, 3, 4097, 129, 1, 2048], [0, 1, 1, 0, 1, 1], 64, 320)
+
+
 @pytest.mark.parametrize("H", [1920, 1000, 200])
 @pytest.mark.parametrize("block_t", [16, None])
 def test_fused_hcl_prefill_partial_group(H, block_t):
