@@ -67,6 +67,18 @@ SIGNATURES = {
         _c_p, _c_i64, _c_i64, _c_i64,             # out, so, T, H
         _c_i64, _c_p,                             # num_blocks, stream
     ],
+    "evo2_hyena_hcl_prefill_noalloc": [
+        _c_p, _c_i64, _c_p,                       # z, sz, short_w
+        _c_p, _c_i64, _c_i64, _c_i64,             # conv_state + strides
+        _c_p, _c_i64, _c_i64,                     # residues + strides
+        _c_p, _c_i64, _c_i64,                     # log_poles + strides
+        _c_p, _c_i64, _c_i64, _c_i64,             # ssm + strides
+        _c_p,                                     # D
+        _c_p, _c_i64, _c_p, _c_i64,               # seq_table, nseq, blocks, sblk
+        _c_p, _c_i64, _c_p, _c_i32,               # tile_table, ntiles, tile_start, block_t
+        _c_p, _c_i64, _c_i64, _c_i64,             # out, so, T, H
+        _c_i64, _c_p,                             # num_blocks, stream
+    ],
     "evo2_iir_segment": [
         _c_p, _c_i64, _c_i64,                     # seq + strides
         _c_p, _c_i64, _c_i64,                     # residues + strides

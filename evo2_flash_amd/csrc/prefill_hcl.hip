@@ -27,6 +27,7 @@
 // current one computes.  Each wave stages, patches and reads only its own 64
 // channels (a 384-byte slice of every z row), so the waves never wait for
 // each other: the sweep has no barrier.
+#include <mutex>
 #include <type_traits>
 
 #include "featurize.h"
@@ -377,19 +378,22 @@ extern "C" int64_t evo2_hcl_workspace_bytes(int64_t ntiles, int64_t H) {
   return ntiles * H * 16 * static_cast<int64_t>(sizeof(float));
 }
 
-extern "C" int evo2_hyena_hcl_prefill(const void *z, int64_t sz, const void *short_w,
-                                      void *conv_state, int64_t cs0, int64_t cs1, int64_t cs2,
-                                      const float *residues, int64_t r0, int64_t r1,
-                                      const float *log_poles, int64_t l0, int64_t l1,
-                                      float *ssm, int64_t m0, int64_t m1, int64_t m2,
-                                      const void *D,
-                                      const int32_t *seq_table, int64_t nseq,
-                                      const int32_t *blocks, int64_t sblk,
-                                      const int32_t *tile_table, int64_t ntiles,
-                                      const int32_t *tile_start, int32_t block_t,
-                                      float *workspace, int64_t workspace_bytes,
-                                      void *out, int64_t so, int64_t T, int64_t H,
-                                      int64_t num_blocks, void *stream) {
+namespace evo2 {
+
+// The fused LI prefill's checks and launches, shared by the entry point that
+// takes a workspace and the one that uses the library's scratch.
+static int hcl_prefill(const void *z, int64_t sz, const void *short_w,
+                       void *conv_state, int64_t cs0, int64_t cs1, int64_t cs2,
+                       const float *residues, int64_t r0, int64_t r1,
+                       const float *log_poles, int64_t l0, int64_t l1,
+                       float *ssm, int64_t m0, int64_t m1, int64_t m2, const void *D,
+                       const int32_t *seq_table, int64_t nseq,
+                       const int32_t *blocks, int64_t sblk,
+                       const int32_t *tile_table, int64_t ntiles,
+                       const int32_t *tile_start, int32_t block_t,
+                       float *workspace, int64_t workspace_bytes,
+                       void *out, int64_t so, int64_t T, int64_t H,
+                       int64_t num_blocks, void *stream) {
   if (T < 0 || H <= 0 || nseq < 0 || ntiles < 0 || num_blocks <= 0)
     return fail(EVO2_ERR_INVALID, "hyena_hcl_prefill: bad sizes");
   if (H % 2) return fail(EVO2_ERR_UNSUPPORTED, "hyena_hcl_prefill: H must be even");
@@ -430,6 +434,101 @@ extern "C" int evo2_hyena_hcl_prefill(const void *z, int64_t sz, const void *sho
   }
   hipLaunchKernelGGL(hcl_conv_window_kernel, sgrid, dim3(64), 0, st, a);
   return check_launch("hcl conv window");
+}
+
+}  // namespace evo2
+
+extern "C" int evo2_hyena_hcl_prefill(const void *z, int64_t sz, const void *short_w,
+                                      void *conv_state, int64_t cs0, int64_t cs1, int64_t cs2,
+                                      const float *residues, int64_t r0, int64_t r1,
+                                      const float *log_poles, int64_t l0, int64_t l1,
+                                      float *ssm, int64_t m0, int64_t m1, int64_t m2,
+                                      const void *D,
+                                      const int32_t *seq_table, int64_t nseq,
+                                      const int32_t *blocks, int64_t sblk,
+                                      const int32_t *tile_table, int64_t ntiles,
+                                      const int32_t *tile_start, int32_t block_t,
+                                      float *workspace, int64_t workspace_bytes,
+                                      void *out, int64_t so, int64_t T, int64_t H,
+                                      int64_t num_blocks, void *stream) {
+  return hcl_prefill(z, sz, short_w, conv_state, cs0, cs1, cs2, residues, r0, r1, log_poles,
+                     l0, l1, ssm, m0, m1, m2, D, seq_table, nseq, blocks, sblk, tile_table,
+                     ntiles, tile_start, block_t, workspace, workspace_bytes, out, so, T, H,
+                     num_blocks, stream);
+}
+
+// ---------------------------------------------------------------------------
+// The LI prefill without a workspace argument, for callers that cannot
+// allocate device memory.  Its tile end states and carries go to `scratch`,
+// a file-scope device array every GPU that runs this library holds for the
+// life of the process.  In host code `scratch` names a host-side stand-in,
+// not device memory: the address a kernel may use is taken once per device
+// with hipGetSymbolAddress, with that device current, and kept in
+// g_scratch_dev.  Calls on one GPU share its array, so calls that overlap on
+// one GPU (concurrent streams) race.  Nothing in it needs clearing between
+// calls: phase 1 writes the end state of every tile before phase 2 reads
+// any, and phase 2 writes every carry before phase 3 reads it.
+namespace evo2 {
+
+constexpr int64_t HCL_SCRATCH_BYTES = int64_t(32) << 20;
+static __device__ __align__(256) float scratch[HCL_SCRATCH_BYTES / sizeof(float)];
+
+constexpr int HCL_MAX_DEVICES = 64;
+static std::mutex g_scratch_mu;
+static float *g_scratch_dev[HCL_MAX_DEVICES];
+
+// This device's address of `scratch` (looked up on the first call made with
+// the device current).
+static int scratch_for_current_device(float **out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess)
+    return fail(EVO2_ERR_DEVICE, "hyena_hcl_prefill_noalloc: hipGetDevice failed: %s",
+                hipGetErrorString(e));
+  if (dev < 0 || dev >= HCL_MAX_DEVICES)
+    return fail(EVO2_ERR_UNSUPPORTED, "hyena_hcl_prefill_noalloc: device %d beyond %d", dev,
+                HCL_MAX_DEVICES);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void *ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+      return fail(EVO2_ERR_DEVICE,
+                  "hyena_hcl_prefill_noalloc: hipGetSymbolAddress(scratch) failed: %s",
+                  hipGetErrorString(e));
+    g_scratch_dev[dev] = static_cast<float *>(ptr);
+  }
+  *out = g_scratch_dev[dev];
+  return EVO2_OK;
+}
+
+}  // namespace evo2
+
+extern "C" int evo2_hyena_hcl_prefill_noalloc(
+    const void *z, int64_t sz, const void *short_w,
+    void *conv_state, int64_t cs0, int64_t cs1, int64_t cs2,
+    const float *residues, int64_t r0, int64_t r1,
+    const float *log_poles, int64_t l0, int64_t l1,
+    float *ssm, int64_t m0, int64_t m1, int64_t m2, const void *D,
+    const int32_t *seq_table, int64_t nseq, const int32_t *blocks, int64_t sblk,
+    const int32_t *tile_table, int64_t ntiles, const int32_t *tile_start, int32_t block_t,
+    void *out, int64_t so, int64_t T, int64_t H, int64_t num_blocks, void *stream) {
+  if (ntiles < 0 || H <= 0)
+    return fail(EVO2_ERR_INVALID, "hyena_hcl_prefill_noalloc: bad sizes");
+  const int64_t need = evo2_hcl_workspace_bytes(ntiles, H);
+  if (need > HCL_SCRATCH_BYTES)
+    return fail(EVO2_ERR_UNSUPPORTED,
+                "hyena_hcl_prefill_noalloc: %lld tiles at H=%lld need %lld bytes of scratch, "
+                "more than its %lld (use evo2_hyena_hcl_prefill with a workspace, or fewer "
+                "tiles)", (long long)ntiles, (long long)H, (long long)need,
+                (long long)HCL_SCRATCH_BYTES);
+  float *work = nullptr;
+  int rc = scratch_for_current_device(&work);
+  if (rc) return rc;
+  return hcl_prefill(z, sz, short_w, conv_state, cs0, cs1, cs2, residues, r0, r1, log_poles,
+                     l0, l1, ssm, m0, m1, m2, D, seq_table, nseq, blocks, sblk, tile_table,
+                     ntiles, tile_start, block_t, work, HCL_SCRATCH_BYTES, out, so, T, H,
+                     num_blocks, stream);
 }
 
 // ---------------------------------------------------------------------------

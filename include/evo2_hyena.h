@@ -152,6 +152,31 @@ int evo2_hyena_hcl_prefill(const void *z, int64_t sz, const void *short_w,
                            int64_t num_blocks, void *stream);
 
 /*
+ * evo2_hyena_hcl_prefill without the workspace argument: the same kernels,
+ * with the tile states in the library's own device scratch (32 MiB per GPU,
+ * held until the process ends).  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * serving loops, harnesses that forbid hipMalloc); it calls no hipMalloc,
+ * hipFree or allocating library routine.  Returns EVO2_ERR_UNSUPPORTED when
+ * evo2_hcl_workspace_bytes(ntiles, H) exceeds 32 MiB, i.e. when
+ * ntiles * H > 524 288 (32 768 tokens at H=4096 with block_t >= 256, or
+ * 65 536 at H=8192 with block_t 1024, fit).  Calls on one GPU share its
+ * scratch: calls that overlap on one GPU (concurrent streams) race.
+ */
+int evo2_hyena_hcl_prefill_noalloc(const void *z, int64_t sz, const void *short_w,
+                                   void *conv_state, int64_t cs0, int64_t cs1, int64_t cs2,
+                                   const float *residues, int64_t r0, int64_t r1,
+                                   const float *log_poles, int64_t l0, int64_t l1,
+                                   float *ssm, int64_t m0, int64_t m1, int64_t m2,
+                                   const void *D,
+                                   const int32_t *seq_table, int64_t nseq,
+                                   const int32_t *blocks, int64_t sblk,
+                                   const int32_t *tile_table, int64_t ntiles,
+                                   const int32_t *tile_start, int32_t block_t,
+                                   void *out, int64_t so, int64_t T, int64_t H,
+                                   int64_t num_blocks, void *stream);
+
+/*
  * One prefill segment of the LI recurrence s_t = p*s_{t-1} + x_t:
  * y (H, L) fp32 and the final state st (H, 16) fp32 (contiguous), from
  * s_prev (H, 16) or zero (NULL).  seq is (H, L) fp32 with any strides.

@@ -65,6 +65,10 @@ def test_validation_before_launch():
     """Calls rejected by argument checks never reach the HIP runtime."""
     lib = _lib.lib()
     n = None
+    # the allocation-free LI prefill refuses more tiles than its 32 MiB scratch holds
+    rc = lib.evo2_hyena_hcl_prefill_noalloc(n, 0, n, n, 0, 0, 0, n, 0, 0, n, 0, 0, n, 0, 0, 0,
+                                            n, n, 1, n, 1, n, 65, n, 1024, n, 0, 1, 8192, 2, n)
+    assert rc == EVO2_ERR_UNSUPPORTED
     rc = lib.evo2_hyena_decode(n, 0, n, n, 0, 0, 0, n, 0, n, 0, 0, n, 0, 0, n, 0, 0, 0, n, n, 0,
                                -1, 4096, 128, 0, 0, 2, n)
     assert rc == EVO2_ERR_INVALID
