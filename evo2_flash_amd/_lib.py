@@ -128,6 +128,15 @@ SIGNATURES = {
         _c_p, _c_i64, _c_i64,                     # out + strides (b, h)
         _c_i64, _c_i64, _c_i64, _c_i64, _c_f, _c_p,  # B, heads, head_dim, L, scale, stream
     ],
+    "evo2_paged_decode_attention": [
+        _c_p, _c_i64, _c_i64,                     # q + strides (b, h)
+        _c_p, _c_i64, _c_i64, _c_i64,             # key pages + strides (page, h, d)
+        _c_p, _c_i64, _c_i64, _c_i64,             # value pages + strides (page, h, l)
+        _c_p, _c_i64,                             # block table, row stride
+        _c_p, _c_p, _c_i64,                       # positions, workspace, bytes
+        _c_p, _c_i64, _c_i64,                     # out + strides (b, h)
+        _c_i64, _c_i64, _c_i64, _c_i64, _c_f, _c_p,  # B, heads, head_dim, max_pages, scale, stream
+    ],
     "evo2_fp8_quantize": [_c_p, _c_i64, _c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_p],
     "evo2_rms_norm": [
         _c_p, _c_i64, _c_p, _c_i64,               # x, sx, residual, sr

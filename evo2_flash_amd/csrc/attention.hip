@@ -1,10 +1,17 @@
 // Decode attention for the whole-model harness: one query token per
-// (sequence, head) against that head's contiguous KV cache, as
-// Evo2Attention computes it at decode (model.py:104-153) with the cache laid
-// out for one-pass streaming:
+// (sequence, head) against that head's KV cache, as Evo2Attention computes it
+// at decode (model.py:104-153), with the cache laid out for one-pass
+// streaming, either contiguous per sequence
 //
 //   keys   (B, heads, head_dim, L)  head_dim-major: position is the unit stride
 //   values (B, heads, L, head_dim)  position-major: dim is the unit stride
+//
+// or in 16-position pages named by a per-sequence block table (the paged
+// cache of the serving engine), page = table[b, l / 16]:
+//
+//   key pages   (pages, heads, head_dim, 16)
+//   value pages (pages, heads, 16, head_dim)
+//
 //   out[b, h] = sum_l softmax_l(scale * q . k_l) v_l  over l <= positions[b]
 //
 // Split over the context (flash decoding): workgroup (c, h, b) takes the
@@ -21,11 +28,15 @@ namespace evo2 {
 
 constexpr int AT_T = 256;              // threads per workgroup
 constexpr int AT_CHUNK = 8 * AT_T;     // positions per chunk (eight per lane)
+constexpr int AT_PAGE = 16;            // positions per page of the paged cache
 
 struct AttnArgs {
   const bf16_t *q; int64_t qb, qh;           // (B, heads, hd), dim stride 1
-  const bf16_t *k; int64_t kb, kh, kd;       // (B, heads, hd, L), position stride 1
-  const bf16_t *v; int64_t vb, vh, vl;       // (B, heads, L, hd), dim stride 1
+  const bf16_t *k; int64_t kb, kh, kd;       // (B, heads, hd, L) or (pages, heads, hd, 16);
+                                             // position stride 1 (kb: sequence or page)
+  const bf16_t *v; int64_t vb, vh, vl;       // (B, heads, L, hd) or (pages, heads, 16, hd);
+                                             // dim stride 1 (vb: sequence or page)
+  const int32_t *tbl; int64_t tbs;           // paged: (B, L / 16) block table, row stride
   const int64_t *pos;                        // (B,) this step's position; length pos + 1
   float *part;                               // (B, heads, nchunk, hd + 2): o, max, sum
   bf16_t *out; int64_t ob, oh;               // (B, heads, hd), dim stride 1
@@ -38,12 +49,13 @@ __device__ __forceinline__ int valid_len(const AttnArgs &p, int b) {
   return static_cast<int>(n < 0 ? 0 : (n > p.L ? p.L : n));
 }
 
-template <int HD>
+template <int HD, bool PAGED>
 __global__ __launch_bounds__(AT_T) void attn_chunk_kernel(AttnArgs p) {
   __shared__ float qs[HD];
   __shared__ float ps[AT_CHUNK];
   __shared__ float red[AT_T / 64];
   __shared__ float osum[AT_T / 64][HD];
+  __shared__ int32_t pages[PAGED ? AT_CHUNK / AT_PAGE : 1];
   const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int n = valid_len(p, b);
@@ -58,16 +70,23 @@ __global__ __launch_bounds__(AT_T) void attn_chunk_kernel(AttnArgs p) {
     return;
   }
   if (t < HD) qs[t] = bf2f(p.q[(int64_t)b * p.qb + (int64_t)h * p.qh + t]);
+  if constexpr (PAGED) {  // the chunk's pages that hold positions below l1
+    if (t < AT_CHUNK / AT_PAGE && l0 + AT_PAGE * t < l1)
+      pages[t] = p.tbl[(int64_t)b * p.tbs + l0 / AT_PAGE + t];
+  }
   __syncthreads();
 
   // scores of positions l0 + 8t .. l0 + 8t + 7 (L % 8 == 0 keeps a group that
-  // starts below l1 inside the cache)
+  // starts below l1 inside the cache; in the paged cache the eight lie in
+  // one page)
   const int lb = l0 + 8 * t;
   float s[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) s[e] = 0.0f;
   if (lb < l1) {
-    const bf16_t *kr = p.k + (int64_t)b * p.kb + (int64_t)h * p.kh + lb;
+    const bf16_t *kr =
+        PAGED ? p.k + (int64_t)pages[(lb - l0) / AT_PAGE] * p.kb + (int64_t)h * p.kh + lb % AT_PAGE
+              : p.k + (int64_t)b * p.kb + (int64_t)h * p.kh + lb;
 #pragma unroll 8
     for (int d = 0; d < HD; ++d) {
       const uint4 kv = *reinterpret_cast<const uint4 *>(kr + (int64_t)d * p.kd);
@@ -112,9 +131,12 @@ __global__ __launch_bounds__(AT_T) void attn_chunk_kernel(AttnArgs p) {
 #pragma unroll
   for (int e = 0; e < 8; ++e) o[e] = 0.0f;
   {
-    const bf16_t *vr = p.v + (int64_t)b * p.vb + (int64_t)h * p.vh + 8 * g;
+    const bf16_t *vr = p.v + (PAGED ? 0 : (int64_t)b * p.vb) + (int64_t)h * p.vh + 8 * g;
     for (int l = l0 + wave * RW + r; l < l1; l += (AT_T / 64) * RW) {
-      const uint4 vv = *reinterpret_cast<const uint4 *>(vr + (int64_t)l * p.vl);
+      const bf16_t *row =
+          PAGED ? vr + (int64_t)pages[(l - l0) / AT_PAGE] * p.vb + (int64_t)(l % AT_PAGE) * p.vl
+                : vr + (int64_t)l * p.vl;
+      const uint4 vv = *reinterpret_cast<const uint4 *>(row);
       const float pl = ps[l - l0];
       o[0] += pl * lo_bf(vv.x); o[1] += pl * hi_bf(vv.x);
       o[2] += pl * lo_bf(vv.y); o[3] += pl * hi_bf(vv.y);
@@ -164,10 +186,10 @@ __global__ __launch_bounds__(HD) void attn_merge_kernel(AttnArgs p) {
   p.out[(int64_t)b * p.ob + (int64_t)h * p.oh + d] = f2bf(nc > 0 ? o / tot : 0.0f);
 }
 
-template <int HD>
+template <int HD, bool PAGED>
 static int launch_attn(const AttnArgs &a, int64_t B, hipStream_t st) {
-  hipLaunchKernelGGL(attn_chunk_kernel<HD>, dim3(a.nchunk, a.heads, static_cast<unsigned>(B)),
-                     dim3(AT_T), 0, st, a);
+  hipLaunchKernelGGL((attn_chunk_kernel<HD, PAGED>),
+                     dim3(a.nchunk, a.heads, static_cast<unsigned>(B)), dim3(AT_T), 0, st, a);
   int rc = check_launch("decode_attention chunks");
   if (rc) return rc;
   hipLaunchKernelGGL(attn_merge_kernel<HD>, dim3(a.heads, static_cast<unsigned>(B)), dim3(HD), 0, st, a);
@@ -207,9 +229,44 @@ extern "C" int evo2_decode_attention(const void *q, int64_t qb, int64_t qh,
       vl % 8 || vh % 8 || vb % 8 || reinterpret_cast<uintptr_t>(v) % 16 || L > 0x7fffffff)
     return fail(EVO2_ERR_UNSUPPORTED, "decode_attention: cache strides or alignment not supported");
   AttnArgs a{static_cast<const bf16_t *>(q), qb, qh, static_cast<const bf16_t *>(k), kb, kh, kd,
-             static_cast<const bf16_t *>(v), vb, vh, vl, positions, workspace,
+             static_cast<const bf16_t *>(v), vb, vh, vl, nullptr, 0, positions, workspace,
              static_cast<bf16_t *>(out), ob, oh, scale, static_cast<int>(heads),
              static_cast<int>(L), static_cast<int>(cdiv(L, AT_CHUNK))};
   hipStream_t st = static_cast<hipStream_t>(stream);
-  return head_dim == 64 ? launch_attn<64>(a, B, st) : launch_attn<128>(a, B, st);
+  return head_dim == 64 ? launch_attn<64, false>(a, B, st) : launch_attn<128, false>(a, B, st);
+}
+
+extern "C" int evo2_paged_decode_attention(const void *q, int64_t qb, int64_t qh,
+                                           const void *k_pages, int64_t kp, int64_t kh, int64_t kd,
+                                           const void *v_pages, int64_t vp, int64_t vh, int64_t vl,
+                                           const int32_t *block_table, int64_t tbs,
+                                           const int64_t *positions, float *workspace,
+                                           int64_t workspace_bytes, void *out, int64_t ob,
+                                           int64_t oh, int64_t B, int64_t heads,
+                                           int64_t head_dim, int64_t max_pages, float scale,
+                                           void *stream) {
+  if (B < 0 || heads <= 0 || max_pages <= 0 || B > 65535 || heads > 65535 ||
+      max_pages > (int64_t(1) << 26))
+    return fail(EVO2_ERR_INVALID, "paged_decode_attention: bad sizes B=%lld heads=%lld pages=%lld",
+                (long long)B, (long long)heads, (long long)max_pages);
+  if (head_dim != 64 && head_dim != 128)
+    return fail(EVO2_ERR_UNSUPPORTED, "paged_decode_attention: head_dim %lld (64 or 128)",
+                (long long)head_dim);
+  if (B == 0) return EVO2_OK;
+  if (!q || !k_pages || !v_pages || !block_table || !positions || !out || !workspace)
+    return fail(EVO2_ERR_INVALID, "paged_decode_attention: null pointer argument");
+  const int64_t L = max_pages * AT_PAGE;
+  if (workspace_bytes < evo2_decode_attention_workspace_bytes(B, heads, head_dim, L))
+    return fail(EVO2_ERR_INVALID, "paged_decode_attention: workspace too small");
+  // 16-byte key loads of eight positions within a page, 16-byte value loads
+  if (kd % 8 || kh % 8 || kp % 8 || reinterpret_cast<uintptr_t>(k_pages) % 16 || kd < AT_PAGE ||
+      vl % 8 || vh % 8 || vp % 8 || reinterpret_cast<uintptr_t>(v_pages) % 16 || vl < head_dim)
+    return fail(EVO2_ERR_UNSUPPORTED,
+                "paged_decode_attention: page strides or alignment not supported");
+  AttnArgs a{static_cast<const bf16_t *>(q), qb, qh, static_cast<const bf16_t *>(k_pages), kp,
+             kh, kd, static_cast<const bf16_t *>(v_pages), vp, vh, vl, block_table, tbs,
+             positions, workspace, static_cast<bf16_t *>(out), ob, oh, scale,
+             static_cast<int>(heads), static_cast<int>(L), static_cast<int>(cdiv(L, AT_CHUNK))};
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return head_dim == 64 ? launch_attn<64, true>(a, B, st) : launch_attn<128, true>(a, B, st);
 }

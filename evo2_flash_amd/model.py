@@ -1,5 +1,5 @@
 """Evo 2 (StripedHyena2) decoder around this build's Hyena mixers, for
-end-to-end decode (the reference's model.py:47-200, restated).
+end-to-end prefill and decode (the reference's model.py:47-200, restated).
 
     x = embed(token)
     for each layer:  pre = RMSNorm(x)
@@ -10,24 +10,26 @@ end-to-end decode (the reference's model.py:47-200, restated).
     logits = RMSNorm(x) @ embed^T                 tied head (model.py:343-348)
 
 The Hyena layers are this build's: RMSNorm kernel, fp8 in_proj on MFMA, the
-fused decode step over the paged state pool, out_proj.  The attention layer
-keeps a contiguous KV cache per layer (keys head_dim-major, values
-position-major) rather than vLLM's paged cache, applies neox-style rotary
-with the config's base and linear scaling (model.py:104-153), and attends
-with this build's split-context decode attention kernel (attention.py),
-which reads each cache once and masks positions past each sequence's; a
-decode step has fixed shapes and captures into one HIP graph.  The
+fused prefill cores and decode step over the paged state pool, out_proj.
+The attention layers keep their KV cache in 16-position pages named by a
+block table that is a seeded random permutation of the pages (page 0 is
+never handed out), apply neox-style rotary with the config's base and
+linear scaling (model.py:104-153), and attend at decode with this build's
+split-context paged decode attention kernel (attention.py), which reads each
+page once and masks positions past each sequence's; a decode step has fixed
+shapes and captures into one HIP graph.  Prefill runs prompts through the
+same layers (the Hyena mixers on their prefill kernels, writing the states
+the decode steps continue from) with causal attention in torch.  The
 projections and MLPs are plain torch on ROCm (outside the mixer hot path).
 
-Weights are random, seeded, in the benchmark's distributions; the Hyena
-state pools and the KV cache are filled with random values that stand in for
-a prefilled prompt.
+Weights are random, seeded, in the benchmark's distributions.
 """
 
 import torch
 from torch import nn
 
-from .attention import decode_attention, workspace as attention_workspace
+from .attention import (PAGE, PagedKVCache, causal_prefill_attention, paged_decode_attention,
+                        workspace as attention_workspace)
 from .metadata import build_metadata
 from .mixers import Linear, load_mixer_params, make_mixer, set_forward_context
 from .norm import Evo2RMSNorm
@@ -66,11 +68,11 @@ def rotary_neox(x, positions, inv_freq, factor):
 
 
 class Evo2Attention(nn.Module):
-    """Decode-time attention: qkv_proj, rotary, KV append, softmax attention
-    over the cache, o_proj with bias (model.py:104-153)."""
+    """qkv_proj, rotary, KV written to the layer's pages, softmax attention
+    over the sequence's positions, o_proj with bias (model.py:104-153)."""
 
-    def __init__(self, config, max_batch, max_ctx, rope_theta=10000.0, rope_factor=1.0,
-                 device=None):
+    def __init__(self, config, num_pages, max_pages, max_batch, rope_theta=10000.0,
+                 rope_factor=1.0, device=None):
         super().__init__()
         h = config.hidden_size
         self.heads = config.num_attention_heads
@@ -80,27 +82,37 @@ class Evo2Attention(nn.Module):
         self.rope_factor = float(rope_factor)
         self.register_buffer("inv_freq", 1.0 / rope_theta ** (
             torch.arange(0, self.hd, 2, device=device, dtype=torch.float32) / self.hd))
-        # keys head_dim-major (B, nh, hd, L), values (B, nh, L, hd): both
-        # products of a decode step then take a contiguous right operand,
-        # (1 x hd)(hd x L) for the scores and (1 x L)(L x hd) for the output
-        self.k_cache = torch.zeros(max_batch, self.heads, self.hd, max_ctx, dtype=torch.bfloat16,
-                                   device=device)
-        self.v_cache = torch.zeros(max_batch, self.heads, max_ctx, self.hd, dtype=torch.bfloat16,
-                                   device=device)
-        self._attn_ws = attention_workspace(max_batch, self.heads, self.hd, max_ctx, device)
+        self.cache = PagedKVCache(num_pages, self.heads, self.hd, device)
+        self._attn_ws = attention_workspace(max_batch, self.heads, self.hd, max_pages * PAGE,
+                                            device)
 
-    def forward_decode(self, x, positions):
-        B = x.shape[0]
+    def _qkv(self, x, positions):
+        n = x.shape[0]
         qkv, _ = self.qkv_proj(x)
-        q, k, v = qkv.view(B, 3, self.heads, self.hd).unbind(1)
-        q = rotary_neox(q, positions, self.inv_freq, self.rope_factor)
-        k = rotary_neox(k, positions, self.inv_freq, self.rope_factor)
-        rows = torch.arange(B, device=x.device)
-        self.k_cache[rows, :, :, positions] = k
-        self.v_cache[rows, :, positions] = v.contiguous()
-        out = decode_attention(q.contiguous(), self.k_cache[:B], self.v_cache[:B], positions,
-                               self.hd ** -0.5, self._attn_ws)            # (B, nh, hd)
+        q, k, v = qkv.view(n, 3, self.heads, self.hd).unbind(1)
+        return (rotary_neox(q, positions, self.inv_freq, self.rope_factor),
+                rotary_neox(k, positions, self.inv_freq, self.rope_factor), v)
+
+    def forward_decode(self, x, positions, block_table):
+        """x (B, H): one token per sequence at `positions` (B,)."""
+        B = x.shape[0]
+        q, k, v = self._qkv(x, positions)
+        self.cache.append(k, v.contiguous(), block_table, positions)
+        out = paged_decode_attention(q.contiguous(), self.cache.k, self.cache.v, block_table,
+                                     positions, self.hd ** -0.5, self._attn_ws)  # (B, nh, hd)
         o, _ = self.o_proj(out.reshape(B, self.heads * self.hd))
+        return o
+
+    def forward_prefill(self, x, nseq, L, block_table):
+        """x (nseq * L, H): prompts of L tokens (positions 0..L-1) of sequences
+        0..nseq-1 of `block_table`, packed in order."""
+        pos = torch.arange(L, device=x.device).repeat(nseq)
+        q, k, v = self._qkv(x, pos)
+        shape = (nseq, L, self.heads, self.hd)
+        q, k, v = (t.reshape(shape).transpose(1, 2).contiguous() for t in (q, k, v))
+        self.cache.write_prompt(k, v, block_table)
+        out = causal_prefill_attention(q, k, v, self.hd ** -0.5)       # (nseq, nh, L, hd)
+        o, _ = self.o_proj(out.transpose(1, 2).reshape(nseq * L, self.heads * self.hd))
         return o
 
 
@@ -117,10 +129,23 @@ class Evo2DecoderLayer(nn.Module):
         self.mixer = mixer
         self.mlp = Evo2MLP(h, config.intermediate_size, use_act=(i == 0), device=device)
 
-    def forward(self, positions, x, token_ids):
+    def forward(self, positions, x, token_ids, block_table):
+        """One decode token per sequence."""
         pre = self.pre_norm(x)
         if self.kind == "attn":
-            m = self.mixer.forward_decode(pre, positions)
+            m = self.mixer.forward_decode(pre, positions, block_table)
+        else:
+            m = self.mixer(pre, token_ids=token_ids)
+        post, x = self.post_norm(m, x)
+        return self.mlp(post) + x
+
+    def forward_prefill(self, x, token_ids, nseq, L, block_table):
+        """Prompts of L tokens of nseq sequences, packed (nseq * L, H); the
+        Hyena mixer reads the step's prefill metadata from the forward
+        context."""
+        pre = self.pre_norm(x)
+        if self.kind == "attn":
+            m = self.mixer.forward_prefill(pre, nseq, L, block_table)
         else:
             m = self.mixer(pre, token_ids=token_ids)
         post, x = self.post_norm(m, x)
@@ -128,21 +153,29 @@ class Evo2DecoderLayer(nn.Module):
 
 
 class Evo2DecodeModel(nn.Module):
-    """The whole model at decode for `max_batch` sequences with up to
-    `max_ctx` positions each.  Each sequence b owns Hyena state block
-    `slots[b]` in every Hyena layer's pool (block 0 is the null block)."""
+    """The whole model for `max_batch` sequences with up to `max_ctx`
+    positions each.  Each sequence b owns Hyena state block `slots[b]` in
+    every Hyena layer's pool (block 0 is the null block) and KV pages
+    `block_table[b]` in every attention layer (a seeded random permutation
+    of pages 1..; page 0 is never used)."""
 
     def __init__(self, config, max_batch, max_ctx, device, rope_theta=10000.0, rope_factor=1.0,
-                 name="evo2"):
+                 name="evo2", page_seed=0):
         super().__init__()
         self.config = config
         h = config.hidden_size
         self.embed = nn.Parameter(torch.empty(config.vocab_size, h, dtype=torch.bfloat16,
                                               device=device), requires_grad=False)
+        self.max_pages = -(-max_ctx // PAGE)
+        num_pages = max_batch * self.max_pages + 1
+        g = torch.Generator().manual_seed(page_seed)
+        perm = torch.randperm(num_pages - 1, generator=g)[:max_batch * self.max_pages] + 1
+        self.block_table = perm.to(torch.int32).view(max_batch, self.max_pages).to(device)
         layers, self.pools = [], {}
         for i in range(config.num_hidden_layers):
             if config.layer_kind(i) == "attn":
-                mixer = Evo2Attention(config, max_batch, max_ctx, rope_theta, rope_factor, device)
+                mixer = Evo2Attention(config, num_pages, self.max_pages, max_batch, rope_theta,
+                                      rope_factor, device)
             else:
                 mixer = make_mixer(config, i, prefix=f"{name}.layers.{i}.mixer", device=device)
                 pool = HyenaStatePool(max_batch + 1, h, device)
@@ -156,8 +189,9 @@ class Evo2DecodeModel(nn.Module):
 
     def init_random(self, seed, state_scale=1.0, kv_scale=1.0):
         """Seeded random weights (projections N(0, 0.02), norms 1, embedding
-        N(0, 1), Hyena parameters as `synthetic.mixer_params`) and random
-        Hyena states and KV entries standing in for a prefilled prompt."""
+        N(0, 1), Hyena parameters as `synthetic.mixer_params`); the Hyena
+        states and KV pages random with the given scales (0 leaves them zero,
+        as before a prefill)."""
         dev = self.embed.device
         g = torch.Generator(device=dev)
         g.manual_seed(seed)
@@ -170,36 +204,66 @@ class Evo2DecodeModel(nn.Module):
                 for mod in (a.qkv_proj, a.o_proj):
                     mod.weight.data.copy_(torch.randn(mod.weight.shape, generator=g, device=dev) * 0.02)
                 a.o_proj.bias.data.copy_(torch.randn(a.o_proj.bias.shape, generator=g, device=dev) * 0.02)
-                a.k_cache.copy_(torch.randn(a.k_cache.shape, generator=g, device=dev) * kv_scale)
-                a.v_cache.copy_(torch.randn(a.v_cache.shape, generator=g, device=dev) * kv_scale)
+                if kv_scale:
+                    a.cache.k.copy_(torch.randn(a.cache.k.shape, generator=g, device=dev) * kv_scale)
+                    a.cache.v.copy_(torch.randn(a.cache.v.shape, generator=g, device=dev) * kv_scale)
+                else:
+                    a.cache.k.zero_()
+                    a.cache.v.zero_()
             else:
                 prm = mixer_params(layer.kind, self.config.hidden_size, seed + 1000 + i, device=dev,
                                    in_proj_fp8=self.config.use_fp8_input_projections)
                 load_mixer_params(layer.mixer, prm)
                 pool = self.pools[i]
                 pool.raw.zero_()
-                pool.kv_cache[0].copy_(torch.randn(pool.kv_cache[0].shape, generator=g,
-                                                   device=dev) * state_scale)
-                pool.kv_cache[1].copy_(torch.randn(pool.kv_cache[1].shape, generator=g,
-                                                   device=dev).to(torch.bfloat16).float()
-                                       * state_scale)
-                pool.kv_cache[2].copy_(torch.randn(pool.kv_cache[2].shape, generator=g,
-                                                   device=dev) * state_scale)
+                if state_scale:
+                    pool.kv_cache[0].copy_(torch.randn(pool.kv_cache[0].shape, generator=g,
+                                                       device=dev) * state_scale)
+                    pool.kv_cache[1].copy_(torch.randn(pool.kv_cache[1].shape, generator=g,
+                                                       device=dev).to(torch.bfloat16).float()
+                                           * state_scale)
+                    pool.kv_cache[2].copy_(torch.randn(pool.kv_cache[2].shape, generator=g,
+                                                       device=dev) * state_scale)
         return self
+
+    def prefill(self, tokens, chunk_seqs=8):
+        """Prompts tokens (B, L) of sequences 0..B-1 through every layer, in
+        groups of `chunk_seqs` sequences: fresh Hyena states (the prefill
+        kernels write each sequence's final state and windows into its
+        blocks) and KV pages for positions 0..L-1.  Returns the logits of the
+        last position (B, vocab)."""
+        B, L = tokens.shape
+        if B > self.max_batch or L > self.max_pages * PAGE:
+            raise ValueError(f"prompts ({B}, {L}) exceed the model's {self.max_batch} sequences "
+                             f"of {self.max_pages * PAGE} positions")
+        last = []
+        for b0 in range(0, B, chunk_seqs):
+            n = min(chunk_seqs, B - b0)
+            tok = tokens[b0:b0 + n].reshape(-1)
+            m = build_metadata(prefill_lens=[L] * n, prefill_slots=self.slots[b0:b0 + n].tolist(),
+                               has_init=[0] * n, device=tokens.device)
+            x = self.embed[tok]
+            with set_forward_context(m):
+                for layer in self.layers:
+                    x = layer.forward_prefill(x, tok, n, L, self.block_table[b0:b0 + n])
+            last.append(x.view(n, L, -1)[:, -1])
+        h = self.norm(torch.cat(last))
+        return torch.nn.functional.linear(h, self.embed)
 
     def decode_step(self, tokens, positions):
         """One token for each of the first B = len(tokens) sequences at the
         given positions: returns logits (B, vocab) and advances every layer's
-        state (Hyena state blocks, KV cache)."""
+        state (Hyena state blocks, KV pages)."""
         B = tokens.shape[0]
         m = getattr(self, "_meta", None)
         if m is None or m.num_decodes != B:
             m = self._meta = build_metadata(decode_slots=self.slots[:B].tolist(),
                                             device=tokens.device)
         x = self.embed[tokens]
+        table = self.block_table[:B]
         with set_forward_context(m):
             for layer in self.layers:
-                x = layer(positions, x, tokens)
+                x = layer(positions, x, tokens, table)
         h = self.norm(x)
         return torch.nn.functional.linear(h, self.embed)
 
@@ -220,5 +284,16 @@ def decode_flops_bytes(config, B, ctx):
     return w, kv
 
 
+def prefill_flops(config, L):
+    """Multiply-add flop of one L-token prefill of one sequence: every
+    projection and MLP over L rows, and causal attention (L^2 / 2 positions
+    per head, two products)."""
+    h, f = config.hidden_size, config.intermediate_size
+    n_attn = len(config.attn_layer_idxs)
+    n_hy = config.num_hidden_layers - n_attn
+    per_tok = config.num_hidden_layers * 3 * h * f + n_attn * 4 * h * h + n_hy * 4 * h * h
+    return 2 * L * per_tok + n_attn * 2 * 2 * h * L * L // 2
+
+
 __all__ = ["Evo2MLP", "Evo2Attention", "Evo2DecoderLayer", "Evo2DecodeModel", "rotary_neox",
-           "decode_flops_bytes"]
+           "decode_flops_bytes", "prefill_flops"]

@@ -287,6 +287,29 @@ int evo2_decode_attention(const void *q, int64_t qb, int64_t qh,
                           float scale, void *stream);
 
 /*
+ * evo2_decode_attention over a paged KV cache of 16-position pages:
+ * position l of sequence b lives in page block_table[b, l / 16] (row stride
+ * tbs) at offset l % 16;
+ *   key pages   (pages, heads, head_dim, 16): strides kp, kh, kd; position stride 1
+ *   value pages (pages, heads, 16, head_dim): strides vp, vh, vl; dim stride 1
+ * Sequence b attends to positions 0..positions[b] (< max_pages * 16); the
+ * workspace is evo2_decode_attention_workspace_bytes(B, heads, head_dim,
+ * max_pages * 16) bytes.
+ *
+ * Serves the attention layers of Evo2Attention at decode
+ * (evo2_flash/model.py:104-153) over the paged cache layout the serving
+ * engine keeps (vLLM's paged attention there, outside the mixer path).
+ */
+int evo2_paged_decode_attention(const void *q, int64_t qb, int64_t qh,
+                                const void *k_pages, int64_t kp, int64_t kh, int64_t kd,
+                                const void *v_pages, int64_t vp, int64_t vh, int64_t vl,
+                                const int32_t *block_table, int64_t tbs,
+                                const int64_t *positions, float *workspace,
+                                int64_t workspace_bytes, void *out, int64_t ob, int64_t oh,
+                                int64_t B, int64_t heads, int64_t head_dim, int64_t max_pages,
+                                float scale, void *stream);
+
+/*
  * Static per-tensor activation quantisation for the fp8 projections:
  * q = e4m3fn(clamp(x / scale[0], -448, 448)), round to nearest even.
  *   x (rows, K) bf16, row stride sx; q (rows, K) e4m3 bytes, row stride sq.

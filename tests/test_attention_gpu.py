@@ -11,7 +11,8 @@ benchmark's context.
 import pytest
 import torch
 
-from evo2_flash_amd.attention import decode_attention, workspace
+from evo2_flash_amd.attention import (PAGE, PagedKVCache, decode_attention,
+                                     paged_decode_attention, workspace)
 
 from _cases import max_rel_err
 
@@ -61,4 +62,29 @@ def test_decode_attention_7b_shape():
     ref = _ref(q, kc, vc, positions, hd ** -0.5)
     print("decode_attention 7B shape", flush=True)
     out = decode_attention(q.to(DEV), kc.to(DEV), vc.to(DEV), positions.to(DEV), hd ** -0.5)
+    assert max_rel_err(out.cpu(), ref) <= 1e-2
+
+
+@pytest.mark.parametrize("hd,max_pages,pos", [(64, 3, [47, 0, 16, 15]),
+                                              (128, 260, [4159, 2047, 2048, 100]),
+                                              (128, 544, [8192, 8703, 17])])
+def test_paged_decode_attention_vs_fp32(hd, max_pages, pos):
+    """The cache in 16-position pages of a random block table (page 0 never
+    used): the same attention as over the dense cache the pages hold."""
+    g = torch.Generator().manual_seed(hd + max_pages)
+    B, nh = len(pos), 4 if hd == 64 else 32
+    num_pages = B * max_pages + 5
+    table = (torch.randperm(num_pages - 1, generator=g)[:B * max_pages] + 1).to(torch.int32)
+    table = table.view(B, max_pages)
+    cache = PagedKVCache(num_pages, nh, hd, "cpu")
+    cache.k.copy_((torch.randn(cache.k.shape, generator=g) * 0.5).to(bf))
+    cache.v.copy_((torch.randn(cache.v.shape, generator=g) * 0.5).to(bf))
+    q = torch.randn(B, nh, hd, generator=g).to(bf)
+    positions = torch.tensor(pos, dtype=torch.int64)
+    kd, vd = cache.dense(table, B, max_pages * PAGE)
+    ref = _ref(q, kd, vd, positions, hd ** -0.5)
+    print(f"paged decode_attention hd={hd} pages={max_pages} pos={pos}", flush=True)
+    out = paged_decode_attention(q.to(DEV), cache.k.to(DEV), cache.v.to(DEV), table.to(DEV),
+                                 positions.to(DEV), hd ** -0.5)
+    assert out.shape == (B, nh, hd)
     assert max_rel_err(out.cpu(), ref) <= 1e-2

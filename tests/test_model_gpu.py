@@ -1,9 +1,16 @@
 """The decoder harness (model.py:47-200 restated around this build's mixers)
 against a CPU composition of the same weights: the oracle for RMSNorm and the
-Hyena mixer step, plain fp32 torch for the MLP and attention, bf16 at the
-same op boundaries.  Three decode steps of three sequences through a
-five-layer model (hcs, hcm, hcl, attention, hcs); logits within 2e-2 and the
-Hyena state pools within the mixer tolerance after every step."""
+Hyena mixer steps, plain fp32 torch for the MLP and attention, bf16 at the
+same op boundaries.  A five-layer model (hcs, hcm, hcl, attention, hcs) with
+the KV cache in 16-position pages of a random block table:
+* three decode steps of three sequences: logits within 2e-2 and the Hyena
+  state pools within the mixer tolerance after every step;
+* a prefill of two prompts: last-position logits within 2e-2, Hyena states
+  and the KV pages of the prompt against the composition;
+* prefill(L) followed by one decode step equals prefill(L + 1) at the last
+  position (logits and states), which ties the prefill and decode paths of
+  every layer kind to each other;
+* the whole decode step captured once as a HIP graph replays like eager steps."""
 
 import pytest
 import torch
@@ -47,12 +54,24 @@ def _attn_ref(a, x, pos, kc, vc):
     return _lin(out.to(bf).view(B, nh * hd), a.o_proj.weight.cpu(), a.o_proj.bias.cpu())
 
 
+def _cfg5(H=256):
+    return HyenaConfig(hidden_size=H, num_hidden_layers=5, num_attention_heads=4,
+                       intermediate_size=384, vocab_size=512, hcs_layer_idxs=[0, 4],
+                       hcm_layer_idxs=[1], hcl_layer_idxs=[2], attn_layer_idxs=[3],
+                       use_fp8_input_projections=True)
+
+
+def _mlp_ref(layer, post):
+    z1 = _lin(post, layer.mlp.l1.weight.cpu())
+    z2 = _lin(post, layer.mlp.l2.weight.cpu())
+    if layer.mlp.use_act:
+        z1 = torch.nn.functional.gelu(z1.float()).to(bf)
+    return _lin((z1.float() * z2.float()).to(bf), layer.mlp.l3.weight.cpu())
+
+
 def test_decode_steps_vs_cpu_composition():
     H, B = 256, 3
-    cfg = HyenaConfig(hidden_size=H, num_hidden_layers=5, num_attention_heads=4,
-                      intermediate_size=384, vocab_size=512, hcs_layer_idxs=[0, 4],
-                      hcm_layer_idxs=[1], hcl_layer_idxs=[2], attn_layer_idxs=[3],
-                      use_fp8_input_projections=True)
+    cfg = _cfg5(H)
     model = Evo2DecodeModel(cfg, max_batch=B, max_ctx=32, device=DEV, rope_theta=10000.0,
                             rope_factor=4.0, name="harness_test")
     model.init_random(seed=11, state_scale=0.5, kv_scale=0.5)
@@ -63,7 +82,7 @@ def test_decode_steps_vs_cpu_composition():
         c.raw.copy_(p.raw.cpu())
         pools[i] = c
     attn = model.layers[3].mixer
-    kc, vc = attn.k_cache.cpu(), attn.v_cache.cpu()
+    kc, vc = (t.cpu() for t in attn.cache.dense(model.block_table, B, 32))
     emb = model.embed.detach().cpu()
     g = torch.Generator().manual_seed(3)
     pos = torch.tensor([10, 4, 17])
@@ -82,12 +101,7 @@ def test_decode_steps_vs_cpu_composition():
                 m = oracle_mixer_step(layer.kind, prm, pre, pools[i], slots, [], [], [], H)
             post, x = oracle.rms_norm(m, layer.post_norm.weight.cpu(), cfg.rms_norm_eps,
                                       residual=x)
-            z1 = _lin(post, layer.mlp.l1.weight.cpu())
-            z2 = _lin(post, layer.mlp.l2.weight.cpu())
-            if layer.mlp.use_act:
-                z1 = torch.nn.functional.gelu(z1.float()).to(bf)
-            x = (_lin((z1.float() * z2.float()).to(bf), layer.mlp.l3.weight.cpu()).float()
-                 + x.float()).to(bf)
+            x = (_mlp_ref(layer, post).float() + x.float()).to(bf)
         ref = _lin(oracle.rms_norm(x, model.norm.weight.cpu(), cfg.rms_norm_eps), emb)
         assert max_rel_err(logits, ref) <= 2e-2, step
         for i, p in model.pools.items():
@@ -139,3 +153,88 @@ def test_decode_step_graph_replays():
         assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), step
         for i in graphed.pools:
             assert torch.equal(graphed.pools[i].raw, eager.pools[i].raw), (step, i)
+
+
+def _prefill_attn_ref(a, x, nseq, L):
+    """fp32 causal attention of layer a over packed prompts x (nseq * L, H);
+    returns the layer output and the rotated keys and values (nseq, nh, L, hd)."""
+    nh, hd = a.heads, a.hd
+    pos = torch.arange(L).repeat(nseq)
+    q, k, v = _lin(x, a.qkv_proj.weight.cpu()).view(nseq * L, 3, nh, hd).unbind(1)
+    inv = a.inv_freq.cpu()
+    q = rotary_neox(q, pos, inv, a.rope_factor)
+    k = rotary_neox(k, pos, inv, a.rope_factor)
+    q, k, v = (t.reshape(nseq, L, nh, hd).transpose(1, 2) for t in (q, k, v))
+    s = (q.float() @ k.float().transpose(-1, -2).contiguous()) * hd ** -0.5
+    s = s.masked_fill(torch.ones(L, L, dtype=torch.bool).triu(1), float("-inf"))
+    o = torch.softmax(s, dim=-1) @ v.float()
+    o = o.to(bf).transpose(1, 2).reshape(nseq * L, nh * hd)
+    return _lin(o, a.o_proj.weight.cpu(), a.o_proj.bias.cpu()), k, v
+
+
+def test_prefill_vs_cpu_composition():
+    """Two fresh 45-token prompts through the model: last-position logits,
+    the Hyena states written for each sequence and the KV pages of the
+    prompt against the CPU composition."""
+    H, B, L = 256, 2, 45
+    cfg = _cfg5(H)
+    model = Evo2DecodeModel(cfg, max_batch=3, max_ctx=64, device=DEV, rope_theta=10000.0,
+                            rope_factor=4.0, name="harness_prefill", page_seed=3)
+    model.init_random(seed=12, state_scale=0.0, kv_scale=0.0)
+    g = torch.Generator().manual_seed(5)
+    tok = torch.tensor([65, 67, 71, 84])[torch.randint(0, 4, (B, L), generator=g)]
+    print("harness prefill", flush=True)
+    logits = model.prefill(tok.to(DEV), chunk_seqs=2).cpu()
+    emb = model.embed.detach().cpu()
+    pools = {i: HyenaStatePool(p.num_blocks, H, "cpu") for i, p in model.pools.items()}
+    slots = model.slots.cpu()[:B].tolist()
+    x = emb[tok.reshape(-1)]
+    for i, layer in enumerate(model.layers):
+        pre = oracle.rms_norm(x, layer.pre_norm.weight.cpu(), cfg.rms_norm_eps)
+        if layer.kind == "attn":
+            m, k_ref, v_ref = _prefill_attn_ref(layer.mixer, pre, B, L)
+        else:
+            prm = {k: v.detach().cpu() for k, v in layer.mixer.named_parameters()}
+            m = oracle_mixer_step(layer.kind, prm, pre, pools[i], [], [L] * B, slots, [0] * B, H)
+        post, x = oracle.rms_norm(m, layer.post_norm.weight.cpu(), cfg.rms_norm_eps, residual=x)
+        x = (_mlp_ref(layer, post).float() + x.float()).to(bf)
+    last = x.view(B, L, H)[:, -1]
+    ref = _lin(oracle.rms_norm(last, model.norm.weight.cpu(), cfg.rms_norm_eps), emb)
+    assert max_rel_err(logits, ref) <= 2e-2
+    for i, p in model.pools.items():
+        assert max_rel_err(p.kv_cache[1].cpu(), pools[i].kv_cache[1]) <= 2e-2, i
+        assert max_rel_err(p.kv_cache[2].cpu(), pools[i].kv_cache[2]) <= 2e-2, i
+    kd, vd = model.layers[3].mixer.cache.dense(model.block_table, B, L)
+    assert max_rel_err(kd.cpu(), k_ref.transpose(-1, -2)) <= 2e-2
+    assert max_rel_err(vd.cpu(), v_ref) <= 2e-2
+
+
+def test_prefill_then_decode_matches_longer_prefill():
+    """prefill(L) + one decode token == prefill(L + 1) at its last position:
+    logits, Hyena states and the new KV entries, for prompts of 40 and 47
+    tokens (the decode position in the middle of a page and at a page start)."""
+    H, B = 256, 2
+    cfg = _cfg5(H)
+    for L in (40, 47):
+        a = Evo2DecodeModel(cfg, max_batch=B, max_ctx=64, device=DEV, rope_theta=10000.0,
+                            rope_factor=4.0, name=f"harness_pd_a{L}", page_seed=9)
+        b = Evo2DecodeModel(cfg, max_batch=B, max_ctx=64, device=DEV, rope_theta=10000.0,
+                            rope_factor=4.0, name=f"harness_pd_b{L}", page_seed=9)
+        a.init_random(seed=21, state_scale=0.0, kv_scale=0.0)
+        b.init_random(seed=21, state_scale=0.0, kv_scale=0.0)
+        g = torch.Generator().manual_seed(L)
+        tok = torch.tensor([65, 67, 71, 84])[torch.randint(0, 4, (B, L + 1), generator=g)].to(DEV)
+        print(f"prefill({L}) + decode vs prefill({L + 1})", flush=True)
+        full = a.prefill(tok)
+        b.prefill(tok[:, :L])
+        step = b.decode_step(tok[:, L].contiguous(), torch.full((B,), L, device=DEV))
+        assert max_rel_err(step.cpu(), full.cpu()) <= 3e-2, L
+        for i in a.pools:
+            assert max_rel_err(b.pools[i].kv_cache[1].cpu(), a.pools[i].kv_cache[1].cpu()) <= 2e-2
+            assert max_rel_err(b.pools[i].kv_cache[2].cpu(), a.pools[i].kv_cache[2].cpu()) <= 2e-2
+            assert torch.equal(b.pools[i].kv_cache[0], a.pools[i].kv_cache[0]) or \
+                max_rel_err(b.pools[i].kv_cache[0].cpu(), a.pools[i].kv_cache[0].cpu()) <= 2e-2
+        ka, va = a.layers[3].mixer.cache.dense(a.block_table, B, L + 1)
+        kb, vb = b.layers[3].mixer.cache.dense(b.block_table, B, L + 1)
+        assert max_rel_err(kb.cpu(), ka.cpu()) <= 2e-2
+        assert max_rel_err(vb.cpu(), va.cpu()) <= 2e-2
