@@ -25,8 +25,8 @@ Also measured in the same run and reported in the same JSON line:
     of the reference torch decode path timed on the host cores.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--no-prefill] [--no-gemm]
-                    [--no-verify] [--no-model]
-                    [--only decode|verify|prefill|gemm|copy|model|config0]
+                    [--no-verify] [--no-model] [--no-model40b]
+                    [--only decode|verify|prefill|gemm|copy|model|config0|model_prefill|model40b]
 """
 
 import argparse
@@ -229,28 +229,30 @@ def bench_decode(steps, warmup, dev, seed=1234):
 
 # ---------------------------------------------------------------- whole model
 CTX_7B = 8192 + 512   # prompt plus the decode steps of the 7B workload
+PROMPT_7B = 8192
+ACGT = (65, 67, 71, 84)
 
 
-def bench_model(steps, dev, B=B_DECODE, seed=21):
-    """The whole 7B-shaped model at decode (32 layers: 27 Hyena on this
-    build's kernels, 5 attention layers on the decode-attention kernel, the
-    projections and MLPs in torch), B sequences (64 for
-    the 7B workload) at positions from 8192 on, rotary base 1e4 with linear scaling 128
-    (evo2-7b-1m.yml:27-29; the checkpoint's base wins, convert.py:524-570).
-    States and KV stand in for the prefilled prompt.  One decode step is one
-    HIP graph replay; the positions advance inside the graph."""
-    from evo2_flash_amd.config import evo2_7b
-    from evo2_flash_amd.model import Evo2DecodeModel, decode_flops_bytes
-
-    cfg = evo2_7b()
-    model = Evo2DecodeModel(cfg, max_batch=B, max_ctx=CTX_7B, device=dev, rope_theta=10000.0,
-                            rope_factor=128.0, name=f"bench_model_b{B}")
-    model.init_random(seed, state_scale=0.5, kv_scale=0.5)
+def _acgt(shape, dev, seed):
     g = torch.Generator(device=dev).manual_seed(seed)
-    tok = torch.tensor([65, 67, 71, 84], device=dev)[
-        torch.randint(0, 4, (B,), generator=g, device=dev)]
-    pos = torch.full((B,), 8192, dtype=torch.int64, device=dev)
+    return torch.tensor(ACGT, device=dev)[torch.randint(0, 4, shape, generator=g, device=dev)]
+
+
+def _sync_time(fn):
+    torch.cuda.synchronize()
+    t = time.perf_counter()
+    out = fn()
+    torch.cuda.synchronize()
+    return out, time.perf_counter() - t
+
+
+def _graph_decode(model, B, pos0, steps, dev, seed):
+    """Replay one captured decode step `steps` times from position pos0 on;
+    returns ms per step."""
+    tok = _acgt((B,), dev, seed)
+    pos = torch.full((B,), pos0, dtype=torch.int64, device=dev)
     model.decode_step(tok, pos)          # warm-up, builds the step's metadata
+    pos.add_(1)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     s = torch.cuda.Stream()
@@ -260,26 +262,137 @@ def bench_model(steps, dev, B=B_DECODE, seed=21):
             model.decode_step(tok, pos)
             pos.add_(1)
     torch.cuda.current_stream().wait_stream(s)
-    n = min(steps, 500)
     graph.replay()
     stream = torch.cuda.current_stream()
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
     t0.record(stream)
-    for _ in range(n):
+    for _ in range(steps):
         graph.replay()
     t1.record(stream)
     torch.cuda.synchronize()
-    ms = t0.elapsed_time(t1) / n
-    wbytes, kvbytes = decode_flops_bytes(cfg, B, 8192 + n)
-    del model, graph
+    del graph
+    return t0.elapsed_time(t1) / steps
+
+
+def bench_model(steps, dev, B=B_DECODE, seed=21):
+    """Config 1 end to end: the whole 7B-shaped model (32 layers: 27 Hyena on
+    this build's kernels, 5 attention layers on 16-position KV pages of a
+    seeded random block table), B sequences each prefilled from an
+    8192-token uniform-ACGT prompt (the mixers' prefill kernels write the
+    states, attention writes the pages), then decode from position 8192 on,
+    one HIP graph replay per step; rotary base 1e4 with linear scaling 128
+    (evo2-7b-1m.yml:27-29).  Projections and MLPs are torch."""
+    from evo2_flash_amd.config import evo2_7b
+    from evo2_flash_amd.model import Evo2DecodeModel, decode_flops_bytes
+
+    cfg = evo2_7b()
+    model = Evo2DecodeModel(cfg, max_batch=B, max_ctx=CTX_7B, device=dev, rope_theta=10000.0,
+                            rope_factor=128.0, name=f"bench_model_b{B}", page_seed=seed)
+    model.init_random(seed, state_scale=0.0, kv_scale=0.0)
+    prompts = _acgt((B, PROMPT_7B), dev, seed + 1)
+    _, t_pre = _sync_time(lambda: model.prefill(prompts, chunk_seqs=8))
+    n = min(steps, 500)
+    ms = _graph_decode(model, B, PROMPT_7B, n, dev, seed + 2)
+    wbytes, kvbytes = decode_flops_bytes(cfg, B, PROMPT_7B + n)
+    del model
     torch.cuda.empty_cache()
     return {"tok_s": round(B / (ms * 1e-3), 1), "ms_per_step": round(ms, 3), "batch": B,
-            "context": f"8192..{8192 + n}", "layers": 32,
+            "context": f"{PROMPT_7B}..{PROMPT_7B + n}", "layers": 32,
+            "prefill": {"prompt_tokens": B * PROMPT_7B, "s": round(t_pre, 2),
+                        "tok_s": round(B * PROMPT_7B / t_pre, 1)},
             "bytes_per_step": {"weights": wbytes, "kv_cache": kvbytes},
             "achieved_GBs": round((wbytes + kvbytes) / (ms * 1e-3) / 1e9, 1),
-            "note": "Hyena mixers and decode attention on this build's kernels; "
-                    "projections and MLP in torch"}
+            "kv": "16-position pages, seeded random block table",
+            "note": "states and KV pages from prefilling the prompts; Hyena mixers and decode "
+                    "attention on this build's kernels; projections and MLP in torch"}
+
+
+def _layer_timers(model):
+    """Wrap each layer's mixer so a run records (kind, start, end) events
+    around it, for the share of the mixers in a prefill."""
+    recs = []
+    for layer in model.layers:
+        mixer = layer.mixer
+        name = "forward_prefill" if layer.kind == "attn" else "forward"
+        orig = getattr(mixer, name)
+
+        def timed(*a, _orig=orig, _kind=layer.kind, **k):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            out = _orig(*a, **k)
+            e1.record()
+            recs.append((_kind, e0, e1))
+            return out
+        setattr(mixer, name, timed)
+    return recs
+
+
+def bench_model_prefill(dev, L=L_PREFILL, reps=3, seed=31):
+    """Config 2 end to end: the whole 7B-shaped model over one L-token
+    uniform-ACGT prompt (norms, fp8 in_proj, the mixer cores, out_proj, MLPs,
+    causal attention), tokens/s; one instrumented run splits the time by
+    layer kind (the Hyena layers' time is in_proj + core + out_proj)."""
+    from evo2_flash_amd.config import evo2_7b
+    from evo2_flash_amd.model import Evo2DecodeModel, prefill_flops
+
+    cfg = evo2_7b()
+    model = Evo2DecodeModel(cfg, max_batch=1, max_ctx=L, device=dev, rope_theta=10000.0,
+                            rope_factor=128.0, name="bench_prefill_model", page_seed=seed)
+    model.init_random(seed, state_scale=0.0, kv_scale=0.0)
+    prompt = _acgt((1, L), dev, seed + 1)
+    model.prefill(prompt, chunk_seqs=1)      # warm-up
+    times = [_sync_time(lambda: model.prefill(prompt, chunk_seqs=1))[1] for _ in range(reps)]
+    t = statistics.median(times)
+    recs = _layer_timers(model)
+    _, t_inst = _sync_time(lambda: model.prefill(prompt, chunk_seqs=1))
+    per = {}
+    for kind, e0, e1 in recs:
+        per[kind] = per.get(kind, 0.0) + e0.elapsed_time(e1) * 1e3
+    fl = prefill_flops(cfg, L)
+    del model
+    torch.cuda.empty_cache()
+    return {"L": L, "ms": round(t * 1e3, 2), "tok_s": round(L / t, 1),
+            "TFLOPs": round(fl / t / 1e12, 1), "flop": fl,
+            "layer_us": {k: round(v, 1) for k, v in per.items()},
+            "instrumented_ms": round(t_inst * 1e3, 2),
+            "note": "whole 7B-shaped model, batch 1; Hyena layers = in_proj + mixer core + "
+                    "out_proj on this build's kernels; attention, MLP and norms' GEMMs in torch"}
+
+
+def bench_model40b(steps, dev, B=32, L=131072, seed=41):
+    """Config 4 end to end: the 40B-shaped model (50 layers, H=8192, attention
+    at 3, 10, 17, 24, 31, 35, 42, 49 as evo2-40b-1m.yml, fp8 in_proj),
+    weights resident (~80 GB), the residual stream at ~1e6 (embedding rows
+    scaled by 1e6), one L-token prompt prefilled once, its KV pages shared by
+    all B sequences and its Hyena states copied to each, then B sequences
+    decode from position L on (one HIP graph replay per step)."""
+    from evo2_flash_amd.config import evo2_40b
+    from evo2_flash_amd.model import Evo2DecodeModel, decode_flops_bytes, prefill_flops
+
+    cfg = evo2_40b()
+    model = Evo2DecodeModel(cfg, max_batch=B, max_ctx=L + 256, device=dev, rope_theta=10000.0,
+                            rope_factor=128.0, name="bench_model_40b", page_seed=seed,
+                            shared_prefix=L)
+    model.init_random(seed, state_scale=0.0, kv_scale=0.0, embed_scale=1e6)
+    prompt = _acgt((L,), dev, seed + 1)
+    logits, t_pre = _sync_time(lambda: model.prefill_shared(prompt))
+    finite = bool(torch.isfinite(logits).all())
+    n = min(steps, 256)
+    ms = _graph_decode(model, B, L, n, dev, seed + 2)
+    wbytes, kvbytes = decode_flops_bytes(cfg, B, L + n)
+    fl = prefill_flops(cfg, L)
+    del model
+    torch.cuda.empty_cache()
+    return {"prefill": {"L": L, "s": round(t_pre, 2), "tok_s": round(L / t_pre, 1),
+                        "TFLOPs": round(fl / t_pre / 1e12, 1), "logits_finite": finite},
+            "decode": {"batch": B, "steps": n, "ms_per_step": round(ms, 3),
+                       "tok_s": round(B / (ms * 1e-3), 1),
+                       "bytes_per_step": {"weights": wbytes, "kv_cache": kvbytes},
+                       "achieved_GBs": round((wbytes + kvbytes) / (ms * 1e-3) / 1e9, 1)},
+            "kv": "one prompt's 16-position pages shared by all sequences through the block "
+                  "table, then one page run per sequence",
+            "residual_scale": 1e6}
 
 
 # ---------------------------------------------------------------- speculative verify
@@ -372,7 +485,10 @@ def bench_prefill(reps, dev, L=L_PREFILL, H=H_7B, seed=77):
     step_us = 9 * sum(v["avg_us"] for v in res.values())
     ideal_us = 27 * prefill_bytes(L, H) / (HBM_PEAK_GBS * 1e3)
     del z
-    return {"tok_s": round(L / (step_us * 1e-6), 1), "us_per_step": round(step_us, 1),
+    return {"scope": "the 27 Hyena mixer cores of the 7B layer map, z -> g (short filter, "
+                     "gate, inner FIR or modal scan, D, x2); in_proj, out_proj, norms, MLPs "
+                     "and attention are in model_prefill",
+            "tok_s": round(L / (step_us * 1e-6), 1), "us_per_step": round(step_us, 1),
             "L": L, "mixer_frac": round(ideal_us / step_us, 4), "per_kind": res}
 
 
@@ -459,7 +575,9 @@ def bench_config0(reps, dev, H=1920, L=2048, seed=11, cpu=True):
             entry.update({"cpu_s": round(cs, 4), "cpu_tok_s": round(L / cs, 1)})
         res[kind] = entry
     del z
-    return {"H": H, "L": L, "cores": n if cpu else None, "cpu_model": _cpu_model() if cpu else None,
+    return {"scope": "one Hyena mixer core per kind, z -> g (short filter, gate, inner FIR or "
+                     "modal scan, D, x2), the same on both legs; projections not included",
+            "H": H, "L": L, "cores": n if cpu else None, "cpu_model": _cpu_model() if cpu else None,
             "cpu_kind": "oracle restatement of the reference torch path" if cpu else None,
             "per_block": res}
 
@@ -549,6 +667,91 @@ def _cpu_baseline_decode(budget_s=20.0):
                        + ", ".join(f"{k}={v:.4f}" for k, v in per.items()))}
 
 
+def _cpu_baseline_layers(L=4096, budget_s=30.0):
+    """The oracle's restatement of the reference torch path for one layer of
+    each Hyena kind at the other configs' shapes, on the host cores:
+    config 2's prefill at H=4096 (L=4096 here, an eighth of the 32768-token
+    prompt; the FIRs scale linearly in L, the FFT convolution as L log L) and
+    config 4's decode step at B=32, H=8192.  Median of 2 after a warm-up."""
+    import oracle
+    from evo2_flash_amd.state import HyenaStatePool
+    from evo2_flash_amd.synthetic import mixer_params, random_slot_table
+
+    n = len(os.sched_getaffinity(0))
+    torch.set_num_threads(n)
+    t_start = time.perf_counter()
+    out = {"cores": n, "cpu_model": _cpu_model(), "kind": "port"}
+    pre, H = {}, H_7B
+    g = torch.Generator().manual_seed(8)
+    z = (torch.randn(L, 3 * H, generator=g) * 1.3).to(torch.bfloat16)
+    for kind in ("hcs", "hcm", "hcl"):
+        prm = mixer_params(kind, H, 77, in_proj_fp8=False)
+        pool = HyenaStatePool(2, H, "cpu")
+        sw = prm["short_filter"].view(3 * H, 3)
+
+        def run(zz, prm=prm, pool=pool, sw=sw, kind=kind):
+            if kind == "hcl":
+                oracle.iir_mixer_prefill(zz, sw, pool.conv_view(), prm["residues"],
+                                         prm["log_poles"][..., 0], pool.ssm_view(), prm["D"],
+                                         [0, zz.shape[0]], [1], [0])
+            else:
+                K = prm["conv"].shape[-1]
+                oracle.fir_mixer_prefill(zz, sw, pool.conv_view(), prm["conv"].view(H, K),
+                                         pool.inner_view(K - 1), prm.get("D"),
+                                         [0, zz.shape[0]], [1], [0])
+        with torch.inference_mode():
+            run(z[:512])
+            ts = []
+            for _ in range(2):
+                t = time.perf_counter()
+                run(z)
+                ts.append(time.perf_counter() - t)
+                if time.perf_counter() - t_start > budget_s:
+                    break
+        sec = statistics.median(ts)
+        pre[kind] = {"s": round(sec, 4), "tok_s": round(L / sec, 1)}
+    step = 9 * sum(v["s"] for v in pre.values())
+    out["prefill_7b"] = {"H": H, "L": L, "per_layer": pre,
+                         "mixer_cores_tok_s": round(L / step, 1),
+                         "note": f"27 mixer cores = 9 x (hcs + hcm + hcl), same scope as the "
+                                 f"GPU prefill leg; L={L} of config 2's {L_PREFILL}"}
+    dec, H, B = {}, 8192, 32
+    for kind in ("hcs", "hcm", "hcl"):
+        prm = mixer_params(kind, H, 78, in_proj_fp8=False)
+        pool = HyenaStatePool(B + 1, H, "cpu")
+        slots = random_slot_table(B, B + 1, 6)
+        zz = (torch.randn(B, 3 * H, generator=g) * 1.3).to(torch.bfloat16)
+        sw = prm["short_filter"].view(3 * H, 3)
+        if kind == "hcl":
+            inner, lp, st = prm["residues"], prm["log_poles"][..., 0], pool.ssm_view()
+        else:
+            inner, lp, st = prm["conv"].view(H, -1), None, pool.inner_view()
+        ts = []
+        with torch.inference_mode():
+            for _ in range(3):
+                t = time.perf_counter()
+                oracle.mixer_decode_unfused(zz, sw, pool.conv_view(), slots, inner, st,
+                                            prm.get("D"), lp)
+                ts.append(time.perf_counter() - t)
+        sec = statistics.median(ts[1:])
+        dec[kind] = {"s": round(sec, 4)}
+    step = 14 * sum(v["s"] for v in dec.values())
+    out["decode_40b"] = {"H": H, "B": B, "per_layer": dec, "mixer_cores_tok_s": round(B / step, 1),
+                         "note": "42 mixer cores = 14 x (hcs + hcm + hcl) of the 40B layer map"}
+    out["s"] = round(time.perf_counter() - t_start, 1)
+    return out
+
+
+def _guarded(fn, *a, **k):
+    """A whole-model leg whose failure (e.g. out of memory on a busy device)
+    is reported in the JSON line rather than ending the run."""
+    try:
+        return fn(*a, **k)
+    except (RuntimeError, torch.OutOfMemoryError) as e:
+        torch.cuda.empty_cache()
+        return {"error": f"{type(e).__name__}: {str(e)[:300]}"}
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -559,8 +762,11 @@ def main(argv=None):
     ap.add_argument("--no-gemm", action="store_true", help="skip the fp8 GEMM leg")
     ap.add_argument("--no-verify", action="store_true", help="skip the speculative verify leg")
     ap.add_argument("--no-model", action="store_true", help="skip the whole-model decode leg")
+    ap.add_argument("--no-model40b", action="store_true",
+                    help="skip the 40B-shaped whole model (131072-token prefill, then B=32 "
+                         "decode; ~20 s, ~150 GB of HBM)")
     ap.add_argument("--only", choices=["decode", "verify", "prefill", "gemm", "copy", "model",
-                                       "config0"],
+                                       "config0", "model_prefill", "model40b"],
                     default=None,
                     help="run one leg only (for profiling); `copy` runs a plain 1 GiB "
                          "device copy, the reference dispatch for scaling HBM counters")
@@ -584,17 +790,22 @@ def main(argv=None):
     gem = bench_gemm(max(5, args.steps // 4), dev) if run("gemm", args.no_gemm) else None
     cf0 = (bench_config0(max(5, args.steps // 4), dev, cpu=not (args.no_cpu or args.only))
            if run("config0", False) else None)
-    mod = bench_model(max(16, args.steps // 2), dev) if run("model", args.no_model) else None
-    if mod:
+    mod = _guarded(bench_model, max(16, args.steps // 2), dev) if run("model", args.no_model) else None
+    mpre = _guarded(bench_model_prefill, dev) if run("model_prefill", args.no_model) else None
+    m40 = (_guarded(bench_model40b, 8, dev) if run("model40b", args.no_model or args.no_model40b)
+           else None)
+    if mod and "error" not in mod:
         # the reference's one published whole-step figure: a plain decode step
         # of the 7B model at batch 8 under full CUDA graphs, 7.85 ms on
         # H100/H200, context length not stated (api.py:384-385)
-        mod["batch8"] = bench_model(max(16, args.steps // 2), dev, B=8)
+        mod["batch8"] = _guarded(bench_model, max(16, args.steps // 2), dev, B=8)
         mod["batch8"]["reference"] = {"ms_per_step": 7.85, "hardware": "H100/H200",
                                       "source": "api.py:384-385",
                                       "note": "plain decode, whole 7B model, batch 8; "
                                               "context length not stated"}
     cpu = None if (args.no_cpu or args.only) else _cpu_baseline_decode()
+    if cpu is not None:
+        cpu["configs"] = _cpu_baseline_layers()
     line = {
         "metric": METRIC,
         "value": round(dec["tok_s"], 1) if dec else None,
@@ -629,6 +840,13 @@ def main(argv=None):
         line["fp8_gemm"] = gem
     if mod:
         line["model_decode"] = mod
+    if mpre:
+        if pre and "error" not in mpre:  # the 27 mixer cores of this run's prefill leg, as a share
+            mpre["mixer_core_us"] = pre["us_per_step"]
+            mpre["mixer_core_share"] = round(pre["us_per_step"] / (mpre["ms"] * 1e3), 4)
+        line["model_prefill"] = mpre
+    if m40:
+        line["model_40b"] = m40
     if cf0:
         line["config0_prefill"] = cf0
     if not args.only:

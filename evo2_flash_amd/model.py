@@ -160,17 +160,29 @@ class Evo2DecodeModel(nn.Module):
     of pages 1..; page 0 is never used)."""
 
     def __init__(self, config, max_batch, max_ctx, device, rope_theta=10000.0, rope_factor=1.0,
-                 name="evo2", page_seed=0):
+                 name="evo2", page_seed=0, shared_prefix=0):
         super().__init__()
         self.config = config
         h = config.hidden_size
         self.embed = nn.Parameter(torch.empty(config.vocab_size, h, dtype=torch.bfloat16,
                                               device=device), requires_grad=False)
         self.max_pages = -(-max_ctx // PAGE)
-        num_pages = max_batch * self.max_pages + 1
+        # With a shared prefix (a multiple of 16 positions) every sequence's
+        # first pages are the same ones: one prompt, prefilled once, whose KV
+        # all sequences read, each then writing its own pages.
+        if shared_prefix % PAGE or shared_prefix > self.max_pages * PAGE:
+            raise ValueError(f"shared_prefix {shared_prefix} must be a multiple of {PAGE} "
+                             f"within max_ctx")
+        sp = shared_prefix // PAGE
+        own = self.max_pages - sp
+        num_pages = sp + max_batch * own + 1
         g = torch.Generator().manual_seed(page_seed)
-        perm = torch.randperm(num_pages - 1, generator=g)[:max_batch * self.max_pages] + 1
-        self.block_table = perm.to(torch.int32).view(max_batch, self.max_pages).to(device)
+        perm = torch.randperm(num_pages - 1, generator=g) + 1
+        table = torch.empty(max_batch, self.max_pages, dtype=torch.int32)
+        table[:, :sp] = perm[:sp].to(torch.int32)
+        table[:, sp:] = perm[sp:].to(torch.int32).view(max_batch, own)
+        self.block_table = table.to(device)
+        self.shared_prefix = shared_prefix
         layers, self.pools = [], {}
         for i in range(config.num_hidden_layers):
             if config.layer_kind(i) == "attn":
@@ -187,15 +199,16 @@ class Evo2DecodeModel(nn.Module):
         self.max_batch = max_batch
         self.slots = torch.arange(1, max_batch + 1, dtype=torch.int32, device=device)
 
-    def init_random(self, seed, state_scale=1.0, kv_scale=1.0):
+    def init_random(self, seed, state_scale=1.0, kv_scale=1.0, embed_scale=1.0):
         """Seeded random weights (projections N(0, 0.02), norms 1, embedding
-        N(0, 1), Hyena parameters as `synthetic.mixer_params`); the Hyena
-        states and KV pages random with the given scales (0 leaves them zero,
-        as before a prefill)."""
+        N(0, embed_scale^2), which sets the residual stream's magnitude;
+        Hyena parameters as `synthetic.mixer_params`); the Hyena states and
+        KV pages random with the given scales (0 leaves them zero, as before
+        a prefill)."""
         dev = self.embed.device
         g = torch.Generator(device=dev)
         g.manual_seed(seed)
-        self.embed.data.copy_(torch.randn(self.embed.shape, generator=g, device=dev))
+        self.embed.data.copy_(torch.randn(self.embed.shape, generator=g, device=dev) * embed_scale)
         for i, layer in enumerate(self.layers):
             for mod in (layer.mlp.l1, layer.mlp.l2, layer.mlp.l3):
                 mod.weight.data.copy_(torch.randn(mod.weight.shape, generator=g, device=dev) * 0.02)
@@ -249,6 +262,20 @@ class Evo2DecodeModel(nn.Module):
             last.append(x.view(n, L, -1)[:, -1])
         h = self.norm(torch.cat(last))
         return torch.nn.functional.linear(h, self.embed)
+
+    def prefill_shared(self, prompt):
+        """Prefill one prompt (L,) with L = shared_prefix into sequence 0 and
+        hand its state to every sequence: the KV pages are shared through the
+        block table, the Hyena state blocks are copied.  Returns the logits
+        of the last position (1, vocab)."""
+        if prompt.shape[0] != self.shared_prefix:
+            raise ValueError(f"the shared prompt has {self.shared_prefix} tokens, "
+                             f"got {prompt.shape[0]}")
+        logits = self.prefill(prompt[None], chunk_seqs=1)
+        src = int(self.slots[0])
+        for pool in self.pools.values():
+            pool.raw[self.slots[1:].long()] = pool.raw[src].clone()
+        return logits
 
     def decode_step(self, tokens, positions):
         """One token for each of the first B = len(tokens) sequences at the
