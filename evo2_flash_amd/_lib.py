@@ -108,6 +108,17 @@ SIGNATURES = {
         _c_p, _c_i64, _c_i64,                     # out + strides (row, channel)
         _c_i64, _c_i64, _c_i64, _c_p,             # B, dim, num_blocks, stream
     ],
+    "evo2_causal_conv1d_update_spec": [
+        _c_p, _c_i64, _c_i64,                     # x + strides (row, channel)
+        _c_p, _c_i64, _c_i64, _c_i64, _c_i32,     # conv_state + strides, state_len
+        _c_p, _c_i64, _c_i64, _c_i32,             # w + strides, K
+        _c_p, _c_i32,                             # bias, activation
+        _c_p, _c_i64, _c_i64, _c_i32,             # slot matrix + strides, columns
+        _c_p, _c_p, _c_p, _c_p,                   # in_col, out_col, num_accepted, qsl
+        _c_i32, _c_i32,                           # max_query_len, pad_slot_id
+        _c_p, _c_i64, _c_i64,                     # out + strides (row, channel)
+        _c_i64, _c_i64, _c_i64, _c_i64, _c_p,     # nreq, T, dim, num_blocks, stream
+    ],
     "evo2_causal_conv1d_fn": [
         _c_p, _c_i64, _c_i64,                     # x + strides (channel, row)
         _c_p, _c_i64, _c_i64, _c_i32,             # w + strides, K

@@ -168,6 +168,84 @@ __global__ __launch_bounds__(SC_CH) void conv_window_kernel(ConvArgs p) {
   for (int k = 0; k < K - 1; ++k) win[k * p.cs2] = f2bf(v[k]);
 }
 
+// Speculative verification, packed varlen rows (vLLM's update convention under
+// num_accepted_tokens + query_start_loc).  The state holds state_len columns,
+// K-1 + (max_query_len - 1) for a verifier of max_query_len positions, and a
+// request's live (K-1)-window starts at column accepted - 1.  A request of q
+// tokens computes its outputs from that window and leaves in its output block
+//   columns [0, keep)        <- old columns [accepted, accepted + keep)
+//   columns [keep, keep + q) <- its q inputs
+// with keep = state_len - max_query_len; later columns are left as they were.
+// After a later step accepts a of these q tokens, the live window therefore
+// starts at column a - 1 again: the last K-1 genuine inputs end at column
+// keep + a - 1 = K - 2 + a - 1 when keep = K - 2.
+struct SpecConvArgs {
+  const bf16_t *x; int64_t xt, xc;          // (T, dim) packed rows
+  const bf16_t *w; int64_t w0, w1;
+  const bf16_t *bias;
+  bf16_t *cs; int64_t cs0, cs1, cs2;        // (blocks, dim, state_len)
+  const int32_t *idx; int64_t si0, si1;     // (nreq, ncols) slot matrix
+  const int32_t *in_col, *out_col;          // per request (null: column 0)
+  const int64_t *accepted;                  // per request, >= 1
+  const int32_t *qsl;                       // (nreq + 1) packed row starts
+  bf16_t *out; int64_t ot, oc;
+  int dim, state_len, max_q, ncols;
+  int64_t num_blocks;
+  int pad_slot;
+  int T;
+};
+
+template <int K, bool SILU>
+__global__ __launch_bounds__(SC_CH) void conv_update_spec_kernel(SpecConvArgs p) {
+  const int c = blockIdx.x * SC_CH + threadIdx.x;
+  const int r = blockIdx.y;
+  if (c >= p.dim) return;
+  const int a = p.qsl[r], e = p.qsl[r + 1];
+  if (e <= a || a < 0 || e > p.T) return;
+  const int q = e - a;
+  const int ic = p.in_col ? p.in_col[r] : 0, oc = p.out_col ? p.out_col[r] : 0;
+  const int64_t in_slot = (ic >= 0 && ic < p.ncols) ? p.idx[(int64_t)r * p.si0 + (int64_t)ic * p.si1] : -1;
+  const int64_t out_slot = (oc >= 0 && oc < p.ncols) ? p.idx[(int64_t)r * p.si0 + (int64_t)oc * p.si1] : -1;
+  const int64_t acc_n = p.accepted[r];
+  const int keep = p.state_len - p.max_q;
+  // requests the convention cannot place: a padding or out-of-range slot,
+  // more rows than the verifier has positions, or an accepted count past the
+  // window; their rows are zero and no state is touched
+  const bool ok = q <= p.max_q && acc_n >= 1 && acc_n <= p.max_q &&
+                  in_slot != p.pad_slot && in_slot >= 0 && in_slot < p.num_blocks &&
+                  out_slot != p.pad_slot && out_slot >= 0 && out_slot < p.num_blocks;
+  if (!ok) {
+    for (int t = a; t < e; ++t) p.out[(int64_t)t * p.ot + (int64_t)c * p.oc] = f2bf(0.0f);
+    return;
+  }
+  const int off = static_cast<int>(acc_n) - 1;
+  const bf16_t *src = p.cs + in_slot * p.cs0 + (int64_t)c * p.cs1;
+  bf16_t *dst = p.cs + out_slot * p.cs0 + (int64_t)c * p.cs1;
+  float s[K - 1];
+#pragma unroll
+  for (int k = 0; k < K - 1; ++k) s[k] = bf2f(src[(int64_t)(off + k) * p.cs2]);
+  float wk[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k) wk[k] = bf2f(p.w[(int64_t)c * p.w0 + k * p.w1]);
+  const float bias = p.bias ? bf2f(p.bias[c]) : 0.0f;
+  for (int t = a; t < e; ++t) {
+    const float x = bf2f(p.x[(int64_t)t * p.xt + (int64_t)c * p.xc]);
+    float acc = bias;
+#pragma unroll
+    for (int k = 0; k < K - 1; ++k) acc += rbf(s[k] * wk[k]);
+    acc += rbf(x * wk[K - 1]);
+    p.out[(int64_t)t * p.ot + (int64_t)c * p.oc] = f2bf(finish<SILU>(acc));
+#pragma unroll
+    for (int k = 0; k + 1 < K - 1; ++k) s[k] = s[k + 1];
+    s[K - 2] = x;
+  }
+  // ascending copy: column i reads column off + 1 + i > i, so in place
+  // (in_slot == out_slot) every old value is read before it is overwritten
+  for (int i = 0; i < keep; ++i) dst[(int64_t)i * p.cs2] = src[(int64_t)(off + 1 + i) * p.cs2];
+  for (int i = 0; i < q; ++i)
+    dst[(int64_t)(keep + i) * p.cs2] = p.x[(int64_t)(a + i) * p.xt + (int64_t)c * p.xc];
+}
+
 template <int K>
 static void launch_update(const ConvArgs &a, int64_t B, bool silu, hipStream_t st) {
   dim3 grid(static_cast<unsigned>(cdiv(a.dim, SC_CH)), static_cast<unsigned>(B));
@@ -259,4 +337,45 @@ extern "C" int evo2_causal_conv1d_fn(const void *x, int64_t xc, int64_t xt,
   if (K == 2) return launch_prefill<2>(a, silu, st);
   if (K == 3) return launch_prefill<3>(a, silu, st);
   return launch_prefill<4>(a, silu, st);
+}
+
+extern "C" int evo2_causal_conv1d_update_spec(
+    const void *x, int64_t xt, int64_t xc,
+    void *conv_state, int64_t cs0, int64_t cs1, int64_t cs2, int32_t state_len,
+    const void *w, int64_t w0, int64_t w1, int32_t K,
+    const void *bias, int32_t activation,
+    const int32_t *indices, int64_t si0, int64_t si1, int32_t ncols,
+    const int32_t *in_col, const int32_t *out_col, const int64_t *num_accepted,
+    const int32_t *query_start_loc, int32_t max_query_len, int32_t pad_slot_id,
+    void *out, int64_t ot, int64_t oc,
+    int64_t nreq, int64_t T, int64_t dim, int64_t num_blocks, void *stream) {
+  const char *fn = "causal_conv1d_update (speculative)";
+  int rc = check_conv(fn, dim, K, activation);
+  if (rc) return rc;
+  if (nreq < 0 || nreq > 65535 || T < 0 || T > 0x7fffffff || num_blocks <= 0 || ncols <= 0)
+    return fail(EVO2_ERR_INVALID, "%s: bad sizes nreq=%lld T=%lld num_blocks=%lld ncols=%d", fn,
+                (long long)nreq, (long long)T, (long long)num_blocks, ncols);
+  if (max_query_len < 1 || state_len < K - 1 + max_query_len - 1)
+    return fail(EVO2_ERR_INVALID,
+                "%s: a state of %d columns cannot hold a %d-position verifier window (K=%d needs "
+                "K-1 + max_query_len-1 columns)", fn, state_len, max_query_len, K);
+  if (nreq == 0) return EVO2_OK;
+  if (!x || !conv_state || !w || !out || !indices || !num_accepted || !query_start_loc)
+    return fail(EVO2_ERR_INVALID, "%s: null pointer argument", fn);
+  SpecConvArgs a{static_cast<const bf16_t *>(x), xt, xc, static_cast<const bf16_t *>(w), w0, w1,
+                 static_cast<const bf16_t *>(bias), static_cast<bf16_t *>(conv_state), cs0, cs1, cs2,
+                 indices, si0, si1, in_col, out_col, num_accepted, query_start_loc,
+                 static_cast<bf16_t *>(out), ot, oc, static_cast<int>(dim), state_len, max_query_len,
+                 ncols, num_blocks, pad_slot_id, static_cast<int>(T)};
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  dim3 grid(static_cast<unsigned>(cdiv(dim, SC_CH)), static_cast<unsigned>(nreq));
+  const bool silu = activation == 1;
+#define EVO2_SPEC_LAUNCH(KW)                                                                   \
+  if (silu) hipLaunchKernelGGL((conv_update_spec_kernel<KW, true>), grid, dim3(SC_CH), 0, st, a); \
+  else hipLaunchKernelGGL((conv_update_spec_kernel<KW, false>), grid, dim3(SC_CH), 0, st, a);
+  if (K == 2) { EVO2_SPEC_LAUNCH(2) }
+  else if (K == 3) { EVO2_SPEC_LAUNCH(3) }
+  else { EVO2_SPEC_LAUNCH(4) }
+#undef EVO2_SPEC_LAUNCH
+  return check_launch(fn);
 }

@@ -301,6 +301,10 @@ __device__ __forceinline__ float quad_move(float v) {
   return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
 }
 
+// VEC: the state rows are 16 contiguous, 16-byte aligned fp32 (one float4 per
+// lane); otherwise each lane moves its four states one by one (a row of the
+// speculative layout is 17 fp32, its last column the position stamp).
+template <bool VEC>
 __global__ __launch_bounds__(256) void iir_verify_kernel(VerifyArgs a) {
   const int lane = threadIdx.x & 63;
   const int qd = lane & 3;
@@ -311,11 +315,19 @@ __global__ __launch_bounds__(256) void iir_verify_kernel(VerifyArgs a) {
   const Req q = request_of(a, r);
   const float4 p4 = *reinterpret_cast<const float4 *>(a.poles + (int64_t)cc * a.p0 + 4 * qd);
   const float4 r4 = *reinterpret_cast<const float4 *>(a.res + (int64_t)cc * a.r0 + 4 * qd);
-  float4 s4 = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (q.src_ok) s4 = *reinterpret_cast<const float4 *>(a.st + q.src * a.ss0 + (int64_t)cc * a.ss1 + 4 * qd);
   const float pv[4] = {p4.x, p4.y, p4.z, p4.w};
   const float rv[4] = {r4.x, r4.y, r4.z, r4.w};
-  float sv[4] = {s4.x, s4.y, s4.z, s4.w};
+  float sv[4] = {0.f, 0.f, 0.f, 0.f};
+  if (q.src_ok) {
+    const float *sp = a.st + q.src * a.ss0 + (int64_t)cc * a.ss1 + 4 * qd * a.ss2;
+    if constexpr (VEC) {
+      const float4 s4 = *reinterpret_cast<const float4 *>(sp);
+      sv[0] = s4.x; sv[1] = s4.y; sv[2] = s4.z; sv[3] = s4.w;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sv[e] = sp[e * a.ss2];
+    }
+  }
   // token inputs up front (up to VQ), so their latencies overlap
   const int n = static_cast<int>(max<int64_t>(0, min<int64_t>(a.Q, q.end - q.first)));
   float xs[VQ];
@@ -334,9 +346,15 @@ __global__ __launch_bounds__(256) void iir_verify_kernel(VerifyArgs a) {
       rr[e] = sv[e] * rv[e];
     }
     const int64_t d = dest_of(a, r, pos);
-    if (d >= 0 && active)
-      *reinterpret_cast<float4 *>(a.st + d * a.ss0 + (int64_t)c * a.ss1 + 4 * qd) =
-          make_float4(sv[0], sv[1], sv[2], sv[3]);
+    if (d >= 0 && active) {
+      float *dp = a.st + d * a.ss0 + (int64_t)c * a.ss1 + 4 * qd * a.ss2;
+      if constexpr (VEC) {
+        *reinterpret_cast<float4 *>(dp) = make_float4(sv[0], sv[1], sv[2], sv[3]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) dp[e * a.ss2] = sv[e];
+      }
+    }
 #pragma unroll
     for (int e = 0; e < 4; ++e) rr[e] = rr[e] + quad_move<0xEE>(rr[e]);  // += state + 8
 #pragma unroll
@@ -417,17 +435,20 @@ extern "C" int evo2_iir_verify(const void *x, int64_t xs0, int64_t xs1, int32_t 
                          num_blocks);
   if (rc) return rc;
   if (!poles || !residues) return fail(EVO2_ERR_INVALID, "iir_verify: null pointer argument");
-  if (p1 != 1 || r1 != 1 || ss2 != 1 || p0 % 4 || r0 % 4 || ss1 % 4 || ss0 % 4 ||
-      reinterpret_cast<uintptr_t>(poles) % 16 || reinterpret_cast<uintptr_t>(residues) % 16 ||
-      reinterpret_cast<uintptr_t>(state) % 16)
+  if (p1 != 1 || r1 != 1 || p0 % 4 || r0 % 4 ||
+      reinterpret_cast<uintptr_t>(poles) % 16 || reinterpret_cast<uintptr_t>(residues) % 16)
     return fail(EVO2_ERR_UNSUPPORTED,
-                "iir_verify: poles, residues and states need 16 contiguous, 16-byte aligned "
-                "fp32 per channel");
+                "iir_verify: poles and residues need 16 contiguous, 16-byte aligned fp32 per "
+                "channel");
+  const bool vec = ss2 == 1 && ss1 % 4 == 0 && ss0 % 4 == 0 &&
+                   reinterpret_cast<uintptr_t>(state) % 16 == 0;
   if (nreq == 0) return EVO2_OK;
   VerifyArgs a{x, xs0, xs1, x_f32, nullptr, 0, 0, poles, p0, p1, residues, r0, r1,
                state, ss0, ss1, ss2, ins, is0, is1, outs, os0, os1,
                starts, ends, accepted, y, ys0, Q, static_cast<int>(H), null_block, num_blocks, T};
   dim3 grid(static_cast<unsigned>(cdiv(H, 64)), static_cast<unsigned>(nreq));
-  hipLaunchKernelGGL(iir_verify_kernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream), a);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (vec) hipLaunchKernelGGL(iir_verify_kernel<true>, grid, dim3(256), 0, st, a);
+  else hipLaunchKernelGGL(iir_verify_kernel<false>, grid, dim3(256), 0, st, a);
   return check_launch("iir_verify");
 }

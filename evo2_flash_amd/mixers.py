@@ -23,12 +23,26 @@ launch between in_proj and out_proj:
 
 With no metadata (the engine's profiling pass) the mixer returns
 out_proj(x2 * x1 * v) as the reference does (mixers.py:1230-1235).  There is
-no CPU path and no speculative-decode path: the kernels run on ROCm devices
-and a step whose metadata is speculative by the reference's predicate
-(mixers.py:930-937) raises.
+no CPU path: the kernels run on ROCm devices.
+
+Speculative decode (`num_spec` > 0 draft tokens, mixers.py:17-35, 952-1074):
+a step whose metadata is speculative by the reference's predicate
+(mixers.py:930-937) runs its decode rows as
+
+  decode rows   in_proj -> causal_conv1d_update (speculative form: the
+                widened window in column 0 of each request's slot row) ->
+                u = x1*v -> fir_snapshots | iir_snapshots (one snapshot per
+                verifier position) -> [+ D*u] -> x2*y -> out_proj
+
+with the live snapshot of each request resolved from the position stamps in
+slice 2 before any state is written, and every snapshot written in the step
+stamped afterwards.  The state pool then carries the speculative layout
+(`state.unified_state_shape(..., num_spec)`); prefill rows and ordinary
+decode rows use the leading K_short-1 columns of the widened window.
 """
 
 import contextlib
+import os
 from typing import Optional
 
 import torch
@@ -40,6 +54,15 @@ from .fp8_emul import static_fp8_linear_emulated
 from .hcl import hcl_block_t, hyena_hcl_prefill
 from .metadata import decode_state_indices, prefill_tables
 from .prefill import fir_prefill_block_t, hyena_fir_prefill
+from .short_conv import PAD_SLOT_ID, causal_conv1d_update
+from .speculative import (accepted_tokens, cache_safe_state_indices, decode_tensors,
+                          query_start_loc_d)
+from .state import unified_state_dtype, unified_state_shape
+from .verify import fir_snapshots, iir_snapshots
+
+# Test-only cross-check (mixers.py:77, 989-998): where the engine does send
+# acceptance counts, they must agree with the stamps.
+_CHECK_VLLM_COUNTS = os.environ.get("EVO2_CHECK_VLLM_COUNTS") == "1"
 
 # ---------------------------------------------------------------- forward context
 # Layers register under their prefix here, as vLLM's
@@ -104,7 +127,7 @@ class HyenaMixerBase(nn.Module):
     views and the operator entry (mixers.py:711-1235)."""
 
     def __init__(self, config, layer_idx, model_config=None, cache_config=None, prefix="",
-                 quant_config=None, device=None):
+                 quant_config=None, device=None, num_spec=0):
         super().__init__()
         self.config = config
         self.layer_idx = layer_idx
@@ -112,6 +135,10 @@ class HyenaMixerBase(nn.Module):
         h = config.hidden_size
         self.hidden = h
         self.k_short = config.short_filter_length
+        # draft tokens per verify step: the engine's speculative config
+        # (num_speculative_tokens, mixers.py:733-736), 0 without speculation
+        self.num_spec = int(num_spec or 0)
+        self._stamp_faults = None
         # Only in_proj is fp8 in the released checkpoints (mixers.py:736-757);
         # out_proj follows the model-wide quantisation, bf16 by default.
         self.in_proj_token_table = None
@@ -174,10 +201,6 @@ class HyenaMixerBase(nn.Module):
         v = self.kv_cache[i].transpose(-1, -2)
         return v if width is None else v[..., :width]
 
-    def _ssm_state(self):
-        """Slice 2, (blocks, H, S) fp32, not transposed (mixers.py:1334-1342)."""
-        return self.kv_cache[2]
-
     def _short_w(self):
         return self.short_filter.view(3 * self.hidden, self.k_short)
 
@@ -202,6 +225,15 @@ class HyenaMixerBase(nn.Module):
                              static_fp8_linear_emulated(hidden_states, emul_w, sc[0], sc[1]))
         return z
 
+    def get_state_shape(self):
+        """The one state spec every Hyena layer declares (mixers.py:892-913)."""
+        cfg = self.config
+        return unified_state_shape(cfg.hidden_size, cfg.short_filter_length,
+                                   cfg.hcm_filter_length, cfg.state_size, self.num_spec)
+
+    def get_state_dtype(self):
+        return unified_state_dtype(self.short_filter.dtype)
+
     @staticmethod
     def is_speculative_decode(m):
         """Whether the decode half of a step carries speculative snapshots
@@ -220,11 +252,132 @@ class HyenaMixerBase(nn.Module):
         if len(self.kv_cache) != 3:
             raise RuntimeError(f"{self.prefix}: kv_cache is not bound (the engine binds the "
                                "layer's three state slices before a step)")
-        if int(m.num_decodes) and self.is_speculative_decode(m):
-            raise NotImplementedError(
-                f"{self.prefix}: speculative decode metadata (a multi-column "
-                "state_indices_tensor_d, num_accepted_tokens, or num_decode_tokens != "
-                "num_decodes) is not supported by these mixers")
+
+    # ---- speculative rollback from position stamps (mixers.py:952-1074)
+    def _position_stamps(self):
+        """(blocks,) fp32 view of slice 2 row 0, last column: the tokens each
+        block's snapshot represents (exact below 2**24)."""
+        return self.kv_cache[2][:, 0, -1]
+
+    def _fault_counter(self, device):
+        if self._stamp_faults is None or self._stamp_faults.device != torch.device(device):
+            self._stamp_faults = torch.zeros((), dtype=torch.int64, device=device)
+        return self._stamp_faults
+
+    def stamp_faults(self):
+        """Decode requests so far whose stamps did not match their computed
+        token count (or, with EVO2_CHECK_VLLM_COUNTS=1, the engine's counts);
+        reading it synchronises.  The reference asserts on the device here
+        (mixers.py:985-998); such a request is clamped to the nearest valid
+        offset as there."""
+        return 0 if self._stamp_faults is None else int(self._stamp_faults)
+
+    def _spec_accepted(self, m):
+        """(num_decodes,) accepted count of the previous step from the stamps
+        (mixers.py:960-999): offset = computed tokens - stamp of column 0, in
+        [0, num_spec] for every request not on the null block; returns
+        offset + 1, clamped."""
+        nd = int(m.num_decodes)
+        computed = getattr(m, "num_computed_tokens_d", None)
+        if computed is None:
+            raise RuntimeError("speculative Hyena decode needs num_computed_tokens_d; it is "
+                               "supplied by metadata.HyenaMamba2MetadataBuilder")
+        slots = m.state_indices_tensor_d[:nd]
+        if slots.dim() == 1:
+            slots = slots[:, None]
+        first = cache_safe_state_indices(slots, self.kv_cache[2])[:, 0].long()
+        offset = computed[:nd].to(torch.int64) - self._position_stamps()[first].to(torch.int64)
+        bad = (first != 0) & ((offset < 0) | (offset > self.num_spec))
+        if _CHECK_VLLM_COUNTS and getattr(m, "num_accepted_tokens", None) is not None:
+            counts = accepted_tokens(m, nd, offset.device)
+            bad = bad | ((first != 0) & (counts != offset + 1))
+        self._fault_counter(offset.device).add_(bad.sum())
+        return offset.clamp(0, self.num_spec) + 1
+
+    def _repair_resumed_prefill_state(self, m):
+        """Align-mode prefix caching: a prefill row continuing from n computed
+        tokens must start from a block stamped n; where it does not and the
+        block of its last computed token is, copy that block (all three
+        slices) over it.  Rows that are fine copy onto themselves
+        (mixers.py:1001-1040)."""
+        if not self.num_spec or not int(m.num_prefills):
+            return
+        computed = getattr(m, "computed_before_p", None)
+        src = getattr(m, "state_src_block_p", None)
+        has_init = getattr(m, "has_initial_states_p", None)
+        if computed is None or src is None or has_init is None:
+            return
+        npf = int(m.num_prefills)
+        dst = m.state_indices_tensor_p[:npf].long()
+        src = src[:npf].long()
+        computed = computed[:npf].to(torch.float32)
+        stamps = self._position_stamps()
+        bad = (has_init[:npf].bool() & (stamps[dst] != computed) & (stamps[src] == computed)
+               & (src != 0) & (dst != 0))
+        take = torch.where(bad, src, dst)
+        for state in self.kv_cache:
+            state[dst] = state[take]
+
+    def _resolve_accepted(self, m):
+        """Stamp-derived accepted counts for a speculative decode step, else
+        None; runs before the layer writes any state (mixers.py:1042-1047)."""
+        if self.num_spec and int(m.num_decodes) and self.is_speculative_decode(m):
+            return self._spec_accepted(m)
+        return None
+
+    def _record_stamps(self, m):
+        """Stamp every snapshot this step wrote: decode column p of a request
+        that had computed n tokens holds n + p + 1, a prefill block its
+        sequence length (mixers.py:1049-1074)."""
+        if not self.num_spec:
+            return
+        stamps = self._position_stamps()
+        nd = int(m.num_decodes)
+        if nd and self.is_speculative_decode(m):
+            ones = torch.ones(nd, device=stamps.device, dtype=torch.long)
+            _, outs, starts, ends, _ = decode_tensors(m, int(m.num_decode_tokens),
+                                                      1 + self.num_spec, ones)
+            outs = cache_safe_state_indices(outs, self.kv_cache[2])
+            steps = torch.arange(outs.shape[1], device=outs.device)
+            active = steps[None, :] < (ends - starts)[:, None]
+            computed = m.num_computed_tokens_d[:nd].to(torch.int64)
+            values = computed[:, None] + steps[None, :] + 1
+            # inactive entries all target the null block, whose value is moot
+            dest = torch.where(active, outs.long(), 0).reshape(-1)
+            stamps.index_put_((dest,), torch.where(active, values, 0).reshape(-1)
+                              .to(stamps.dtype))
+        npf = int(m.num_prefills)
+        if npf:
+            stamps[m.state_indices_tensor_p[:npf].long()] = (
+                m.seq_lens[nd:nd + npf].to(stamps.dtype))
+
+    def _spec_short_conv(self, z_d, m, accepted):
+        """(x2, x1, v) of the decode rows of a speculative step through the
+        widened short window (mixers.py:1153-1193)."""
+        conv_state = self._conv_state(0)
+        nreq = int(m.num_decodes)
+        slots = m.state_indices_tensor_d
+        idx = cache_safe_state_indices(slots, conv_state)
+        if idx.dim() == 1:
+            idx = idx[:, None]
+        sched = getattr(m, "block_idx_last_scheduled_token", None)
+        comp = getattr(m, "block_idx_last_computed_token", None)
+        acc = accepted if accepted is not None else accepted_tokens(m, nreq, z_d.device)
+        zf = causal_conv1d_update(
+            z_d, conv_state, self._short_w(), None, activation=None,
+            conv_state_indices=idx[:nreq],
+            block_idx_last_scheduled_token=None if sched is None else sched[:nreq],
+            initial_state_idx=None if comp is None else comp[:nreq],
+            num_accepted_tokens=acc, query_start_loc=query_start_loc_d(m, nreq, z_d.device),
+            max_query_len=idx.shape[1], pad_slot_id=PAD_SLOT_ID)
+        return zf[:, 0::3], zf[:, 1::3], zf[:, 2::3]
+
+    def _spec_tensors(self, m, num_tokens, state, accepted):
+        """Verify metadata for the inner operator's snapshots (mixers.py:578-598)."""
+        ins, outs, starts, ends, acc = decode_tensors(m, num_tokens, 1 + self.num_spec,
+                                                      accepted)
+        return (cache_safe_state_indices(ins, state), cache_safe_state_indices(outs, state),
+                starts, ends, acc)
 
     @staticmethod
     def _unpad(out, hidden_states, n_actual):
@@ -253,9 +406,9 @@ class HyenaFIRMixer(HyenaMixerBase):
     only for K >= 128."""
 
     def __init__(self, config, layer_idx, model_config=None, cache_config=None, prefix="",
-                 k_inner=None, quant_config=None, device=None):
+                 k_inner=None, quant_config=None, device=None, num_spec=0):
         super().__init__(config, layer_idx, model_config, cache_config, prefix, quant_config,
-                         device)
+                         device, num_spec)
         h = config.hidden_size
         self.k_inner = k_inner or config.inner_filter_length(layer_idx)
         self.conv = nn.Parameter(torch.empty(h, 1, self.k_inner, device=device,
@@ -287,28 +440,46 @@ class HyenaFIRMixer(HyenaMixerBase):
         else:
             self._decode_taps = taps
 
+    def _spec_decode(self, z_d, m, accepted, inner_state):
+        """g = x2 * (FIR(u) [+ D*u]) for the decode rows of a speculative step,
+        one inner snapshot per verifier position (mixers.py:1264-1275, 1286-1298)."""
+        x2, x1, v = self._spec_short_conv(z_d, m, accepted)
+        u = x1 * v
+        w = self.conv.view(self.hidden, self.k_inner)
+        y = fir_snapshots(u, w, inner_state,
+                          self._spec_tensors(m, u.shape[0], inner_state, accepted))
+        if self.has_D:
+            y = y + self.D.to(y.dtype) * u
+        return x2 * y
+
     def _forward_impl(self, hidden_states, token_ids=None):
         m = self._meta()
         if m is None:
             return self._profile_run(hidden_states, token_ids)
         self._check_meta(m)
+        self._repair_resumed_prefill_state(m)
+        accepted = self._resolve_accepted(m)  # before any state is written
         if self._decode_taps is None or self._decode_taps.device != self.conv.device:
             self.process_weights_after_loading()
         nd, npt = int(m.num_decode_tokens), int(m.num_prefill_tokens)
         z = self._project(hidden_states[:nd + npt], token_ids)
         sw = self._short_w()
-        conv_state = self._conv_state(0)
+        window = self._conv_state(0, self.k_short - 1)
         inner_state = self._conv_state(1, self.k_inner - 1)
         parts = []
         if nd:
-            parts.append(hyena_decode(z[:nd], sw, conv_state, decode_state_indices(m),
-                                      self._decode_taps, inner_state, self.D))
+            if self.is_speculative_decode(m):
+                parts.append(self._spec_decode(z[:nd], m, accepted, inner_state))
+            else:
+                parts.append(hyena_decode(z[:nd], sw, window, decode_state_indices(m),
+                                          self._decode_taps, inner_state, self.D))
         if npt:
             bt = fir_prefill_block_t(self.k_inner, npt, self.hidden)
             seq_t, til_t, _ = prefill_tables(m, bt, z.device)
             parts.append(hyena_fir_prefill(
-                z[nd:nd + npt], sw, conv_state, self.conv.view(self.hidden, self.k_inner),
+                z[nd:nd + npt], sw, window, self.conv.view(self.hidden, self.k_inner),
                 inner_state, self.D, seq_t, m.state_indices_tensor_p, til_t, bt))
+        self._record_stamps(m)
         return self._finish(parts, hidden_states, nd + npt)
 
 
@@ -317,9 +488,9 @@ class HyenaIIRMixer(HyenaMixerBase):
     (mixers.py:1308-1401).  `log_poles` (H, S, 1) and `residues` (H, S) fp32."""
 
     def __init__(self, config, layer_idx, model_config=None, cache_config=None, prefix="",
-                 quant_config=None, device=None):
+                 quant_config=None, device=None, num_spec=0):
         super().__init__(config, layer_idx, model_config, cache_config, prefix, quant_config,
-                         device)
+                         device, num_spec)
         h, s = config.hidden_size, config.state_size
         self.state_size = s
         self.log_poles = nn.Parameter(torch.empty(h, s, 1, device=device, dtype=torch.float32),
@@ -332,27 +503,52 @@ class HyenaIIRMixer(HyenaMixerBase):
     def process_weights_after_loading(self):
         pass
 
+    def _ssm_state(self):
+        """Slice 2 without the speculative stamp column: (blocks, H, S) fp32,
+        not transposed (mixers.py:666-678, 1334-1342)."""
+        st = self.kv_cache[2]
+        width = self.state_size + (1 if self.num_spec else 0)
+        if st.shape[-2:] != (self.hidden, width):
+            raise RuntimeError(f"{self.prefix}: temporal state cache has trailing shape "
+                               f"{tuple(st.shape[-2:])}, expected {(self.hidden, width)}")
+        return st[..., :self.state_size] if self.num_spec else st
+
+    def _spec_decode(self, z_d, m, accepted, ssm, lp, res):
+        """g = x2 * (LI(u) + u*D) for the decode rows of a speculative step, one
+        state snapshot per verifier position (mixers.py:1366-1378, 1396)."""
+        x2, x1, v = self._spec_short_conv(z_d, m, accepted)
+        x1v = x1 * v
+        y = iir_snapshots(x1v, torch.exp(lp), res, ssm,
+                          self._spec_tensors(m, x1v.shape[0], ssm, accepted))
+        return (y + x1v * self.D.to(y.dtype)) * x2
+
     def _forward_impl(self, hidden_states, token_ids=None):
         m = self._meta()
         if m is None:
             return self._profile_run(hidden_states, token_ids)
         self._check_meta(m)
+        self._repair_resumed_prefill_state(m)
+        accepted = self._resolve_accepted(m)  # before any state is written
         nd, npt = int(m.num_decode_tokens), int(m.num_prefill_tokens)
         z = self._project(hidden_states[:nd + npt], token_ids)
         sw = self._short_w()
-        conv_state = self._conv_state(0)
+        window = self._conv_state(0, self.k_short - 1)
         ssm = self._ssm_state()
         lp = self.log_poles[..., 0]
         res = self.residues
         parts = []
         if nd:
-            parts.append(hyena_decode(z[:nd], sw, conv_state, decode_state_indices(m), res, ssm,
-                                      self.D, log_poles=lp))
+            if self.is_speculative_decode(m):
+                parts.append(self._spec_decode(z[:nd], m, accepted, ssm, lp, res))
+            else:
+                parts.append(hyena_decode(z[:nd], sw, window, decode_state_indices(m), res, ssm,
+                                          self.D, log_poles=lp))
         if npt:
             bt = hcl_block_t(npt, self.hidden)
             seq_t, til_t, ts_t = prefill_tables(m, bt, z.device)
-            parts.append(hyena_hcl_prefill(z[nd:nd + npt], sw, conv_state, res, lp, ssm, self.D,
+            parts.append(hyena_hcl_prefill(z[nd:nd + npt], sw, window, res, lp, ssm, self.D,
                                            seq_t, m.state_indices_tensor_p, til_t, ts_t, bt))
+        self._record_stamps(m)
         return self._finish(parts, hidden_states, nd + npt)
 
 
@@ -391,16 +587,17 @@ def _register_op():
 _register_op()
 
 
-def make_mixer(config, layer_idx, prefix="", quant_config=None, device=None):
-    """The mixer of a Hyena layer, as Evo2DecoderLayer builds it (model.py:163-182)."""
+def make_mixer(config, layer_idx, prefix="", quant_config=None, device=None, num_spec=0):
+    """The mixer of a Hyena layer, as Evo2DecoderLayer builds it (model.py:163-182);
+    `num_spec` is the engine's speculative token count (0 without speculation)."""
     kind = config.layer_kind(layer_idx)
     if kind == "hcl":
         return HyenaIIRMixer(config, layer_idx, prefix=prefix, quant_config=quant_config,
-                             device=device)
+                             device=device, num_spec=num_spec)
     if kind in ("hcs", "hcm"):
         return HyenaFIRMixer(config, layer_idx, prefix=prefix,
                              k_inner=config.inner_filter_length(layer_idx),
-                             quant_config=quant_config, device=device)
+                             quant_config=quant_config, device=device, num_spec=num_spec)
     raise ValueError(f"layer {layer_idx} is an attention layer")
 
 

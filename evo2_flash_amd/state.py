@@ -8,6 +8,11 @@ Every Hyena layer declares one spec (mixers.py:870-917, model.py:277-333):
 The three slices of a block share one padded page, so each slice's block
 stride is the page size in that slice's element type, not its own size.
 Views are oldest-first windows; block 0 is the null block.
+
+With speculative decoding of `num_spec` draft tokens (mixers.py:887-900) the
+conv window widens to K_short-1+num_spec columns and the LI slice gains a
+17th column whose row 0 holds the block's position stamp: the number of
+tokens the block's snapshot represents (mixers.py:952-958).
 """
 
 import torch
@@ -15,13 +20,15 @@ import torch
 NULL_BLOCK = 0
 
 
-def unified_state_shape(hidden, k_short=3, k_inner_max=128, state_size=16):
-    """Native shapes per block: ((K_short-1, 3H), (K_max-1, H), (H, S)).
+def unified_state_shape(hidden, k_short=3, k_inner_max=128, state_size=16, num_spec=0):
+    """Native shapes per block: ((K_short-1+num_spec, 3H), (K_max-1, H),
+    (H, S + [num_spec > 0])) (mixers.py:892-900).
 
     The first two are vLLM's (state_len, dim) conv layout, normalised to
     (dim, state_len) by `conv_view` (mixers.py:858-868, 940-949).
     """
-    return ((k_short - 1, 3 * hidden), (k_inner_max - 1, hidden), (hidden, state_size))
+    return ((k_short - 1 + num_spec, 3 * hidden), (k_inner_max - 1, hidden),
+            (hidden, state_size + (1 if num_spec else 0)))
 
 
 def unified_state_dtype(model_dtype=torch.bfloat16):
@@ -29,8 +36,8 @@ def unified_state_dtype(model_dtype=torch.bfloat16):
     return (model_dtype, torch.float32, torch.float32)
 
 
-def page_bytes(hidden, k_short=3, k_inner_max=128, state_size=16, align=256):
-    shapes = unified_state_shape(hidden, k_short, k_inner_max, state_size)
+def page_bytes(hidden, k_short=3, k_inner_max=128, state_size=16, align=256, num_spec=0):
+    shapes = unified_state_shape(hidden, k_short, k_inner_max, state_size, num_spec)
     dtypes = unified_state_dtype()
     total = 0
     for shp, dt in zip(shapes, dtypes):
@@ -51,12 +58,14 @@ class HyenaStatePool:
     """
 
     def __init__(self, num_blocks, hidden, device, k_short=3, k_inner_max=128,
-                 state_size=16, page_align=256, dtype=torch.bfloat16):
+                 state_size=16, page_align=256, dtype=torch.bfloat16, num_spec=0):
         self.num_blocks = num_blocks
         self.hidden = hidden
-        shapes = unified_state_shape(hidden, k_short, k_inner_max, state_size)
+        self.state_size = state_size
+        self.num_spec = num_spec
+        shapes = unified_state_shape(hidden, k_short, k_inner_max, state_size, num_spec)
         dtypes = unified_state_dtype(dtype)
-        self.page = page_bytes(hidden, k_short, k_inner_max, state_size, page_align)
+        self.page = page_bytes(hidden, k_short, k_inner_max, state_size, page_align, num_spec)
         self.raw = torch.zeros(num_blocks, self.page, dtype=torch.uint8, device=device)
         views, off = [], 0
         for shp, dt in zip(shapes, dtypes):
@@ -83,8 +92,16 @@ class HyenaStatePool:
         return v if width is None else v[..., :width]
 
     def ssm_view(self):
-        """(blocks, H, 16) fp32 (mixers.py:1334-1342)."""
-        return self.kv_cache[2]
+        """(blocks, H, 16) fp32 (mixers.py:1334-1342): the recurrence part of
+        slice 2, without the stamp column."""
+        return self.kv_cache[2][..., :self.state_size]
+
+    def stamps(self):
+        """(blocks,) fp32 view of the position stamps (mixers.py:952-958);
+        only with num_spec > 0."""
+        if not self.num_spec:
+            raise ValueError("position stamps exist only with speculative decoding (num_spec > 0)")
+        return self.kv_cache[2][:, 0, -1]
 
     def zero_(self):
         self.raw.zero_()

@@ -240,6 +240,42 @@ int evo2_causal_conv1d_update(const void *x, int64_t xb, int64_t xc,
                               int64_t B, int64_t dim, int64_t num_blocks, void *stream);
 
 /*
+ * The same update for speculative verification: request r owns packed rows
+ * [query_start_loc[r], query_start_loc[r + 1]) of x (T, dim) (at most
+ * max_query_len of them) and the slot row indices[r, :] (ncols columns).
+ * It reads the window of slot indices[r, in_col[r]] (column 0 when in_col is
+ * NULL) at columns num_accepted[r]-1 .. num_accepted[r]+K-3, runs its rows
+ * through it with the rounding above, and leaves in slot
+ * indices[r, out_col[r]] (column 0 when NULL):
+ *   columns [0, keep)        <- old columns [num_accepted[r], num_accepted[r] + keep)
+ *   columns [keep, keep + q) <- its q inputs,   keep = state_len - max_query_len,
+ * later columns untouched, so after a later step accepts a of the q rows the
+ * live window starts at column a - 1.  The conv state is (blocks, dim,
+ * state_len) with state_len >= K-1 + max_query_len-1.  A request with a
+ * padding or out-of-range slot, more than max_query_len rows or num_accepted
+ * outside [1, max_query_len] gets zero rows and touches no state; rows no
+ * request covers are not written.  K in {2, 3, 4}.
+ *
+ * Replaces vLLM's causal_conv1d_update called with num_accepted_tokens,
+ * query_start_loc and max_query_len (and, for prefix caching,
+ * block_idx_last_scheduled_token / initial_state_idx as out_col / in_col),
+ * as the reference's mixers call it for speculative decode
+ * (evo2_flash/mixers.py:1153-1193; window convention mixers.py:222-240).
+ */
+int evo2_causal_conv1d_update_spec(const void *x, int64_t xt, int64_t xc,
+                                   void *conv_state, int64_t cs0, int64_t cs1, int64_t cs2,
+                                   int32_t state_len,
+                                   const void *w, int64_t w0, int64_t w1, int32_t K,
+                                   const void *bias, int32_t activation,
+                                   const int32_t *indices, int64_t si0, int64_t si1, int32_t ncols,
+                                   const int32_t *in_col, const int32_t *out_col,
+                                   const int64_t *num_accepted, const int32_t *query_start_loc,
+                                   int32_t max_query_len, int32_t pad_slot_id,
+                                   void *out, int64_t ot, int64_t oc,
+                                   int64_t nreq, int64_t T, int64_t dim, int64_t num_blocks,
+                                   void *stream);
+
+/*
  * Short causal depthwise convolution over packed prefill segments: segment j
  * is rows [query_start_loc[j], query_start_loc[j + 1]) of x, with slot
  * cache_indices[j] (or j when NULL).  Its left context is the slot's window
@@ -414,8 +450,11 @@ int evo2_fir_verify(const void *x, int64_t xs0, int64_t xs1, int32_t x_f32,
  * Replaces triton_verifier._iir_kernel, iir_snapshots and iir_one
  * (evo2_flash/triton_verifier.py:83-122, 146-155, 170-178).
  *
- *   poles, residues  (H, 16) fp32, strides p0/p1, r0/r1 (unit state stride)
- *   state            (blocks, H, 16) fp32 view, strides ss0, ss1, ss2 = 1
+ *   poles, residues  (H, 16) fp32, strides p0/p1, r0/r1 (unit state stride,
+ *                    16-byte aligned rows)
+ *   state            (blocks, H, 16) fp32 view, any strides (16-byte aligned
+ *                    contiguous rows take the vector path; the speculative
+ *                    layout's 17-column rows, mixers.py:892-900, the other)
  *   other arguments as evo2_fir_verify.
  */
 int evo2_iir_verify(const void *x, int64_t xs0, int64_t xs1, int32_t x_f32,

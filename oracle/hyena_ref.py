@@ -20,6 +20,7 @@ __all__ = [
     "fir_decode_snapshots", "iir_decode_snapshots", "fir_verify_emulated",
     "iir_verify_emulated", "STATE_ACC_BUDGET", "fast_accum_mm", "fp8_linear_fast_accum",
     "causal_conv1d_update_ref", "causal_conv1d_ref", "iir_final_state_recurrence",
+    "causal_conv1d_update_spec_ref", "mixer_decode_speculative",
 ]
 
 # mixers.py:72-74: bound on the (H, blk, L) temporary of the LI final state.
@@ -237,6 +238,66 @@ def causal_conv1d_update_ref(x, conv_state, w, bias=None, activation=None, slots
     return out
 
 
+def causal_conv1d_update_spec_ref(x, conv_state, w, slots, accepted, qsl, max_query_len,
+                                  in_col=None, out_col=None, pad_slot_id=-1):
+    """vLLM's causal_conv1d_update in its speculative varlen form, as the
+    mixers call it for a verify step (mixers.py:1176-1193), with the window
+    convention mixers.py:222-240 states: before the step the window holds
+    [h_1 .. h_M]; the step leaves [h_2 .. h_M, d_1 .. d_q]; after a later
+    step accepts a of the q rows its live window starts at column a - 1.
+
+    Request r owns rows qsl[r]..qsl[r+1]-1 of x (T, dim); its input block is
+    slots[r, in_col[r]] and its output block slots[r, out_col[r]] (column 0
+    when None).  The live (K-1)-window starts at column accepted[r] - 1; the
+    output block's columns become [old cols accepted[r] .. accepted[r]+keep-1,
+    the q inputs], keep = state_len - max_query_len, later columns unchanged.
+    Rounding as `causal_conv1d_update_ref`.  Padding or out-of-range slots,
+    q > max_query_len or accepted outside [1, max_query_len]: zero rows, no
+    state.  conv_state (blocks, dim, state_len) updated in place.  Returns
+    (T, dim) fp32 holding bf16 values, zero on rows no request covers.
+
+    Parity unpinned against vLLM itself (its kernel is not in the reference);
+    pinned by the special case q = accepted = 1, max_query_len = 1, which is
+    `causal_conv1d_update_ref`, and by the rollback invariant the convention
+    exists for (tests/test_oracle.py).
+    """
+    T, dim = x.shape
+    K = w.shape[1]
+    wf = w.float()
+    state_len = conv_state.shape[2]
+    keep = state_len - max_query_len
+    out = torch.zeros(T, dim, dtype=torch.float32)
+    for r in range(len(qsl) - 1):
+        a, e = int(qsl[r]), int(qsl[r + 1])
+        if e <= a:
+            continue
+        q = e - a
+        ic = 0 if in_col is None else int(in_col[r])
+        oc = 0 if out_col is None else int(out_col[r])
+        src, dst, acc_n = int(slots[r, ic]), int(slots[r, oc]), int(accepted[r])
+        nb = conv_state.shape[0]
+        if (q > max_query_len or not 1 <= acc_n <= max_query_len
+                or src == pad_slot_id or dst == pad_slot_id
+                or not (0 <= src < nb and 0 <= dst < nb)):
+            continue
+        off = acc_n - 1
+        old = conv_state[src].float().clone()             # (dim, state_len)
+        s = old[:, off:off + K - 1].clone()
+        for t in range(a, e):
+            xt = x[t].float()
+            acc = torch.zeros(dim)
+            for k in range(K - 1):
+                acc = acc + bf(s[:, k] * wf[:, k])
+            acc = acc + bf(xt * wf[:, K - 1])
+            out[t] = bf(acc)
+            s = torch.cat([s[:, 1:], xt[:, None]], dim=1)
+        new = conv_state[dst].float().clone()
+        new[:, :keep] = old[:, off + 1:off + 1 + keep]
+        new[:, keep:keep + q] = x[a:e].float().t()
+        conv_state[dst] = new.to(conv_state.dtype)
+    return out
+
+
 def causal_conv1d_ref(x_p, w, bias, activation, qsl, slots, has_init, state, pad_slot_id=-1):
     """vLLM's causal_conv1d_fn over packed prefill segments as the mixers call
     it (mixers.py:1138-1150), with the update kernel's rounding (see
@@ -379,6 +440,49 @@ def mixer_decode_unfused(z, short_w, conv_state, slots, inner, inner_state, D=No
     if D is not None:
         y = y + D.to(y.dtype) * u
     return x2 * y
+
+
+def mixer_decode_speculative(z, short_w, conv_state, inner, inner_state, D, slots, qsl,
+                             accepted, max_query_len, poles=None, ins=None, outs=None,
+                             in_col=None, out_col=None, emulate_kernels=True):
+    """Decode rows of a speculative step between in_proj and out_proj
+    (mixers.py:1277-1305 for the FIR, 1327-1401 for the LI, speculative
+    branches): the widened short window (`causal_conv1d_update_spec_ref`),
+    u = x1*v, the inner operator with one snapshot per verifier position
+    (`fir_verify_emulated` / `iir_verify_emulated`, or with
+    emulate_kernels=False the reference's torch paths
+    `fir_decode_snapshots` / `iir_decode_snapshots`), then [+ D*u] and * x2
+    in bf16.  `poles` (H, 16) selects the LI operator with `inner` the
+    residues; else `inner` is the FIR taps (H, K).  Snapshot slots default to
+    the slot matrix (ins = outs = slots).  States are updated in place.
+    Returns g (T, H) bf16, zero on rows no request covers.
+    """
+    T = z.shape[0]
+    zf = causal_conv1d_update_spec_ref(z, conv_state, short_w, slots, accepted, qsl,
+                                       max_query_len, in_col, out_col).to(torch.bfloat16)
+    x2, x1, v = _split(zf)
+    u = x1 * v
+    n = len(qsl) - 1
+    starts = torch.as_tensor([int(qsl[r]) for r in range(n)], dtype=torch.long)
+    ends = torch.as_tensor([int(qsl[r + 1]) for r in range(n)], dtype=torch.long)
+    ins = slots if ins is None else ins
+    outs = slots if outs is None else outs
+    acc = torch.as_tensor([int(a) for a in accepted], dtype=torch.long)
+    if poles is not None:
+        fn = iir_verify_emulated if emulate_kernels else iir_decode_snapshots
+        y = fn(u, poles.float(), inner.float(), inner_state, ins, outs, starts, ends, acc)
+        return (y + u * D.to(y.dtype)) * x2
+    K = inner.shape[1]
+    fn = fir_verify_emulated if emulate_kernels else fir_decode_snapshots
+    y = fn(u, inner, inner_state[..., : K - 1], ins, outs, starts, ends, acc)
+    if D is not None:
+        y = y + D.to(y.dtype) * u
+    g = x2 * y
+    covered = torch.zeros(T, dtype=torch.bool)
+    for r in range(n):
+        covered[int(qsl[r]):int(qsl[r + 1])] = True
+    g[~covered] = 0
+    return g
 
 
 # ------------------------------------------------------------ speculative verify

@@ -80,16 +80,6 @@ def test_forward_context_and_cpu_refusal():
     assert get_forward_context().attn_metadata is None
 
 
-def test_speculative_metadata_rejected():
-    cfg = HyenaConfig(hidden_size=128, num_hidden_layers=1, hcs_layer_idxs=[0])
-    mixer = make_mixer(cfg, 0, prefix="host.spec.0")
-    m = build_metadata(decode_slots=[1], device="cpu")
-    m.num_accepted_tokens = torch.ones(1, dtype=torch.int32)
-    mixer.kv_cache = HyenaStatePool(2, 128, "cpu").kv_cache
-    with pytest.raises(NotImplementedError):
-        mixer._check_meta(m)
-
-
 def _spec_mixer(prefix):
     cfg = HyenaConfig(hidden_size=128, num_hidden_layers=1, hcs_layer_idxs=[0])
     mixer = make_mixer(cfg, 0, prefix=prefix)
@@ -99,8 +89,8 @@ def _spec_mixer(prefix):
 
 def test_speculative_predicate_is_the_reference_one():
     """Each of the reference's three conditions alone marks a step
-    speculative (mixers.py:930-937); the mixers refuse such a step before any
-    state is touched."""
+    speculative (mixers.py:930-937), which sends its decode rows through the
+    snapshot path."""
     mixer = _spec_mixer("host.spec.pred")
     plain = build_metadata(decode_slots=[1, 2], device="cpu")
     assert not mixer.is_speculative_decode(plain)
@@ -110,14 +100,14 @@ def test_speculative_predicate_is_the_reference_one():
     two_col.state_indices_tensor_d = torch.tensor([[1, 3], [2, 0]], dtype=torch.int32)
     assert two_col.num_decode_tokens == two_col.num_decodes
     assert mixer.is_speculative_decode(two_col)
-    with pytest.raises(NotImplementedError, match="speculative"):
-        mixer._check_meta(two_col)
     # more decode tokens than requests with a 1-D slot table
     packed = build_metadata(decode_slots=[1, 2], device="cpu")
     packed.num_decode_tokens = 4
     assert mixer.is_speculative_decode(packed)
-    with pytest.raises(NotImplementedError, match="speculative"):
-        mixer._check_meta(packed)
+    # acceptance counts alone
+    counted = build_metadata(decode_slots=[1], device="cpu")
+    counted.num_accepted_tokens = torch.ones(1, dtype=torch.int32)
+    assert mixer.is_speculative_decode(counted)
     # a (nd, 1) column is not speculative
     one_col = build_metadata(decode_slots=[1, 2], device="cpu")
     one_col.state_indices_tensor_d = torch.tensor([[1], [2]], dtype=torch.int32)

@@ -1,8 +1,9 @@
 """Host-side behaviour of the short-convolution and final-state entry points
 (no GPU): CPU tensors are refused (there is no CPU path) except where the
 reference's own contract returns None for them (`iir_final_state`,
-triton_prefill.py:360-361), and the speculative / prefix-caching forms that
-this build does not implement raise NotImplementedError before any work.
+triton_prefill.py:360-361), and the forms this build does not implement
+(packed rows without acceptance counts, the prefill's prefix-caching
+arguments) raise NotImplementedError before any work.
 """
 
 import pytest
@@ -34,8 +35,14 @@ def test_unsupported_forms_raise():
     x = torch.zeros(2, 6, dtype=bf)
     st = torch.zeros(3, 6, 2, dtype=bf)
     w = torch.zeros(6, 3, dtype=bf)
-    with pytest.raises(NotImplementedError, match="speculative"):
+    with pytest.raises(NotImplementedError, match="non-speculative varlen"):
+        causal_conv1d_update(x, st, w, None, query_start_loc=torch.tensor([0, 2]))
+    with pytest.raises(NotImplementedError, match="query_start_loc"):
         causal_conv1d_update(x, st, w, None, num_accepted_tokens=torch.ones(2, dtype=torch.int32))
+    with pytest.raises(RuntimeError, match="GPU only"):
+        causal_conv1d_update(x, st, w, None, conv_state_indices=torch.tensor([[1], [2]]),
+                             num_accepted_tokens=torch.ones(2, dtype=torch.int32),
+                             query_start_loc=torch.tensor([0, 1, 2], dtype=torch.int32))
     with pytest.raises(NotImplementedError, match="prefix-caching"):
         causal_conv1d_fn(x.t(), w, None, conv_states=st,
                          query_start_loc=torch.tensor([0, 2], dtype=torch.int32),

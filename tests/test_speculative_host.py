@@ -1,0 +1,252 @@
+"""Speculative decode plumbing without a GPU.
+
+The oracle's widened short window (`causal_conv1d_update_spec_ref`) is pinned
+by the special case that reduces it to the ordinary update, by the window
+layout the reference states (mixers.py:222-240), and by the rollback
+invariant the layout exists for: after any accepted prefix of a verify step,
+the next step computes what one-token-at-a-time decoding of the accepted
+tokens would.  The position-stamp rollback of the mixers (mixers.py:952-1074)
+is torch index arithmetic and runs here on CPU tensors: stamps written per
+snapshot, accepted counts resolved from them, mismatches counted, and the
+align-mode repair of a resumed prefill.
+"""
+
+import pytest
+import torch
+
+import oracle
+from evo2_flash_amd.config import HyenaConfig
+from evo2_flash_amd.metadata import (HyenaMamba2Metadata, HyenaMamba2MetadataBuilder,
+                                     Mamba2Metadata, build_metadata)
+from evo2_flash_amd.mixers import make_mixer
+from evo2_flash_amd.speculative import cache_safe_state_indices, decode_tensors
+from evo2_flash_amd.state import HyenaStatePool, page_bytes, unified_state_shape
+
+
+def _rand_window(nb, dim, width, seed):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(nb, dim, width, generator=g) * 1.2).to(torch.bfloat16)
+
+
+def test_spec_update_reduces_to_plain_update():
+    """One verifier position, accepted 1, one row per request: the ordinary
+    update, outputs and windows."""
+    dim, K, nb = 24, 3, 6
+    g = torch.Generator().manual_seed(1)
+    w = torch.randn(dim, K, generator=g).to(torch.bfloat16)
+    x = torch.randn(4, dim, generator=g).to(torch.bfloat16)
+    st = _rand_window(nb, dim, K - 1, 2)
+    st2 = st.clone()
+    slots = torch.tensor([[3], [1], [5], [2]])
+    ref = oracle.causal_conv1d_update_ref(x, st, w, slots=[3, 1, 5, 2])
+    out = oracle.causal_conv1d_update_spec_ref(x, st2, w, slots, [1, 1, 1, 1],
+                                               [0, 1, 2, 3, 4], 1)
+    assert torch.equal(out, ref)
+    assert torch.equal(st2, st)
+
+
+def test_spec_update_window_layout():
+    """Before [h1..hM], after a full verify step [h2..hM, d1..dq]
+    (mixers.py:228-233, M = K-1, state K-1+q-1 columns)."""
+    dim, K, q = 5, 3, 4
+    st = _rand_window(2, dim, K - 1 + q - 1, 3)
+    h = st[1].clone()
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(q, dim, generator=g).to(torch.bfloat16)
+    w = torch.randn(dim, K, generator=g).to(torch.bfloat16)
+    oracle.causal_conv1d_update_spec_ref(x, st, w, torch.tensor([[1]]), [1], [0, q], q)
+    assert torch.equal(st[1, :, :K - 2], h[:, 1:K - 1])
+    assert torch.equal(st[1, :, K - 2:K - 2 + q], x.t())
+
+
+@pytest.mark.parametrize("K", [2, 3, 4])
+def test_spec_update_rollback_invariant(K):
+    """Verify steps with ragged draft counts and random acceptance reproduce
+    the one-token-at-a-time history of the accepted tokens."""
+    dim, nspec = 16, 3
+    Q = nspec + 1
+    g = torch.Generator().manual_seed(10 + K)
+    w = torch.randn(dim, K, generator=g).to(torch.bfloat16)
+    width = K - 1 + nspec
+    st = torch.zeros(2, dim, width, dtype=torch.bfloat16)
+    start = (torch.randn(K - 1, dim, generator=g)).to(torch.bfloat16)
+    st[1, :, :K - 1] = start.t()               # a prefill leaves the window in front
+    hist = list(start)
+    accepted = 1
+    for step in range(12):
+        q = int(torch.randint(1, Q + 1, (1,), generator=g))
+        x = torch.randn(q, dim, generator=g).to(torch.bfloat16)
+        out = oracle.causal_conv1d_update_spec_ref(x, st, w, torch.tensor([[1]]), [accepted],
+                                                   [0, q], Q)
+        # brute force: token t sees the last K-1 genuine inputs before it
+        seen = list(hist)
+        for t in range(q):
+            window = torch.stack(seen[-(K - 1):] + [x[t]], dim=1).float()  # (dim, K)
+            acc = torch.zeros(dim)
+            for k in range(K):
+                acc = acc + oracle.bf(window[:, k] * w[:, k].float())
+            assert torch.equal(out[t], oracle.bf(acc)), (step, t)
+            seen.append(x[t])
+        accepted = int(torch.randint(1, q + 1, (1,), generator=g))
+        hist = hist + list(x[:accepted])
+
+
+def test_state_shape_with_spec():
+    H = 64
+    assert unified_state_shape(H, num_spec=3) == ((5, 3 * H), (127, H), (H, 17))
+    assert unified_state_shape(H) == ((2, 3 * H), (127, H), (H, 16))
+    assert page_bytes(H, align=1, num_spec=3) == 5 * 3 * H * 2 + 127 * H * 4 + H * 17 * 4
+    pool = HyenaStatePool(3, H, "cpu", num_spec=3)
+    assert pool.conv_view().shape == (3, 3 * H, 5)
+    assert pool.ssm_view().shape == (3, H, 16)
+    pool.stamps()[2] = 77.0
+    assert pool.kv_cache[2][2, 0, 16] == 77.0 and pool.ssm_view()[2].abs().sum() == 0
+    with pytest.raises(ValueError, match="stamps"):
+        HyenaStatePool(2, H, "cpu").stamps()
+
+
+_PFX = iter(range(10 ** 6))
+
+
+def _mixer(kind, num_spec=3, H=32, blocks=12):
+    idx = {"hcs": 0, "hcm": 1, "hcl": 2}[kind]
+    cfg = HyenaConfig(hidden_size=H, num_hidden_layers=3, hcs_layer_idxs=[0],
+                      hcm_layer_idxs=[1], hcl_layer_idxs=[2])
+    m = make_mixer(cfg, idx, prefix=f"host.specmix.{kind}.{next(_PFX)}", num_spec=num_spec)
+    pool = HyenaStatePool(blocks, H, "cpu", num_spec=num_spec)
+    m.kv_cache = pool.kv_cache
+    assert m.get_state_shape() == unified_state_shape(H, num_spec=num_spec)
+    return m, pool
+
+
+def _spec_meta(slots, qlens, computed, prefill=None, seq_lens=None):
+    """Decode requests with slot rows `slots` and query lengths `qlens`."""
+    nd = len(qlens)
+    qsl = [0]
+    for n in qlens:
+        qsl.append(qsl[-1] + n)
+    m = HyenaMamba2Metadata(num_decodes=nd, num_decode_tokens=qsl[-1])
+    m.state_indices_tensor_d = torch.tensor(slots, dtype=torch.int32)
+    m.query_start_loc_d = torch.tensor(qsl, dtype=torch.int32)
+    m.num_computed_tokens_d = torch.tensor(computed, dtype=torch.int32)
+    if prefill:
+        lens, pslots = prefill
+        p = build_metadata(prefill_lens=lens, prefill_slots=pslots, has_init=[0] * len(lens),
+                           device="cpu")
+        m.num_prefills, m.num_prefill_tokens = p.num_prefills, p.num_prefill_tokens
+        m.query_start_loc_p, m.has_initial_states_p = p.query_start_loc_p, p.has_initial_states_p
+        m.state_indices_tensor_p = p.state_indices_tensor_p
+    if seq_lens is not None:
+        m.seq_lens = torch.tensor(seq_lens, dtype=torch.int32)
+    return m
+
+
+@pytest.mark.parametrize("kind", ["hcs", "hcl"])
+def test_stamps_record_and_resolve(kind):
+    """A verify step from n tokens stamps column p with n + p + 1 (only the
+    columns its rows reach) and prefill blocks with their lengths; the next
+    step, having computed n + a tokens, resolves accepted = a."""
+    mixer, pool = _mixer(kind)
+    st = pool.stamps()
+    slots = [[1, 2, 3, 4], [5, 6, 7, 8]]
+    m = _spec_meta(slots, [4, 2], [10, 30], prefill=([7], [9]), seq_lens=[14, 32, 7])
+    st[1], st[5] = 10, 30                       # live snapshots of the previous step
+    acc = mixer._resolve_accepted(m)
+    assert acc.tolist() == [1, 1] and mixer.stamp_faults() == 0
+    mixer._record_stamps(m)
+    assert st[1:5].tolist() == [11, 12, 13, 14]
+    assert st[5:7].tolist() == [31, 32] and st[7:9].tolist() == [0, 0]
+    assert st[9] == 7
+    # next step: request 0 accepted 3 of its 4 rows, request 1 both of its 2
+    m2 = _spec_meta(slots, [1, 3], [13, 32])
+    assert mixer._resolve_accepted(m2).tolist() == [3, 2]
+    assert mixer.stamp_faults() == 0
+
+
+def test_stamp_mismatch_is_counted_and_clamped():
+    mixer, pool = _mixer("hcm")
+    st = pool.stamps()
+    st[1], st[5] = 10, 30
+    m = _spec_meta([[1, 2, 3, 4], [5, 6, 7, 8]], [1, 1], [9, 40])   # -1 and +10: both bad
+    assert mixer._resolve_accepted(m).tolist() == [1, 4]
+    assert mixer.stamp_faults() == 2
+    # requests on the null block are exempt
+    m0 = _spec_meta([[0, 0, 0, 0]], [1], [123])
+    mixer._resolve_accepted(m0)
+    assert mixer.stamp_faults() == 2
+
+
+def test_resolve_needs_computed_counts():
+    mixer, _ = _mixer("hcs")
+    m = _spec_meta([[1, 2, 3, 4]], [2], [5])
+    m.num_computed_tokens_d = None
+    with pytest.raises(RuntimeError, match="num_computed_tokens_d"):
+        mixer._resolve_accepted(m)
+    # without speculation configured nothing is resolved
+    plain, _ = _mixer("hcs", num_spec=0)
+    assert plain._resolve_accepted(m) is None
+
+
+def test_repair_resumed_prefill_state():
+    """A prefill row resuming from n computed tokens whose block is not
+    stamped n takes its state (all three slices) from the block of its last
+    computed token when that one is stamped n (mixers.py:1001-1040)."""
+    mixer, pool = _mixer("hcl")
+    g = torch.Generator().manual_seed(5)
+    pool.raw.copy_(torch.randint(0, 255, pool.raw.shape, generator=g, dtype=torch.uint8))
+    st = pool.stamps()
+    st[2], st[3] = 5.0, 40.0     # row 0: dst 2 stale, src 3 good  -> repaired
+    st[4], st[6] = 40.0, 40.0    # row 1: dst 4 already right      -> untouched
+    st[7], st[8] = 1.0, 2.0      # row 2: neither matches          -> untouched
+    before = pool.raw.clone()
+    m = build_metadata(prefill_lens=[3, 3, 3], prefill_slots=[2, 4, 7], has_init=[1, 1, 1],
+                       device="cpu")
+    m.computed_before_p = torch.tensor([40, 40, 40])
+    m.state_src_block_p = torch.tensor([3, 6, 8])
+    mixer._repair_resumed_prefill_state(m)
+    for i in range(3):   # bitwise (random bytes hold NaNs)
+        assert torch.equal(pool.kv_cache[i][2].contiguous().view(torch.uint8),
+                           pool.kv_cache[i][3].contiguous().view(torch.uint8))
+    changed = (pool.raw != before).any(dim=1).nonzero().view(-1).tolist()
+    assert changed == [2]
+
+
+def test_metadata_builder():
+    b = HyenaMamba2MetadataBuilder(max_num_seqs=8, block_size=16, device="cpu",
+                                   mamba_cache_mode="align")
+    base = Mamba2Metadata(num_decodes=2, num_decode_tokens=5, num_prefills=2,
+                          num_prefill_tokens=9)
+    table = torch.tensor([[1, 2, 3], [4, 5, 6], [7, 8, 9], [10, 11, 12]], dtype=torch.int32)
+    m = b.build(base, torch.tensor([33, 7, 0, 17]), table)
+    assert isinstance(m, HyenaMamba2Metadata) and m.num_prefill_tokens == 9
+    assert m.num_computed_tokens_d.tolist() == [33, 7]
+    assert m.num_computed_tokens_d.data_ptr() == b.decode_num_computed_tokens.data_ptr()
+    assert m.computed_before_p.tolist() == [0, 17]
+    # cp = 0 -> null block; cp = 17 -> the block holding token 16 (column 1)
+    assert m.state_src_block_p.tolist() == [0, 11]
+    m2 = b.build(base, torch.tensor([40, 8, 0, 1]), table)
+    assert m2.num_computed_tokens_d.data_ptr() == m.num_computed_tokens_d.data_ptr()
+    assert m.num_computed_tokens_d.tolist() == [40, 8]   # refreshed in place
+    assert m2.state_src_block_p.tolist() == [0, 10]
+    plain = HyenaMamba2MetadataBuilder(8, 16, "cpu").build(base, torch.tensor([1, 2, 3, 4]))
+    assert plain.computed_before_p is None and plain.state_src_block_p is None
+
+
+def test_decode_tensors_and_cache_all_slots():
+    m = _spec_meta([[1, 2, 3, 4, 5, 6], [7, 8, 9, 10, 11, 12]], [2, 3], [0, 0])
+    ins, outs, starts, ends, acc = decode_tensors(m, 5, 4)
+    assert torch.equal(ins, outs) and ins.shape == (2, 6)
+    assert starts.tolist() == [0, 2] and ends.tolist() == [2, 5] and acc.tolist() == [1, 1]
+    m.num_accepted_tokens = torch.tensor([3, 0])
+    assert decode_tensors(m, 5, 4)[4].tolist() == [3, 1]      # clamped to >= 1
+    m.block_idx_last_scheduled_token_prev_step = torch.tensor([0, 2])
+    m.block_idx_last_scheduled_token = torch.tensor([1, 1])
+    ins, outs, *_ = decode_tensors(m, 5, 4)
+    assert ins.tolist() == [[1, 2, 3, 4], [9, 10, 11, 12]]
+    assert outs.tolist() == [[2, 3, 4, 5], [8, 9, 10, 11]]
+    with pytest.raises(ValueError, match="query_start_loc_d"):
+        m.query_start_loc_d = None
+        decode_tensors(m, 5, 4)
+    # profiling-sized pools map a wide slot matrix to the null block
+    assert cache_safe_state_indices(torch.ones(2, 4, dtype=torch.int32),
+                                    torch.zeros(5, 3)).sum() == 0
