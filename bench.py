@@ -604,6 +604,20 @@ def bench_gemm(reps, dev, M=8192, K=4096, seed=5):
         tf = flop / (avg * 1e-6) / 1e12
         out[name] = {"M": M, "N": N, "K": K, "avg_us": round(avg, 2), "median_us": round(med, 2),
                      "TFLOPs": round(tf, 1), "frac": round(tf / FP8_PEAK_TFLOPS, 4)}
+        # the platform library's fp8 GEMM on the same operands, for reference
+        # (torch._scaled_mm -> hipBLASLt); not on any product path
+        try:
+            one = torch.ones((), device=dev)
+            ref = lambda: torch._scaled_mm(x8, w8.t(), scale_a=one, scale_b=one,  # noqa: E731
+                                           out_dtype=torch.bfloat16)
+            ref()
+            torch.cuda.synchronize()
+            ravg, _ = _timed(ref, reps, stream)
+            out[name]["library_us"] = round(ravg, 2)
+            out[name]["library_TFLOPs"] = round(flop / (ravg * 1e-6) / 1e12, 1)
+        except RuntimeError as e:  # the platform has no fp8 library GEMM for these inputs
+            out[name]["library_us"] = None
+            out[name]["library_error"] = str(e).splitlines()[0][:120]
     qavg, _ = _timed(lambda: quantize_input(x, xs), reps, stream)
     out["quantize"] = {"avg_us": round(qavg, 2), "bytes": M * K * 3,
                        "achieved_GBs": round(M * K * 3 / (qavg * 1e-6) / 1e9, 1)}

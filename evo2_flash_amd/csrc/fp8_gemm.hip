@@ -222,6 +222,231 @@ __global__ __launch_bounds__(256) void fp8_gemm_kernel(GemmArgs p) {
 }
 
 // ---------------------------------------------------------------------------
+// Persistent form of the same tile.  One workgroup per CU walks the output
+// tiles t = blockIdx.x, blockIdx.x + gridDim.x, ..., and its global -> LDS
+// ring runs straight across tile boundaries: the slices of the next tile are
+// already loading while the current one finishes its last steps and writes
+// its epilogue, so a tile's start-up latency is paid once per workgroup
+// rather than once per tile.  Four ring stages (32 KB of W and 32 KB of X
+// each), refilled three K steps ahead; the unrolled step pattern (stage,
+// fragment buffer) repeats every four steps, which divides the K steps of a
+// tile (K a multiple of 256).  Tile order: workgroup b runs on XCD b mod 8,
+// so with a grid of 256 the 32 tiles an XCD runs at once are made one block
+// of 4 W tiles x 8 X tiles, whose operands that XCD's L2 then serves 8 and 4
+// times over.
+constexpr int P_STAGES = 4;
+
+__device__ __forceinline__ void persist_tile(int t, int tiles_n, bool grouped, int &bn, int &bm) {
+  if (grouped) {
+    const int q = t & 7, i = (t >> 3) & 31, r = t >> 8;  // XCD, slot, round
+    const int blk = r * 8 + q;
+    const int nbn = tiles_n >> 2;
+    bn = (blk % nbn) * 4 + (i & 3);
+    bm = (blk / nbn) * 8 + (i >> 2);
+  } else {
+    bn = t % tiles_n;
+    bm = t / tiles_n;
+  }
+}
+
+__global__ __launch_bounds__(256) void fp8_gemm_persist_kernel(GemmArgs p, int tiles_n, int tiles_m,
+                                                               int grouped) {
+  __shared__ __align__(16) uint8_t w0[G_STAGE], w1[G_STAGE], w2[G_STAGE], w3[G_STAGE];
+  __shared__ __align__(16) uint8_t x0[G_STAGE], x1[G_STAGE], x2[G_STAGE], x3[G_STAGE];
+  constexpr int DB = 4;       // 1 KB DMA blocks per operand, wave and stage
+  constexpr int DMA = 2 * DB; // refill loads per wave and step
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wn = (wave & 1) * 128;   // wave's W rows
+  const int wm = (wave >> 1) * 128;  // wave's X rows
+  const int total = tiles_n * tiles_m;
+  const int KT = p.K / G_BK;
+  const int ntile = (total - static_cast<int>(blockIdx.x) + static_cast<int>(gridDim.x) - 1) /
+                    static_cast<int>(gridDim.x);
+  const int nsteps = ntile * KT;
+
+  // Operands through buffer descriptors over the whole matrices (their byte
+  // extents fit 32 bits, checked on the host): a 32-bit lane offset for the
+  // lane's row and chunk within the DMA tile, the K offset in an SGPR.
+  const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t *>(p.w), 0, static_cast<int>((int64_t)(p.N - 1) * p.sw + p.K), 0x00020000);
+  const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t *>(p.x), 0, static_cast<int>((int64_t)(p.M - 1) * p.sx + p.K), 0x00020000);
+  // DMA: one wave instruction fills 1 KB = 16 rows of 64 bytes; lane i writes
+  // row i/4, physical chunk i%4, which holds logical chunk (i%4) ^ ((row >> 2) & 3).
+  int vw[DB], vx[DB];  // lane offsets of the tile the refills are loading
+  auto dma_tile = [&](int j) __attribute__((always_inline)) {
+    int bn, bm;
+    persist_tile(static_cast<int>(blockIdx.x) + j * static_cast<int>(gridDim.x), tiles_n, grouped != 0, bn, bm);
+#pragma unroll
+    for (int i = 0; i < DB; ++i) {
+      const int row = (wave * DB + i) * 16 + lane / 4;
+      const int chunk = ((lane & 3) ^ ((row >> 2) & 3)) << 4;
+      vw[i] = (bn * G_BN + row) * static_cast<int>(p.sw) + chunk;
+      vx[i] = (bm * G_BM + row) * static_cast<int>(p.sx) + chunk;
+    }
+  };
+  auto stage_w = [&](auto stage) __attribute__((always_inline)) -> uint8_t * {
+    constexpr int S = decltype(stage)::value;
+    return S == 0 ? w0 : S == 1 ? w1 : S == 2 ? w2 : w3;
+  };
+  auto stage_x = [&](auto stage) __attribute__((always_inline)) -> uint8_t * {
+    constexpr int S = decltype(stage)::value;
+    return S == 0 ? x0 : S == 1 ? x1 : S == 2 ? x2 : x3;
+  };
+  // Slice q of this workgroup's step sequence (tile q / KT, K step q % KT)
+  // into a stage; slices past the end re-read the last one, so every step
+  // issues the same loads and the wait counts stay exact.
+  int dma_t = 0;  // tile whose offsets vw / vx hold
+  auto issue = [&](auto stage, int q) __attribute__((always_inline)) {
+    q = min(q, nsteps - 1);
+    const int tq = q / KT;  // uniform
+    if (tq != dma_t) {
+      dma_t = tq;
+      dma_tile(tq);
+    }
+    const int koff = (q - tq * KT) * G_BK;
+    uint8_t *lw = stage_w(stage);
+    uint8_t *lx = stage_x(stage);
+#pragma unroll
+    for (int j = 0; j < DB; ++j) {
+      const int blk = wave * DB + j;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(wrs, (lds_void *)(lw + blk * 1024), 16, vw[j], koff, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, (lds_void *)(lx + blk * 1024), 16, vx[j], koff, 0, 0);
+    }
+  };
+
+  const int g = lane >> 5;   // lane group: k bytes [32g, 32g + 32) of the step
+  const int lr = lane & 31;  // row within a 32-row MFMA tile
+  auto frag_off = [&](int r, int half) __attribute__((always_inline)) {
+    return r * G_BK + (((2 * g + half) ^ ((r >> 2) & 3)) << 4);
+  };
+  auto read_frags = [&](auto stage, i32x8 fa[4], i32x8 fb[4]) __attribute__((always_inline)) {
+    const uint8_t *lw = stage_w(stage);
+    const uint8_t *lx = stage_x(stage);
+    // in the order the next step consumes them (tn-major MFMAs: every X
+    // fragment and W fragment 0 first)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int rx = wm + 32 * t + lr;
+      const uint4 b0 = *reinterpret_cast<const uint4 *>(lx + frag_off(rx, 0));
+      const uint4 b1 = *reinterpret_cast<const uint4 *>(lx + frag_off(rx, 1));
+      fb[t] = i32x8{(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w, (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int rw = wn + 32 * t + lr;
+      const uint4 a0 = *reinterpret_cast<const uint4 *>(lw + frag_off(rw, 0));
+      const uint4 a1 = *reinterpret_cast<const uint4 *>(lw + frag_off(rw, 1));
+      fa[t] = i32x8{(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w, (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
+    }
+  };
+
+  f32x16 acc[4][4];
+  auto zero_acc = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+  };
+  auto mma = [&](const i32x8 fa[4], const i32x8 fb[4]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int tn = 0; tn < 4; ++tn)
+#pragma unroll
+      for (int tm = 0; tm < 4; ++tm)
+        acc[tn][tm] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa[tn], fb[tm], acc[tn][tm],
+                                                                       0, 0, 0, 0, 0, 0);
+  };
+  const float scale = p.sx_scale[0] * p.sw_scale[0];
+  // Epilogue of tile j: lane holds, for X row m = m0 + wm + 32 tm + lr, the
+  // W rows n = n0 + wn + 32 tn + 8 q + 4 g + i (i < 4) in acc[tn][tm][4 q + i].
+  auto epilogue = [&](int j) __attribute__((always_inline)) {
+    int bn, bm;
+    persist_tile(static_cast<int>(blockIdx.x) + j * static_cast<int>(gridDim.x), tiles_n, grouped != 0, bn, bm);
+    // whole tiles only (the host checks M and N are multiples of 256 and the
+    // output rows 8-byte aligned)
+    const int n0 = bn * G_BN, m0 = bm * G_BM;
+#pragma unroll
+    for (int tm = 0; tm < 4; ++tm) {
+      bf16_t *orow = p.out + (int64_t)(m0 + wm + 32 * tm + lr) * p.so;
+#pragma unroll
+      for (int tn = 0; tn < 4; ++tn) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int n = n0 + wn + 32 * tn + 8 * q + 4 * g;
+          float v[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) v[i] = acc[tn][tm][4 * q + i] * scale;
+          if (p.bias) {
+            const uint2 bb = *reinterpret_cast<const uint2 *>(p.bias + n);
+            v[0] += lo_bf(bb.x);
+            v[1] += hi_bf(bb.x);
+            v[2] += lo_bf(bb.y);
+            v[3] += hi_bf(bb.y);
+          }
+          *reinterpret_cast<uint2 *>(orow + n) = make_uint2(pack_bf(v[0], v[1]), pack_bf(v[2], v[3]));
+        }
+      }
+    }
+  };
+
+  // Step s: MFMAs of slice s (stage s % 4, fragments read during step s - 1)
+  // while reading slice s + 1's fragments; first wait for slice s + 1's loads
+  // (slice s + 2 stays in flight) and a barrier (every wave's loads for s + 1
+  // have landed; every wave has read slice s - 1, whose stage is refilled
+  // with slice s + 3 right after).  The first step after an epilogue also has
+  // its stores outstanding, and loads and stores retire in order: waiting for
+  // at most 63 then covers slices s + 1 and s + 2 and one store.
+  i32x8 fa[2][4], fb[2][4];
+  auto step = [&](auto stage, auto fbuf, int s, bool after_epilogue) __attribute__((always_inline)) {
+    constexpr int S = decltype(stage)::value;
+    constexpr int B = decltype(fbuf)::value;
+    if (after_epilogue) vmcnt_wait<63>();
+    else vmcnt_wait<DMA>();
+    __builtin_amdgcn_s_barrier();
+    issue(std::integral_constant<int, (S + 3) % P_STAGES>{}, s + 3);
+    read_frags(std::integral_constant<int, (S + 1) % P_STAGES>{}, fa[B ^ 1], fb[B ^ 1]);
+    mma(fa[B], fb[B]);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      if (i < DMA) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+    }
+  };
+
+  dma_tile(0);
+  using std::integral_constant;
+  issue(integral_constant<int, 0>{}, 0);
+  issue(integral_constant<int, 1>{}, 1);
+  issue(integral_constant<int, 2>{}, 2);
+  vmcnt_wait<2 * DMA>();  // slice 0 (slices 1 and 2 in flight)
+  __builtin_amdgcn_s_barrier();
+  read_frags(integral_constant<int, 0>{}, fa[0], fb[0]);
+  zero_acc();
+  int s = 0;
+  for (int j = 0; j < ntile; ++j) {
+    // K steps of tile j in fours (KT is a multiple of 4): the stage and
+    // fragment buffer of a step are fixed by its position in the four
+    for (int k = 0; k < KT; k += 4, s += 4) {
+      step(integral_constant<int, 0>{}, integral_constant<int, 0>{}, s, k == 0 && j > 0);
+      step(integral_constant<int, 1>{}, integral_constant<int, 1>{}, s + 1, false);
+      step(integral_constant<int, 2>{}, integral_constant<int, 0>{}, s + 2, false);
+      step(integral_constant<int, 3>{}, integral_constant<int, 1>{}, s + 3, false);
+    }
+    epilogue(j);
+    zero_acc();
+  }
+  // No direct-to-LDS write may still be landing when the workgroup's LDS is
+  // handed to the next one.
+  vmcnt_wait<0>();
+}
+
+// ---------------------------------------------------------------------------
 // Decode-sized GEMMs (M <= 64 rows, e.g. the in_proj of a 64-sequence decode
 // step): the weight stream is the whole cost (N x K bytes against 64 x K of
 // activations), so the kernel is built to keep HBM busy rather than the
@@ -420,6 +645,20 @@ __global__ __launch_bounds__(256) void fp8_quantize_kernel(const bf16_t *x, int6
 
 using namespace evo2;
 
+// Compute units of the current device (0 if the query fails), cached per
+// device ordinal.
+static int cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
 extern "C" int evo2_fp8_quantize(const void *x, int64_t sx, void *q, int64_t sq,
                                  const float *scale, int64_t rows, int64_t K, void *stream) {
   if (rows < 0 || K < 0 || rows > 65535 * 64LL)
@@ -473,7 +712,21 @@ extern "C" int evo2_fp8_gemm(const void *x8, int64_t sx, const void *w8, int64_t
       launch_small<2>(a, st);
     return check_launch("fp8_gemm");
   }
-  dim3 grid(static_cast<unsigned>(cdiv(N, G_BN)), static_cast<unsigned>(cdiv(M, G_BM)));
-  hipLaunchKernelGGL(fp8_gemm_kernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream), a);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t tiles_n = cdiv(N, G_BN), tiles_m = cdiv(M, G_BM);
+  const int ncu = cu_count();
+  // the persistent form once every CU has a tile; its ring needs K to be a
+  // multiple of four K steps and the operands to fit 32-bit buffer offsets
+  if (ncu > 0 && tiles_n * tiles_m >= ncu && K % (P_STAGES * G_BK) == 0 &&
+      M % G_BM == 0 && N % G_BN == 0 && so % 4 == 0 && reinterpret_cast<uintptr_t>(out) % 8 == 0 &&
+      (!bias || reinterpret_cast<uintptr_t>(bias) % 8 == 0) &&
+      (N - 1) * sw + K < (int64_t(1) << 31) && (M - 1) * sx + K < (int64_t(1) << 31)) {
+    const int grouped = ncu == 256 && tiles_n % 4 == 0 && tiles_m % 8 == 0;
+    hipLaunchKernelGGL(fp8_gemm_persist_kernel, dim3(static_cast<unsigned>(ncu)), dim3(256), 0, st, a,
+                       static_cast<int>(tiles_n), static_cast<int>(tiles_m), grouped);
+    return check_launch("fp8_gemm");
+  }
+  dim3 grid(static_cast<unsigned>(tiles_n), static_cast<unsigned>(tiles_m));
+  hipLaunchKernelGGL(fp8_gemm_kernel, grid, dim3(256), 0, st, a);
   return check_launch("fp8_gemm");
 }

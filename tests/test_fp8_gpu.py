@@ -3,7 +3,11 @@
 * activation quantisation bit-exact against torch's e4m3fn conversion of
   clamp(x / s, +-448) (fp8_emul.py:76-78), including saturation and ties;
 * GEMM known answers: small-integer e4m3 operands whose fp32 sums are exact,
-  so the bf16 output must equal the oracle bit for bit;
+  so the bf16 output must equal the oracle bit for bit, on each kernel: the
+  decode-sized one, the 256x256 tile one and its persistent form (whole
+  tiles, at least one per CU), in both tile orders of the latter (XCD
+  blocks of 4 x 8 tiles, and row-major with some workgroups taking one
+  tile more);
 * GEMM within 2e-2 max relative error of the dequantised bf16 reference on
   random operands, at ragged shapes, at decode sizes (M <= 64, the 7B and
   40B in_proj) and at both config-3 shapes (M=8192, K=4096 -> N=12288 and
@@ -53,6 +57,34 @@ def test_gemm_known_answer(M, N, K):
     acc = x8.float().double() @ w8.float().double().t()   # exact
     ref = (acc.float() * 0.5 * 0.25).to(torch.bfloat16)
     assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+
+
+# Persistent 256x256 form: (2048, 8192) has 8 x 32 tiles (the XCD-block
+# order); (3328, 5120) has 13 x 20 = 260 tiles over 256 workgroups (row-major
+# order, four workgroups take a second tile).
+@pytest.mark.parametrize("M,N,K", [(2048, 8192, 512), (3328, 5120, 768)])
+def test_gemm_known_answer_persistent(M, N, K):
+    g = torch.Generator().manual_seed(M + N + K)
+    x8 = _small_int_e4m3((M, K), g)
+    w8 = _small_int_e4m3((N, K), g)
+    xs, ws = torch.tensor([0.5]), torch.tensor([0.25])
+    print(f"persistent gemm M={M} N={N} K={K}", flush=True)
+    out = fp8_gemm(x8.to(DEV), w8.to(DEV), xs.to(DEV), ws.to(DEV)).cpu()
+    acc = x8.float() @ w8.float().t()   # exact: |sums| < 2^24
+    ref = (acc * 0.5 * 0.25).to(torch.bfloat16)
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+
+
+def test_static_linear_persistent_with_bias():
+    M, N, K = 4096, 4096, 1024   # 16 x 16 tiles
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    w8, ws = quantize_weight_e4m3(torch.randn(N, K, generator=g) * 0.02)
+    xs = torch.tensor([6.0 / 448])
+    bias = (torch.randn(N, generator=g) * 0.02).to(torch.bfloat16)
+    out = static_fp8_linear(x.to(DEV), w8.to(DEV), xs.to(DEV), ws.to(DEV), bias.to(DEV)).cpu()
+    ref = oracle.fp8_linear_dequant(x, w8, xs, ws, bias)
+    assert max_rel_err(out, ref) <= 2e-2
 
 
 @pytest.mark.parametrize("M,N,K", [(64, 12288, 4096), (333, 4096, 4096), (1000, 640, 1920),
