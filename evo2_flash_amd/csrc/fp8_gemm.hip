@@ -465,10 +465,9 @@ constexpr int S_BK = 128;                 // bytes of K per step
 constexpr int S_ROWS = 64;                // activation rows (max M)
 constexpr int S_DEPTH = 8;                // steps in flight
 constexpr int S_STAGE = S_ROWS * S_BK;    // 8 KB of activations per step
-constexpr int SMALL_WIDE_MIN_GROUPS = 128;  // 64-row groups from N = 64 * this (measured)
 typedef __attribute__((ext_vector_type(4))) float f32x4;
 
-template <int WPG>  // waves per workgroup (2 or 4): 16 W rows each
+template <int WPG>  // waves per workgroup (2, 3 or 4): 16 W rows each
 __global__ __launch_bounds__(256) void fp8_gemm_small_kernel(GemmArgs p) {
   // one variable per stage: the compiler then sees which stage each
   // direct-to-LDS load writes and waits only for that stage's loads
@@ -482,19 +481,22 @@ __global__ __launch_bounds__(256) void fp8_gemm_small_kernel(GemmArgs p) {
   };
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6) & (WPG - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n0 = blockIdx.x * 16 * WPG;
   const int g = lane >> 4;   // K bytes [32g, 32g + 32) of a step
   const int lr = lane & 15;  // row within a 16-row tile
   const int KT = p.K / S_BK;
 
   // activation DMA: the 8 blocks of a stage (1 KB = 8 rows each) are split
-  // over the waves, block XB * wave + j for j < XB
-  constexpr int XB = 8 / WPG;
+  // over the waves, block wave + WPG j for j < XB; with three waves the
+  // last wave's third block repeats block 7 (the same bytes to the same
+  // place), so every wave issues XB loads and the wait counts stay uniform
+  constexpr int XB = (8 + WPG - 1) / WPG;
+  auto xblock = [&](int j) __attribute__((always_inline)) { return min(wave + WPG * j, 7); };
   int xoff[XB];
 #pragma unroll
   for (int j = 0; j < XB; ++j) {
-    const int row = (XB * wave + j) * 8 + lane / 8;
+    const int row = xblock(j) * 8 + lane / 8;
     const int lchunk = (lane & 7) ^ ((row >> 1) & 7);
     xoff[j] = min(row, p.M - 1) * (int)p.sx + 16 * lchunk;
   }
@@ -509,7 +511,7 @@ __global__ __launch_bounds__(256) void fp8_gemm_small_kernel(GemmArgs p) {
 #pragma unroll
     for (int j = 0; j < XB; ++j)
       __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint4 *>(p.x + k0 + xoff[j]),
-                                       (lds_void *)(stage_of(slot) + (XB * wave + j) * 1024), 16,
+                                       (lds_void *)(stage_of(slot) + xblock(j) * 1024), 16,
                                        0, 0);
     const uint4 a0 = *reinterpret_cast<const uint4 *>(wrow + k0);
     const uint4 a1 = *reinterpret_cast<const uint4 *>(wrow + k0 + 16);
@@ -704,12 +706,27 @@ extern "C" int evo2_fp8_gemm(const void *x8, int64_t sx, const void *w8, int64_t
              w_scale, static_cast<const bf16_t *>(bias), static_cast<bf16_t *>(out), so,
              static_cast<int>(M), static_cast<int>(N), static_cast<int>(K)};
   if (M <= S_ROWS && K % S_BK == 0 && sx * S_ROWS < (int64_t(1) << 31)) {
-    // 64 W rows per workgroup from N = 8192 (the 7B in_proj: 192 groups), else 32
+    // Waves per workgroup (16 W rows each): the count whose workgroups fill
+    // the CUs most evenly (groups / (rounds x CUs)), the larger on a tie.
+    // Measured with 9 rotating weights: the 7B in_proj (N=12288) 17.1 us with
+    // 3 (256 groups) against 18.6 with 4 (192) and 21.3 with 2; the 40B one
+    // (N=24576, K=8192) 46.0 / 52.5 / 64.5 us; N=4096 11.2 us with 2 against
+    // 12.6 with 3 and 14.1 with 4.
     hipStream_t st = static_cast<hipStream_t>(stream);
-    if (N >= 64 * SMALL_WIDE_MIN_GROUPS)
-      launch_small<4>(a, st);
-    else
-      launch_small<2>(a, st);
+    const int ncu = cu_count() > 0 ? cu_count() : 256;
+    int best_w = 4;
+    double best_eff = -1.0;
+    for (int w = 4; w >= 2; --w) {
+      const int64_t groups = cdiv(N, 16 * w);
+      const double eff = double(groups) / double(cdiv(groups, ncu) * ncu);
+      if (eff > best_eff + 1e-9) {
+        best_eff = eff;
+        best_w = w;
+      }
+    }
+    if (best_w == 4) launch_small<4>(a, st);
+    else if (best_w == 3) launch_small<3>(a, st);
+    else launch_small<2>(a, st);
     return check_launch("fp8_gemm");
   }
   hipStream_t st = static_cast<hipStream_t>(stream);
