@@ -436,7 +436,92 @@ def bench_verify(reps, dev, H=H_7B, B=B_DECODE, Q=4, seed=9):
         res[kind] = {"avg_us": round(avg, 2), "median_us": round(med, 2), "bytes": nbytes,
                      "achieved_GBs": round(nbytes / (avg * 1e-6) / 1e9, 1),
                      "frac": round(nbytes / (avg * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
-    return {"requests": B, "tokens_per_request": Q, "per_kind": res}
+    steps = _bench_verify_mixers(reps, dev, H, B, Q, seed)
+    for kind, v in steps.items():
+        res[kind]["mixer_step"] = v
+    return {"requests": B, "tokens_per_request": Q, "per_kind": res,
+            "mixer_step_scope": "whole mixer forward of a verify step: fp8 in_proj, speculative "
+                                "short window, snapshot verify, gate, bf16 out_proj, stamps "
+                                "(plus one small stamp-reset launch per step), captured in one "
+                                "HIP graph per step; eager launches timed beside it"}
+
+
+def _bench_verify_mixers(reps, dev, H, B, Q, seed):
+    """A whole speculative verify step through each mixer kind (num_spec =
+    Q - 1): B requests of Q tokens, slot rows of Q distinct blocks, the
+    previous step's accepted count resolved from the position stamps."""
+    from evo2_flash_amd.config import HyenaConfig
+    from evo2_flash_amd.metadata import HyenaMamba2Metadata
+    from evo2_flash_amd.mixers import load_mixer_params, make_mixer, set_forward_context
+    from evo2_flash_amd.state import HyenaStatePool
+    from evo2_flash_amd.synthetic import mixer_params
+
+    cfg = HyenaConfig(hidden_size=H, num_hidden_layers=3, hcs_layer_idxs=[0], hcm_layer_idxs=[1],
+                      hcl_layer_idxs=[2], use_fp8_input_projections=True)
+    nblk = B * Q + 1
+    slots = (torch.arange(B * Q, device=dev, dtype=torch.int32) + 1).view(B, Q)
+    computed = 8192
+    m = HyenaMamba2Metadata()
+    m.num_decodes, m.num_decode_tokens = B, B * Q
+    m.state_indices_tensor_d = slots
+    m.query_start_loc_d = torch.arange(B + 1, device=dev, dtype=torch.int32) * Q
+    m.num_computed_tokens_d = torch.full((B,), computed, device=dev, dtype=torch.int32)
+    m.seq_lens = torch.full((B,), computed + Q, device=dev, dtype=torch.int32)
+    g = torch.Generator(device=dev).manual_seed(seed + 1)
+    hs = torch.randn(B * Q, H, generator=g, device=dev).to(torch.bfloat16)
+    stream = torch.cuda.current_stream()
+    out = {}
+    for kind, layer in (("hcs", 0), ("hcm", 1), ("hcl", 2)):
+        mixer = make_mixer(cfg, layer, prefix=f"bench.verify.{kind}", device=dev, num_spec=Q - 1)
+        load_mixer_params(mixer, mixer_params(kind, H, seed + layer, in_proj_fp8=True))
+        pool = HyenaStatePool(nblk, H, dev, num_spec=Q - 1)
+        for t in pool.kv_cache:
+            t.copy_(torch.randn(t.shape, generator=g, device=dev).to(t.dtype))
+        mixer.kv_cache = pool.kv_cache
+
+        live = slots[:, 0].long()
+
+        def fn(mixer=mixer, pool=pool, live=live):
+            # stamps of the live snapshots: the previous step accepted 2 tokens
+            pool.stamps().index_fill_(0, live, float(computed - 1))
+            with set_forward_context(m):
+                return mixer(hs)
+
+        start = [t.clone() for t in pool.kv_cache]
+
+        def restore(pool=pool, start=start):
+            for t, t0 in zip(pool.kv_cache, start):
+                t.copy_(t0)
+
+        ref = fn().clone()
+        torch.cuda.synchronize()
+        faults = mixer.stamp_faults()
+        eager_avg, eager_med = _timed(fn, max(4, reps // 2), stream)
+        # the same step captured once and replayed: each replay from the
+        # restored pool must reproduce the eager output bit for bit
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            restore()
+            fn()
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            res_g = fn()
+        exact = True
+        for _ in range(3):
+            restore()
+            graph.replay()
+            torch.cuda.synchronize()
+            exact = exact and torch.equal(res_g.view(torch.int16), ref.view(torch.int16))
+        avg, med = _timed(graph.replay, reps, stream)
+        out[kind] = {"graph_avg_us": round(avg, 2), "graph_median_us": round(med, 2),
+                     "tokens_per_s": round(B * Q / (avg * 1e-6), 1),
+                     "eager_avg_us": round(eager_avg, 2), "eager_median_us": round(eager_med, 2),
+                     "graph_matches_eager": exact, "stamp_faults": faults}
+        del mixer, pool, graph, start
+        torch.cuda.empty_cache()
+    return out
 
 
 # ---------------------------------------------------------------- prefill

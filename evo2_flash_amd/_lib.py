@@ -161,6 +161,7 @@ SIGNATURES = {
         _c_p, _c_i64, _c_i64, _c_i64, _c_i64,     # out, so, M, N, K
         _c_p,                                     # stream
     ],
+    "evo2_fp8_gemm_persist_order": [_c_i64, _c_i64, ctypes.c_int, _c_p, _c_p],
     "evo2_fp8_fast_accum_gemm": [
         _c_p, _c_i64, _c_p, _c_i64,               # a8, sa, b_t, sb
         _c_p, _c_p,                               # input_scale, weight_scale
@@ -191,7 +192,8 @@ SIGNATURES = {
 }
 
 RESTYPES = {"evo2_last_error": ctypes.c_char_p, "evo2_hcl_workspace_bytes": ctypes.c_int64,
-            "evo2_decode_attention_workspace_bytes": ctypes.c_int64}
+            "evo2_decode_attention_workspace_bytes": ctypes.c_int64,
+            "evo2_fp8_gemm_persist_order": ctypes.c_int64}
 
 _lock = threading.Lock()
 _lib = None

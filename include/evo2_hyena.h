@@ -372,6 +372,20 @@ int evo2_fp8_gemm(const void *x8, int64_t sx, const void *w8, int64_t sw,
                   void *out, int64_t so, int64_t M, int64_t N, int64_t K, void *stream);
 
 /*
+ * The order in which evo2_fp8_gemm's persistent kernel (one workgroup per
+ * compute unit, 256 x 256 output tiles) walks a grid of tiles_n x tiles_m
+ * tiles on a device with ncu compute units: tile t, run by workgroup
+ * t mod ncu, is output tile (bn[t], bm[t]).  Fills bn / bm (tiles_n * tiles_m
+ * entries each, both may be NULL) and returns 1 for the XCD-grouped order,
+ * 0 for row-major, -1 for bad sizes.  Host only, no GPU needed.
+ *
+ * No counterpart in the reference (its GEMM is a library call): a planning
+ * query for callers and tests that check the tile order covers every tile.
+ */
+int64_t evo2_fp8_gemm_persist_order(int64_t tiles_n, int64_t tiles_m, int ncu,
+                                    int32_t *bn, int32_t *bm);
+
+/*
  * Software model of Hopper's fp8 "fast accumulation" GEMM (bit-exact):
  * per group of 32 consecutive k, e = max(max_k e(a_k) + e(b_k), e(acc)) with
  * e(x) = floor(log2|x|); the accumulator and every product are truncated

@@ -151,3 +151,34 @@ def test_verify_wrappers_check_metadata():
             torch.zeros(2), torch.zeros(2), torch.ones(2))
     with pytest.raises(RuntimeError, match="no CPU fallback"):
         fir_snapshots(x, torch.zeros(8, 7, dtype=torch.bfloat16), torch.zeros(4, 8, 6), meta)
+
+
+@needs_lib
+def test_fp8_persist_order_covers_every_tile():
+    """The persistent GEMM's tile order is a bijection onto the tile grid for
+    every grid shape, including block counts that leave the last round of the
+    XCD-grouped order part-filled (48 x 8 tiles: 12 blocks of 4 x 8); while
+    the rounds are whole, the 32 tiles one XCD runs at once form one block."""
+    import numpy as np
+    lib = _lib.lib()
+    for ncu in (256, 80):
+        for tn in range(1, 65, 3 if ncu == 256 else 7):
+            for tm in range(1, 41, 1 if ncu == 256 else 5):
+                total = tn * tm
+                bn = np.full(total, -1, dtype=np.int32)
+                bm = np.full(total, -1, dtype=np.int32)
+                grouped = lib.evo2_fp8_gemm_persist_order(tn, tm, ncu, bn.ctypes.data,
+                                                          bm.ctypes.data)
+                assert grouped == (1 if ncu == 256 and tn % 4 == 0 and tm % 8 == 0 else 0)
+                assert bn.min() >= 0 and bn.max() < tn and bm.min() >= 0 and bm.max() < tm, \
+                    (ncu, tn, tm)
+                assert len(np.unique(bm.astype(np.int64) * tn + bn)) == total, (ncu, tn, tm)
+                if grouped:
+                    whole = (tn // 4) * (tm // 8) // 8 * 256
+                    t = np.arange(whole)
+                    for key in np.unique((t >> 8) * 8 + (t & 7)):
+                        sel = ((t >> 8) * 8 + (t & 7)) == key
+                        assert len(np.unique(bn[:whole][sel] // 4)) == 1
+                        assert len(np.unique(bm[:whole][sel] // 8)) == 1
+    assert lib.evo2_fp8_gemm_persist_order(48, 8, 256, None, None) == 1
+    assert lib.evo2_fp8_gemm_persist_order(0, 8, 256, None, None) == -1

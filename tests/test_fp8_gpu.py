@@ -4,10 +4,11 @@
   clamp(x / s, +-448) (fp8_emul.py:76-78), including saturation and ties;
 * GEMM known answers: small-integer e4m3 operands whose fp32 sums are exact,
   so the bf16 output must equal the oracle bit for bit, on each kernel: the
-  decode-sized one, the 256x256 tile one and its persistent form (whole
-  tiles, at least one per CU), in both tile orders of the latter (XCD
-  blocks of 4 x 8 tiles, and row-major with some workgroups taking one
-  tile more);
+  decode-sized one, the mid-sized one, the 256x256 tile one and its
+  persistent form (whole tiles, at least one per CU), in both tile orders
+  of the latter (XCD
+  blocks of 4 x 8 tiles, whole rounds and a part-filled last round, and
+  row-major with some workgroups taking one tile more);
 * GEMM within 2e-2 max relative error of the dequantised bf16 reference on
   random operands, at ragged shapes, at decode sizes (M <= 64, the 7B and
   40B in_proj) and at both config-3 shapes (M=8192, K=4096 -> N=12288 and
@@ -44,10 +45,20 @@ def _small_int_e4m3(shape, g):
     return (torch.randint(-6, 7, shape, generator=g).float()).to(E4M3)
 
 
-# M <= 64 with K a multiple of 128 runs the decode-sized kernel (weights
-# streamed into registers, 16x16x128 MFMA); the others the 256x256-tile one.
-@pytest.mark.parametrize("M,N,K", [(256, 256, 128), (64, 384, 256), (300, 512, 1920),
-                                   (1, 64, 128), (5, 130, 1920), (64, 4096, 4096)])
+# With K a multiple of 128 the weight-streaming kernels take M <= 64, and
+# larger M while ceil(M / 256) x N <= 24576: 16 W rows per wave in registers,
+# 16x16x128 MFMA, mb = 1..4 blocks of 64 activation rows per workgroup by the
+# number of 16 x 64 wave tiles (<= 1024: 1, <= 2048: 2, else up to 4) and a
+# second grid dimension over the row blocks; the others run the 256x256-tile
+# kernel (K = 192 here, or too much work).
+@pytest.mark.parametrize("M,N,K", [(64, 384, 256), (1, 64, 128), (5, 130, 1920),
+                                   (64, 4096, 4096),                      # mb 1, one row block
+                                   (65, 200, 256), (130, 96, 384), (300, 512, 1920),
+                                   (1000, 130, 640),                      # mb 1, gridded over M
+                                   (128, 12288, 256), (100, 10000, 384),  # mb 2
+                                   (192, 12288, 256), (170, 12000, 256),  # mb 3
+                                   (256, 12288, 512), (500, 12288, 256),  # mb 4
+                                   (256, 256, 192), (1100, 6400, 640)])   # 256x256 tiles
 def test_gemm_known_answer(M, N, K):
     g = torch.Generator().manual_seed(M + N)
     x8 = _small_int_e4m3((M, K), g)
@@ -60,9 +71,11 @@ def test_gemm_known_answer(M, N, K):
 
 
 # Persistent 256x256 form: (2048, 8192) has 8 x 32 tiles (the XCD-block
-# order); (3328, 5120) has 13 x 20 = 260 tiles over 256 workgroups (row-major
-# order, four workgroups take a second tile).
-@pytest.mark.parametrize("M,N,K", [(2048, 8192, 512), (3328, 5120, 768)])
+# order); (2048, 12288) has 8 x 48 = 384 tiles, twelve blocks of 4 x 8, so
+# the XCD-block order's second round is half full and its last four blocks
+# go out tile by tile; (3328, 5120) has 13 x 20 = 260 tiles over 256
+# workgroups (row-major order, four workgroups take a second tile).
+@pytest.mark.parametrize("M,N,K", [(2048, 8192, 512), (2048, 12288, 512), (3328, 5120, 768)])
 def test_gemm_known_answer_persistent(M, N, K):
     g = torch.Generator().manual_seed(M + N + K)
     x8 = _small_int_e4m3((M, K), g)
