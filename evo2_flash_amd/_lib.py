@@ -189,6 +189,17 @@ SIGNATURES = {
         _c_p, _c_i64, _c_i64, _c_i64, _c_i64,     # y, ys0, nreq, T, H
         _c_i32, _c_i64, _c_p,                     # null_block, num_blocks, stream
     ],
+    "evo2_spec_accepted": [
+        _c_p, _c_i64, _c_i64,                     # stamps, stride, num_blocks
+        _c_p, _c_i64, _c_p, _c_p,                 # slots, si0, computed, counts
+        _c_i32, _c_i64, _c_p, _c_p, _c_p,         # num_spec, nreq, accepted, faults, stream
+    ],
+    "evo2_spec_record_stamps": [
+        _c_p, _c_i64, _c_i64,                     # stamps, stride, num_blocks
+        _c_p, _c_i64, _c_i64, _c_i64,             # slots + strides, ncols
+        _c_p, _c_p, _c_p, _c_i64, _c_i64,         # out_col, qsl, computed, nreq, width
+        _c_p, _c_p, _c_i64, _c_p,                 # prefill_blocks, seq_lens, npf, stream
+    ],
 }
 
 RESTYPES = {"evo2_last_error": ctypes.c_char_p, "evo2_hcl_workspace_bytes": ctypes.c_int64,

@@ -56,7 +56,7 @@ from .metadata import decode_state_indices, prefill_tables
 from .prefill import fir_prefill_block_t, hyena_fir_prefill
 from .short_conv import PAD_SLOT_ID, causal_conv1d_update
 from .speculative import (accepted_tokens, cache_safe_state_indices, decode_tensors,
-                          query_start_loc_d)
+                          query_start_loc_d, record_stamps, spec_accepted)
 from .state import unified_state_dtype, unified_state_shape
 from .verify import fir_snapshots, iir_snapshots
 
@@ -273,10 +273,10 @@ class HyenaMixerBase(nn.Module):
         return 0 if self._stamp_faults is None else int(self._stamp_faults)
 
     def _spec_accepted(self, m):
-        """(num_decodes,) accepted count of the previous step from the stamps
-        (mixers.py:960-999): offset = computed tokens - stamp of column 0, in
-        [0, num_spec] for every request not on the null block; returns
-        offset + 1, clamped."""
+        """(num_decodes,) accepted count of the previous step from the stamps,
+        one launch (mixers.py:960-999): offset = computed tokens - stamp of
+        column 0, in [0, num_spec] for every request not on the null block;
+        returns offset + 1, clamped."""
         nd = int(m.num_decodes)
         computed = getattr(m, "num_computed_tokens_d", None)
         if computed is None:
@@ -285,14 +285,15 @@ class HyenaMixerBase(nn.Module):
         slots = m.state_indices_tensor_d[:nd]
         if slots.dim() == 1:
             slots = slots[:, None]
-        first = cache_safe_state_indices(slots, self.kv_cache[2])[:, 0].long()
-        offset = computed[:nd].to(torch.int64) - self._position_stamps()[first].to(torch.int64)
-        bad = (first != 0) & ((offset < 0) | (offset > self.num_spec))
+        # a slot matrix naming more blocks than the pool holds puts every
+        # request on the null block (mixers.py:527-541)
+        if self.kv_cache[2].shape[0] < slots.numel():
+            slots = None
+        counts = None
         if _CHECK_VLLM_COUNTS and getattr(m, "num_accepted_tokens", None) is not None:
-            counts = accepted_tokens(m, nd, offset.device)
-            bad = bad | ((first != 0) & (counts != offset + 1))
-        self._fault_counter(offset.device).add_(bad.sum())
-        return offset.clamp(0, self.num_spec) + 1
+            counts = accepted_tokens(m, nd, computed.device)
+        return spec_accepted(self._position_stamps(), slots, computed[:nd], self.num_spec,
+                             self._fault_counter(computed.device), counts)
 
     def _repair_resumed_prefill_state(self, m):
         """Align-mode prefix caching: a prefill row continuing from n computed
@@ -326,30 +327,35 @@ class HyenaMixerBase(nn.Module):
         return None
 
     def _record_stamps(self, m):
-        """Stamp every snapshot this step wrote: decode column p of a request
-        that had computed n tokens holds n + p + 1, a prefill block its
-        sequence length (mixers.py:1049-1074)."""
+        """Stamp every snapshot this step wrote, one launch: decode column p
+        of a request that had computed n tokens holds n + p + 1, a prefill
+        block its sequence length (mixers.py:1049-1074)."""
         if not self.num_spec:
             return
         stamps = self._position_stamps()
-        nd = int(m.num_decodes)
+        nd, npf = int(m.num_decodes), int(m.num_prefills)
+        slots = qsl = computed = out_col = None
+        width = 0
         if nd and self.is_speculative_decode(m):
-            ones = torch.ones(nd, device=stamps.device, dtype=torch.long)
-            _, outs, starts, ends, _ = decode_tensors(m, int(m.num_decode_tokens),
-                                                      1 + self.num_spec, ones)
-            outs = cache_safe_state_indices(outs, self.kv_cache[2])
-            steps = torch.arange(outs.shape[1], device=outs.device)
-            active = steps[None, :] < (ends - starts)[:, None]
-            computed = m.num_computed_tokens_d[:nd].to(torch.int64)
-            values = computed[:, None] + steps[None, :] + 1
-            # inactive entries all target the null block, whose value is moot
-            dest = torch.where(active, outs.long(), 0).reshape(-1)
-            stamps.index_put_((dest,), torch.where(active, values, 0).reshape(-1)
-                              .to(stamps.dtype))
-        npf = int(m.num_prefills)
-        if npf:
-            stamps[m.state_indices_tensor_p[:npf].long()] = (
-                m.seq_lens[nd:nd + npf].to(stamps.dtype))
+            slots = m.state_indices_tensor_d[:nd]
+            if slots.dim() == 1:
+                slots = slots[:, None]
+            qsl = query_start_loc_d(m, nd, stamps.device)
+            computed = m.num_computed_tokens_d[:nd]
+            # the written columns: prefix caching's window from the block of
+            # the last scheduled token, else the slot row (mixers.py:444-456)
+            width = slots.shape[1]
+            if (getattr(m, "block_idx_last_scheduled_token_prev_step", None) is not None
+                    and getattr(m, "block_idx_last_scheduled_token", None) is not None):
+                width = min(width, 1 + self.num_spec)
+                out_col = m.block_idx_last_scheduled_token[:nd]
+            if self.kv_cache[2].shape[0] < nd * width:
+                slots = None   # every request on the null block (mixers.py:527-541)
+        if not npf and qsl is None:
+            return
+        record_stamps(stamps, slots, qsl, computed, width, out_col,
+                      m.state_indices_tensor_p[:npf] if npf else None,
+                      m.seq_lens[nd:nd + npf] if npf else None)
 
     def _spec_short_conv(self, z_d, m, accepted):
         """(x2, x1, v) of the decode rows of a speculative step through the

@@ -481,6 +481,45 @@ int evo2_iir_verify(const void *x, int64_t xs0, int64_t xs1, int32_t x_f32,
                     void *y, int64_t ys0, int64_t nreq, int64_t T, int64_t H,
                     int32_t null_block, int64_t num_blocks, void *stream);
 
+/*
+ * Accepted counts of the previous speculative step from the position stamps
+ * (slice 2 row 0 last column of every state block: the tokens its snapshot
+ * represents).  For r < nreq: offset = computed[r] - stamps[slots[r * si0] * ss],
+ * accepted[r] = clamp(offset, 0, num_spec) + 1.  A request whose block is
+ * not the null block (0) with offset outside [0, num_spec], or with
+ * counts[r] != offset + 1 when counts is not NULL, adds one to *faults
+ * (int64), as does a block outside [0, num_blocks) (its stamp is not read).
+ * slots NULL puts every request on the null block.
+ *   stamps fp32, stride ss (elements); slots, computed, counts int32;
+ *   accepted (nreq,) int64 out.
+ *
+ * Replaces the stamp lookup and check of the reference's speculative decode
+ * (evo2_flash/mixers.py:960-999), whose device-side assert aborts the process
+ * on ROCm; faults are counted instead.
+ */
+int evo2_spec_accepted(const float *stamps, int64_t ss, int64_t num_blocks,
+                       const int32_t *slots, int64_t si0, const int32_t *computed,
+                       const int32_t *counts, int num_spec, int64_t nreq,
+                       int64_t *accepted, void *faults, void *stream);
+
+/*
+ * Stamps of the snapshots a step wrote.  Decode request r < nreq (query
+ * length qsl[r+1] - qsl[r], computed[r] tokens before the step) stamps
+ * block slots[r * si0 + (out_col[r] + p) * si1] with computed[r] + p + 1 for
+ * p < min(width, query length) (out_col NULL: column p); prefill block
+ * prefill_blocks[j] gets seq_lens[j], j < npf.  The null block, blocks
+ * outside [0, num_blocks) and columns outside [0, ncols) are not written;
+ * slots NULL writes no decode stamp.  All index arrays int32.
+ *
+ * Replaces the reference's stamp recording (evo2_flash/mixers.py:1049-1074).
+ */
+int evo2_spec_record_stamps(float *stamps, int64_t ss, int64_t num_blocks,
+                            const int32_t *slots, int64_t si0, int64_t si1, int64_t ncols,
+                            const int32_t *out_col, const int32_t *qsl,
+                            const int32_t *computed, int64_t nreq, int64_t width,
+                            const int32_t *prefill_blocks, const int32_t *seq_lens,
+                            int64_t npf, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -21,6 +21,7 @@ __all__ = [
     "iir_verify_emulated", "STATE_ACC_BUDGET", "fast_accum_mm", "fp8_linear_fast_accum",
     "causal_conv1d_update_ref", "causal_conv1d_ref", "iir_final_state_recurrence",
     "causal_conv1d_update_spec_ref", "mixer_decode_speculative",
+    "spec_accepted_ref", "record_stamps_ref",
 ]
 
 # mixers.py:72-74: bound on the (H, blk, L) temporary of the LI final state.
@@ -483,6 +484,60 @@ def mixer_decode_speculative(z, short_w, conv_state, inner, inner_state, D, slot
         covered[int(qsl[r]):int(qsl[r + 1])] = True
     g[~covered] = 0
     return g
+
+
+# ------------------------------------------------------------ position stamps
+def spec_accepted_ref(stamps, slots, computed, num_spec, counts=None):
+    """(accepted, faults) of a speculative decode step from the position
+    stamps (mixers.py:960-999): request r on slot row slots[r] (a list; the
+    first entry names its live-snapshot column 0 block) that has computed n
+    tokens finds offset = n - stamps[slots[r][0]]; accepted = clamp(offset,
+    0, num_spec) + 1.  A request not on the null block (0) whose offset lies
+    outside [0, num_spec] -- or, with `counts`, whose count differs from
+    offset + 1 -- is a fault (the reference asserts; here it is counted).
+    `slots` None puts every request on the null block (mixers.py:527-541).
+    A slot outside the pool is a fault and reads no stamp."""
+    acc, faults = [], 0
+    nb = len(stamps)
+    for r in range(len(computed)):
+        first = 0 if slots is None else int(slots[r][0])
+        inside = 0 <= first < nb
+        stamp = int(float(stamps[first])) if inside else 0
+        off = int(computed[r]) - stamp
+        bad = (not inside) or (first != 0 and (off < 0 or off > num_spec))
+        if counts is not None and inside and first != 0 and int(counts[r]) != off + 1:
+            bad = True
+        faults += int(bad)
+        acc.append(min(max(off, 0), num_spec) + 1)
+    return acc, faults
+
+
+def record_stamps_ref(stamps, slots, qsl, computed, width, out_col=None, prefill_blocks=(),
+                      seq_lens=()):
+    """Stamps after a step (mixers.py:1049-1074), as a new list: decode
+    request r (query length qsl[r+1] - qsl[r], computed n tokens) stamps
+    block slots[r][out_col[r] + p] with n + p + 1 for p < min(width, query
+    length); prefill block j gets seq_lens[j].  The null block (0), slots
+    outside the pool and columns past the slot row are left alone (the
+    reference also writes the null block, whose stamp nothing reads).
+    `slots` None writes no decode stamp (all requests on the null block)."""
+    out = [float(v) for v in stamps]
+    nb = len(out)
+
+    def put(block, value):
+        if 0 < block < nb:
+            out[block] = float(value)
+
+    if slots is not None:
+        for r in range(len(qsl) - 1):
+            qlen = int(qsl[r + 1]) - int(qsl[r])
+            for p in range(min(width, qlen)):
+                col = (0 if out_col is None else int(out_col[r])) + p
+                if 0 <= col < len(slots[r]):
+                    put(int(slots[r][col]), int(computed[r]) + p + 1)
+    for b, n in zip(prefill_blocks, seq_lens):
+        put(int(b), int(n))
+    return out
 
 
 # ------------------------------------------------------------ speculative verify

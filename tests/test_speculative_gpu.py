@@ -12,6 +12,11 @@
   whose live snapshots the mixer must find from the position stamps alone.
   Outputs within 1e-2 of the oracle's composition from the same projection
   rows; every snapshot and window of the verify rows bitwise; stamps exact.
+* The stamp kernels against `oracle.spec_accepted_ref` /
+  `oracle.record_stamps_ref` on random pools: accepted counts and fault
+  totals (null-block rows, out-of-range offsets, a slot outside the pool,
+  the engine-count cross-check) and every stamp after recording (ragged
+  query lengths, shifted windows, prefill blocks), exact.
 """
 
 import itertools
@@ -24,6 +29,7 @@ from evo2_flash_amd.config import HyenaConfig
 from evo2_flash_amd.metadata import HyenaMamba2Metadata
 from evo2_flash_amd.mixers import load_mixer_params, make_mixer, set_forward_context
 from evo2_flash_amd.short_conv import causal_conv1d_update
+from evo2_flash_amd.speculative import record_stamps, spec_accepted
 from evo2_flash_amd.state import HyenaStatePool
 from evo2_flash_amd.synthetic import mixer_params
 from evo2_flash_amd.verify import iir_snapshots
@@ -247,3 +253,52 @@ def test_speculative_mixer_steps_vs_oracle(kind):
     assert max_rel_err(out, ref) <= 1e-2
     _check_verify_blocks(kind, prm, gp, before, qlens, computed)
     assert mixer.stamp_faults() == 0
+
+
+@pytest.mark.parametrize("seed,with_counts,shifted", [(0, False, False), (1, True, False),
+                                                      (2, False, True)])
+def test_stamp_kernels_vs_oracle(seed, with_counts, shifted):
+    g = torch.Generator().manual_seed(seed)
+    nblk, nreq, ncols, nspec = 300, 37, 6 if shifted else 4, 3
+    pool = HyenaStatePool(nblk, 64, DEV, num_spec=nspec)
+    stamps = pool.stamps()
+    base = torch.randint(0, 5000, (nblk,), generator=g).float()
+    stamps.copy_(base.to(DEV))
+    perm = (torch.randperm(nblk - 1, generator=g)[: nreq * ncols] + 1).view(nreq, ncols)
+    slots = perm.to(torch.int32)
+    slots[3] = 0                                   # a padded request on the null block
+    slots[5, 0] = nblk + 7                         # a slot outside the pool
+    first = slots[:, 0].long().clamp(0, nblk - 1)
+    off = torch.randint(-2, nspec + 3, (nreq,), generator=g)   # some outside [0, nspec]
+    computed = (base[first].long() + off).clamp_min(0).to(torch.int32)
+    counts = None
+    if with_counts:
+        counts = (off.clamp(0, nspec) + 1).to(torch.int32)
+        counts[::4] += 1                           # disagree on every fourth request
+    faults = torch.zeros((), dtype=torch.int64, device=DEV)
+    print(f"stamp kernels seed={seed} counts={with_counts} shifted={shifted}", flush=True)
+    acc = spec_accepted(stamps, slots.to(DEV), computed.to(DEV), nspec, faults,
+                        None if counts is None else counts.to(DEV))
+    ref_acc, ref_faults = oracle.spec_accepted_ref(base.tolist(), slots.tolist(),
+                                                   computed.tolist(), nspec,
+                                                   None if counts is None else counts.tolist())
+    assert acc.cpu().tolist() == ref_acc
+    assert int(faults) == ref_faults and ref_faults > 0
+
+    qlens = torch.randint(0, nspec + 3, (nreq,), generator=g)
+    qsl = torch.cat([torch.zeros(1, dtype=torch.long), qlens.cumsum(0)]).to(torch.int32)
+    out_col = torch.randint(0, ncols - nspec, (nreq,), generator=g).to(torch.int32) \
+        if shifted else None
+    width = 1 + nspec
+    # prefill blocks are never decode slots of the same step
+    free = sorted(set(range(1, nblk)) - set(slots.view(-1).tolist()))
+    pf_blocks = torch.tensor([0, free[0], free[-1]], dtype=torch.int32)
+    pf_lens = torch.tensor([11, 2222, 4096], dtype=torch.int32)
+    before = stamps.cpu().tolist()
+    record_stamps(stamps, slots.to(DEV), qsl.to(DEV), computed.to(DEV), width,
+                  None if out_col is None else out_col.to(DEV), pf_blocks.to(DEV),
+                  pf_lens.to(DEV))
+    ref = oracle.record_stamps_ref(before, slots.tolist(), qsl.tolist(), computed.tolist(),
+                                   width, None if out_col is None else out_col.tolist(),
+                                   pf_blocks.tolist(), pf_lens.tolist())
+    assert stamps.cpu().tolist() == ref

@@ -141,39 +141,55 @@ def _spec_meta(slots, qlens, computed, prefill=None, seq_lens=None):
     return m
 
 
-@pytest.mark.parametrize("kind", ["hcs", "hcl"])
-def test_stamps_record_and_resolve(kind):
-    """A verify step from n tokens stamps column p with n + p + 1 (only the
-    columns its rows reach) and prefill blocks with their lengths; the next
-    step, having computed n + a tokens, resolves accepted = a."""
-    mixer, pool = _mixer(kind)
-    st = pool.stamps()
+def test_stamps_record_and_resolve():
+    """The oracle's stamp rules on a hand-checked step: a verify step from n
+    tokens stamps column p with n + p + 1 (only the columns its rows reach)
+    and prefill blocks with their lengths; the next step, having computed
+    n + a tokens, resolves accepted = a (mixers.py:960-999, 1049-1074)."""
+    st = [0.0] * 12
     slots = [[1, 2, 3, 4], [5, 6, 7, 8]]
-    m = _spec_meta(slots, [4, 2], [10, 30], prefill=([7], [9]), seq_lens=[14, 32, 7])
     st[1], st[5] = 10, 30                       # live snapshots of the previous step
-    acc = mixer._resolve_accepted(m)
-    assert acc.tolist() == [1, 1] and mixer.stamp_faults() == 0
-    mixer._record_stamps(m)
-    assert st[1:5].tolist() == [11, 12, 13, 14]
-    assert st[5:7].tolist() == [31, 32] and st[7:9].tolist() == [0, 0]
+    acc, faults = oracle.spec_accepted_ref(st, slots, [10, 30], 3)
+    assert acc == [1, 1] and faults == 0
+    st = oracle.record_stamps_ref(st, slots, [0, 4, 6], [10, 30], 4,
+                                  prefill_blocks=[9], seq_lens=[7])
+    assert st[1:5] == [11, 12, 13, 14]
+    assert st[5:7] == [31, 32] and st[7:9] == [0, 0]
     assert st[9] == 7
     # next step: request 0 accepted 3 of its 4 rows, request 1 both of its 2
-    m2 = _spec_meta(slots, [1, 3], [13, 32])
-    assert mixer._resolve_accepted(m2).tolist() == [3, 2]
-    assert mixer.stamp_faults() == 0
+    assert oracle.spec_accepted_ref(st, slots, [13, 32], 3) == ([3, 2], 0)
+    # a window that starts at column 2 (prefix caching's block pointer)
+    st2 = oracle.record_stamps_ref([0.0] * 12, [[1, 2, 3, 4, 5, 6]], [0, 3], [50], 4,
+                                   out_col=[2])
+    assert st2[3:6] == [51, 52, 53] and st2[1:3] == [0, 0] and st2[6] == 0
+    # the null block, slots outside the pool and columns past the row are not written
+    st3 = oracle.record_stamps_ref([5.0] * 4, [[0, 9, 2]], [0, 4], [1], 4, out_col=[0])
+    assert st3 == [5.0, 5.0, 4.0, 5.0]
 
 
 def test_stamp_mismatch_is_counted_and_clamped():
-    mixer, pool = _mixer("hcm")
-    st = pool.stamps()
+    st = [0.0] * 12
     st[1], st[5] = 10, 30
-    m = _spec_meta([[1, 2, 3, 4], [5, 6, 7, 8]], [1, 1], [9, 40])   # -1 and +10: both bad
-    assert mixer._resolve_accepted(m).tolist() == [1, 4]
-    assert mixer.stamp_faults() == 2
-    # requests on the null block are exempt
-    m0 = _spec_meta([[0, 0, 0, 0]], [1], [123])
-    mixer._resolve_accepted(m0)
-    assert mixer.stamp_faults() == 2
+    acc, faults = oracle.spec_accepted_ref(st, [[1, 2, 3, 4], [5, 6, 7, 8]], [9, 40], 3)
+    assert acc == [1, 4] and faults == 2        # -1 and +10: both bad
+    # requests on the null block are exempt; a slot outside the pool is a fault
+    assert oracle.spec_accepted_ref(st, [[0, 0, 0, 0]], [123], 3)[1] == 0
+    assert oracle.spec_accepted_ref(st, [[12, 0, 0, 0]], [0], 3)[1] == 1
+    assert oracle.spec_accepted_ref(st, None, [123], 3)[1] == 0
+    # the engine's counts cross-check
+    assert oracle.spec_accepted_ref(st, [[1, 2, 3, 4]], [12], 3, counts=[3]) == ([3], 0)
+    assert oracle.spec_accepted_ref(st, [[1, 2, 3, 4]], [12], 3, counts=[2]) == ([3], 1)
+
+
+@pytest.mark.parametrize("kind", ["hcs", "hcl"])
+def test_stamp_kernels_refuse_cpu_tensors(kind):
+    """The mixers resolve and record stamps with HIP kernels only."""
+    mixer, pool = _mixer(kind)
+    m = _spec_meta([[1, 2, 3, 4], [5, 6, 7, 8]], [4, 2], [10, 30], seq_lens=[14, 32])
+    with pytest.raises(RuntimeError, match="GPU only"):
+        mixer._resolve_accepted(m)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        mixer._record_stamps(m)
 
 
 def test_resolve_needs_computed_counts():
