@@ -1,6 +1,8 @@
 // Varlen Hyena FIR prefill for gfx950: hcs (K=7) and hcm (K=128).
 //
-// Two forms share one kernel template:
+// The fused hcm core over tiles of 256 rows or more runs on the matrix cores
+// (fir128_mfma_kernel, below); everything else uses the VALU kernel here.
+// Two forms share the VALU kernel template:
 //  * FUSED: the mixer's whole prefill core between in_proj and out_proj:
 //    z (T, 3H) -> short K=3 filter -> u = x1*v -> FIR(u) [+ D*u] -> g = x2*y.
 //  * U_IN: the reference's `fir_prefill` (triton_prefill.py:462-496): the
@@ -470,6 +472,348 @@ __global__ __launch_bounds__(FirGeom<K>::NT, FirGeom<K>::MIN_WAVES) void fir_pre
 }
 
 // ---------------------------------------------------------------------------
+// hcm (K = 128) fused prefill on the matrix cores.  Per channel the FIR is a
+// Toeplitz product: for 16 output rows T + i (i < 16) and the 160-row window
+// W[j] = u[T - 144 + j],
+//
+//   y[T + i] = sum_j A[i][j] W[j],   A[i][j] = w[j - i - 17] (0 outside 0..127),
+//
+// so 16 blocks of 16 rows, T = s0 + 16 n, are one v_mfma_f32_16x16x32_bf16
+// chain of five k-steps: A (16 x 160, the channel's taps) times B (160 x 16,
+// column n = the window of block n).  A depends on the channel only, so each
+// wave builds the fragments of its four channels once per tile and keeps
+// them in registers; the B fragments are aligned 8-row slices of the
+// channel-major u ring.  u and the taps are bf16, so every product is exact
+// and only the fp32 summation order differs from a per-tap loop.
+//
+// A workgroup owns 16 channels and one tile of rows, swept in 256-row
+// sub-tiles:
+//   produce:  thread (channel tid % 16, 16 rows) turns staged z rows into u
+//             (to the ring) and x2 (kept in registers), as the dot2 kernel;
+//   MFMA:     wave w runs the chains of channels 4w..4w+3 and writes bf16(y)
+//             to a channel-major buffer;
+//   epilogue: the thread that produced a row finishes it: [+ D*u] then * x2.
+// The ring keeps 144 rows of history (the oldest row a window reaches).
+// Workgroup order: the four 16-channel groups of a 64-channel block are
+// workgroups b, b + 8, b + 16, b + 24, which run on one XCD back to back, so
+// the 384-byte z row slice of the block is fetched into that XCD's L2 once.
+namespace mfir {
+constexpr int CH = 16;             // channels per workgroup
+constexpr int NWAVE = 4;
+constexpr int CPW = CH / NWAVE;    // channels per wave in the MFMA phase
+constexpr int RS = 256;            // rows per sub-tile
+constexpr int HIST = 144;          // history rows a sub-tile's windows reach
+constexpr int RING = 512;          // ring rows per channel (power of two >= HIST + RS)
+constexpr int KS = 5;              // MFMA k-steps (160-row window)
+constexpr int ZW = 3 * CH;         // staged bf16 per z row
+constexpr int ZROWS = RS + 2;      // staged z rows (sub-tile + short-filter halo)
+constexpr int TAPW = 176;          // zero-padded taps per channel for the A build
+static_assert(HIST + RS <= RING && HIST % 16 == 0, "ring geometry");
+static_assert(CH * TAPW <= ZROWS * ZW, "the tap table borrows the z staging buffer");
+}  // namespace mfir
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
+typedef __attribute__((ext_vector_type(4))) float f32x4_t;
+typedef __attribute__((ext_vector_type(4))) int i32x4_t;
+
+template <bool HAS_D>
+__global__ __launch_bounds__(256, 2) void fir128_mfma_kernel(FirArgs p, int64_t ntiles, int64_t units) {
+  using namespace mfir;
+  // channel rows padded by 8 bf16 (16 bytes): consecutive channels start 4
+  // banks apart, so the 16 channels a b128 access touches spread over all 64
+  __shared__ __align__(16) bf16_t ring[CH][RING + 8];
+  __shared__ __align__(16) bf16_t zst[ZROWS * ZW];
+  __shared__ __align__(16) bf16_t ybuf[CH][RS + 8];
+
+  // ---- workgroup -> (tile, 16-channel group)
+  const int L = blockIdx.x;
+  const int jslot = L >> 3;
+  const int64_t unit = (static_cast<int64_t>(jslot >> 2) << 3) + (L & 7);
+  if (unit >= units) return;  // uniform: padding of the grid to whole XCD rounds
+  const int tile = static_cast<int>(unit % ntiles);
+  const int c0 = static_cast<int>(unit / ntiles) * 64 + (jslot & 3) * CH;
+  if (c0 >= p.H) return;  // uniform
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // produce / epilogue role: channel pc, rows 16 prg .. 16 prg + 15 of a sub-tile
+  const int pc = tid & (CH - 1);
+  const int prg = tid >> 4;
+  const int c = c0 + pc;
+  const bool active = c < p.H;
+  const int cl = active ? c : p.H - 1;
+
+  SegInfo S;
+  {
+    const int seg = p.tiles[2 * tile];
+    S.t0 = p.tiles[2 * tile + 1];
+    S.a = p.seq[3 * seg];
+    S.e = p.seq[3 * seg + 1];
+    S.blk = p.blocks[seg * p.sblk];
+    S.init = p.seq[3 * seg + 2] != 0 && S.blk >= 0 && S.blk < p.num_blocks;
+    S.t_end = min(S.t0 + p.block_t, S.e);
+  }
+  if (S.t0 >= S.t_end) return;  // uniform
+
+  // ---- A fragments: lane (i = lane % 16, kg = lane / 16), k-step s, element
+  // e holds A[i][32 s + 8 kg + e] = w[32 s + 8 kg + e - i - 17], read from a
+  // zero-padded copy of the taps (tp[ch][x] = w[x - 32]) staged in zst.
+  bf16x8_t A[CPW][KS];
+  {
+    bf16_t *tp = zst;
+    for (int i = tid; i < CH * TAPW; i += 256) {
+      const int ch = i / TAPW, k = i - ch * TAPW - 32;
+      bf16_t v = 0;
+      if (k >= 0 && k < 128 && c0 + ch < p.H) v = p.w[(int64_t)(c0 + ch) * p.w0 + k];
+      tp[i] = v;
+    }
+    __syncthreads();
+    const int ai = lane & 15, kg = lane >> 4;
+#pragma unroll
+    for (int cc = 0; cc < CPW; ++cc)
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          A[cc][s][e] = __builtin_bit_cast(__bf16, tp[(wave * CPW + cc) * TAPW + 32 * s + 8 * kg + e - ai + 15]);
+    __syncthreads();  // zst is the z staging buffer from here on
+  }
+
+  ShortTaps wsp[3];
+#pragma unroll
+  for (int i = 0; i < 3; ++i) wsp[i] = short_taps(p.ws, 3 * (int64_t)cl + i);
+  const float *stc = S.init ? p.st + S.blk * p.st0 + (int64_t)cl * p.st1 : nullptr;
+  float dval = 0.0f;
+  if constexpr (HAS_D) dval = bf2f(p.D[cl]);
+  const bool vec_z = (c0 + CH <= p.H) && (p.sx % 8 == 0) &&
+                     ((reinterpret_cast<uintptr_t>(p.x) & 15) == 0) &&
+                     p.sx * ZROWS < (int64_t(1) << 30);  // 32-bit lane byte offsets
+
+  // ---- z rows [rs, rs + nrows) of the 48 sub-channels into zst (row pitch
+  // 48 bf16 = 6 chunks of 16 bytes) with direct-to-LDS loads; rows outside
+  // [a, t_end) are skipped.  `fix` (after the loads landed) writes the rows
+  // a - 2 and a - 1 from the conv window (zero without one) and, when z is not
+  // 16-byte addressable, every staged row element by element.
+  auto prefetch = [&](int rs, int nrows) {
+    if (!vec_z) return;
+    const char *base = reinterpret_cast<const char *>(p.x + (int64_t)rs * p.sx + 3 * c0);
+    const int nch = nrows * 6;
+    const bool interior = rs >= S.a && rs + nrows <= S.t_end;  // uniform
+    for (int j = 0;; ++j) {
+      const int cw = wave + NWAVE * j;  // wave-uniform
+      if (cw * 64 >= nch) break;
+      const int i = cw * 64 + lane;
+      const int row = i / 6;
+      bool ok = i < nch;
+      if (!interior) ok = ok && rs + row >= S.a && rs + row < S.t_end;
+      const uint32_t off = 2u * static_cast<uint32_t>(row * static_cast<int>(p.sx) + 8 * (i - 6 * row));
+      if (ok)
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint4 *>(base + off),
+                                         (__attribute__((address_space(3))) void *)(zst + cw * 512),
+                                         16, 0, 0);
+    }
+  };
+  auto fix = [&](int rs, int nrows) {
+    const bf16_t *conv = S.init ? p.cs + S.blk * p.cs0 : nullptr;
+    if (vec_z && rs >= S.a) return;  // uniform: nothing to patch
+    for (int i = tid; i < nrows * ZW; i += 256) {
+      const int row = i / ZW, col = i - ZW * row;
+      const int t = rs + row;
+      const bool inside = t >= S.a && t < S.t_end;
+      const bool left = t < S.a && t >= S.a - 2;
+      if ((vec_z && inside) || !(inside || left)) continue;
+      const int ch = 3 * c0 + col;
+      bf16_t b = 0;
+      if (ch < 3 * p.H) {
+        if (inside) b = p.x[(int64_t)t * p.sx + ch];
+        else if (conv) b = conv[ch * p.cs1 + (t - S.a + 2) * p.cs2];
+      }
+      zst[i] = b;
+    }
+  };
+  auto land = [&]() { __builtin_amdgcn_s_waitcnt(0); };
+  auto ring_pos = [&](int t) { return (t - S.t0 + HIST) & (RING - 1); };
+  // output rows of this tile through a buffer descriptor that ends at the
+  // tile's last row (16-byte stores of whole 16-channel groups)
+  const bool vec_out = (c0 + CH <= p.H) && (p.so % 8 == 0) &&
+                       ((reinterpret_cast<uintptr_t>(p.out) & 15) == 0) &&
+                       (int64_t)(S.t_end - S.t0) * p.so * 2 < (int64_t(1) << 31);
+  const __amdgpu_buffer_rsrc_t ores = __builtin_amdgcn_make_buffer_rsrc(
+      p.out + (int64_t)S.t0 * p.so + c0, 0,
+      vec_out ? static_cast<int>((int64_t)(S.t_end - S.t0) * p.so * 2) : 0, 0x00020000);
+
+  // ---- u and x2 of this thread's 16 rows r0 .. r0 + 15 (z row t staged at
+  // t - rs); u goes to the ring as two b128 stores, x2 to xq as row pairs.
+  auto produce16 = [&](int r0, int rs, uint32_t (&xq)[8]) {
+    uint32_t upk[8];
+    if (r0 >= S.a && r0 + 16 <= S.t_end) {  // interior rows: pairs through v_dot2
+#pragma unroll
+      for (int g = 0; g < 2; ++g) {
+        const int sb = r0 - rs - 2 + 8 * g;  // staged row of z[r0 + 8 g - 2]
+        uint32_t P[9][3];
+#pragma unroll
+        for (int k = 0; k < 9; ++k)
+#pragma unroll
+          for (int i = 0; i < 3; ++i)
+            P[k][i] = pair_bf(zst[(sb + k) * ZW + 3 * pc + i], zst[(sb + k + 1) * ZW + 3 * pc + i]);
+#pragma unroll
+        for (int r = 0; r < 8; r += 2) {
+          float y0[3], y1[3];
+          short_rows2(P[r], P[r + 1], P[r + 2], wsp, y0, y1);
+          upk[4 * g + r / 2] = pack_bf(y0[1] * y0[2], y1[1] * y1[2]);
+          xq[4 * g + r / 2] = pack_bf(y0[0], y1[0]);
+        }
+      }
+    } else {  // rows at a segment start or past the tile end, one at a time
+#pragma unroll
+      for (int q = 0; q < 8; ++q) upk[q] = xq[q] = 0u;
+#pragma unroll 1
+      for (int r = 0; r < 16; ++r) {
+        const int t = r0 + r;
+        float u = 0.0f, x2 = 0.0f;
+        if (t < S.a) {
+          const int col = 127 + (t - S.a);
+          if (stc && col >= 0) u = stc[(int64_t)col * p.st2];
+        } else if (t < S.t_end) {
+          float y3[3];
+          const int sr = t - rs;
+          for (int i = 0; i < 3; ++i)
+            y3[i] = short_dot_rbf(pair_bf(zst[(sr - 2) * ZW + 3 * pc + i], zst[(sr - 1) * ZW + 3 * pc + i]),
+                                  pair_bf(zst[(sr - 1) * ZW + 3 * pc + i], zst[sr * ZW + 3 * pc + i]),
+                                  wsp[i]);
+          x2 = y3[0];
+          u = rbf(y3[1] * y3[2]);
+        }
+        const uint32_t ub = f2bf(u), xb = f2bf(x2);
+        // row r lands in the low (even r) or high (odd r) half of pair r / 2
+        const int sh = 16 * (r & 1);
+        for (int q = 0; q < 8; ++q) {
+          if (q == r / 2) {
+            upk[q] |= ub << sh;
+            xq[q] |= xb << sh;
+          }
+        }
+      }
+    }
+    const int pos = ring_pos(r0);
+    *reinterpret_cast<uint4 *>(&ring[pc][pos]) = make_uint4(upk[0], upk[1], upk[2], upk[3]);
+    *reinterpret_cast<uint4 *>(&ring[pc][pos + 8]) = make_uint4(upk[4], upk[5], upk[6], upk[7]);
+  };
+
+  // ---- halo: rows t0 - 144 .. t0 - 1 (nine row groups)
+  {
+    const int hs = S.t0 - HIST;
+    prefetch(hs - 2, HIST + 2);
+    land();
+    fix(hs - 2, HIST + 2);
+    __syncthreads();
+    uint32_t xd[8];
+    if (prg < HIST / 16) produce16(hs + 16 * prg, hs - 2, xd);
+    __syncthreads();  // zst free
+  }
+  prefetch(S.t0 - 2, ZROWS);
+
+  const int ai = lane & 15, kg = lane >> 4;
+  for (int s0 = S.t0; s0 < S.t_end; s0 += RS) {
+    const int nz = min(RS, S.t_end - s0) + 2;  // staged rows this sub-tile uses
+    // this sub-tile's z rows: after the first sub-tile they were issued
+    // before the previous epilogue's two buffer stores per wave, which may
+    // stay in flight (loads and stores retire in order); the first sub-tile
+    // and the element-wise store path wait for everything
+    if (vec_out && s0 > S.t0) vmcnt_wait<2>();
+    else land();
+    fix(s0 - 2, nz);
+    __syncthreads();  // staged rows visible
+    uint32_t xq[8];
+    produce16(s0 + 16 * prg, s0 - 2, xq);
+    __syncthreads();  // ring complete; zst free
+    if (s0 + RS < S.t_end) prefetch(s0 + RS - 2, min(RS, S.t_end - s0 - RS) + 2);
+
+    // ---- MFMA: column block n = lane % 16 reads rows s0 + 16 n - 144 + 32 s
+    // + 8 kg .. + 7, an aligned 8-row slice of the ring
+    f32x4_t acc[CPW];
+#pragma unroll
+    for (int cc = 0; cc < CPW; ++cc) acc[cc] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    const int bpos = (s0 - S.t0) + 16 * ai + 8 * kg;  // ring position of the step-0 slice
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      bf16x8_t B[CPW];
+#pragma unroll
+      for (int cc = 0; cc < CPW; ++cc)
+        B[cc] = *reinterpret_cast<const bf16x8_t *>(&ring[wave * CPW + cc][(bpos + 32 * s) & (RING - 1)]);
+#pragma unroll
+      for (int cc = 0; cc < CPW; ++cc)
+        acc[cc] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[cc][s], B[cc], acc[cc], 0, 0, 0);
+    }
+    // lane holds y[s0 + 16 n + 4 kg + e], e < 4, of each channel
+#pragma unroll
+    for (int cc = 0; cc < CPW; ++cc) {
+      const uint32_t lo = pack_bf(acc[cc][0], acc[cc][1]), hi = pack_bf(acc[cc][2], acc[cc][3]);
+      *reinterpret_cast<uint2 *>(&ybuf[wave * CPW + cc][16 * ai + 4 * kg]) = make_uint2(lo, hi);
+    }
+    __syncthreads();  // ybuf complete
+
+    // ---- epilogue: bf16(y) [+ D*u] then * x2 for rows s0 + 16 prg + r
+    const int r0 = s0 + 16 * prg;
+    const uint4 y4a = *reinterpret_cast<const uint4 *>(&ybuf[pc][16 * prg]);
+    const uint4 y4b = *reinterpret_cast<const uint4 *>(&ybuf[pc][16 * prg + 8]);
+    const uint32_t yq[8] = {y4a.x, y4a.y, y4a.z, y4a.w, y4b.x, y4b.y, y4b.z, y4b.w};
+    uint32_t uq[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+    if constexpr (HAS_D) {
+      const int pos = ring_pos(r0);
+      const uint4 u4a = *reinterpret_cast<const uint4 *>(&ring[pc][pos]);
+      const uint4 u4b = *reinterpret_cast<const uint4 *>(&ring[pc][pos + 8]);
+      uq[0] = u4a.x; uq[1] = u4a.y; uq[2] = u4a.z; uq[3] = u4a.w;
+      uq[4] = u4b.x; uq[5] = u4b.y; uq[6] = u4b.z; uq[7] = u4b.w;
+    }
+    uint32_t gq[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      float y0 = lo_bf(yq[q]), y1 = hi_bf(yq[q]);
+      if constexpr (HAS_D) {
+        y0 = rbf_valu(y0 + rbf_valu(dval * lo_bf(uq[q])));
+        y1 = rbf_valu(y1 + rbf_valu(dval * hi_bf(uq[q])));
+      }
+      gq[q] = pack_bf(lo_bf(xq[q]) * y0, hi_bf(xq[q]) * y1);
+    }
+    // g goes out through LDS as row-major 16-byte chunks (8 channels of a
+    // row): gbuf (RS rows x CH channels) reuses ybuf once every thread has
+    // read its y rows
+    __syncthreads();
+    bf16_t *gbuf = &ybuf[0][0];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      gbuf[(16 * prg + 2 * q) * CH + pc] = static_cast<bf16_t>(gq[q] & 0xffffu);
+      gbuf[(16 * prg + 2 * q + 1) * CH + pc] = static_cast<bf16_t>(gq[q] >> 16);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int qi = tid + 256 * k, row = qi >> 1, half = qi & 1;
+      const uint4 v = *reinterpret_cast<const uint4 *>(&gbuf[row * CH + 8 * half]);
+      if (vec_out) {
+        // rows past the tile end fall outside the descriptor and are dropped
+        __builtin_amdgcn_raw_buffer_store_b128(
+            __builtin_bit_cast(i32x4_t, v), ores,
+            ((s0 - S.t0 + row) * static_cast<int>(p.so) + 8 * half) * 2, 0, 0);
+      } else {
+        const int t = s0 + row;
+        const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+        for (int e = 0; e < 8; ++e) {
+          const int ce = c0 + 8 * half + e;
+          if (t < S.t_end && ce < p.H)
+            p.out[(int64_t)t * p.so + ce] = static_cast<bf16_t>(w4[e >> 1] >> (16 * (e & 1)));
+        }
+      }
+    }
+    // the next produce overwrites ring rows this sub-tile's windows read
+    // (all done: the barrier before the epilogue follows every wave's MFMAs)
+    // and rows disjoint from those the epilogue reads; gbuf is read before
+    // the next produce's barrier, after which the MFMAs rewrite it as ybuf
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Window update after a prefill launch: per segment and channel, the new
 // windows are the last inputs of cat(old window, segment) (mixers.py:380-382),
 // oldest first.  The update is in place, and for a segment shorter than the
@@ -675,8 +1019,22 @@ extern "C" int evo2_hyena_fir_prefill(const void *z, int64_t sz, const void *sho
     return fail(EVO2_ERR_UNSUPPORTED, "hyena_fir_prefill: K=128 taps must be contiguous (H, 128) rows");
   if (ntiles) {
     const bool hasD = D != nullptr;
-    if (K == 128) hasD ? launch_fir<128, true, true>(a, ntiles, st) : launch_fir<128, false, true>(a, ntiles, st);
-    else hasD ? launch_fir<7, true, true>(a, ntiles, st) : launch_fir<7, false, true>(a, ntiles, st);
+    if (K == 128 && block_t >= mfir::RS) {
+      // the matrix-core kernel once a tile holds a whole 256-row sub-tile
+      const int64_t units = ntiles * cdiv(H, 64);
+      const int64_t nwg = 4 * cdiv(units, 8) * 8;
+      if (nwg > 0x7fffffff) return fail(EVO2_ERR_UNSUPPORTED, "hyena_fir_prefill: grid too large");
+      if (hasD)
+        hipLaunchKernelGGL(fir128_mfma_kernel<true>, dim3(static_cast<unsigned>(nwg)), dim3(256), 0, st, a,
+                           ntiles, units);
+      else
+        hipLaunchKernelGGL(fir128_mfma_kernel<false>, dim3(static_cast<unsigned>(nwg)), dim3(256), 0, st, a,
+                           ntiles, units);
+    } else if (K == 128) {
+      hasD ? launch_fir<128, true, true>(a, ntiles, st) : launch_fir<128, false, true>(a, ntiles, st);
+    } else {
+      hasD ? launch_fir<7, true, true>(a, ntiles, st) : launch_fir<7, false, true>(a, ntiles, st);
+    }
     rc = check_launch("hyena_fir_prefill");
     if (rc) return rc;
   }

@@ -10,10 +10,15 @@ import torch
 
 from . import _lib
 
-# Rows per tile.  A tile is swept in 64-row sub-tiles with the FIR history in
-# LDS, so longer tiles amortise the (K-1)-row halo; shorter ones add
-# parallelism when there are few tokens.
-_MAX_BLOCK_T = {7: 1024, 128: 2048}
+# Rows per tile.  A tile is swept in sub-tiles with the FIR history in LDS,
+# so longer tiles amortise the (K-1)-row halo; shorter ones add parallelism
+# when there are few tokens.  The fused K=128 core runs on the matrix cores
+# once a tile holds a 256-row sub-tile, with four 16-channel workgroups per
+# 64-channel block: at 7B/32k on one MI355X 466 us with 4096-row tiles,
+# 477 with 2048, 494 with 1024, 564 with 512, 532 with 8192 (too few
+# workgroups).
+_MAX_BLOCK_T = {7: 1024, 128: 4096}
+_MFMA_MIN_BLOCK_T = 256
 _TARGET_WORKGROUPS = 2048
 # Long filters: below 256 rows the 127-row halo is a third or more of a
 # tile's reads, and on one MI355X 256-row tiles beat 64-row ones by 10-22%
@@ -26,14 +31,16 @@ _LONG_FILTER_MIN_WORKGROUPS = 128
 def fir_prefill_block_t(k, num_tokens=None, hidden=None):
     """Rows per prefill tile for filter length k; the tile table is built for
     this value.  With `num_tokens` and `hidden` it shrinks (to a multiple of
-    64) until the launch has enough workgroups to fill the GPU; for filters
-    longer than 8 taps it stops at 256 rows once the launch has 128
-    workgroups."""
+    64) until the launch has enough workgroups to fill the GPU (counting the
+    fused K=128 core's four 16-channel workgroups per 64-channel block at
+    tiles of 256 rows or more); for filters longer than 8 taps it stops at
+    256 rows once the launch has 128 workgroups."""
     bt = _MAX_BLOCK_T.get(int(k), 1024)
     if num_tokens is not None and hidden is not None:
         cblocks = max(1, (int(hidden) + 63) // 64)
         while bt > 64:
-            nwg = ((int(num_tokens) + bt - 1) // bt) * cblocks
+            groups = cblocks * (4 if int(k) > 8 and bt >= _MFMA_MIN_BLOCK_T else 1)
+            nwg = ((int(num_tokens) + bt - 1) // bt) * groups
             if nwg >= _TARGET_WORKGROUPS:
                 break
             if (int(k) > 8 and bt <= _LONG_FILTER_MIN_BLOCK_T

@@ -8,7 +8,11 @@
 * state windows: copies of inputs, so bit-exact where the inputs are given
   (conv window, fir_prefill window);
 * chunked prefill: prefill(L) equals prefill(a) + prefill(L-a) continued,
-  bit for bit (outputs and windows);
+  bit for bit (outputs and windows) on the VALU kernels; on the hcm
+  matrix-core kernel outputs agree within 1e-2 (the MFMA's K-sum order
+  depends on where a row's 16-row block starts) and windows bitwise;
+* the hcm matrix-core kernel over multi-sub-tile, short, empty and
+  continuing segments and a part-filled 16-channel group;
 * decode after prefill(L) matches the last row of prefill(L+1).
 """
 
@@ -136,6 +140,55 @@ def test_fused_split_invariance(kind, split):
     yb = _run_fused(prm, K, z[split:], slots, gp2, seqb, tilb, bt, H)
     torch.cuda.synchronize()
     assert torch.equal(y1.view(torch.int16), torch.cat([ya, yb]).view(torch.int16))
+    assert torch.equal(gp1.raw, gp2.raw)
+
+
+# The hcm fused core on the matrix cores (tiles of >= 256 rows): segments of
+# several 256-row sub-tiles, shorter than the 144-row history, empty, and
+# continuing from a window; H = 200 leaves a last 16-channel group half full.
+MFMA_CASES = [
+    (256, [700, 5, 0, 300, 1, 290], [0, 1, 0, 1, 1, 0], 256),
+    (256, [1100, 130], [1, 0], 512),
+    (200, [513, 40], [1, 1], 256),
+]
+
+
+@pytest.mark.parametrize("H,lens,has_init,block_t", MFMA_CASES)
+def test_fused_hcm_mfma_vs_oracle(H, lens, has_init, block_t):
+    nblk = len(lens) + 3
+    prm, K, z, slots, pool = _fused_case("hcm", H, lens, has_init, nblk, seed=31)
+    gp = clone_pool(pool, DEV)
+    qsl, seq_t, tiles_t = _tables(lens, has_init, block_t)
+    print(f"fused hcm (matrix cores) H={H} lens={lens} block_t={block_t}", flush=True)
+    gout = _run_fused(prm, K, z, slots, gp, seq_t, tiles_t, block_t, H).cpu()
+    ref = oracle.fir_mixer_prefill(z, prm["short_filter"].view(3 * H, 3), pool.conv_view(),
+                                   prm["conv"].view(H, K), pool.inner_view(K - 1), prm.get("D"),
+                                   qsl, slots, has_init)
+    assert max_rel_err(gout, ref) <= 1e-2
+    assert torch.equal(gp.kv_cache[0].cpu(), pool.kv_cache[0])
+    assert max_rel_err(gp.kv_cache[1].cpu(), pool.kv_cache[1]) <= 1e-2
+    assert torch.equal(gp.kv_cache[2].cpu(), pool.kv_cache[2])
+
+
+@pytest.mark.parametrize("split", [1, 100, 257, 700])
+def test_fused_hcm_mfma_split(split):
+    """Chunked prefill on the matrix-core path: one 1100-row segment against
+    split + continuation.  An output's products sit at other positions of
+    the MFMA's K sum when its 16-row block starts elsewhere, so outputs agree
+    to rounding (1e-2) rather than bitwise; the windows are copies of u and
+    agree bitwise."""
+    H, L, nblk, bt = 128, 1100, 4, 256
+    prm, K, z, slots, pool = _fused_case("hcm", H, [L], [0], nblk, seed=19)
+    gp1 = clone_pool(pool, DEV)
+    _, seq1, til1 = _tables([L], [0], bt)
+    y1 = _run_fused(prm, K, z, slots, gp1, seq1, til1, bt, H)
+    gp2 = clone_pool(pool, DEV)
+    _, seqa, tila = _tables([split], [0], bt)
+    ya = _run_fused(prm, K, z[:split], slots, gp2, seqa, tila, bt, H)
+    _, seqb, tilb = _tables([L - split], [1], bt)
+    yb = _run_fused(prm, K, z[split:], slots, gp2, seqb, tilb, bt, H)
+    torch.cuda.synchronize()
+    assert max_rel_err(torch.cat([ya, yb]).cpu(), y1.cpu()) <= 1e-2
     assert torch.equal(gp1.raw, gp2.raw)
 
 
