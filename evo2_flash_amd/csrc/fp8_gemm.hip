@@ -467,10 +467,10 @@ __global__ __launch_bounds__(256) void fp8_gemm_persist_kernel(GemmArgs p, int t
 
 // ---------------------------------------------------------------------------
 // Decode-sized GEMMs (M <= 64 rows, e.g. the in_proj of a 64-sequence decode
-// step): the weight stream is the whole cost (N x K bytes against 64 x K of
-// activations), so the kernel is built to keep HBM busy rather than the
-// matrix pipe.  A workgroup owns 16 W rows per wave (four waves, or two
-// when N is below 8192) and all M rows;
+// step, and, over blocks of 64 rows, verify-sized ones): the weight stream is
+// the whole cost (N x K bytes against 64 x K of activations), so the kernel
+// is built to keep HBM busy rather than the matrix pipe.  A workgroup owns
+// 16 W rows per wave (two to four waves) and one block of up to 64 rows;
 // v_mfma_f32_16x16x128_f8f6f4 with the weight as operand A.  Each wave
 // streams its 16 W rows straight into VGPRs, S_DEPTH K steps (128 bytes)
 // ahead; the activation slice of every step (64 rows x 128 bytes) goes
@@ -485,6 +485,24 @@ constexpr int S_ROWS = 64;                // activation rows (max M)
 constexpr int S_DEPTH = 8;                // steps in flight
 constexpr int S_STAGE = S_ROWS * S_BK;    // 8 KB of activations per step
 typedef __attribute__((ext_vector_type(4))) float f32x4;
+
+// Workgroup -> (weight slice x, activation block y) for the weight-streaming
+// kernel, over a 1-D grid of 8 * gy * ceil(gx / 8) workgroups: workgroup b
+// runs on XCD b mod 8, so the gy blocks that read weight slice x are
+// workgroups 8 (gy (x / 8) + y) + x mod 8 -- one XCD, back to back -- and the
+// slice comes from HBM once, the other reads hitting that XCD's L2.  Padding
+// workgroups (x >= gx) return at once.
+__device__ __forceinline__ bool stream_tile(int gx, int gy, int &x, int &y) {
+  const int L = blockIdx.x;
+  const int j = L >> 3;
+  y = j % gy;
+  x = (j / gy) * 8 + (L & 7);
+  return x < gx;
+}
+
+static inline dim3 stream_grid(int64_t gx, int64_t gy) {
+  return dim3(static_cast<unsigned>(8 * gy * cdiv(gx, 8)));
+}
 
 template <int WPG>  // waves per workgroup (2, 3 or 4): 16 W rows each
 __global__ __launch_bounds__(256) void fp8_gemm_small_kernel(GemmArgs p) {
@@ -501,8 +519,11 @@ __global__ __launch_bounds__(256) void fp8_gemm_small_kernel(GemmArgs p) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int n0 = blockIdx.x * 16 * WPG;
-  const int m0 = blockIdx.y * S_ROWS;  // 64-row block of the activations
+  int bx, by;
+  if (!stream_tile((p.N + 16 * WPG - 1) / (16 * WPG), (p.M + S_ROWS - 1) / S_ROWS, bx, by))
+    return;  // uniform: grid padding
+  const int n0 = bx * 16 * WPG;
+  const int m0 = by * S_ROWS;  // 64-row block of the activations
   const int mrows = p.M - m0;          // >= 1 (the grid covers M exactly)
   const uint8_t *xbase = p.x + (int64_t)m0 * p.sx;
   const int g = lane >> 4;   // K bytes [32g, 32g + 32) of a step
@@ -635,201 +656,19 @@ __global__ __launch_bounds__(256) void fp8_gemm_small_kernel(GemmArgs p) {
 
 template <int WPG>
 static void launch_small(const GemmArgs &a, hipStream_t stream) {
-  dim3 grid(static_cast<unsigned>(cdiv(a.N, 16 * WPG)), static_cast<unsigned>(cdiv(a.M, S_ROWS)));
+  const dim3 grid = stream_grid(cdiv(a.N, 16 * WPG), cdiv(a.M, S_ROWS));
   hipLaunchKernelGGL((fp8_gemm_small_kernel<WPG>), grid, dim3(64 * WPG), 0, stream, a);
 }
 
-// ---------------------------------------------------------------------------
-// Mid-sized GEMMs (M up to a few hundred rows, e.g. a speculative verify
-// step's 64 requests x 4 positions): the decode kernel's layout -- each wave
-// streams its 16 W rows into VGPRs and runs v_mfma_f32_16x16x128_f8f6f4 with
-// the weight as operand A -- with every workgroup covering MB blocks of 64
-// activation rows, so the weight stream is read once per 64 MB rows instead
-// of once per 64.  The activation slices of a step (64 MB rows x 128 bytes)
-// go through a ring of M_DEPTH LDS stages; the weight runs W_DEPTH steps
-// ahead in registers.  Each step issues its activation loads before its
-// weight loads: loads retire in order, so the wait for an activation stage
-// never waits on the deeper weight prefetch.
-constexpr int M_DEPTH = 4;   // activation stages in LDS
-constexpr int W_DEPTH = 8;   // weight steps in registers
-
-// the weight-streaming kernels take GEMMs with ceil(M / 256) x N up to this
-// (M <= 512 at N = 12288, M <= 1024 at N = 4096); past it the 256 x 256 tiles
-#ifndef MID_MAX_WORK
-#define MID_MAX_WORK 24576
+// The weight-streaming kernel reads the weight once per 64-row block, so its
+// cost grows with ceil(M / 64) x N x K, while up to one round of 256 x 256
+// tiles costs one tile's K loop.  Measured with the weights streaming from
+// HBM (K = 4096, us, stream / tiles): M=256, N=12288 42 / 62; M=512 75 / 62;
+// M=512, N=4096 25 / 41; M=1024 48 / 43; M=256, N=24576, K=8192 138 / 115.
+// Streaming takes ceil(M / 64) x N up to this; M <= 64 always streams.
+#ifndef STREAM_MAX_WORK
+#define STREAM_MAX_WORK 60000
 #endif
-
-template <int WPG, int MB>  // waves per workgroup (16 W rows each), 64-row blocks
-__global__ __launch_bounds__(256) void fp8_gemm_mid_kernel(GemmArgs p) {
-  constexpr int ROWS = 64 * MB;
-  constexpr int STAGE = ROWS * S_BK;
-  __shared__ __align__(16) uint8_t s0[STAGE], s1[STAGE], s2[STAGE], s3[STAGE];
-  auto stage_of = [&](auto slot) __attribute__((always_inline)) -> uint8_t * {
-    constexpr int J = decltype(slot)::value % M_DEPTH;
-    static_assert(M_DEPTH == 4, "four stage variables");
-    return J == 0 ? s0 : J == 1 ? s1 : J == 2 ? s2 : s3;
-  };
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int n0 = blockIdx.x * 16 * WPG;
-  const int m0 = blockIdx.y * ROWS;
-  const int mrows = p.M - m0;  // >= 1 (the grid covers M exactly)
-  const uint8_t *xbase = p.x + (int64_t)m0 * p.sx;
-  const int g = lane >> 4;   // K bytes [32g, 32g + 32) of a step
-  const int lr = lane & 15;  // row within a 16-row tile
-  const int KT = p.K / S_BK;
-
-  // activation DMA: the NB blocks of a stage (1 KB = 8 rows each) split over
-  // the waves as block wave + WPG j, j < XB; surplus loads repeat the last
-  // block (the same bytes to the same place), so the wait counts stay uniform
-  constexpr int NB = 8 * MB;
-  constexpr int XB = (NB + WPG - 1) / WPG;
-  auto xblock = [&](int j) __attribute__((always_inline)) { return min(wave + WPG * j, NB - 1); };
-  int xoff[XB];
-#pragma unroll
-  for (int j = 0; j < XB; ++j) {
-    const int row = xblock(j) * 8 + lane / 8;
-    const int lchunk = (lane & 7) ^ ((row >> 1) & 7);
-    xoff[j] = min(row, mrows - 1) * (int)p.sx + 16 * lchunk;
-  }
-  const uint8_t *wrow = p.w + (int64_t)min(n0 + 16 * wave + lr, p.N - 1) * p.sw + 32 * g;
-  i32x8 wf[W_DEPTH];
-  auto issue_x = [&](auto slot, int k) __attribute__((always_inline)) {
-    const int k0 = min(k, KT - 1) * S_BK;
-#pragma unroll
-    for (int j = 0; j < XB; ++j)
-      __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint4 *>(xbase + k0 + xoff[j]),
-                                       (lds_void *)(stage_of(slot) + xblock(j) * 1024), 16, 0, 0);
-  };
-  auto issue_w = [&](auto slot, int k) __attribute__((always_inline)) {
-    constexpr int J = decltype(slot)::value % W_DEPTH;
-    const int k0 = min(k, KT - 1) * S_BK;
-    const uint4 a0 = *reinterpret_cast<const uint4 *>(wrow + k0);
-    const uint4 a1 = *reinterpret_cast<const uint4 *>(wrow + k0 + 16);
-    wf[J] = i32x8{(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w, (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
-  };
-  f32x4 acc[MB][4];
-#pragma unroll
-  for (int b = 0; b < MB; ++b)
-#pragma unroll
-    for (int t = 0; t < 4; ++t) acc[b][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  // activation fragments of 64-row block b of a stage (rows 64 b + 16 t + lr)
-  auto read_x = [&](auto slot, int b, i32x8 (&xf)[4]) __attribute__((always_inline)) {
-    const uint8_t *xst = stage_of(slot);
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int r = 64 * b + 16 * t + lr;
-      const int sw = (r >> 1) & 7;
-      const uint4 b0 = *reinterpret_cast<const uint4 *>(xst + r * S_BK + (((2 * g) ^ sw) << 4));
-      const uint4 b1 = *reinterpret_cast<const uint4 *>(xst + r * S_BK + (((2 * g + 1) ^ sw) << 4));
-      xf[t] = i32x8{(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w,
-                    (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
-    }
-  };
-  // Step k: block 0 of stage k is already in xa[B0].  Wait until stage k + 1
-  // has landed (in issue order only step k - 2's weight loads and step k - 1's
-  // loads may still fly: XB + 4; fewer in flight during the first two steps,
-  // where the count is conservative), then a barrier makes every wave's share
-  // visible and every wave has consumed stage k - 1, which is refilled with
-  // step k + 3.  While block b's MFMAs run, block b + 1 (or block 0 of stage
-  // k + 1) is read.
-  i32x8 xa[2][4];
-  auto step = [&](auto kslot, auto b0buf, int k) __attribute__((always_inline)) {
-    constexpr int J = decltype(kslot)::value;  // k mod W_DEPTH
-    constexpr int B0 = decltype(b0buf)::value;
-    vmcnt_wait<XB + 4>();
-    __builtin_amdgcn_s_barrier();
-    issue_x(std::integral_constant<int, (J + 3) % M_DEPTH>{}, k + 3);
-    issue_w(std::integral_constant<int, (J + 7) % W_DEPTH>{}, k + 7);
-    // a step past the end of K multiplies a zero weight fragment (its loads
-    // re-read the last slice), so every step has the same straight-line shape
-    const bool live = k < KT;  // uniform
-    i32x8 w = wf[J];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) w[e] = live ? w[e] : 0;
-#pragma unroll
-    for (int b = 0; b < MB; ++b) {
-      if (b + 1 < MB)
-        read_x(std::integral_constant<int, J % M_DEPTH>{}, b + 1, xa[(B0 + b + 1) & 1]);
-      else
-        read_x(std::integral_constant<int, (J + 1) % M_DEPTH>{}, 0, xa[(B0 + b + 1) & 1]);
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        acc[b][t] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(w, xa[(B0 + b) & 1][t],
-                                                                     acc[b][t], 0, 0, 0, 0, 0, 0);
-        asm volatile("" : "+a"(acc[b][t]));
-      }
-    }
-  };
-  using std::integral_constant;
-  issue_x(integral_constant<int, 0>{}, 0);
-  issue_w(integral_constant<int, 0>{}, 0);
-  issue_x(integral_constant<int, 1>{}, 1);
-  issue_w(integral_constant<int, 1>{}, 1);
-  issue_x(integral_constant<int, 2>{}, 2);
-  issue_w(integral_constant<int, 2>{}, 2);
-  issue_w(integral_constant<int, 3>{}, 3);
-  issue_w(integral_constant<int, 4>{}, 4);
-  issue_w(integral_constant<int, 5>{}, 5);
-  issue_w(integral_constant<int, 6>{}, 6);
-  vmcnt_wait<2 * XB + 14>();  // stage 0 landed
-  __builtin_amdgcn_s_barrier();
-  read_x(integral_constant<int, 0>{}, 0, xa[0]);
-  for (int k = 0; k < KT; k += W_DEPTH) {
-    step(integral_constant<int, 0>{}, integral_constant<int, 0>{}, k);
-    step(integral_constant<int, 1>{}, integral_constant<int, (1 * MB) & 1>{}, k + 1);
-    step(integral_constant<int, 2>{}, integral_constant<int, (2 * MB) & 1>{}, k + 2);
-    step(integral_constant<int, 3>{}, integral_constant<int, (3 * MB) & 1>{}, k + 3);
-    step(integral_constant<int, 4>{}, integral_constant<int, (4 * MB) & 1>{}, k + 4);
-    step(integral_constant<int, 5>{}, integral_constant<int, (5 * MB) & 1>{}, k + 5);
-    step(integral_constant<int, 6>{}, integral_constant<int, (6 * MB) & 1>{}, k + 6);
-    step(integral_constant<int, 7>{}, integral_constant<int, (7 * MB) & 1>{}, k + 7);
-  }
-  vmcnt_wait<0>();  // no DMA may still target this workgroup's LDS
-
-  // lane holds out[m = 64 b + 16 t + lr][n = n0 + 16 wave + 4 g + i] in acc[b][t][i]
-  const float scale = p.sx_scale[0] * p.sw_scale[0];
-  const int n = n0 + 16 * wave + 4 * g;
-  float bias[4] = {0.f, 0.f, 0.f, 0.f};
-  if (p.bias) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) bias[i] = bf2f(p.bias[min(n + i, p.N - 1)]);
-  }
-#pragma unroll
-  for (int b = 0; b < MB; ++b) {
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int m = 64 * b + 16 * t + lr;
-      if (m >= mrows) continue;
-      bf16_t *o = p.out + (int64_t)(m0 + m) * p.so + n;
-      float v[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) v[i] = acc[b][t][i] * scale + bias[i];
-      if (n + 4 <= p.N && (reinterpret_cast<uintptr_t>(o) & 7) == 0) {
-        *reinterpret_cast<uint2 *>(o) = make_uint2(pack_bf(v[0], v[1]), pack_bf(v[2], v[3]));
-      } else {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (n + i < p.N) o[i] = f2bf(v[i]);
-      }
-    }
-  }
-}
-
-template <int WPG, int MB>
-static void launch_mid(const GemmArgs &a, hipStream_t stream) {
-  dim3 grid(static_cast<unsigned>(cdiv(a.N, 16 * WPG)), static_cast<unsigned>(cdiv(a.M, 64 * MB)));
-  hipLaunchKernelGGL((fp8_gemm_mid_kernel<WPG, MB>), grid, dim3(64 * WPG), 0, stream, a);
-}
-
-template <int MB>
-static void launch_mid_w(int wpg, const GemmArgs &a, hipStream_t stream) {
-  if (wpg == 4) launch_mid<4, MB>(a, stream);
-  else if (wpg == 3) launch_mid<3, MB>(a, stream);
-  else launch_mid<2, MB>(a, stream);
-}
 
 // x (rows, K) bf16 -> e4m3fn(clamp(x / s, -448, 448)) (fp8_emul.py:76-78),
 // two values per v_cvt_pk_fp8_f32 (round to nearest even).
@@ -920,46 +759,32 @@ extern "C" int evo2_fp8_gemm(const void *x8, int64_t sx, const void *w8, int64_t
              w_scale, static_cast<const bf16_t *>(bias), static_cast<bf16_t *>(out), so,
              static_cast<int>(M), static_cast<int>(N), static_cast<int>(K)};
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (K % S_BK == 0 && sx * (M < 256 ? M : 256) < (int64_t(1) << 31) &&
-      (M <= S_ROWS || cdiv(M, 256) * N <= MID_MAX_WORK)) {
-    // Weight-streaming kernels: mb 64-row activation blocks per workgroup
-    // (1: the decode kernel, gridded over M) chosen by the number of 16 x 64
-    // wave tiles -- few tiles need every wave the chip can run, many need the
-    // weight stream read fewer times -- then the waves per workgroup (16 W
-    // rows each) whose workgroups fill the CUs most evenly (groups / (rounds
-    // x CUs)), the larger on a tie.  Sweeps over mb in 1..4 and 2..4 waves
-    // (K=4096): this picks the fastest or within 8% of it at M = 128, 192,
-    // 256, 512 with N = 12288 and M = 128, 256, 512, 1024 with N = 4096, e.g.
-    // 19.9 us at M=128 and 30.8 at M=256 for N=12288; 7B decode in_proj
-    // (M=64, N=12288) 17.1 us with 3 waves against 18.6 with 4 and 21.3
-    // with 2.
+  if (K % S_BK == 0 && sx * S_ROWS < (int64_t(1) << 31) &&
+      (M <= S_ROWS || cdiv(M, S_ROWS) * N <= STREAM_MAX_WORK)) {
+    // The weight-streaming kernel, over ceil(M / 64) blocks of 64 rows, with
+    // the waves per workgroup (16 W rows each) whose workgroups fill the CUs
+    // most evenly (groups / (rounds x CUs)), the larger on a tie.  Measured
+    // with the weights streaming from HBM (9 rotating weights, more than the
+    // 256 MB infinity cache holds), K = 4096: the 7B decode in_proj (M=64,
+    // N=12288) 17.1 us with 3 waves against 18.9 with 4 and 21.8 with 2; at
+    // M = 128 / 192 / 256 / 512, N = 12288: 25.9 / 37.1 / 42.0 / 75.8 us, the
+    // fastest of this kernel and of workgroups covering 2-4 row blocks per
+    // weight load (which only won while the weights stayed cache-resident).
     const int ncu = cu_count() > 0 ? cu_count() : 256;
-    const int64_t tiles = cdiv(N, 16) * cdiv(M, S_ROWS);
-    const int64_t blocks = cdiv(M, S_ROWS);
-    const int mb = static_cast<int>(tiles <= 1024 ? 1 : tiles <= 2048 ? (blocks < 2 ? blocks : 2)
-                                                                      : (blocks < 4 ? blocks : 4));
-    const int64_t ycols = cdiv(M, S_ROWS * mb);
+    const int64_t yblocks = cdiv(M, S_ROWS);
     int best_w = 4;
     double best_eff = -1.0;
     for (int w = 4; w >= 2; --w) {
-      const int64_t groups = cdiv(N, 16 * w) * ycols;
+      const int64_t groups = cdiv(N, 16 * w) * yblocks;
       const double eff = double(groups) / double(cdiv(groups, ncu) * ncu);
       if (eff > best_eff + 1e-9) {
         best_eff = eff;
         best_w = w;
       }
     }
-    if (mb == 1) {
-      if (best_w == 4) launch_small<4>(a, st);
-      else if (best_w == 3) launch_small<3>(a, st);
-      else launch_small<2>(a, st);
-    } else if (mb == 2) {
-      launch_mid_w<2>(best_w, a, st);
-    } else if (mb == 3) {
-      launch_mid_w<3>(best_w, a, st);
-    } else {
-      launch_mid_w<4>(best_w, a, st);
-    }
+    if (best_w == 4) launch_small<4>(a, st);
+    else if (best_w == 3) launch_small<3>(a, st);
+    else launch_small<2>(a, st);
     return check_launch("fp8_gemm");
   }
   const int64_t tiles_n = cdiv(N, G_BN), tiles_m = cdiv(M, G_BM);

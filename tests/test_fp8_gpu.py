@@ -4,8 +4,8 @@
   clamp(x / s, +-448) (fp8_emul.py:76-78), including saturation and ties;
 * GEMM known answers: small-integer e4m3 operands whose fp32 sums are exact,
   so the bf16 output must equal the oracle bit for bit, on each kernel: the
-  decode-sized one, the mid-sized one, the 256x256 tile one and its
-  persistent form (whole tiles, at least one per CU), in both tile orders
+  decode-sized one (also gridded over blocks of 64 rows), the 256x256 tile
+  one and its persistent form (whole tiles, at least one per CU), in both tile orders
   of the latter (XCD
   blocks of 4 x 8 tiles, whole rounds and a part-filled last round, and
   row-major with some workgroups taking one tile more);
@@ -45,20 +45,19 @@ def _small_int_e4m3(shape, g):
     return (torch.randint(-6, 7, shape, generator=g).float()).to(E4M3)
 
 
-# With K a multiple of 128 the weight-streaming kernels take M <= 64, and
-# larger M while ceil(M / 256) x N <= 24576: 16 W rows per wave in registers,
-# 16x16x128 MFMA, mb = 1..4 blocks of 64 activation rows per workgroup by the
-# number of 16 x 64 wave tiles (<= 1024: 1, <= 2048: 2, else up to 4) and a
-# second grid dimension over the row blocks; the others run the 256x256-tile
-# kernel (K = 192 here, or too much work).
+# With K a multiple of 128 the weight-streaming kernel takes M <= 64, and
+# larger M over blocks of 64 rows while ceil(M / 64) x N <= 60000 (16 W rows
+# per wave in registers, 16x16x128 MFMA, the blocks of one weight slice on
+# one XCD); the others run the 256x256-tile kernel (K = 192 here, or too much
+# work).
 @pytest.mark.parametrize("M,N,K", [(64, 384, 256), (1, 64, 128), (5, 130, 1920),
-                                   (64, 4096, 4096),                      # mb 1, one row block
+                                   (64, 4096, 4096),                      # one row block
                                    (65, 200, 256), (130, 96, 384), (300, 512, 1920),
-                                   (1000, 130, 640),                      # mb 1, gridded over M
-                                   (128, 12288, 256), (100, 10000, 384),  # mb 2
-                                   (192, 12288, 256), (170, 12000, 256),  # mb 3
-                                   (256, 12288, 512), (500, 12288, 256),  # mb 4
-                                   (256, 256, 192), (1100, 6400, 640)])   # 256x256 tiles
+                                   (1000, 130, 640), (128, 12288, 256), (100, 10000, 384),
+                                   (192, 12288, 256), (170, 12000, 256),
+                                   (256, 12288, 512),                     # gridded over M
+                                   (256, 256, 192), (1100, 6400, 640),
+                                   (500, 12288, 256)])                    # 256x256 tiles
 def test_gemm_known_answer(M, N, K):
     g = torch.Generator().manual_seed(M + N)
     x8 = _small_int_e4m3((M, K), g)
