@@ -12,10 +12,10 @@
 // Time is split into tiles of `block_t` rows (the same tile table as the FIR
 // prefill) so that the launch has parallelism beyond H/256 workgroups:
 //   phase 1  per tile, the end state of a scan started from zero;
-//   phase 2  per segment and channel, the carry into every tile
+//   phase 2  per segment, channel and pole, the carry into every tile
 //            C_j = p^(L_{j-1}) C_{j-1} + E_{j-1}, C_0 = the cached state
-//            (continuation) or 0, as a scan over tiles with wavefront
-//            shuffles; the segment's final state goes to the cache
+//            (continuation) or 0, as one FMA chain over the tiles; the
+//            segment's final state goes to the cache
 //            (mixers.py:1391-1394);
 //   phase 3  per tile, the scan again from its carry, the readout and the
 //            mixer tail g = bf16(bf16(bf16(y) + bf16(u D)) x2) (mixers.py:1397).
@@ -264,86 +264,63 @@ __global__ __launch_bounds__(256, PHASE == 3 ? 4 : 5) void hcl_scan_kernel(HclAr
   }
 }
 
-// Phase 2: the carry across tiles as a wavefront scan.  Tile i of a segment
-// maps its entering state s to p^len_i (.) s + E_i (E_i: its end state from
-// a zero start), so the state entering tile i is the composition of the maps
-// of tiles 0..i-1 applied to the segment's initial state.  One wavefront per
-// channel: lane l holds tile l of a window of 64 tiles and the 64 prefix
-// compositions come out of an inclusive scan over lanes in log2(64) = 6
-// shuffle steps, (A, B) <- (A A', A B' + B) with (A', B') from lane l - d.
-// Windows of 64 tiles chain serially through the last lane's composition.
-// The carries replace the tile end states in `work`; the state after the
-// last tile is returned in S.
-__device__ __forceinline__ void carry_scan(float *work, int64_t H, int c, int j0, int n,
-                                           int first_t0, int block_t, int e, const float lpv[16],
-                                           float S[16]) {
-  const int lane = threadIdx.x & 63;
-  for (int w0 = 0; w0 < n; w0 += 64) {
-    const int l = w0 + lane;
-    const bool valid = l < n;
-    const int len = valid ? min(first_t0 + (l + 1) * block_t, e) - (first_t0 + l * block_t) : 0;
-    float A[16], B[16];
-    const float4 *wp = reinterpret_cast<const float4 *>(work + ((int64_t)(j0 + (valid ? l : 0)) * H + c) * 16);
+// Phase 2: the carry across tiles.  Tile l of a segment maps its entering
+// state s to p^len_l (.) s + E_l (E_l: its end state from a zero start), so
+// the state entering tile l is C_l = p^len_{l-1} (.) C_{l-1} + E_{l-1}, with
+// C_0 the segment's initial state.  One lane per (channel, pole): the chain
+// is one FMA per tile, and consecutive lanes read consecutive floats of the
+// tile end states, 16 tiles per batch of loads.  (A wavefront-per-channel
+// form that composed the maps with a 6-step shuffle scan over 64 tiles ran
+// the 7B/32k carry slower, ~23 us against ~17.)  The carries replace the end
+// states in `work`; the state after the last tile is returned.
+__device__ __forceinline__ float carry_chain(float *work, int64_t H, int c, int i, int j0, int n,
+                                             int first_t0, int block_t, int e, float lpv,
+                                             float S) {
+  const float afull = expf(lpv * static_cast<float>(block_t));
+  float *wp = work + ((int64_t)j0 * H + c) * 16 + i;
+  const int64_t ts = H * 16;  // floats between tiles
+  int t = first_t0;
+  for (int b = 0; b < n; b += 16) {
+    float E[16];
+    const float *rp = wp;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const float4 v = valid ? wp[q] : make_float4(0.f, 0.f, 0.f, 0.f);
-      B[4 * q] = v.x; B[4 * q + 1] = v.y; B[4 * q + 2] = v.z; B[4 * q + 3] = v.w;
+    for (int q = 0; q < 16; ++q) {
+      E[q] = b + q < n ? *rp : 0.0f;
+      rp += ts;
     }
 #pragma unroll
-    for (int i = 0; i < 16; ++i) A[i] = valid ? expf(lpv[i] * static_cast<float>(len)) : 1.0f;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const float Ap = __shfl_up(A[i], d), Bp = __shfl_up(B[i], d);
-        if (lane >= d) {
-          B[i] = fmaf(A[i], Bp, B[i]);
-          A[i] = A[i] * Ap;
-        }
+    for (int q = 0; q < 16; ++q) {
+      if (b + q < n) {  // uniform
+        *wp = S;  // the carry into tile b + q
+        wp += ts;
+        const int len = min(t + block_t, e) - t;
+        t += block_t;
+        const float A = len == block_t ? afull : expf(lpv * static_cast<float>(len));
+        S = fmaf(A, S, E[q]);
       }
     }
-    // carry into tile l: the composition of tiles < l applied to S
-    float C[16], Sn[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const float Ap = __shfl_up(A[i], 1), Bp = __shfl_up(B[i], 1);
-      C[i] = lane == 0 ? S[i] : fmaf(Ap, S[i], Bp);
-      Sn[i] = fmaf(__shfl(A[i], 63), S[i], __shfl(B[i], 63));
-    }
-    if (valid) {
-      float4 *wq = reinterpret_cast<float4 *>(work + ((int64_t)(j0 + l) * H + c) * 16);
-#pragma unroll
-      for (int q = 0; q < 4; ++q) wq[q] = make_float4(C[4 * q], C[4 * q + 1], C[4 * q + 2], C[4 * q + 3]);
-    }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) S[i] = Sn[i];
   }
+  return S;
 }
 
-// One wavefront per (segment, channel); writes the segment's final state to
-// the cache (mixers.py:1391-1394).
+// One lane per (segment, channel, pole); writes the segment's final state
+// to the cache (mixers.py:1391-1394).
 __global__ __launch_bounds__(256) void hcl_carry_kernel(HclArgs p) {
   const int seg = blockIdx.x;
-  const int c = blockIdx.y * 4 + (threadIdx.x >> 6);
-  if (c >= p.H) return;  // wave-uniform
+  const int gi = blockIdx.y * 256 + threadIdx.x;
+  const int c = gi >> 4, i = gi & 15;
+  if (c >= p.H) return;
   const int a = p.seq[3 * seg], e = p.seq[3 * seg + 1];
   if (e <= a) return;
   const int64_t blk = p.blocks[seg * p.sblk];
   if (blk < 0 || blk >= p.num_blocks) return;
   const bool init = p.seq[3 * seg + 2] != 0;
-  float *st = p.ssm + blk * p.m0 + (int64_t)c * p.m1;
-  float S[16], lpv[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    S[i] = init ? st[i * p.m2] : 0.0f;
-    lpv[i] = p.lp[(int64_t)c * p.l0 + i * p.l1];
-  }
+  float *st = p.ssm + blk * p.m0 + (int64_t)c * p.m1 + i * p.m2;
+  float S = init ? *st : 0.0f;
+  const float lpv = p.lp[(int64_t)c * p.l0 + i * p.l1];
   const int j0 = p.tile_start[seg], n = p.tile_start[seg + 1] - j0;
-  if (n > 0) carry_scan(p.work, p.H, c, j0, n, p.tiles[2 * j0 + 1], p.block_t, e, lpv, S);
-  if ((threadIdx.x & 63) == 0) {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) st[i * p.m2] = S[i];
-  }
+  if (n > 0) S = carry_chain(p.work, p.H, c, i, j0, n, p.tiles[2 * j0 + 1], p.block_t, e, lpv, S);
+  *st = S;
 }
 
 // Conv window update for the LI prefill: same contract as the FIR window
@@ -421,7 +398,7 @@ static int hcl_prefill(const void *z, int64_t sz, const void *short_w,
     int rc = check_launch("hcl phase 1");
     if (rc) return rc;
   }
-  dim3 cgrid(static_cast<unsigned>(nseq), static_cast<unsigned>(cdiv(H, 4)));
+  dim3 cgrid(static_cast<unsigned>(nseq), static_cast<unsigned>(cdiv(H, 16)));
   hipLaunchKernelGGL(hcl_carry_kernel, cgrid, dim3(256), 0, st, a);
   dim3 sgrid(static_cast<unsigned>(nseq), static_cast<unsigned>(cdiv(H, 64)));
   int rc = check_launch("hcl phase 2");
@@ -586,19 +563,13 @@ __global__ __launch_bounds__(256) void iir_scan_kernel(IirArgs p) {
 }
 
 __global__ __launch_bounds__(256) void iir_carry_kernel(IirArgs p) {
-  const int c = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (c >= p.H) return;  // wave-uniform
-  float S[16], lpv[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    S[i] = p.sp ? p.sp[(int64_t)c * p.sp0 + i * p.sp1] : 0.0f;
-    lpv[i] = p.lp[(int64_t)c * p.l0 + i * p.l1];
-  }
-  if (p.ntiles > 0) carry_scan(p.work, p.H, c, 0, p.ntiles, 0, p.block_t, p.L, lpv, S);
-  if ((threadIdx.x & 63) == 0) {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) p.st[(int64_t)c * 16 + i] = S[i];
-  }
+  const int gi = blockIdx.x * 256 + threadIdx.x;
+  const int c = gi >> 4, i = gi & 15;  // one lane per (channel, pole)
+  if (c >= p.H) return;
+  float S = p.sp ? p.sp[(int64_t)c * p.sp0 + i * p.sp1] : 0.0f;
+  const float lpv = p.lp[(int64_t)c * p.l0 + i * p.l1];
+  if (p.ntiles > 0) S = carry_chain(p.work, p.H, c, i, 0, p.ntiles, 0, p.block_t, p.L, lpv, S);
+  p.st[(int64_t)c * 16 + i] = S;
 }
 
 // h[d, l] = sum_s residues[d, s] * exp(log_poles[d, s] * t[l])  (triton_hcl.py:46-74)
@@ -647,7 +618,7 @@ extern "C" int evo2_iir_segment(const float *seq, int64_t xh, int64_t xl,
     int rc = check_launch("iir_segment phase 1");
     if (rc) return rc;
   }
-  hipLaunchKernelGGL(iir_carry_kernel, dim3(static_cast<unsigned>(cdiv(H, 4))), dim3(256), 0, strm, a);
+  hipLaunchKernelGGL(iir_carry_kernel, dim3(static_cast<unsigned>(cdiv(H, 16))), dim3(256), 0, strm, a);
   int rc = check_launch("iir_segment phase 2");
   if (rc) return rc;
   if (ntiles) {
@@ -684,7 +655,7 @@ extern "C" int evo2_iir_final_state(const float *seq, int64_t xh, int64_t xl,
     int rc = check_launch("iir_final_state phase 1");
     if (rc) return rc;
   }
-  hipLaunchKernelGGL(iir_carry_kernel, dim3(static_cast<unsigned>(cdiv(H, 4))), dim3(256), 0, strm, a);
+  hipLaunchKernelGGL(iir_carry_kernel, dim3(static_cast<unsigned>(cdiv(H, 16))), dim3(256), 0, strm, a);
   return check_launch("iir_final_state phase 2");
 }
 
