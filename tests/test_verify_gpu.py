@@ -45,8 +45,11 @@ def _meta_dev(meta, strided):
 @pytest.mark.parametrize("kind", ["hcs", "hcm"])
 @pytest.mark.parametrize("H,x_dtype,strided", [(256, torch.bfloat16, False),
                                                (4096, torch.bfloat16, True),
-                                               (192, torch.float32, True)])
+                                               (192, torch.float32, True),
+                                               (193, torch.bfloat16, False)])
 def test_fir_snapshots_bitwise(kind, H, x_dtype, strided):
+    """H = 192 leaves the channel-pair hcm kernel a part-filled last
+    workgroup; an odd H takes the one-channel-per-lane form."""
     nreq, Q, nblk = 9, 4, 90
     prm, x, state, meta = verify_case(kind, H, nreq, Q, nblk, seed=H + Q, x_dtype=x_dtype)
     K = prm["conv"].shape[-1]
