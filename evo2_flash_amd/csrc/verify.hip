@@ -94,33 +94,59 @@ __device__ __forceinline__ void store_y(const VerifyArgs &a, int64_t t, int c, f
 // CPW channels.  Every output and snapshot of the step is a function of the
 // source window and the step's tokens alone: with e = window ++ (x_0 ..
 // x_{n-1}), snapshot p is e[p+1 .. p+127] and y_p sums e[p .. p+126] against
-// the taps plus last * x_p.  So e is staged in LDS once, and then every wave
-// issues its share of all snapshot stores back to back (no barrier between
-// tokens, so the memory system sees every store of the step at once) and
-// computes whole outputs for its positions.
+// the taps plus last * x_p.  So e is staged in LDS once; every wave then
+// computes the outputs of its positions and issues its share of all snapshot
+// stores back to back (no barrier between tokens, so the memory system sees
+// every store of the step at once, and they drain while the next workgroup
+// stages its window).
 //  * copies: with CPW = 128 a lane moves a channel pair (8 bytes; 512 bytes
 //    of a column per wave instruction), with CPW = 64 one channel (the form
-//    for a state view whose channels are not unit-stride pairs);
-//  * stores: wave m writes the columns k = m (mod 4) of every snapshot, in
-//    position order, so a block named by two positions ends with the later
-//    one's contents, as the reference's sequential writes leave it;
-//  * sums: lane = channel, 64 channels at a time; wave m computes y_p for
-//    p = m (mod 4) with the reference's 16 accumulators (k = 16 j + 4 m' + l
-//    over j in order), combined as ((A0 + A1) + A2) + A3 per l, then
-//    (l0 + l2) + (l1 + l3), plus last * x.
+//    for a state view whose channels are not unit-stride aligned pairs);
+//  * waves: NW = 4 x (channels per lane); wave m stages and stores the
+//    columns k = m (mod NW), so a block named by two positions ends with the
+//    later one's contents (in position order per column, as the reference's
+//    sequential writes leave it);
+//  * sums: lane = channel; wave m takes the 64 channels of half m / 4 and the
+//    positions p = m (mod 4), with the reference's 16 accumulators
+//    (k = 16 j + 4 m' + l over j in order), combined as ((A0 + A1) + A2) + A3
+//    per l, then (l0 + l2) + (l1 + l3), plus last * x.  Its taps are fetched
+//    before the window, so their latency hides under the staging.
+// 64 x 4 requests at 7B width (671 MB moved): 212 us with 64 channels and 4
+// waves, 197 with channel pairs, 171 with 8 waves, 160 with the sums before
+// the stores and the taps first (one process; all bitwise equal).
 constexpr int VQ = 16;
 
 template <int CPW>
-__global__ __launch_bounds__(256) void fir128_verify_kernel(VerifyArgs a) {
+__global__ __launch_bounds__(4 * CPW, 4) void fir128_verify_kernel(VerifyArgs a) {
   static_assert(CPW == 64 || CPW == 128, "one channel or one channel pair per lane");
   constexpr int CPL = CPW / 64;  // channels per lane in the copies
+  constexpr int NW = 4 * CPL;    // waves per workgroup
   __shared__ float e[127 + VQ][CPW];
   const int lane = threadIdx.x & 63;
-  const int m = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) & 3;
+  const int m = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) % NW;
   const int64_t r = blockIdx.y;
   const int cbase = blockIdx.x * CPW;
   const Req q = request_of(a, r);
   const int n = static_cast<int>(max<int64_t>(0, min<int64_t>(a.Q, q.end - q.first)));
+
+  // this wave's sums: channel cbase + 64 (m / 4) + lane, positions m % 4 + 4 i
+  const int p0 = m & 3;
+  const int c = cbase + 64 * (m >> 2) + lane;
+  const bool active = c < a.H;
+  const int cc = active ? c : 0;
+  // the channel's taps as bf16 pairs (tap k = half k & 1 of W[k / 2])
+  uint32_t W[64];
+  const bf16_t *wrow = a.w + (int64_t)cc * a.w0;
+  if (a.w1 == 1 && a.w0 % 8 == 0 && (reinterpret_cast<uintptr_t>(a.w) & 15) == 0) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const uint4 v = reinterpret_cast<const uint4 *>(wrow)[i];
+      W[4 * i] = v.x; W[4 * i + 1] = v.y; W[4 * i + 2] = v.z; W[4 * i + 3] = v.w;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 64; ++i) W[i] = pair_bf(wrow[(2 * i) * a.w1], wrow[(2 * i + 1) * a.w1]);
+  }
 
   // the lane's channels in the copies: cbase + CPL lane + (0 .. CPL-1); with
   // CPL = 2, H is even, so a pair is wholly inside H or wholly past it
@@ -128,7 +154,7 @@ __global__ __launch_bounds__(256) void fir128_verify_kernel(VerifyArgs a) {
   const bool cact = cl < a.H;
   const int ccl = cact ? cl : 0;
   const float *src = a.st + q.src * a.ss0 + (int64_t)ccl * a.ss1;
-  for (int k = m; k < 127; k += 4) {
+  for (int k = m; k < 127; k += NW) {
     if constexpr (CPL == 2) {
       const float2 v = (q.src_ok && cact) ? *reinterpret_cast<const float2 *>(src + (int64_t)k * a.ss2)
                                           : make_float2(0.0f, 0.0f);
@@ -137,47 +163,15 @@ __global__ __launch_bounds__(256) void fir128_verify_kernel(VerifyArgs a) {
       e[k][lane] = (q.src_ok && cact) ? src[(int64_t)k * a.ss2] : 0.0f;
     }
   }
-  for (int p = m; p < n; p += 4)
+  for (int p = m; p < n; p += NW)
 #pragma unroll
     for (int i = 0; i < CPL; ++i) e[127 + p][CPL * lane + i] = cact ? load_x(a, q.first + p, cl + i) : 0.0f;
   __syncthreads();
 
-  for (int p = 0; p < n; ++p) {
-    const int64_t d = dest_of(a, r, p);
-    if (d >= 0 && cact) {
-      float *dst = a.st + d * a.ss0 + (int64_t)cl * a.ss1;
-#pragma unroll 8
-      for (int k = m; k < 127; k += 4) {
-        if constexpr (CPL == 2)
-          *reinterpret_cast<float2 *>(dst + (int64_t)k * a.ss2) =
-              *reinterpret_cast<const float2 *>(&e[p + 1 + k][2 * lane]);
-        else
-          dst[(int64_t)k * a.ss2] = e[p + 1 + k][lane];
-      }
-    }
-  }
-  if (m >= n) return;  // uniform: no position for this wave
-
-#pragma unroll 1
-  for (int h = 0; h < CPL; ++h) {
-    const int c = cbase + 64 * h + lane;  // lane = channel in the sums
-    const bool active = c < a.H;
-    const int cc = active ? c : 0;
-    // the channel's taps as bf16 pairs (tap k = half k & 1 of W[k / 2])
-    uint32_t W[64];
-    const bf16_t *wrow = a.w + (int64_t)cc * a.w0;
-    if (a.w1 == 1 && a.w0 % 8 == 0 && (reinterpret_cast<uintptr_t>(a.w) & 15) == 0) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const uint4 v = reinterpret_cast<const uint4 *>(wrow)[i];
-        W[4 * i] = v.x; W[4 * i + 1] = v.y; W[4 * i + 2] = v.z; W[4 * i + 3] = v.w;
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 64; ++i) W[i] = pair_bf(wrow[(2 * i) * a.w1], wrow[(2 * i + 1) * a.w1]);
-    }
+  if (p0 < n) {  // uniform
+    const int hc = 64 * (m >> 2) + lane;  // the channel's LDS column
     const float last = hi_bf(W[63]);
-    for (int p = m; p < n; p += 4) {
+    for (int p = p0; p < n; p += 4) {
       // the taps stay packed (64 VGPRs): an empty asm per position keeps the
       // compiler from hoisting 127 converted fp32 taps out of this loop
 #pragma unroll
@@ -196,15 +190,30 @@ __global__ __launch_bounds__(256) void fir128_verify_kernel(VerifyArgs a) {
             const int k = 16 * j + 4 * i + l;
             if (k < 127) {
               const float wk = (k & 1) ? hi_bf(W[k >> 1]) : lo_bf(W[k >> 1]);
-              acc[i][l] = acc[i][l] + e[p + k][64 * h + lane] * wk;
+              acc[i][l] = acc[i][l] + e[p + k][hc] * wk;
             }
           }
       }
       float pl[4];
 #pragma unroll
       for (int l = 0; l < 4; ++l) pl[l] = ((acc[0][l] + acc[1][l]) + acc[2][l]) + acc[3][l];
-      const float yv = ((pl[0] + pl[2]) + (pl[1] + pl[3])) + last * e[127 + p][64 * h + lane];
+      const float yv = ((pl[0] + pl[2]) + (pl[1] + pl[3])) + last * e[127 + p][hc];
       if (active) store_y(a, q.first + p, c, yv);
+    }
+  }
+
+  for (int p = 0; p < n; ++p) {
+    const int64_t d = dest_of(a, r, p);
+    if (d >= 0 && cact) {
+      float *dst = a.st + d * a.ss0 + (int64_t)cl * a.ss1;
+#pragma unroll 8
+      for (int k = m; k < 127; k += NW) {
+        if constexpr (CPL == 2)
+          *reinterpret_cast<float2 *>(dst + (int64_t)k * a.ss2) =
+              *reinterpret_cast<const float2 *>(&e[p + 1 + k][2 * lane]);
+        else
+          dst[(int64_t)k * a.ss2] = e[p + 1 + k][lane];
+      }
     }
   }
 }
@@ -447,7 +456,7 @@ extern "C" int evo2_fir_verify(const void *x, int64_t xs0, int64_t xs1, int32_t 
                        (reinterpret_cast<uintptr_t>(state) & 7) == 0;
     if (Q <= VQ && pairs) {
       dim3 grid(static_cast<unsigned>(cdiv(H, 128)), static_cast<unsigned>(nreq));
-      hipLaunchKernelGGL(fir128_verify_kernel<128>, grid, dim3(256), 0, st, a);
+      hipLaunchKernelGGL(fir128_verify_kernel<128>, grid, dim3(512), 0, st, a);
     } else {
       dim3 grid(static_cast<unsigned>(cdiv(H, 64)), static_cast<unsigned>(nreq));
       if (Q <= VQ)
