@@ -5,8 +5,14 @@
 //   n = bf16(n * H^-1/2);  n = bf16(n + eps)      eps outside the sqrt
 //   y = bf16(w * bf16(s / n))         correctly rounded division
 //
-// One wavefront per row; each lane keeps its slice of the row in registers
-// (packed bf16), so the row is read once and written once.  Optionally the
+// Many rows: one wavefront per row; each lane keeps its slice of the row in
+// registers (packed bf16), so the row is read once and written once.  Few
+// rows (decode batches): a workgroup per row, one 16-byte chunk per thread,
+// so a row's 4096 correctly rounded divisions are spread over 512 lanes
+// instead of 64.  Both sum the squares in one order: each 8-value chunk from
+// zero, the chunks of lane l (l, l + 64, l + 128, ...) in turn, then a
+// butterfly over the 64 lanes, so a row's result does not depend on how
+// many rows the launch has.  Optionally the
 // normalised row is also quantised for the fp8 in_proj that consumes it,
 // q = e4m3fn(clamp(y / input_scale, +-448)) (fp8_emul.py:76-78), which saves
 // the separate quantisation pass over y; y itself may then be skipped.
@@ -30,6 +36,73 @@ struct NormArgs {
   float inv_sqrt_h;
 };
 
+// s = bf16(x + residual) for chunk j of a row, written to the s output.
+__device__ __forceinline__ uint4 add_chunk(const NormArgs &p, int64_t row, int j, uint4 v) {
+  const uint4 b = reinterpret_cast<const uint4 *>(p.r + row * p.sr)[j];
+  const uint32_t av[4] = {v.x, v.y, v.z, v.w};
+  const uint32_t bv[4] = {b.x, b.y, b.z, b.w};
+  uint32_t o[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) o[e] = pack_bf(lo_bf(av[e]) + lo_bf(bv[e]), hi_bf(av[e]) + hi_bf(bv[e]));
+  const uint4 s = make_uint4(o[0], o[1], o[2], o[3]);
+  reinterpret_cast<uint4 *>(p.s + row * p.ss)[j] = s;
+  return s;
+}
+
+// fp32 sum of the squares of a chunk's 8 values, in element order from zero.
+__device__ __forceinline__ float chunk_sumsq(uint4 v) {
+  const uint32_t av[4] = {v.x, v.y, v.z, v.w};
+  float cs = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float a = lo_bf(av[e]), b = hi_bf(av[e]);
+    cs = cs + a * a;
+    cs = cs + b * b;
+  }
+  return cs;
+}
+
+__device__ __forceinline__ float lane_butterfly(float acc) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) acc = acc + __shfl_xor(acc, off);
+  return acc;
+}
+
+// n = bf16(bf16(bf16(sqrt(sum)) * H^-1/2) + eps)
+__device__ __forceinline__ float row_norm(float sumsq, const NormArgs &p) {
+  float n = rbf(sqrtf(sumsq));
+  n = rbf(n * p.inv_sqrt_h);
+  return rbf(n + p.eps);
+}
+
+// y = bf16(w * bf16(s / n)) for chunk j (and its e4m3 quantisation).
+template <bool QUANT>
+__device__ __forceinline__ void norm_chunk(const NormArgs &p, int64_t row, int j, uint4 v, float n) {
+  const uint4 wv = reinterpret_cast<const uint4 *>(p.w)[j];
+  const uint32_t av[4] = {v.x, v.y, v.z, v.w};
+  const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
+  uint32_t o[4];
+  float yv[8];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    yv[2 * e] = rbf(lo_bf(ww[e]) * rbf(lo_bf(av[e]) / n));
+    yv[2 * e + 1] = rbf(hi_bf(ww[e]) * rbf(hi_bf(av[e]) / n));
+    o[e] = pack_bf(yv[2 * e], yv[2 * e + 1]);
+  }
+  if (p.y) reinterpret_cast<uint4 *>(p.y + row * p.sy)[j] = make_uint4(o[0], o[1], o[2], o[3]);
+  if constexpr (QUANT) {
+    const float qs = p.qscale[0];
+    int lo = 0, hi = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) yv[e] = fminf(fmaxf(yv[e] / qs, -448.0f), 448.0f);
+    lo = __builtin_amdgcn_cvt_pk_fp8_f32(yv[0], yv[1], lo, false);
+    lo = __builtin_amdgcn_cvt_pk_fp8_f32(yv[2], yv[3], lo, true);
+    hi = __builtin_amdgcn_cvt_pk_fp8_f32(yv[4], yv[5], hi, false);
+    hi = __builtin_amdgcn_cvt_pk_fp8_f32(yv[6], yv[7], hi, true);
+    reinterpret_cast<uint2 *>(p.q + row * p.sq)[j] = make_uint2(static_cast<uint32_t>(lo), static_cast<uint32_t>(hi));
+  }
+}
+
 // CH = 16-byte chunks (8 values) per lane; H = 512 * CH for the vector path.
 template <int CH, bool ADD, bool QUANT>
 __global__ __launch_bounds__(256) void rms_norm_vec_kernel(NormArgs p) {
@@ -41,65 +114,39 @@ __global__ __launch_bounds__(256) void rms_norm_vec_kernel(NormArgs p) {
 #pragma unroll
   for (int i = 0; i < CH; ++i) v[i] = xr[lane + 64 * i];
   if constexpr (ADD) {
-    const uint4 *rr = reinterpret_cast<const uint4 *>(p.r + row * p.sr);
-    uint4 *sr = reinterpret_cast<uint4 *>(p.s + row * p.ss);
 #pragma unroll
-    for (int i = 0; i < CH; ++i) {
-      const uint4 b = rr[lane + 64 * i];
-      const uint32_t av[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
-      const uint32_t bv[4] = {b.x, b.y, b.z, b.w};
-      uint32_t o[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        o[e] = pack_bf(lo_bf(av[e]) + lo_bf(bv[e]), hi_bf(av[e]) + hi_bf(bv[e]));
-      v[i] = make_uint4(o[0], o[1], o[2], o[3]);
-      sr[lane + 64 * i] = v[i];
-    }
+    for (int i = 0; i < CH; ++i) v[i] = add_chunk(p, row, lane + 64 * i, v[i]);
   }
   float acc = 0.0f;
 #pragma unroll
-  for (int i = 0; i < CH; ++i) {
-    const uint32_t av[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+  for (int i = 0; i < CH; ++i) acc = acc + chunk_sumsq(v[i]);
+  const float n = row_norm(lane_butterfly(acc), p);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float a = lo_bf(av[e]), b = hi_bf(av[e]);
-      acc = acc + a * a;
-      acc = acc + b * b;
-    }
+  for (int i = 0; i < CH; ++i) norm_chunk<QUANT>(p, row, lane + 64 * i, v[i], n);
+}
+
+// Few rows: workgroup = one row of H = 512 CH, thread t holds chunk t (wave
+// i, lane l: chunk l + 64 i, as lane l's i-th chunk in the per-row form).
+// The chunk sums meet in LDS and wave 0 adds lane l's CH of them in order i.
+template <int CH, bool ADD, bool QUANT>
+__global__ __launch_bounds__(64 * CH) void rms_norm_row_kernel(NormArgs p) {
+  __shared__ float part[CH][64];
+  __shared__ float nrow;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int64_t row = blockIdx.x;
+  uint4 v = reinterpret_cast<const uint4 *>(p.x + row * p.sx)[t];
+  if constexpr (ADD) v = add_chunk(p, row, t, v);
+  part[wave][lane] = chunk_sumsq(v);
+  __syncthreads();
+  if (wave == 0) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < CH; ++i) acc = acc + part[i][lane];
+    const float n = row_norm(lane_butterfly(acc), p);
+    if (lane == 0) nrow = n;
   }
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) acc = acc + __shfl_xor(acc, off);
-  float n = rbf(sqrtf(acc));
-  n = rbf(n * p.inv_sqrt_h);
-  n = rbf(n + p.eps);
-  const uint4 *wr = reinterpret_cast<const uint4 *>(p.w);
-  const float qs = QUANT ? p.qscale[0] : 1.0f;
-#pragma unroll
-  for (int i = 0; i < CH; ++i) {
-    const uint4 wv = wr[lane + 64 * i];
-    const uint32_t av[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
-    const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
-    uint32_t o[4];
-    float yv[8];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      yv[2 * e] = rbf(lo_bf(ww[e]) * rbf(lo_bf(av[e]) / n));
-      yv[2 * e + 1] = rbf(hi_bf(ww[e]) * rbf(hi_bf(av[e]) / n));
-      o[e] = pack_bf(yv[2 * e], yv[2 * e + 1]);
-    }
-    if (p.y) reinterpret_cast<uint4 *>(p.y + row * p.sy)[lane + 64 * i] = make_uint4(o[0], o[1], o[2], o[3]);
-    if constexpr (QUANT) {
-      int lo = 0, hi = 0;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) yv[e] = fminf(fmaxf(yv[e] / qs, -448.0f), 448.0f);
-      lo = __builtin_amdgcn_cvt_pk_fp8_f32(yv[0], yv[1], lo, false);
-      lo = __builtin_amdgcn_cvt_pk_fp8_f32(yv[2], yv[3], lo, true);
-      hi = __builtin_amdgcn_cvt_pk_fp8_f32(yv[4], yv[5], hi, false);
-      hi = __builtin_amdgcn_cvt_pk_fp8_f32(yv[6], yv[7], hi, true);
-      reinterpret_cast<uint2 *>(p.q + row * p.sq)[lane + 64 * i] =
-          make_uint2(static_cast<uint32_t>(lo), static_cast<uint32_t>(hi));
-    }
-  }
+  __syncthreads();
+  norm_chunk<QUANT>(p, row, t, v, nrow);
 }
 
 // Any H, any unit-stride rows: one wavefront per row, element by element.
@@ -136,10 +183,28 @@ __global__ __launch_bounds__(256) void rms_norm_scalar_kernel(NormArgs p) {
   }
 }
 
+// Up to this many rows a launch takes a workgroup per row (the per-row
+// wavefront form leaves most of the chip idle and each wave's 8 H/512
+// divisions serial).
+#ifndef NORM_ROW_SPLIT_MAX
+#define NORM_ROW_SPLIT_MAX 2048
+#endif
+
+template <int CH, bool ADD, bool QUANT>
+static void launch_rows(const NormArgs &a, hipStream_t st) {
+  hipLaunchKernelGGL((rms_norm_row_kernel<CH, ADD, QUANT>), dim3(static_cast<unsigned>(a.T)),
+                     dim3(64 * CH), 0, st, a);
+}
+
 template <bool ADD, bool QUANT>
 static void launch_norm(const NormArgs &a, bool vec, hipStream_t st) {
   dim3 grid(static_cast<unsigned>(cdiv(a.T, 4)));
-  if (vec && a.H == 1024) {
+  if (vec && a.T <= NORM_ROW_SPLIT_MAX && (a.H == 1024 || a.H == 2048 || a.H == 4096 || a.H == 8192)) {
+    if (a.H == 1024) launch_rows<2, ADD, QUANT>(a, st);
+    else if (a.H == 2048) launch_rows<4, ADD, QUANT>(a, st);
+    else if (a.H == 4096) launch_rows<8, ADD, QUANT>(a, st);
+    else launch_rows<16, ADD, QUANT>(a, st);
+  } else if (vec && a.H == 1024) {
     hipLaunchKernelGGL((rms_norm_vec_kernel<2, ADD, QUANT>), grid, dim3(256), 0, st, a);
   } else if (vec && a.H == 2048) {
     hipLaunchKernelGGL((rms_norm_vec_kernel<4, ADD, QUANT>), grid, dim3(256), 0, st, a);

@@ -46,6 +46,25 @@ def test_rms_norm_vs_oracle(T, H):
     assert max_rel_err(y2.cpu(), yr) <= 1e-2
 
 
+@pytest.mark.parametrize("H", [4096, 8192, 1024])
+def test_rms_norm_batch_invariant(H):
+    """A launch of few rows takes a workgroup per row, one of many rows a
+    wavefront per row; both sum the squares in one order, so a row's y, s
+    and q are the same bits whichever form (and batch) it ran in."""
+    x, r, w = _case(2100, H, 3.0, H + 11)
+    scale = torch.tensor([6.0 / 448]).to(DEV)
+    xd, rd, wd = x.to(DEV), r.to(DEV), w.to(DEV)
+    q_all, y_all, s_all = rms_norm_fp8(xd, wd, 1e-6, scale, residual=rd, keep_y=True)
+    for lo, hi in ((0, 7), (1000, 1064), (2099, 2100)):
+        q, y, s = rms_norm_fp8(xd[lo:hi], wd, 1e-6, scale, residual=rd[lo:hi], keep_y=True)
+        assert torch.equal(y, y_all[lo:hi]), (lo, hi)
+        assert torch.equal(s, s_all[lo:hi]), (lo, hi)
+        assert torch.equal(q.view(torch.uint8), q_all[lo:hi].view(torch.uint8)), (lo, hi)
+    assert torch.equal(rms_norm(xd[:5], wd, 1e-6), rms_norm(xd, wd, 1e-6)[:5])
+    yr, _ = oracle.rms_norm(x[:64], w, 1e-6, r[:64])
+    assert max_rel_err(y_all[:64].cpu(), yr) <= 1e-2
+
+
 @pytest.mark.parametrize("H", [4096, 1920])
 def test_rms_norm_large_residual_stream(H):
     """Residual streams of magnitude ~1e6 (bf16 range stress of the 40B case)."""
