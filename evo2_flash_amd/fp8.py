@@ -52,16 +52,25 @@ def fp8_gemm(x8, w8, x_scale, w_scale, bias=None, out=None):
         bias = bias.to(torch.bfloat16).contiguous()
     if out is None:
         out = torch.empty(M, N, dtype=torch.bfloat16, device=x8.device)
+    elif (out.dtype != torch.bfloat16 or out.shape != (M, N) or out.stride(1) != 1
+          or out.device != x8.device):
+        raise ValueError(f"fp8_gemm: out must be ({M}, {N}) bf16 on {x8.device} with unit "
+                         f"column stride, got {tuple(out.shape)} {out.dtype} stride {out.stride()}")
     _lib.call("evo2_fp8_gemm", _lib.ptr(x8), x8.stride(0), _lib.ptr(w8), w8.stride(0),
               _lib.ptr(xs), _lib.ptr(ws), _lib.ptr(bias), _lib.ptr(out), out.stride(0),
               M, N, K, _lib.stream_of(x8))
     return out
 
 
-def static_fp8_linear(x, weight, input_scale, weight_scale, bias=None):
-    """vLLM's static W8A8 linear: (..., K) bf16 -> (..., N) bf16."""
+def static_fp8_linear(x, weight, input_scale, weight_scale, bias=None, out=None):
+    """vLLM's static W8A8 linear: (..., K) bf16 -> (..., N) bf16; a 2-D x may
+    write its result into `out` (M, N) bf16 with unit column stride."""
     K = x.shape[-1]
     x8 = quantize_input(x.reshape(-1, K), input_scale)
+    if out is not None:
+        if x.dim() != 2 or out.shape != (x.shape[0], weight.shape[0]) or out.stride(1) != 1:
+            raise ValueError("static_fp8_linear: out must be (M, N) with unit column stride")
+        return fp8_gemm(x8, weight, input_scale, weight_scale, bias, out=out)
     out = fp8_gemm(x8, weight, input_scale, weight_scale, bias)
     return out.reshape(*x.shape[:-1], weight.shape[0])
 
@@ -86,6 +95,6 @@ class Fp8StaticLinear(nn.Module):
         self.bias = (nn.Parameter(torch.zeros(out_features, dtype=torch.bfloat16, device=device),
                                   requires_grad=False) if bias else None)
 
-    def forward(self, x):
+    def forward(self, x, out=None):
         return static_fp8_linear(x, self.weight, self.input_scale, self.weight_scale,
-                                 self.bias), None
+                                 self.bias, out=out), None

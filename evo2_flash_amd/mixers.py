@@ -108,8 +108,16 @@ class Linear(nn.Module):
         self.bias = (nn.Parameter(torch.zeros(out_features, device=device, dtype=dtype),
                                   requires_grad=False) if bias else None)
 
-    def forward(self, x):
-        return torch.nn.functional.linear(x, self.weight, self.bias), None
+    def forward(self, x, out=None):
+        """x (..., in) -> ((..., out), None); a 2-D x may write its result into
+        `out` (the same GEMM F.linear runs: addmm with the bias)."""
+        if out is None:
+            return torch.nn.functional.linear(x, self.weight, self.bias), None
+        if self.bias is not None:
+            torch.addmm(self.bias, x, self.weight.t(), out=out)
+        else:
+            torch.mm(x, self.weight.t(), out=out)
+        return out, None
 
 
 class ProjectionTap(nn.Module):
@@ -400,8 +408,17 @@ class HyenaMixerBase(nn.Module):
         out, _ = self.out_proj(y)
         return out
 
-    def _finish(self, parts, hidden_states, n):
+    def _finish(self, parts, hidden_states, n, output=None):
+        """out_proj of the step's rows.  With `output` (the operator's buffer,
+        contiguous, hidden_states' shape and dtype) the projection writes its
+        rows there directly and the padding rows are zeroed, with no copy."""
         g = torch.cat(parts, dim=0) if len(parts) > 1 else parts[0]
+        if (output is not None and output.shape == hidden_states.shape
+                and output.dtype == hidden_states.dtype and output.is_contiguous()):
+            self.out_proj(g, out=output[:n])
+            if n < output.shape[0]:
+                output[n:].zero_()
+            return output
         out, _ = self.out_proj(g)
         return self._unpad(out, hidden_states, n)
 
@@ -458,7 +475,7 @@ class HyenaFIRMixer(HyenaMixerBase):
             y = y + self.D.to(y.dtype) * u
         return x2 * y
 
-    def _forward_impl(self, hidden_states, token_ids=None):
+    def _forward_impl(self, hidden_states, token_ids=None, output=None):
         m = self._meta()
         if m is None:
             return self._profile_run(hidden_states, token_ids)
@@ -486,7 +503,7 @@ class HyenaFIRMixer(HyenaMixerBase):
                 z[nd:nd + npt], sw, window, self.conv.view(self.hidden, self.k_inner),
                 inner_state, self.D, seq_t, m.state_indices_tensor_p, til_t, bt))
         self._record_stamps(m)
-        return self._finish(parts, hidden_states, nd + npt)
+        return self._finish(parts, hidden_states, nd + npt, output)
 
 
 class HyenaIIRMixer(HyenaMixerBase):
@@ -528,7 +545,7 @@ class HyenaIIRMixer(HyenaMixerBase):
                           self._spec_tensors(m, x1v.shape[0], ssm, accepted))
         return (y + x1v * self.D.to(y.dtype)) * x2
 
-    def _forward_impl(self, hidden_states, token_ids=None):
+    def _forward_impl(self, hidden_states, token_ids=None, output=None):
         m = self._meta()
         if m is None:
             return self._profile_run(hidden_states, token_ids)
@@ -555,7 +572,7 @@ class HyenaIIRMixer(HyenaMixerBase):
             parts.append(hyena_hcl_prefill(z[nd:nd + npt], sw, window, res, lp, ssm, self.D,
                                            seq_t, m.state_indices_tensor_p, til_t, ts_t, bt))
         self._record_stamps(m)
-        return self._finish(parts, hidden_states, nd + npt)
+        return self._finish(parts, hidden_states, nd + npt, output)
 
 
 # ---------------------------------------------------------------- operator
@@ -567,7 +584,9 @@ def evo2_hyena_mixer(hidden_states: torch.Tensor, output: torch.Tensor,
     """The mixer as one opaque operator that writes `output` in place
     (mixers.py:1404-1410)."""
     layer = static_forward_context[layer_name]
-    output.copy_(layer._forward_impl(hidden_states, token_ids))
+    res = layer._forward_impl(hidden_states, token_ids, output=output)
+    if res is not output:
+        output.copy_(res)
 
 
 def evo2_hyena_mixer_fake(hidden_states: torch.Tensor, output: torch.Tensor,
