@@ -399,7 +399,8 @@ def bench_model40b(steps, dev, B=32, L=131072, seed=41):
 def bench_verify(reps, dev, H=H_7B, B=B_DECODE, Q=4, seed=9):
     """The inner operators of a speculative verify step, 7B shape: B requests
     of Q = 4 tokens (3 drafts) each, every request reading its accepted
-    snapshot and writing a snapshot per token.  Bytes per launch: the source
+    snapshot and writing a snapshot per token (launch times from graph
+    replays).  Bytes per launch: the source
     state and the Q snapshots (fp32), the token rows in and out (bf16 for
     the FIRs, fp32 for LI as the mixers pass them), the parameters once."""
     from evo2_flash_amd.synthetic import mixer_params
@@ -431,7 +432,11 @@ def bench_verify(reps, dev, H=H_7B, B=B_DECODE, Q=4, seed=9):
             cols, xb, pbytes = K - 1, 2, H * K * 2
         fn()
         torch.cuda.synchronize()
-        avg, med = _timed(fn, reps, stream)
+        # replayed from a graph of 8 calls, as a serving step runs them (eager
+        # calls of the 10-20 us kernels would time the Python wrapper)
+        g_k = _graph(fn, 8)
+        avg, med = _timed(g_k.replay, max(4, reps // 4), stream)
+        avg, med = avg / 8, med / 8
         nbytes = B * (1 + Q) * H * cols * 4 + 2 * B * Q * H * xb + pbytes
         res[kind] = {"avg_us": round(avg, 2), "median_us": round(med, 2), "bytes": nbytes,
                      "achieved_GBs": round(nbytes / (avg * 1e-6) / 1e9, 1),
