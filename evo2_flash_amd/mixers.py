@@ -413,7 +413,7 @@ class HyenaMixerBase(nn.Module):
         contiguous, hidden_states' shape and dtype) the projection writes its
         rows there directly and the padding rows are zeroed, with no copy."""
         g = torch.cat(parts, dim=0) if len(parts) > 1 else parts[0]
-        if (output is not None and output.shape == hidden_states.shape
+        if (output is not None and output.dim() == 2 and output.shape == hidden_states.shape
                 and output.dtype == hidden_states.dtype and output.is_contiguous()):
             self.out_proj(g, out=output[:n])
             if n < output.shape[0]:
