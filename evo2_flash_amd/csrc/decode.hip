@@ -387,7 +387,7 @@ __global__ __launch_bounds__(256) void hcm_decode_split_kernel(DecodeArgs a) {
       static_cast<int>(WT ? (126 * a.wi1 + a.H) * 2 : ((int64_t)(a.H - 1) * a.wi0 + 128) * 2),
       0x00020000);
 
-  // Taps stay packed as loaded (bf16 pairs) and are widened at use (145
+  // Taps stay packed as loaded (bf16 pairs) and are widened at use (149
   // VGPRs: three waves per SIMD).  WT: tw[j][l] = (h0, h0+1) of
   // tap k; otherwise tw[j][2c], tw[j][2c+1] = taps (4m..4m+3) of channel h0+c.
   // They go out before the slot lookup, the window columns after it.
@@ -413,10 +413,42 @@ __global__ __launch_bounds__(256) void hcm_decode_split_kernel(DecodeArgs a) {
       }
     }
   }
+  // wave 0's epilogue operands that do not depend on the slot either (the
+  // last tap and D) go out with the taps: fetched after the stores, they put
+  // a memory round trip at the end of every workgroup
+  uint32_t lastraw = 0u, draw = 0u;
+  // and so do its short-filter inputs that do not depend on the slot
+  uint32_t zraw[3], wsraw[9];
+  if (m == 0) {
+    if constexpr (WT) lastraw = *reinterpret_cast<const uint32_t *>(w + (int64_t)127 * a.wi1 + hc);
+    else lastraw = pair_bf(w[(int64_t)hc * a.wi0 + 127], w[(int64_t)(hc + 1) * a.wi0 + 127]);
+    if constexpr (HAS_D) draw = *reinterpret_cast<const uint32_t *>(a.D + hc);
+    const uint32_t *zr = reinterpret_cast<const uint32_t *>(a.z + b * a.sz + 3 * (int64_t)hc);
+    const uint32_t *wsp = reinterpret_cast<const uint32_t *>(a.ws + 9 * (int64_t)hc);
+#pragma unroll
+    for (int i = 0; i < 3; ++i) zraw[i] = zr[i];
+#pragma unroll
+    for (int i = 0; i < 9; ++i) wsraw[i] = wsp[i];
+  }
   __builtin_amdgcn_sched_barrier(0);
   int64_t blk;
   const bool live = row_slot(a, b, blk);  // uniform
   float *s = a.st + blk * a.is0 + hc;  // is1 == 1: the pair is one float2
+  // wave 0's conv window goes out before the window columns: the column
+  // loads return in order, so a load issued after them would hold the short
+  // filter until the whole window had arrived
+  uint32_t c0raw[3], c1raw[3];
+  uint32_t *c0p = nullptr, *c1p = nullptr;
+  if (m == 0) {
+    bf16_t *cbase = a.cs + blk * a.cs0 + 3 * (int64_t)hc;
+    c0p = reinterpret_cast<uint32_t *>(cbase);
+    c1p = reinterpret_cast<uint32_t *>(cbase + a.cs2);
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      c0raw[i] = c0p[i];
+      c1raw[i] = c1p[i];
+    }
+  }
   // The window moves through buffer loads and stores on a descriptor of this
   // block's window (records = its byte extent, checked on the host to fit 32
   // bits): one lane offset in a VGPR, the column offset in an SGPR, so no
@@ -445,27 +477,10 @@ __global__ __launch_bounds__(256) void hcm_decode_split_kernel(DecodeArgs a) {
     return (l & 1) ? hi_bf(t) : lo_bf(t);
   };
 
-  // Wave 0: the short filter on the 6 sub-channels of the pair and the gate.
-  uint32_t zraw[3], c1raw[3];
+  // Wave 0: the short filter on the 6 sub-channels of the pair and the gate,
+  // while the window columns are still arriving.
   float x2[2] = {0.f, 0.f}, u[2] = {0.f, 0.f};
-  uint32_t *c0p = nullptr, *c1p = nullptr;
-  if (m == 0) {
-    const uint32_t *zr = reinterpret_cast<const uint32_t *>(a.z + b * a.sz + 3 * (int64_t)hc);
-    const uint32_t *wsp = reinterpret_cast<const uint32_t *>(a.ws + 9 * (int64_t)hc);
-    bf16_t *cbase = a.cs + blk * a.cs0 + 3 * (int64_t)hc;
-    c0p = reinterpret_cast<uint32_t *>(cbase);
-    c1p = reinterpret_cast<uint32_t *>(cbase + a.cs2);
-    uint32_t c0raw[3], wsraw[9];
-#pragma unroll
-    for (int i = 0; i < 3; ++i) {
-      zraw[i] = zr[i];
-      c0raw[i] = c0p[i];
-      c1raw[i] = c1p[i];
-    }
-#pragma unroll
-    for (int i = 0; i < 9; ++i) wsraw[i] = wsp[i];
-    pair_featurize(zraw, c0raw, c1raw, wsraw, x2, u);
-  }
+  if (m == 0) pair_featurize(zraw, c0raw, c1raw, wsraw, x2, u);
 
   float acc[2][4];
 #pragma unroll
@@ -499,15 +514,7 @@ __global__ __launch_bounds__(256) void hcm_decode_split_kernel(DecodeArgs a) {
       }
   }
   if (m != 0 || !active) return;
-  float last[2];
-  if constexpr (WT) {
-    const uint32_t t = *reinterpret_cast<const uint32_t *>(w + (int64_t)127 * a.wi1 + h0);
-    last[0] = lo_bf(t);
-    last[1] = hi_bf(t);
-  } else {
-    last[0] = bf2f(w[(int64_t)h0 * a.wi0 + 127]);
-    last[1] = bf2f(w[(int64_t)(h0 + 1) * a.wi0 + 127]);
-  }
+  const float last[2] = {lo_bf(lastraw), hi_bf(lastraw)};
   float y[2];
 #pragma unroll
   for (int c = 0; c < 2; ++c) {
@@ -528,9 +535,8 @@ __global__ __launch_bounds__(256) void hcm_decode_split_kernel(DecodeArgs a) {
     }
   }
   if constexpr (HAS_D) {
-    const uint32_t dv = *reinterpret_cast<const uint32_t *>(a.D + h0);
-    y[0] = rbf(y[0] + rbf(lo_bf(dv) * u[0]));
-    y[1] = rbf(y[1] + rbf(hi_bf(dv) * u[1]));
+    y[0] = rbf(y[0] + rbf(lo_bf(draw) * u[0]));
+    y[1] = rbf(y[1] + rbf(hi_bf(draw) * u[1]));
   }
   *reinterpret_cast<uint32_t *>(a.out + b * a.so + h0) =
       pack_bf(x2[0] * y[0], x2[1] * y[1]) & live_mask(live);
