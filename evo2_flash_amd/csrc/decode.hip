@@ -445,8 +445,8 @@ __global__ __launch_bounds__(256) void hcm_decode_split_kernel(DecodeArgs a) {
     c1p = reinterpret_cast<uint32_t *>(cbase + a.cs2);
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
-      c0raw[i] = c0p[i];
-      c1raw[i] = c1p[i];
+      c0raw[i] = ld_nt(c0p + i);
+      c1raw[i] = ld_nt(c1p + i);
     }
   }
   // The window moves through buffer loads and stores on a descriptor of this
@@ -456,6 +456,13 @@ __global__ __launch_bounds__(256) void hcm_decode_split_kernel(DecodeArgs a) {
   // shifted stores after the barrier.
   const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(
       a.st + blk * a.is0, 0, static_cast<int>((126 * a.is2 + a.H) * 4), 0x00020000);
+  // The window's loads and stores carry the non-temporal hint: read once and
+  // rewritten once per step, its 2 MB per row are streamed rather than kept
+  // in the caches.  Measured at 7B (64 rows, in graphs): 56.8 us plain, 49.2
+  // with both loads and stores non-temporal, 56.5 with the loads alone; the
+  // whole 27-core step 0.715 -> 0.614 ms, as the 276 MB stream no longer
+  // evicts what the other kernels reuse.  The hcs and hcl kernels keep plain
+  // accesses: the hint there made the step slower (0.617 ms).
   const int ls = 4 * hc;
   float2 v[8][4];
 #pragma unroll
@@ -464,7 +471,7 @@ __global__ __launch_bounds__(256) void hcm_decode_split_kernel(DecodeArgs a) {
     for (int l = 0; l < 4; ++l) {
       const int k = 16 * j + 4 * m + l;
       if (k < 127) {
-        const auto t = __builtin_amdgcn_raw_buffer_load_b64(srs, ls, static_cast<int>(k * a.is2 * 4), 0);
+        const auto t = __builtin_amdgcn_raw_buffer_load_b64(srs, ls, static_cast<int>(k * a.is2 * 4), CPOL_NT);
         v[j][l] = make_float2(__int_as_float(t[0]), __int_as_float(t[1]));
       } else {
         v[j][l] = make_float2(0.f, 0.f);
@@ -509,7 +516,7 @@ __global__ __launch_bounds__(256) void hcm_decode_split_kernel(DecodeArgs a) {
         if (k >= 1 && k < 127) {
           typedef __attribute__((ext_vector_type(2))) int i32x2;
           const i32x2 t = {__float_as_int(v[j][l].x), __float_as_int(v[j][l].y)};
-          __builtin_amdgcn_raw_buffer_store_b64(t, srs, ls, static_cast<int>((k - 1) * a.is2 * 4), 0);
+          __builtin_amdgcn_raw_buffer_store_b64(t, srs, ls, static_cast<int>((k - 1) * a.is2 * 4), CPOL_NT);
         }
       }
   }
@@ -527,11 +534,11 @@ __global__ __launch_bounds__(256) void hcm_decode_split_kernel(DecodeArgs a) {
     y[c] = rbf(((p[0] + p[2]) + (p[1] + p[3])) + last[c] * u[c]);
   }
   if (live) {
-    *reinterpret_cast<float2 *>(s + 126 * a.is2) = make_float2(u[0], u[1]);
+    st_nt(reinterpret_cast<float2 *>(s + 126 * a.is2), make_float2(u[0], u[1]));
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
-      c0p[i] = c1raw[i];
-      c1p[i] = zraw[i];
+      st_nt(c0p + i, c1raw[i]);
+      st_nt(c1p + i, zraw[i]);
     }
   }
   if constexpr (HAS_D) {
