@@ -71,28 +71,21 @@ __device__ __forceinline__ void vmcnt_wait() {
   __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
-// Cache-policy operand of the buffer and direct-to-LDS intrinsics: bit 1 is
-// the non-temporal hint on gfx950.  Streams read or written once per launch
-// (decode state windows, snapshots) carry it.
+// Cache-policy operand of the buffer intrinsics: bit 1 is the non-temporal
+// hint on gfx950.  The hcm decode window, read and rewritten in place once
+// per step, carries it (measured: not the snapshot stores of the verify
+// kernel, not the decode GEMM's weight stream, not the hcs / hcl windows).
 constexpr int CPOL_NT = 2;
 
 // The same hint on plain pointer accesses (clang's non-temporal builtins take
 // clang vector types, not HIP's float2 / float4 structs).
 typedef float nt_f32x2 __attribute__((ext_vector_type(2)));
-typedef float nt_f32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ float2 ld_nt(const float2 *p) {
   const nt_f32x2 v = __builtin_nontemporal_load(reinterpret_cast<const nt_f32x2 *>(p));
   return make_float2(v.x, v.y);
 }
-__device__ __forceinline__ float4 ld_nt(const float4 *p) {
-  const nt_f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const nt_f32x4 *>(p));
-  return make_float4(v.x, v.y, v.z, v.w);
-}
 __device__ __forceinline__ void st_nt(float2 *p, float2 v) {
   __builtin_nontemporal_store(nt_f32x2{v.x, v.y}, reinterpret_cast<nt_f32x2 *>(p));
-}
-__device__ __forceinline__ void st_nt(float4 *p, float4 v) {
-  __builtin_nontemporal_store(nt_f32x4{v.x, v.y, v.z, v.w}, reinterpret_cast<nt_f32x4 *>(p));
 }
 template <typename T>
 __device__ __forceinline__ T ld_nt(const T *p) { return __builtin_nontemporal_load(p); }
