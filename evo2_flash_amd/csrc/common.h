@@ -74,7 +74,8 @@ __device__ __forceinline__ void vmcnt_wait() {
 // Cache-policy operand of the buffer intrinsics: bit 1 is the non-temporal
 // hint on gfx950.  The hcm decode window, read and rewritten in place once
 // per step, carries it (measured: not the snapshot stores of the verify
-// kernel, not the decode GEMM's weight stream, not the hcs / hcl windows).
+// kernel, the decode GEMM's weight stream, the prefill streams, the decode
+// attention's KV pages or the hcs / hcl windows, where it was level or slower).
 constexpr int CPOL_NT = 2;
 
 // The same hint on plain pointer accesses (clang's non-temporal builtins take
