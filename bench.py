@@ -886,8 +886,8 @@ def main(argv=None):
                          "device copy, the reference dispatch for scaling HBM counters")
     args = ap.parse_args(argv)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(DESIGN.md describes how the path would shard). Run with --gpus 1.",
+        print("bench.py measures one GPU only: the mixer path has no multi-GPU form "
+              "(it would shard over sequences and channels). Run with --gpus 1.",
               file=sys.stderr)
         return 2
     if not torch.cuda.is_available():
