@@ -56,8 +56,8 @@ template <int K>
 struct FirGeom {
   static constexpr int KP = (K + 1) & ~1;  // taps padded to even (zero tap first)
   static constexpr int NP = KP / 2;        // tap pairs
-  // rows per sub-tile: 64 for hcm; 32 for hcs, whose smaller staging lets
-  // more workgroups share a CU (its time goes to memory, not arithmetic)
+  // rows per sub-tile: 64 for hcm; 32 for hcs, whose time goes to memory,
+  // not arithmetic (its two z staging buffers keep four workgroups on a CU)
   static constexpr int RS = K > 8 ? 64 : 32;
   static constexpr int NWAVE = 4;          // waves per workgroup
   static constexpr int NT = 64 * NWAVE;    // threads per workgroup
@@ -107,7 +107,12 @@ template <int K, bool HAS_D, bool FUSED>
 __global__ __launch_bounds__(FirGeom<K>::NT, FirGeom<K>::MIN_WAVES) void fir_prefill_kernel(FirArgs p) {
   using G = FirGeom<K>;
   __shared__ __align__(16) bf16_t ring[64][G::PITCH];
-  __shared__ __align__(16) bf16_t zst[FUSED ? G::ZROWS : 1][G::ZPITCH];
+  // z staging: two buffers for the fused 7-tap core (the next sub-tile's rows
+  // load while this one computes, and the one after is issued as soon as a
+  // buffer frees), one otherwise
+  constexpr int NB = (FUSED && K <= 8) ? 2 : 1;
+  __shared__ __align__(16) bf16_t zbuf[NB][FUSED ? G::ZROWS : 1][G::ZPITCH];
+  bf16_t (*zst)[G::ZPITCH] = zbuf[0];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -349,15 +354,39 @@ __global__ __launch_bounds__(FirGeom<K>::NT, FirGeom<K>::MIN_WAVES) void fir_pre
     land();
     fix(S.t0 - 2);
     __syncthreads();
+    if constexpr (NB == 2) {
+      if (S.t0 + G::RS < S.t_end) {
+        zst = zbuf[1];
+        prefetch(S.t0 + G::RS - 2);
+      }
+    }
   }
 
-  for (int s0 = S.t0; s0 < S.t_end; s0 += G::RS) {
+  int bi = 0;
+  for (int s0 = S.t0; s0 < S.t_end; s0 += G::RS, bi ^= 1) {
+    if constexpr (NB == 2) zst = zbuf[bi];
     uint32_t xq[G::RW / 2];  // x2 of this wave's rows, packed row pairs
     produce(s0 + wave * G::RW, s0 - 2, RWC{}, FUSED ? xq : nullptr);
     __syncthreads();  // ring complete; zst free
     const bool more = s0 + G::RS < S.t_end;
+    // NB == 2: the prefetch of two sub-tiles ahead into the buffer just freed;
+    // its loads and this sub-tile's output stores are the vector-memory ops
+    // issued after the next sub-tile's loads (counted for the wait below
+    // when both are whole)
+    int after = -1;
     if constexpr (FUSED) {
-      if (more) prefetch(s0 + G::RS - 2);
+      if constexpr (NB == 1) {
+        if (more) prefetch(s0 + G::RS - 2);
+      } else {
+        const int rs2 = s0 + 2 * G::RS - 2;
+        if (s0 + 2 * G::RS < S.t_end) {
+          prefetch(rs2);
+          if (vec_z && rs2 >= S.a && rs2 + G::ZROWS <= S.t_end)
+            after = (ZW - wave + G::NWAVE - 1) / G::NWAVE;  // this wave's DMA instructions
+        } else {
+          after = 0;
+        }
+      }
     }
 
     // ---- FIR for rows s0 + 16*wave + r, r < 16
@@ -463,7 +492,18 @@ __global__ __launch_bounds__(FirGeom<K>::NT, FirGeom<K>::MIN_WAVES) void fir_pre
     }
     if constexpr (FUSED && !EARLY_LAND) {
       if (more) {
-        land();
+        if constexpr (NB == 2) {
+          // wait for the next sub-tile's rows only: the ops issued after them
+          // are this wave's prefetch and its RW / 2 row-pair stores
+          const int n = full && after >= 0 ? after + G::RW / 2 : -1;  // uniform
+          if (n == G::RW / 2 + 4) vmcnt_wait<G::RW / 2 + 4>();
+          else if (n == G::RW / 2 + 3) vmcnt_wait<G::RW / 2 + 3>();
+          else if (n == G::RW / 2) vmcnt_wait<G::RW / 2>();
+          else land();
+          zst = zbuf[bi ^ 1];
+        } else {
+          land();
+        }
         fix(s0 + G::RS - 2);
       }
     }
