@@ -858,12 +858,15 @@ __global__ __launch_bounds__(256, 2) void fir128_mfma_kernel(FirArgs p, int64_t 
 // windows are the last inputs of cat(old window, segment) (mixers.py:380-382),
 // oldest first.  The update is in place, and for a segment shorter than the
 // window destination column q reads old column q + (e - a), so every value is
-// gathered into registers first and written after a workgroup barrier.  A
-// workgroup owns 64 channels of one segment: with W = 127 its four waves take
-// 32 columns each, with W = 6 each wave owns its own 64 channels.  The conv
-// window (2 columns of the 3 sub-channels) rides along with the first wave of
-// each channel block.  u near the segment start is recomputed through the
-// short filter from z and the old conv window (FUSED), or read from u rows.
+// gathered first and written after a workgroup barrier.  A workgroup owns 64
+// channels of one segment (lane = channel for the gather: coalesced z rows);
+// its waves park the values in LDS column by column, and after the barrier
+// the block goes out in channel-major order, consecutive lanes on
+// consecutive columns, so a window row is written as contiguous words rather
+// than one word per channel.  The conv window (2 columns of the 3
+// sub-channels) rides along with the first wave.  u near the segment start
+// is recomputed through the short filter from z and the old conv window
+// (FUSED), or read from u rows.
 struct WinArgs {
   const bf16_t *x; int64_t sx;              // z (FUSED) or u rows
   const bf16_t *ws;
@@ -877,67 +880,81 @@ struct WinArgs {
   int64_t num_blocks;
 };
 
-template <int W>
+template <int W, int S>
 __global__ __launch_bounds__(256) void window_update_kernel(WinArgs p) {
-  constexpr int NW = W > 32 ? 4 : 1;          // waves per channel block
-  constexpr int CPW = (W + NW - 1) / NW;      // window columns per wave
-  constexpr int CB = 4 / NW;                  // channel blocks per workgroup
+  constexpr int PER = (W + S - 1) / S;  // window columns per workgroup when split
+  constexpr int CPW = (PER + 3) / 4;    // columns per wave per round
+  constexpr int VP = 65;                // LDS floats per staged column (odd: no bank conflicts)
+  __shared__ float vbuf[W][VP];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int part = wave % NW;
-  const int c = (blockIdx.y * CB + wave / NW) * 64 + lane;
+  const int cb = blockIdx.y * 64;
+  const int c = cb + lane;
   const bool active = c < p.H;
   const int cl = active ? c : p.H - 1;
   const int seg = blockIdx.x;
   const int64_t a = p.seq[3 * seg], e = p.seq[3 * seg + 1];
   const int64_t blk = p.blocks[seg * p.sblk];
   if (e <= a || blk < 0 || blk >= p.num_blocks) return;  // uniform over the block
+  // A segment of at least W + 2 rows reads no old window, so its columns are
+  // split over the S workgroups of blockIdx.z; a shorter one is done whole
+  // by the first, which reads every old value before it writes any.
+  const bool split = e - a >= W + 2;
+  if (!split && blockIdx.z != 0) return;
+  const int r0 = split ? blockIdx.z : 0, r1 = split ? blockIdx.z + 1 : S;
   const bool init = p.seq[3 * seg + 2] != 0;
   const bf16_t *conv_old = init ? p.cs + blk * p.cs0 : nullptr;
   ShortCtx ctx{p.x, p.sx, conv_old, p.cs1, p.cs2, a, init};
-  float *st = p.st + blk * p.st0 + (int64_t)cl * p.st1;
+  float *stb = p.st + blk * p.st0;
+  float *st = stb + (int64_t)cl * p.st1;
+  const int64_t last = e - 1;
 
-  // ---- gather
-  const int q0 = part * CPW;
-  const int64_t src0 = e - W + q0;
-  float v[CPW];
-  if (p.fused) {
-    float wsf[2][3], zm2[2], zm1[2];
+  // ---- gather, one round per split.  Every load of a round is issued
+  // before the first use: rows past the segment end (padding columns) are
+  // clamped to its last row and their values discarded, and a window that
+  // reaches before the segment start takes the slower per-row path.
+  for (int round = r0; round < r1; ++round) {  // uniform
+    const int q0 = round * PER + wave * CPW;
+    const int qn = min(round * PER + PER, W);
+    const int64_t src0 = e - W + q0;
+    float v[CPW];
+    if (p.fused) {
+      float wsf[2][3], zz[CPW + 2][2];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+      for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int j = 0; j < 3; ++j) wsf[i][j] = bf2f(p.ws[(3 * (int64_t)cl + 1 + i) * 3 + j]);
-      zm2[i] = z_at(ctx, src0 - 2, 3 * (int64_t)cl + 1 + i);
-      zm1[i] = z_at(ctx, src0 - 1, 3 * (int64_t)cl + 1 + i);
-    }
+        for (int j = 0; j < 3; ++j) wsf[i][j] = bf2f(p.ws[(3 * (int64_t)cl + 1 + i) * 3 + j]);
+      if (src0 - 2 >= a) {  // uniform
 #pragma unroll
-    for (int q = 0; q < CPW; ++q) {
-      const int64_t src = src0 + q;
-      float y[2];
+        for (int r = 0; r < CPW + 2; ++r)
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        // columns past the window (the last wave's padding) would read row e
-        const float z0 = (q0 + q < W) ? z_at(ctx, src, 3 * (int64_t)cl + 1 + i) : 0.0f;
-        y[i] = short_out(zm2[i], zm1[i], z0, wsf[i]);
-        zm2[i] = zm1[i];
-        zm1[i] = z0;
+          for (int i = 0; i < 2; ++i)
+            zz[r][i] = bf2f(p.x[min(src0 - 2 + r, last) * p.sx + 3 * (int64_t)cl + 1 + i]);
+      } else {
+#pragma unroll
+        for (int r = 0; r < CPW + 2; ++r)
+#pragma unroll
+          for (int i = 0; i < 2; ++i)
+            zz[r][i] = src0 - 2 + r <= last ? z_at(ctx, src0 - 2 + r, 3 * (int64_t)cl + 1 + i)
+                                            : 0.0f;
       }
-      v[q] = rbf(y[0] * y[1]);
+#pragma unroll
+      for (int q = 0; q < CPW; ++q)
+        v[q] = rbf(short_out(zz[q][0], zz[q + 1][0], zz[q + 2][0], wsf[0]) *
+                   short_out(zz[q][1], zz[q + 1][1], zz[q + 2][1], wsf[1]));
+    } else {
+#pragma unroll
+      for (int q = 0; q < CPW; ++q) v[q] = bf2f(p.x[min(max(src0 + q, a), last) * p.sx + cl]);
     }
-  } else {
 #pragma unroll
     for (int q = 0; q < CPW; ++q) {
-      const int64_t src = src0 + q;
-      v[q] = (src >= a && q0 + q < W) ? bf2f(p.x[src * p.sx + cl]) : 0.0f;
+      if (q0 + q >= qn) break;  // uniform
+      if (src0 + q < a) v[q] = init ? st[(q0 + q + (e - a)) * p.st2] : 0.0f;
+      vbuf[q0 + q][lane] = v[q];
     }
-  }
-#pragma unroll
-  for (int q = 0; q < CPW; ++q) {
-    const int64_t src = src0 + q;
-    if (src < a) v[q] = (init && q0 + q < W) ? st[(q0 + q + (e - a)) * p.st2] : 0.0f;
   }
   bf16_t cv[2][3];
-  const bool do_conv = p.conv && part == 0;
+  const bool do_conv = p.conv && wave == 0 && blockIdx.z == 0;
   bf16_t *cw = p.cs + blk * p.cs0;
   if (do_conv) {
 #pragma unroll
@@ -951,14 +968,20 @@ __global__ __launch_bounds__(256) void window_update_kernel(WinArgs p) {
       }
     }
   }
-  __syncthreads();  // every old value is in registers before any write
+  __syncthreads();  // every old value is read before any write
 
-  // ---- write
-  if (!active) return;
-#pragma unroll
-  for (int q = 0; q < CPW; ++q)
-    if (q0 + q < W) st[(q0 + q) * p.st2] = v[q];
-  if (do_conv) {
+  // ---- write columns [c0, c1) of the block's 64 channels
+  const int c0 = r0 * PER, c1 = min(W, r1 * PER), ncol = c1 - c0;
+  if (p.st2 == 1) {
+    const int nch = min(64, p.H - cb);
+    for (int f = threadIdx.x; f < nch * ncol; f += 256) {
+      const int cc = f / ncol, q = c0 + f - cc * ncol;
+      stb[(int64_t)(cb + cc) * p.st1 + q] = vbuf[q][cc];
+    }
+  } else if (active) {
+    for (int q = c0; q < c1; ++q) st[q * p.st2] = vbuf[q][lane];
+  }
+  if (do_conv && active) {
 #pragma unroll
     for (int q = 0; q < 2; ++q)
 #pragma unroll
@@ -974,13 +997,13 @@ static void launch_fir(const FirArgs &a, int64_t ntiles, hipStream_t st) {
 
 static int launch_window(const WinArgs &w, int K, int64_t nseq, hipStream_t st) {
   if (nseq == 0) return EVO2_OK;
-  if (K == 128) {
-    dim3 grid(static_cast<unsigned>(nseq), static_cast<unsigned>(cdiv(w.H, 64)));
-    hipLaunchKernelGGL(window_update_kernel<127>, grid, dim3(256), 0, st, w);
-  } else {
-    dim3 grid(static_cast<unsigned>(nseq), static_cast<unsigned>(cdiv(w.H, 256)));
-    hipLaunchKernelGGL(window_update_kernel<6>, grid, dim3(256), 0, st, w);
-  }
+  const unsigned gy = static_cast<unsigned>(cdiv(w.H, 64));
+  if (K == 128)
+    hipLaunchKernelGGL((window_update_kernel<127, 4>), dim3(static_cast<unsigned>(nseq), gy, 4),
+                       dim3(256), 0, st, w);
+  else
+    hipLaunchKernelGGL((window_update_kernel<6, 1>), dim3(static_cast<unsigned>(nseq), gy, 1),
+                       dim3(256), 0, st, w);
   return check_launch("prefill window update");
 }
 
