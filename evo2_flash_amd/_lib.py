@@ -161,6 +161,16 @@ SIGNATURES = {
         _c_p, _c_i64, _c_i64, _c_i64, _c_i64,     # out, so, M, N, K
         _c_p,                                     # stream
     ],
+    "evo2_fp8_pack_weight": [
+        _c_p, _c_i64, _c_p, _c_i64, _c_i64,       # w8, sw, wp, N, K
+        _c_p,                                     # stream
+    ],
+    "evo2_fp8_gemm_packed": [
+        _c_p, _c_i64, _c_p,                       # x8, sx, wp
+        _c_p, _c_p, _c_p,                         # x_scale, w_scale, bias
+        _c_p, _c_i64, _c_i64, _c_i64, _c_i64,     # out, so, M, N, K
+        _c_p,                                     # stream
+    ],
     "evo2_fp8_gemm_persist_order": [_c_i64, _c_i64, ctypes.c_int, _c_p, _c_p],
     "evo2_fp8_fast_accum_gemm": [
         _c_p, _c_i64, _c_p, _c_i64,               # a8, sa, b_t, sb

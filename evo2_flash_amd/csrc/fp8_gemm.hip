@@ -504,7 +504,10 @@ static inline dim3 stream_grid(int64_t gx, int64_t gy) {
   return dim3(static_cast<unsigned>(8 * gy * cdiv(gx, 8)));
 }
 
-template <int WPG>  // waves per workgroup (2, 3 or 4): 16 W rows each
+// PACKED: the weight in the decode layout written by fp8_pack_kernel (each
+// wave's 16 rows x 128 bytes of a K step are one contiguous 2 KB block, in
+// the order the fragments are loaded), so the weight stream is sequential.
+template <int WPG, bool PACKED>  // waves per workgroup (2, 3 or 4): 16 W rows each
 __global__ __launch_bounds__(256) void fp8_gemm_small_kernel(GemmArgs p) {
   // one variable per stage: the compiler then sees which stage each
   // direct-to-LDS load writes and waits only for that stage's loads
@@ -544,7 +547,9 @@ __global__ __launch_bounds__(256) void fp8_gemm_small_kernel(GemmArgs p) {
     xoff[j] = min(row, mrows - 1) * (int)p.sx + 16 * lchunk;
   }
   // weight rows of this wave, straight into registers
-  const uint8_t *wrow = p.w + (int64_t)min(n0 + 16 * wave + lr, p.N - 1) * p.sw + 32 * g;
+  const uint8_t *wrow =
+      PACKED ? p.w + (int64_t)min((n0 >> 4) + wave, (p.N >> 4) - 1) * KT * 2048 + 16 * lane
+             : p.w + (int64_t)min(n0 + 16 * wave + lr, p.N - 1) * p.sw + 32 * g;
   i32x8 wf[S_DEPTH];
   auto issue = [&](auto slot, int k) __attribute__((always_inline)) {
     constexpr int J = decltype(slot)::value;
@@ -556,8 +561,10 @@ __global__ __launch_bounds__(256) void fp8_gemm_small_kernel(GemmArgs p) {
       __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint4 *>(xbase + k0 + xoff[j]),
                                        (lds_void *)(stage_of(slot) + xblock(j) * 1024), 16,
                                        0, 0);
-    const uint4 a0 = *reinterpret_cast<const uint4 *>(wrow + k0);
-    const uint4 a1 = *reinterpret_cast<const uint4 *>(wrow + k0 + 16);
+    // packed: the step's block, halves 1 KB apart; else bytes [32 g, 32 g + 32)
+    const int64_t wo = PACKED ? min(k, KT - 1) * 2048 : k0;
+    const uint4 a0 = *reinterpret_cast<const uint4 *>(wrow + wo);
+    const uint4 a1 = *reinterpret_cast<const uint4 *>(wrow + wo + (PACKED ? 1024 : 16));
     wf[J] = i32x8{(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w, (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
   };
   f32x4 acc[4];
@@ -654,10 +661,27 @@ __global__ __launch_bounds__(256) void fp8_gemm_small_kernel(GemmArgs p) {
   }
 }
 
-template <int WPG>
+template <int WPG, bool PACKED>
 static void launch_small(const GemmArgs &a, hipStream_t stream) {
   const dim3 grid = stream_grid(cdiv(a.N, 16 * WPG), cdiv(a.M, S_ROWS));
-  hipLaunchKernelGGL((fp8_gemm_small_kernel<WPG>), grid, dim3(64 * WPG), 0, stream, a);
+  hipLaunchKernelGGL((fp8_gemm_small_kernel<WPG, PACKED>), grid, dim3(64 * WPG), 0, stream, a);
+}
+
+// Decode weight layout: 16-row group G, K step k (128 bytes), half h, lane
+// l = r + 16 q holds W[16 G + r][128 k + 32 q + 16 h .. + 16) at byte
+// ((G * K / 128 + k) * 2 + h) * 1024 + 16 l.  One thread per 16 bytes.
+__global__ __launch_bounds__(256) void fp8_pack_kernel(const uint8_t *w, int64_t sw, uint8_t *wp,
+                                                       int64_t chunks, int KT) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= chunks) return;
+  const int l = static_cast<int>(i & 63);
+  const int64_t blk = i >> 6;  // (G * KT + k) * 2 + h
+  const int h = static_cast<int>(blk & 1);
+  const int64_t gk = blk >> 1;
+  const int k = static_cast<int>(gk % KT);
+  const int64_t G = gk / KT;
+  const uint8_t *src = w + (16 * G + (l & 15)) * sw + 128 * k + 32 * (l >> 4) + 16 * h;
+  *reinterpret_cast<uint4 *>(wp + 16 * i) = *reinterpret_cast<const uint4 *>(src);
 }
 
 // The weight-streaming kernel reads the weight once per 64-row block, so its
@@ -714,6 +738,34 @@ static int cu_count() {
   return cached[dev];
 }
 
+// The weight-streaming kernel with the waves per workgroup (16 W rows each)
+// whose workgroups fill the CUs most evenly (groups / (rounds x CUs)), the
+// larger on a tie.  Measured with the weights streaming from HBM (9 rotating
+// weights, more than the 256 MB infinity cache holds), K = 4096: the 7B
+// decode in_proj (M=64, N=12288) 17.1 us with 3 waves against 18.9 with 4 and
+// 21.8 with 2; at M = 128 / 192 / 256 / 512, N = 12288: 25.9 / 37.1 / 42.0 /
+// 75.8 us, the fastest of this kernel and of workgroups covering 2-4 row
+// blocks per weight load (which only won while the weights stayed
+// cache-resident).
+template <bool PACKED>
+static void launch_stream(const GemmArgs &a, hipStream_t st) {
+  const int ncu = cu_count() > 0 ? cu_count() : 256;
+  const int64_t yblocks = cdiv(a.M, S_ROWS);
+  int best_w = 4;
+  double best_eff = -1.0;
+  for (int w = 4; w >= 2; --w) {
+    const int64_t groups = cdiv(a.N, 16 * w) * yblocks;
+    const double eff = double(groups) / double(cdiv(groups, ncu) * ncu);
+    if (eff > best_eff + 1e-9) {
+      best_eff = eff;
+      best_w = w;
+    }
+  }
+  if (best_w == 4) launch_small<4, PACKED>(a, st);
+  else if (best_w == 3) launch_small<3, PACKED>(a, st);
+  else launch_small<2, PACKED>(a, st);
+}
+
 extern "C" int evo2_fp8_quantize(const void *x, int64_t sx, void *q, int64_t sq,
                                  const float *scale, int64_t rows, int64_t K, void *stream) {
   if (rows < 0 || K < 0 || rows > 65535 * 64LL)
@@ -761,30 +813,8 @@ extern "C" int evo2_fp8_gemm(const void *x8, int64_t sx, const void *w8, int64_t
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (K % S_BK == 0 && sx * S_ROWS < (int64_t(1) << 31) &&
       (M <= S_ROWS || cdiv(M, S_ROWS) * N <= STREAM_MAX_WORK)) {
-    // The weight-streaming kernel, over ceil(M / 64) blocks of 64 rows, with
-    // the waves per workgroup (16 W rows each) whose workgroups fill the CUs
-    // most evenly (groups / (rounds x CUs)), the larger on a tie.  Measured
-    // with the weights streaming from HBM (9 rotating weights, more than the
-    // 256 MB infinity cache holds), K = 4096: the 7B decode in_proj (M=64,
-    // N=12288) 17.1 us with 3 waves against 18.9 with 4 and 21.8 with 2; at
-    // M = 128 / 192 / 256 / 512, N = 12288: 25.9 / 37.1 / 42.0 / 75.8 us, the
-    // fastest of this kernel and of workgroups covering 2-4 row blocks per
-    // weight load (which only won while the weights stayed cache-resident).
-    const int ncu = cu_count() > 0 ? cu_count() : 256;
-    const int64_t yblocks = cdiv(M, S_ROWS);
-    int best_w = 4;
-    double best_eff = -1.0;
-    for (int w = 4; w >= 2; --w) {
-      const int64_t groups = cdiv(N, 16 * w) * yblocks;
-      const double eff = double(groups) / double(cdiv(groups, ncu) * ncu);
-      if (eff > best_eff + 1e-9) {
-        best_eff = eff;
-        best_w = w;
-      }
-    }
-    if (best_w == 4) launch_small<4>(a, st);
-    else if (best_w == 3) launch_small<3>(a, st);
-    else launch_small<2>(a, st);
+    // the weight-streaming kernel over ceil(M / 64) blocks of 64 rows
+    launch_stream<false>(a, st);
     return check_launch("fp8_gemm");
   }
   const int64_t tiles_n = cdiv(N, G_BN), tiles_m = cdiv(M, G_BM);
@@ -803,6 +833,50 @@ extern "C" int evo2_fp8_gemm(const void *x8, int64_t sx, const void *w8, int64_t
   dim3 grid(static_cast<unsigned>(tiles_n), static_cast<unsigned>(tiles_m));
   hipLaunchKernelGGL(fp8_gemm_kernel, grid, dim3(256), 0, st, a);
   return check_launch("fp8_gemm");
+}
+
+extern "C" int evo2_fp8_pack_weight(const void *w8, int64_t sw, void *wp, int64_t N, int64_t K,
+                                    void *stream) {
+  if (N <= 0 || K <= 0 || N % 16 || K % S_BK)
+    return fail(EVO2_ERR_UNSUPPORTED,
+                "fp8_pack_weight: N=%lld must be a multiple of 16 and K=%lld of %d", (long long)N,
+                (long long)K, S_BK);
+  if (!w8 || !wp) return fail(EVO2_ERR_INVALID, "fp8_pack_weight: null pointer argument");
+  if (sw < K || sw % 16 || reinterpret_cast<uintptr_t>(w8) % 16 ||
+      reinterpret_cast<uintptr_t>(wp) % 16)
+    return fail(EVO2_ERR_UNSUPPORTED, "fp8_pack_weight: rows must be 16-byte aligned");
+  const int64_t chunks = N * K / 16;
+  if (cdiv(chunks, 256) > 0x7fffffff) return fail(EVO2_ERR_UNSUPPORTED, "fp8_pack_weight: too large");
+  hipLaunchKernelGGL(fp8_pack_kernel, dim3(static_cast<unsigned>(cdiv(chunks, 256))), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint8_t *>(w8), sw,
+                     static_cast<uint8_t *>(wp), chunks, static_cast<int>(K / S_BK));
+  return check_launch("fp8_pack_weight");
+}
+
+extern "C" int evo2_fp8_gemm_packed(const void *x8, int64_t sx, const void *wp,
+                                    const float *x_scale, const float *w_scale, const void *bias,
+                                    void *out, int64_t so, int64_t M, int64_t N, int64_t K,
+                                    void *stream) {
+  if (M < 0 || N <= 0 || K <= 0)
+    return fail(EVO2_ERR_INVALID, "fp8_gemm_packed: bad sizes M=%lld N=%lld K=%lld", (long long)M,
+                (long long)N, (long long)K);
+  if (M == 0) return EVO2_OK;
+  if (!x8 || !wp || !x_scale || !w_scale || !out)
+    return fail(EVO2_ERR_INVALID, "fp8_gemm_packed: null pointer argument");
+  if (N % 16 || K % S_BK)
+    return fail(EVO2_ERR_UNSUPPORTED,
+                "fp8_gemm_packed: N=%lld must be a multiple of 16 and K=%lld of %d", (long long)N,
+                (long long)K, S_BK);
+  if (sx % 16 || reinterpret_cast<uintptr_t>(x8) % 16 || reinterpret_cast<uintptr_t>(wp) % 16)
+    return fail(EVO2_ERR_UNSUPPORTED, "fp8_gemm_packed: operands must be 16-byte aligned");
+  if (sx * S_ROWS >= (int64_t(1) << 31) || cdiv(M, S_ROWS) * cdiv(N, 32) * 8 > 0x7fffffff ||
+      N > 0x7fffffff)
+    return fail(EVO2_ERR_UNSUPPORTED, "fp8_gemm_packed: problem too large");
+  GemmArgs a{static_cast<const uint8_t *>(x8), sx, static_cast<const uint8_t *>(wp), K, x_scale,
+             w_scale, static_cast<const bf16_t *>(bias), static_cast<bf16_t *>(out), so,
+             static_cast<int>(M), static_cast<int>(N), static_cast<int>(K)};
+  launch_stream<true>(a, static_cast<hipStream_t>(stream));
+  return check_launch("fp8_gemm_packed");
 }
 
 extern "C" int64_t evo2_fp8_gemm_persist_order(int64_t tiles_n, int64_t tiles_m, int ncu, int32_t *bn,

@@ -62,16 +62,77 @@ def fp8_gemm(x8, w8, x_scale, w_scale, bias=None, out=None):
     return out
 
 
-def static_fp8_linear(x, weight, input_scale, weight_scale, bias=None, out=None):
+PACK_MAX_ROWS = 64  # rows up to which a packed weight copy is used
+
+
+def packable(N, K):
+    """Whether an (N, K) weight has a decode layout (fp8_pack_weight)."""
+    return N % 16 == 0 and K % 128 == 0
+
+
+def fp8_pack_weight(w8):
+    """The decode layout of an (N, K) e4m3 weight (N a multiple of 16, K of
+    128): each 16-row group's 128-byte K step as one contiguous 2 KB block,
+    in the order the decode GEMM loads it.  Returned as an (N, K) e4m3
+    tensor whose bytes are in that order (only fp8_gemm_packed reads it)."""
+    _lib.require_device(w8)
+    if w8.dtype != E4M3 or w8.dim() != 2:
+        raise ValueError("fp8_pack_weight: w8 must be an (N, K) float8_e4m3fn tensor")
+    N, K = w8.shape
+    if not packable(N, K):
+        raise ValueError(f"fp8_pack_weight: N={N} must be a multiple of 16 and K={K} of 128")
+    if w8.stride(1) != 1 or w8.stride(0) % 16:
+        w8 = w8.contiguous()
+    wp = torch.empty(N, K, dtype=E4M3, device=w8.device)
+    _lib.call("evo2_fp8_pack_weight", _lib.ptr(w8), w8.stride(0), _lib.ptr(wp), N, K,
+              _lib.stream_of(w8))
+    return wp
+
+
+def fp8_gemm_packed(x8, wp, x_scale, w_scale, bias=None, out=None):
+    """fp8_gemm with the weight in the decode layout (fp8_pack_weight); the
+    same result bits.  For decode-sized M (<= 64 rows)."""
+    _lib.require_device(x8, wp, x_scale, w_scale, bias)
+    if x8.dtype != E4M3 or wp.dtype != E4M3:
+        raise ValueError("fp8_gemm_packed operands must be float8_e4m3fn")
+    M, K = x8.shape
+    N, K2 = wp.shape
+    if K != K2 or not wp.is_contiguous():
+        raise ValueError(f"fp8_gemm_packed: wp must be a packed (N, {K}) weight")
+    if x8.stride(1) != 1:
+        x8 = x8.contiguous()
+    xs = x_scale.to(torch.float32).reshape(1)
+    ws = w_scale.to(torch.float32).reshape(1)
+    if bias is not None:
+        bias = bias.to(torch.bfloat16).contiguous()
+    if out is None:
+        out = torch.empty(M, N, dtype=torch.bfloat16, device=x8.device)
+    elif (out.dtype != torch.bfloat16 or out.shape != (M, N) or out.stride(1) != 1
+          or out.device != x8.device):
+        raise ValueError(f"fp8_gemm_packed: out must be ({M}, {N}) bf16 on {x8.device} with "
+                         f"unit column stride, got {tuple(out.shape)} {out.dtype}")
+    _lib.call("evo2_fp8_gemm_packed", _lib.ptr(x8), x8.stride(0), _lib.ptr(wp),
+              _lib.ptr(xs), _lib.ptr(ws), _lib.ptr(bias), _lib.ptr(out), out.stride(0),
+              M, N, K, _lib.stream_of(x8))
+    return out
+
+
+def static_fp8_linear(x, weight, input_scale, weight_scale, bias=None, out=None, packed=None):
     """vLLM's static W8A8 linear: (..., K) bf16 -> (..., N) bf16; a 2-D x may
-    write its result into `out` (M, N) bf16 with unit column stride."""
+    write its result into `out` (M, N) bf16 with unit column stride.  With
+    `packed` (fp8_pack_weight(weight)), inputs of at most 64 rows take the
+    decode GEMM on it (the same result bits)."""
     K = x.shape[-1]
     x8 = quantize_input(x.reshape(-1, K), input_scale)
+    gemm = fp8_gemm
+    w = weight
+    if packed is not None and x8.shape[0] <= PACK_MAX_ROWS:
+        gemm, w = fp8_gemm_packed, packed
     if out is not None:
         if x.dim() != 2 or out.shape != (x.shape[0], weight.shape[0]) or out.stride(1) != 1:
             raise ValueError("static_fp8_linear: out must be (M, N) with unit column stride")
-        return fp8_gemm(x8, weight, input_scale, weight_scale, bias, out=out)
-    out = fp8_gemm(x8, weight, input_scale, weight_scale, bias)
+        return gemm(x8, w, input_scale, weight_scale, bias, out=out)
+    out = gemm(x8, w, input_scale, weight_scale, bias)
     return out.reshape(*x.shape[:-1], weight.shape[0])
 
 
@@ -95,6 +156,26 @@ class Fp8StaticLinear(nn.Module):
         self.bias = (nn.Parameter(torch.zeros(out_features, dtype=torch.bfloat16, device=device),
                                   requires_grad=False) if bias else None)
 
+    def decode_weight(self):
+        """The weight in the decode layout, made on first use and again after
+        the weight changes (kept beside the checkpoint copy; not state).  None
+        while a HIP graph is being captured and no copy exists yet, and for
+        shapes without a decode layout."""
+        w = self.weight
+        if not packable(*w.shape) or not w.is_cuda:
+            return None
+        key = (w.data_ptr(), w._version)
+        cached = getattr(self, "_decode_w", None)
+        if cached is not None and cached[0] == key:
+            return cached[1]
+        if torch.cuda.is_current_stream_capturing():
+            return None
+        wp = fp8_pack_weight(w.detach())
+        self._decode_w = (key, wp)
+        return wp
+
     def forward(self, x, out=None):
+        rows = x.numel() // max(x.shape[-1], 1)
+        packed = self.decode_weight() if 0 < rows <= PACK_MAX_ROWS else None
         return static_fp8_linear(x, self.weight, self.input_scale, self.weight_scale,
-                                 self.bias, out=out), None
+                                 self.bias, out=out, packed=packed), None

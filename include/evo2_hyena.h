@@ -372,6 +372,38 @@ int evo2_fp8_gemm(const void *x8, int64_t sx, const void *w8, int64_t sw,
                   void *out, int64_t so, int64_t M, int64_t N, int64_t K, void *stream);
 
 /*
+ * The decode layout of an e4m3 weight for evo2_fp8_gemm_packed: w8 (N, K),
+ * row stride sw bytes (16-byte aligned rows), into wp (N * K bytes, 16-byte
+ * aligned).  With KT = K / 128, byte b of the 16-byte chunk
+ * ((G * KT + k) * 2 + h) * 64 + r + 16 q of wp is w8[16 G + r][128 k + 32 q
+ * + 16 h + b]: each 16-row group's 128-byte K step is one contiguous 2 KB
+ * block, in the order the decode kernel's fragments load it.  N must be a
+ * multiple of 16 and K of 128.  Asynchronous on `stream`.
+ *
+ * No counterpart in the reference (its weights stay in the checkpoint
+ * layout): a one-time re-layout, kept beside the checkpoint copy, for
+ * decode-sized GEMMs that stream the whole weight per step.
+ */
+int evo2_fp8_pack_weight(const void *w8, int64_t sw, void *wp, int64_t N, int64_t K,
+                         void *stream);
+
+/*
+ * evo2_fp8_gemm with the weight in the decode layout written by
+ * evo2_fp8_pack_weight (same x8, scales, bias, out and result bits as
+ * evo2_fp8_gemm on the unpacked weight; N a multiple of 16, K of 128).  Runs
+ * the weight-streaming kernel over ceil(M / 64) blocks of 64 rows, so it is
+ * meant for M <= 64 (a decode step's in_proj).  The weight stream is
+ * sequential per wave: the 7B decode in_proj (M=64, K=4096, N=12288) with the
+ * weights streaming from HBM takes ~15.4 us against ~17.4 us unpacked.
+ *
+ * No counterpart in the reference: the decode-step form of the in_proj GEMM
+ * (mixers.py:741-757, 1076-1092) for callers that keep a packed copy.
+ */
+int evo2_fp8_gemm_packed(const void *x8, int64_t sx, const void *wp,
+                         const float *x_scale, const float *w_scale, const void *bias,
+                         void *out, int64_t so, int64_t M, int64_t N, int64_t K, void *stream);
+
+/*
  * The order in which evo2_fp8_gemm's persistent kernel (one workgroup per
  * compute unit, 256 x 256 output tiles) walks a grid of tiles_n x tiles_m
  * tiles on a device with ncu compute units: tile t, run by workgroup

@@ -87,6 +87,13 @@ def test_validation_before_launch():
     assert rc == EVO2_ERR_INVALID and b"block_t" in lib.evo2_last_error()
     rc = lib.evo2_fp8_gemm(n, 16, n, 16, n, n, n, n, 0, 64, 4096, 4000, n)
     assert rc == EVO2_ERR_INVALID  # null pointers are checked before K
+    rc = lib.evo2_fp8_pack_weight(n, 4096, n, 12280, 4096, n)
+    assert rc == EVO2_ERR_UNSUPPORTED and b"multiple of 16" in lib.evo2_last_error()
+    rc = lib.evo2_fp8_pack_weight(n, 4096, n, 12288, 4096, n)
+    assert rc == EVO2_ERR_INVALID  # null pointers
+    rc = lib.evo2_fp8_gemm_packed(n, 16, n, n, n, n, n, 0, 64, 4096, 4096, n)
+    assert rc == EVO2_ERR_INVALID  # null pointers
+    assert lib.evo2_fp8_gemm_packed(n, 16, n, n, n, n, n, 0, 0, 4096, 4096, n) == EVO2_OK
     rc = lib.evo2_hyena_hcl_prefill(n, 0, n, n, 0, 0, 0, n, 0, 0, n, 0, 0, n, 0, 0, 0, n, n, 1, n,
                                     0, n, 1, n, 40, n, 0, n, 0, 10, 4096, 2, n)
     assert rc == EVO2_ERR_INVALID and b"block_t" in lib.evo2_last_error()

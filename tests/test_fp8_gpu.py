@@ -129,3 +129,56 @@ def test_config3_shapes(N):
     # dequantised bf16 reference of the unquantised activations, as the north star states it
     ref_bf = ((x8.float() * xs).to(torch.bfloat16).float() @ (w8.float() * ws).to(torch.bfloat16).float().t())
     assert max_rel_err(out, ref_bf) <= 2e-2
+
+
+@pytest.mark.parametrize("M,N,K", [(64, 12288, 4096), (1, 48, 128), (7, 4112, 256),
+                                   (64, 4096, 4096), (100, 512, 384), (32, 24576, 8192)])
+def test_packed_weight_same_bits(M, N, K):
+    """The decode weight layout (fp8_pack_weight) read by fp8_gemm_packed
+    gives the unpacked GEMM's bits, at decode shapes, at N not a multiple of
+    any workgroup's row count (the clamped last row group) and at M > 64
+    (two row blocks); and its bytes are the documented permutation."""
+    from evo2_flash_amd.fp8 import fp8_gemm_packed, fp8_pack_weight
+    gen = torch.Generator(device=DEV).manual_seed(M + N)
+    x8 = (torch.randn(M, K, generator=gen, device=DEV) * 2).to(E4M3)
+    w8 = (torch.randn(N, K, generator=gen, device=DEV) * 0.5).to(E4M3)
+    xs = torch.tensor([0.7], device=DEV)
+    ws = torch.tensor([0.3], device=DEV)
+    bias = (torch.randn(N, generator=gen, device=DEV) * 0.1).to(torch.bfloat16)
+    wp = fp8_pack_weight(w8)
+    perm = w8.view(torch.uint8).view(N // 16, 16, K // 128, 4, 2, 16).permute(0, 2, 4, 3, 1, 5)
+    assert torch.equal(wp.view(torch.uint8).view(-1), perm.reshape(-1))
+    for b in (None, bias):
+        ref = fp8_gemm(x8, w8, xs, ws, b)
+        out = fp8_gemm_packed(x8, wp, xs, ws, b)
+        assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+
+
+def test_linear_module_decode_copy():
+    """Fp8StaticLinear takes its packed copy for inputs of at most 64 rows,
+    the row-major weight above; the copy follows an in-place weight update."""
+    from evo2_flash_amd.fp8 import Fp8StaticLinear
+    N, K = 4096, 1024
+    lin = Fp8StaticLinear(K, N, bias=True, device=DEV)
+    gen = torch.Generator(device=DEV).manual_seed(5)
+    w8, ws = quantize_weight_e4m3(torch.randn(N, K, generator=gen, device=DEV) * 0.02)
+    with torch.no_grad():
+        lin.weight.copy_(w8)
+        lin.weight_scale.copy_(ws)
+        lin.input_scale.fill_(6.0 / 448)
+        lin.bias.copy_((torch.randn(N, generator=gen, device=DEV) * 0.02).to(torch.bfloat16))
+    for M in (1, 64, 65):
+        x = torch.randn(M, K, generator=gen, device=DEV).to(torch.bfloat16)
+        y, _ = lin(x)
+        ref = static_fp8_linear(x, lin.weight, lin.input_scale, lin.weight_scale, lin.bias)
+        assert torch.equal(y.view(torch.int16), ref.view(torch.int16)), M
+    first = lin.decode_weight()
+    assert first is not None and lin.decode_weight() is first
+    w2, _ = quantize_weight_e4m3(torch.randn(N, K, generator=gen, device=DEV) * 0.02)
+    with torch.no_grad():
+        lin.weight.copy_(w2)
+    x = torch.randn(8, K, generator=gen, device=DEV).to(torch.bfloat16)
+    y, _ = lin(x)
+    ref = static_fp8_linear(x, lin.weight, lin.input_scale, lin.weight_scale, lin.bias)
+    assert torch.equal(y.view(torch.int16), ref.view(torch.int16))
+    assert lin.decode_weight() is not first
