@@ -73,9 +73,10 @@ __device__ __forceinline__ void vmcnt_wait() {
 
 // Cache-policy operand of the buffer intrinsics: bit 1 is the non-temporal
 // hint on gfx950.  The hcm decode window, read and rewritten in place once
-// per step, carries it (measured: not the snapshot stores of the verify
-// kernel, the decode GEMM's weight stream, the prefill streams, the decode
-// attention's KV pages or the hcs / hcl windows, where it was level or slower).
+// per step, and the packed decode GEMM's sequential weight stream carry it
+// (measured: not the snapshot stores of the verify kernel, the row-major
+// decode GEMM weight, the prefill streams, the decode attention's KV pages or
+// the hcs / hcl windows, where it was level or slower).
 constexpr int CPOL_NT = 2;
 
 // The same hint on plain pointer accesses (clang's non-temporal builtins take

@@ -29,6 +29,7 @@
 namespace evo2 {
 
 typedef __attribute__((ext_vector_type(8))) int i32x8;
+typedef __attribute__((ext_vector_type(4))) int i32x4;
 typedef __attribute__((ext_vector_type(16))) float f32x16;
 typedef __attribute__((address_space(3))) void lds_void;
 
@@ -561,11 +562,19 @@ __global__ __launch_bounds__(256) void fp8_gemm_small_kernel(GemmArgs p) {
       __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint4 *>(xbase + k0 + xoff[j]),
                                        (lds_void *)(stage_of(slot) + xblock(j) * 1024), 16,
                                        0, 0);
-    // packed: the step's block, halves 1 KB apart; else bytes [32 g, 32 g + 32)
-    const int64_t wo = PACKED ? min(k, KT - 1) * 2048 : k0;
-    const uint4 a0 = *reinterpret_cast<const uint4 *>(wrow + wo);
-    const uint4 a1 = *reinterpret_cast<const uint4 *>(wrow + wo + (PACKED ? 1024 : 16));
-    wf[J] = i32x8{(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w, (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
+    // packed: the step's block, halves 1 KB apart, with the non-temporal
+    // hint (a sequential stream read once: 3-5% faster; on the row-major
+    // weight the hint cost 12%); else bytes [32 g, 32 g + 32) of the row
+    if constexpr (PACKED) {
+      const int64_t wo = min(k, KT - 1) * 2048;
+      const i32x4 a0 = ld_nt(reinterpret_cast<const i32x4 *>(wrow + wo));
+      const i32x4 a1 = ld_nt(reinterpret_cast<const i32x4 *>(wrow + wo + 1024));
+      wf[J] = i32x8{a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+    } else {
+      const uint4 a0 = *reinterpret_cast<const uint4 *>(wrow + k0);
+      const uint4 a1 = *reinterpret_cast<const uint4 *>(wrow + k0 + 16);
+      wf[J] = i32x8{(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w, (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
+    }
   };
   f32x4 acc[4];
 #pragma unroll

@@ -394,7 +394,7 @@ int evo2_fp8_pack_weight(const void *w8, int64_t sw, void *wp, int64_t N, int64_
  * the weight-streaming kernel over ceil(M / 64) blocks of 64 rows, so it is
  * meant for M <= 64 (a decode step's in_proj).  The weight stream is
  * sequential per wave: the 7B decode in_proj (M=64, K=4096, N=12288) with the
- * weights streaming from HBM takes ~15.4 us against ~17.4 us unpacked.
+ * weights streaming from HBM takes ~15.0 us against ~17.4 us unpacked.
  *
  * No counterpart in the reference: the decode-step form of the in_proj GEMM
  * (mixers.py:741-757, 1076-1092) for callers that keep a packed copy.
