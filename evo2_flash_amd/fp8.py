@@ -62,7 +62,14 @@ def fp8_gemm(x8, w8, x_scale, w_scale, bias=None, out=None):
     return out
 
 
-PACK_MAX_ROWS = 64  # rows up to which a packed weight copy is used
+STREAM_MAX_WORK = 60000  # evo2_fp8_gemm streams the weight while ceil(M / 64) * N <= this
+
+
+def streams_weight(M, N):
+    """Whether evo2_fp8_gemm takes its weight-streaming kernel for M rows
+    (always at M <= 64; over 64-row blocks while ceil(M / 64) * N is at most
+    STREAM_MAX_WORK): the shapes where a packed weight copy is read instead."""
+    return 0 < M and (M <= 64 or -(-M // 64) * N <= STREAM_MAX_WORK)
 
 
 def packable(N, K):
@@ -91,7 +98,8 @@ def fp8_pack_weight(w8):
 
 def fp8_gemm_packed(x8, wp, x_scale, w_scale, bias=None, out=None):
     """fp8_gemm with the weight in the decode layout (fp8_pack_weight); the
-    same result bits.  For decode-sized M (<= 64 rows)."""
+    same result bits.  Streams the weight once per 64-row block of x, so it
+    is for the shapes streams_weight() accepts (decode and verify steps)."""
     _lib.require_device(x8, wp, x_scale, w_scale, bias)
     if x8.dtype != E4M3 or wp.dtype != E4M3:
         raise ValueError("fp8_gemm_packed operands must be float8_e4m3fn")
@@ -121,12 +129,13 @@ def static_fp8_linear(x, weight, input_scale, weight_scale, bias=None, out=None,
     """vLLM's static W8A8 linear: (..., K) bf16 -> (..., N) bf16; a 2-D x may
     write its result into `out` (M, N) bf16 with unit column stride.  With
     `packed` (fp8_pack_weight(weight)), inputs of at most 64 rows take the
-    decode GEMM on it (the same result bits)."""
+    decode GEMM on it wherever the weight would be streamed (the same result
+    bits)."""
     K = x.shape[-1]
     x8 = quantize_input(x.reshape(-1, K), input_scale)
     gemm = fp8_gemm
     w = weight
-    if packed is not None and x8.shape[0] <= PACK_MAX_ROWS:
+    if packed is not None and streams_weight(x8.shape[0], weight.shape[0]):
         gemm, w = fp8_gemm_packed, packed
     if out is not None:
         if x.dim() != 2 or out.shape != (x.shape[0], weight.shape[0]) or out.stride(1) != 1:
@@ -176,6 +185,6 @@ class Fp8StaticLinear(nn.Module):
 
     def forward(self, x, out=None):
         rows = x.numel() // max(x.shape[-1], 1)
-        packed = self.decode_weight() if 0 < rows <= PACK_MAX_ROWS else None
+        packed = self.decode_weight() if streams_weight(rows, self.out_features) else None
         return static_fp8_linear(x, self.weight, self.input_scale, self.weight_scale,
                                  self.bias, out=out, packed=packed), None

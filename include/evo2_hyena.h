@@ -392,7 +392,8 @@ int evo2_fp8_pack_weight(const void *w8, int64_t sw, void *wp, int64_t N, int64_
  * evo2_fp8_pack_weight (same x8, scales, bias, out and result bits as
  * evo2_fp8_gemm on the unpacked weight; N a multiple of 16, K of 128).  Runs
  * the weight-streaming kernel over ceil(M / 64) blocks of 64 rows, so it is
- * meant for M <= 64 (a decode step's in_proj).  The weight stream is
+ * meant for the shapes where evo2_fp8_gemm streams too (M <= 64, or
+ * ceil(M / 64) * N <= 60000: decode and verify steps).  The weight stream is
  * sequential per wave: the 7B decode in_proj (M=64, K=4096, N=12288) with the
  * weights streaming from HBM takes ~15.0 us against ~17.4 us unpacked.
  *

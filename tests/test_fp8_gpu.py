@@ -132,7 +132,8 @@ def test_config3_shapes(N):
 
 
 @pytest.mark.parametrize("M,N,K", [(64, 12288, 4096), (1, 48, 128), (7, 4112, 256),
-                                   (64, 4096, 4096), (100, 512, 384), (32, 24576, 8192)])
+                                   (64, 4096, 4096), (100, 512, 384), (32, 24576, 8192),
+                                   (256, 12288, 4096)])
 def test_packed_weight_same_bits(M, N, K):
     """The decode weight layout (fp8_pack_weight) read by fp8_gemm_packed
     gives the unpacked GEMM's bits, at decode shapes, at N not a multiple of
@@ -155,8 +156,9 @@ def test_packed_weight_same_bits(M, N, K):
 
 
 def test_linear_module_decode_copy():
-    """Fp8StaticLinear takes its packed copy for inputs of at most 64 rows,
-    the row-major weight above; the copy follows an in-place weight update."""
+    """Fp8StaticLinear takes its packed copy where the GEMM streams the weight
+    (decode and verify-sized inputs), the row-major weight above; same bits;
+    the copy follows an in-place weight update."""
     from evo2_flash_amd.fp8 import Fp8StaticLinear
     N, K = 4096, 1024
     lin = Fp8StaticLinear(K, N, bias=True, device=DEV)
@@ -167,7 +169,7 @@ def test_linear_module_decode_copy():
         lin.weight_scale.copy_(ws)
         lin.input_scale.fill_(6.0 / 448)
         lin.bias.copy_((torch.randn(N, generator=gen, device=DEV) * 0.02).to(torch.bfloat16))
-    for M in (1, 64, 65):
+    for M in (1, 64, 65, 2000):
         x = torch.randn(M, K, generator=gen, device=DEV).to(torch.bfloat16)
         y, _ = lin(x)
         ref = static_fp8_linear(x, lin.weight, lin.input_scale, lin.weight_scale, lin.bias)
