@@ -80,19 +80,22 @@ def test_spec_short_conv_vs_oracle(K, nspec, moved):
     assert torch.equal(_bits(gst.cpu()), _bits(st))
 
 
-def test_iir_verify_on_stamped_rows():
+@pytest.mark.parametrize("H,width", [(320, 17), (200, 17), (96, 20), (64, 40)])
+def test_iir_verify_on_stamped_rows(H, width):
     """The speculative LI slice has 17 fp32 per channel (stride 17): the
-    verify kernel's strided path, bitwise, leaving column 16 alone."""
-    H, nreq, Q, nb = 320, 6, 4, 64
+    verify kernel's strided path (also at an H that leaves part of a
+    workgroup empty and at wider rows), bitwise, leaving the columns past the
+    16 states alone."""
+    nreq, Q, nb = 6, 4, 64
     prm, x, state, meta = verify_case("hcl", H, nreq, Q, nb, seed=7)
     ins, outs, starts, ends, accepted = meta
     poles = torch.exp(prm["log_poles"][..., 0].float())
     res = prm["residues"].float()
-    wide = torch.randn(nb, H, 17, generator=torch.Generator().manual_seed(8))
+    wide = torch.randn(nb, H, width, generator=torch.Generator().manual_seed(8))
     wide[..., :16] = state
     gwide = wide.to(DEV)
     gmeta = tuple(t.to(DEV) for t in meta)
-    print(f"iir verify stamped rows H={H}", flush=True)
+    print(f"iir verify stamped rows H={H} width={width}", flush=True)
     y = iir_snapshots(x.to(DEV), poles.to(DEV), res.to(DEV), gwide[..., :16], gmeta).cpu()
     ref_state = wide.clone()
     ref = oracle.iir_verify_emulated(x, poles, res, ref_state[..., :16], ins, outs, starts, ends,
