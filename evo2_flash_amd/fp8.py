@@ -164,6 +164,34 @@ class Fp8StaticLinear(nn.Module):
                                         requires_grad=False)
         self.bias = (nn.Parameter(torch.zeros(out_features, dtype=torch.bfloat16, device=device),
                                   requires_grad=False) if bias else None)
+        # The engine's loader calls `param.weight_loader(param, tensor)` when a
+        # parameter has one (a plain `param.data.copy_` would not be seen by
+        # the decode copy below).
+        self.weight.weight_loader = self._load_weight
+
+    def _load_weight(self, param, loaded):
+        """Copy a checkpoint tensor into the weight and rewrite the decode copy
+        in place (a HIP graph captured before the reload reads the new
+        weight)."""
+        param.data.copy_(loaded.to(param.dtype).view_as(param))
+        self.refresh_decode_weight()
+
+    def refresh_decode_weight(self):
+        """Rewrite an existing decode copy from the current weight, in place;
+        code that writes the weight other than through its weight_loader or
+        in-place tensor ops (`.data`) calls this afterwards."""
+        cached = getattr(self, "_decode_w", None)
+        if cached is None:
+            return
+        w, wp = self.weight.detach(), cached[1]
+        if w.shape != wp.shape or w.device != wp.device or not packable(*w.shape):
+            self._decode_w = None
+            return
+        if w.stride(1) != 1 or w.stride(0) % 16:
+            w = w.contiguous()
+        _lib.call("evo2_fp8_pack_weight", _lib.ptr(w), w.stride(0), _lib.ptr(wp), w.shape[0],
+                  w.shape[1], _lib.stream_of(w))
+        self._decode_w = ((self.weight.data_ptr(), self.weight._version), wp)
 
     def decode_weight(self):
         """The weight in the decode layout, made on first use and again after

@@ -184,3 +184,17 @@ def test_linear_module_decode_copy():
     ref = static_fp8_linear(x, lin.weight, lin.input_scale, lin.weight_scale, lin.bias)
     assert torch.equal(y.view(torch.int16), ref.view(torch.int16))
     assert lin.decode_weight() is not first
+    # the engine's loader path and a write through .data (which leaves the
+    # version counter alone) followed by refresh_decode_weight()
+    kept = lin.decode_weight()
+    for load in ("loader", "data"):
+        w3, _ = quantize_weight_e4m3(torch.randn(N, K, generator=gen, device=DEV) * 0.02)
+        if load == "loader":
+            lin.weight.weight_loader(lin.weight, w3)
+        else:
+            lin.weight.data.copy_(w3)
+            lin.refresh_decode_weight()
+        assert lin.decode_weight() is kept  # rewritten in place
+        y, _ = lin(x)
+        ref = static_fp8_linear(x, lin.weight, lin.input_scale, lin.weight_scale, lin.bias)
+        assert torch.equal(y.view(torch.int16), ref.view(torch.int16)), load
