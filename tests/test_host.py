@@ -210,3 +210,22 @@ def test_conv_reload_refreshes_decode_taps():
     mixer.conv.weight_loader(mixer.conv, new)
     assert mixer._decode_taps is taps  # same storage: captured graphs stay valid
     assert torch.equal(taps, new.view(H, 128))
+
+
+def test_packed_weight_rules():
+    """Where the fp8 linear reads its packed decode copy: the shapes where
+    evo2_fp8_gemm streams the weight (M <= 64, or ceil(M / 64) * N <= 60000,
+    the constant the C dispatcher uses), for weights with a decode layout
+    (N a multiple of 16, K of 128)."""
+    import re
+    from evo2_flash_amd.fp8 import STREAM_MAX_WORK, packable, streams_weight
+    src = open(__file__.replace("tests/test_host.py",
+                                "evo2_flash_amd/csrc/fp8_gemm.hip")).read()
+    assert int(re.search(r"#define STREAM_MAX_WORK (\d+)", src).group(1)) == STREAM_MAX_WORK
+    assert streams_weight(1, 10 ** 6) and streams_weight(64, 10 ** 6)
+    assert not streams_weight(0, 12288)
+    assert streams_weight(256, 12288)                 # verify-sized in_proj: 4 x 12288
+    assert streams_weight(320, 12000) and not streams_weight(320, 12001)
+    assert not streams_weight(8192, 12288)
+    assert packable(12288, 4096) and packable(16, 128)
+    assert not packable(12280, 4096) and not packable(4096, 4000)
