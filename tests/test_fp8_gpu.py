@@ -198,3 +198,37 @@ def test_linear_module_decode_copy():
         y, _ = lin(x)
         ref = static_fp8_linear(x, lin.weight, lin.input_scale, lin.weight_scale, lin.bias)
         assert torch.equal(y.view(torch.int16), ref.view(torch.int16)), load
+
+
+def test_linear_decode_copy_in_graph():
+    """A HIP graph captured on the packed decode GEMM replays the eager
+    result, and after a reload through the weight's loader (which rewrites
+    the copy in place) it computes with the new weight."""
+    from evo2_flash_amd.fp8 import Fp8StaticLinear
+    N, K, M = 2048, 1024, 16
+    lin = Fp8StaticLinear(K, N, bias=False, device=DEV)
+    gen = torch.Generator(device=DEV).manual_seed(11)
+    w8, ws = quantize_weight_e4m3(torch.randn(N, K, generator=gen, device=DEV) * 0.02)
+    lin.weight.weight_loader(lin.weight, w8)
+    with torch.no_grad():
+        lin.weight_scale.copy_(ws)
+        lin.input_scale.fill_(6.0 / 448)
+    x = torch.randn(M, K, generator=gen, device=DEV).to(torch.bfloat16)
+    out = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
+    lin(x, out=out)  # eager: makes the decode copy
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(graph, stream=s):
+            lin(x, out=out)
+    torch.cuda.current_stream().wait_stream(s)
+    for w in (w8, quantize_weight_e4m3(torch.randn(N, K, generator=gen, device=DEV) * 0.02)[0]):
+        lin.weight.weight_loader(lin.weight, w)
+        for _ in range(3):
+            out.zero_()
+            graph.replay()
+            torch.cuda.synchronize()
+            ref = static_fp8_linear(x, lin.weight, lin.input_scale, lin.weight_scale)
+            assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
