@@ -33,6 +33,7 @@
 #include <type_traits>
 
 #include "featurize.h"
+#include "stripe.h"
 
 namespace evo2 {
 
@@ -1080,7 +1081,17 @@ extern "C" int evo2_hyena_fir_prefill(const void *z, int64_t sz, const void *sho
             seq_table, blocks, sblk, tile_table, static_cast<int>(H), block_t, num_blocks};
   if (K == 128 && (w1 != 1 || w0 % 8 || reinterpret_cast<uintptr_t>(w) % 16))
     return fail(EVO2_ERR_UNSUPPORTED, "hyena_fir_prefill: K=128 taps must be contiguous (H, 128) rows");
-  if (ntiles) {
+  StripeArgs sa{static_cast<const bf16_t *>(z), sz, static_cast<const bf16_t *>(short_w),
+                static_cast<const bf16_t *>(conv_state), cs0, cs1, cs2,
+                static_cast<const bf16_t *>(w), w0, inner_state, st0, st1, st2,
+                nullptr, 0, 0, nullptr, 0, 0, nullptr, 0, 0, 0,
+                static_cast<const bf16_t *>(D), static_cast<bf16_t *>(out), so, seq_table, nseq,
+                blocks, sblk, static_cast<int>(H), num_blocks};
+  if (ntiles && K == 128 && stripe_supported(sa, T, block_t)) {
+    // whole segments per tile: the single-pass kernel (FIR history in LDS)
+    rc = launch_stripe(sa, STRIPE_HCM, st);
+    if (rc) return rc;
+  } else if (ntiles) {
     const bool hasD = D != nullptr;
     if (K == 128 && block_t >= mfir::RS) {
       // the matrix-core kernel once a tile holds a whole 256-row sub-tile

@@ -31,6 +31,7 @@
 #include <type_traits>
 
 #include "featurize.h"
+#include "stripe.h"
 
 namespace evo2 {
 
@@ -387,6 +388,25 @@ static int hcl_prefill(const void *z, int64_t sz, const void *short_w,
   if (ntiles > 0x7fffffff || cdiv(H, HCL_CH) > 65535)
     return fail(EVO2_ERR_UNSUPPORTED, "hyena_hcl_prefill: grid too large");
   hipStream_t st = static_cast<hipStream_t>(stream);
+  {
+    // whole segments per tile: the single-pass kernel (no carry pass, z read once)
+    StripeArgs sa{static_cast<const bf16_t *>(z), sz, static_cast<const bf16_t *>(short_w),
+                  static_cast<const bf16_t *>(conv_state), cs0, cs1, cs2, nullptr, 0,
+                  nullptr, 0, 0, 0, residues, r0, r1, log_poles, l0, l1, ssm, m0, m1, m2,
+                  static_cast<const bf16_t *>(D), static_cast<bf16_t *>(out), so, seq_table, nseq,
+                  blocks, sblk, static_cast<int>(H), num_blocks};
+    if (stripe_supported(sa, T, block_t)) {
+      int rc = launch_stripe(sa, STRIPE_HCL, st);
+      if (rc) return rc;
+      HclArgs wa{static_cast<const bf16_t *>(z), sz, nullptr, static_cast<const bf16_t *>(conv_state),
+                 cs0, cs1, cs2, nullptr, 0, 0, nullptr, 0, 0, nullptr, 0, 0, 0, nullptr, nullptr, 0,
+                 seq_table, blocks, sblk, nullptr, nullptr, nullptr, static_cast<int>(H), block_t,
+                 num_blocks};
+      hipLaunchKernelGGL(hcl_conv_window_kernel, dim3(static_cast<unsigned>(nseq),
+                         static_cast<unsigned>(cdiv(H, 64))), dim3(64), 0, st, wa);
+      return check_launch("hcl conv window");
+    }
+  }
   HclArgs a{static_cast<const bf16_t *>(z), sz, static_cast<const bf16_t *>(short_w),
             static_cast<const bf16_t *>(conv_state), cs0, cs1, cs2, residues, r0, r1,
             log_poles, l0, l1, ssm, m0, m1, m2, static_cast<const bf16_t *>(D),

@@ -14,6 +14,7 @@ ignored: there is no torch path.
 import torch
 
 from . import _lib
+from .prefill import stripe_block_t
 
 # Rows per tile of the chunked scan: shorter tiles add parallelism, longer
 # ones amortise the carry pass.  Multiples of 16 (the LDS sub-tile).
@@ -21,8 +22,14 @@ _HCL_BLOCK_T = 1024
 _TARGET_WORKGROUPS = 1024
 
 
-def hcl_block_t(num_tokens=None, hidden=None):
-    """Rows per tile for the LI prefill tile table."""
+def hcl_block_t(num_tokens=None, hidden=None, max_segment=None):
+    """Rows per tile for the LI prefill tile table.  A step whose work spreads
+    over the GPU in whole segments (`stripe_block_t`) takes the single-pass
+    kernel (one tile per segment); otherwise tiles shrink until the tiled
+    scan has ~1024 workgroups."""
+    bt = stripe_block_t(num_tokens, hidden, max_segment)
+    if bt is not None:
+        return bt
     bt = _HCL_BLOCK_T
     if num_tokens is not None and hidden is not None:
         groups = max(1, (int(hidden) + 255) // 256)

@@ -52,7 +52,7 @@ from .decode import channel_major_taps, hyena_decode
 from .fp8 import Fp8StaticLinear
 from .fp8_emul import static_fp8_linear_emulated
 from .hcl import hcl_block_t, hyena_hcl_prefill
-from .metadata import decode_state_indices, prefill_tables
+from .metadata import decode_state_indices, longest_prefill_segment, prefill_tables
 from .prefill import fir_prefill_block_t, hyena_fir_prefill
 from .short_conv import PAD_SLOT_ID, causal_conv1d_update
 from .speculative import (accepted_tokens, cache_safe_state_indices, decode_tensors,
@@ -497,7 +497,7 @@ class HyenaFIRMixer(HyenaMixerBase):
                 parts.append(hyena_decode(z[:nd], sw, window, decode_state_indices(m),
                                           self._decode_taps, inner_state, self.D))
         if npt:
-            bt = fir_prefill_block_t(self.k_inner, npt, self.hidden)
+            bt = fir_prefill_block_t(self.k_inner, npt, self.hidden, longest_prefill_segment(m))
             seq_t, til_t, _ = prefill_tables(m, bt, z.device)
             parts.append(hyena_fir_prefill(
                 z[nd:nd + npt], sw, window, self.conv.view(self.hidden, self.k_inner),
@@ -567,7 +567,7 @@ class HyenaIIRMixer(HyenaMixerBase):
                 parts.append(hyena_decode(z[:nd], sw, window, decode_state_indices(m), res, ssm,
                                           self.D, log_poles=lp))
         if npt:
-            bt = hcl_block_t(npt, self.hidden)
+            bt = hcl_block_t(npt, self.hidden, longest_prefill_segment(m))
             seq_t, til_t, ts_t = prefill_tables(m, bt, z.device)
             parts.append(hyena_hcl_prefill(z[nd:nd + npt], sw, window, res, lp, ssm, self.D,
                                            seq_t, m.state_indices_tensor_p, til_t, ts_t, bt))

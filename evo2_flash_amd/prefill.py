@@ -28,13 +28,47 @@ _LONG_FILTER_MIN_BLOCK_T = 256
 _LONG_FILTER_MIN_WORKGROUPS = 128
 
 
-def fir_prefill_block_t(k, num_tokens=None, hidden=None):
+# Single-pass form of the hcm and hcl cores (csrc/prefill_stripe.hip): a
+# workgroup sweeps one whole segment for 16 channels, so a launch is
+# segments x H/16 workgroups, each as long as its segment.  It is chosen
+# while the longest segment is at most _STRIPE_BALANCE times the rows one of
+# the _STRIPE_CUS compute units would sweep with the work spread evenly (at
+# one 32k-token segment that is H >= 2731), and the launch passes a tile
+# table of whole segments (block_t >= the step's rows).
+_STRIPE_CUS = 256
+_STRIPE_BALANCE = 1.5
+_STRIPE_GROUP = 16
+
+
+def stripe_block_t(num_tokens, hidden, max_segment=None):
+    """block_t that selects the single-pass kernels for a step of
+    `num_tokens` prefill rows whose longest segment has `max_segment` rows
+    (default: one segment), or None when the tiled kernels fit better."""
+    if num_tokens is None or hidden is None or int(num_tokens) <= 0:
+        return None
+    T, H = int(num_tokens), int(hidden)
+    if H % _STRIPE_GROUP:
+        return None
+    longest = T if max_segment is None else max(1, int(max_segment))
+    even = T * (H // _STRIPE_GROUP) / _STRIPE_CUS
+    if longest > _STRIPE_BALANCE * even:
+        return None
+    return (T + 63) // 64 * 64
+
+
+def fir_prefill_block_t(k, num_tokens=None, hidden=None, max_segment=None):
     """Rows per prefill tile for filter length k; the tile table is built for
-    this value.  With `num_tokens` and `hidden` it shrinks (to a multiple of
-    64) until the launch has enough workgroups to fill the GPU (counting the
-    fused K=128 core's four 16-channel workgroups per 64-channel block at
-    tiles of 256 rows or more); for filters longer than 8 taps it stops at
-    256 rows once the launch has 128 workgroups."""
+    this value.  For k = 128, a step whose work spreads over the GPU in whole
+    segments takes the single-pass kernel (`stripe_block_t`).  Otherwise, with
+    `num_tokens` and `hidden` it shrinks (to a multiple of 64) until the
+    launch has enough workgroups to fill the GPU (counting the fused K=128
+    core's four 16-channel workgroups per 64-channel block at tiles of 256
+    rows or more); for filters longer than 8 taps it stops at 256 rows once
+    the launch has 128 workgroups."""
+    if int(k) == 128:
+        bt = stripe_block_t(num_tokens, hidden, max_segment)
+        if bt is not None:
+            return bt
     bt = _MAX_BLOCK_T.get(int(k), 1024)
     if num_tokens is not None and hidden is not None:
         cblocks = max(1, (int(hidden) + 63) // 64)
