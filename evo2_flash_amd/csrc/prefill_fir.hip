@@ -1086,9 +1086,9 @@ extern "C" int evo2_hyena_fir_prefill(const void *z, int64_t sz, const void *sho
                 static_cast<const bf16_t *>(w), w0, inner_state, st0, st1, st2,
                 nullptr, 0, 0, nullptr, 0, 0, nullptr, 0, 0, 0,
                 static_cast<const bf16_t *>(D), static_cast<bf16_t *>(out), so, seq_table, nseq,
-                blocks, sblk, static_cast<int>(H), num_blocks};
-  if (ntiles && K == 128 && stripe_supported(sa, T, block_t)) {
-    // whole segments per tile: the single-pass kernel (FIR history in LDS)
+                blocks, sblk, tile_table, ntiles, block_t, static_cast<int>(H), num_blocks};
+  if (ntiles && K == 128 && stripe_supported(sa, STRIPE_HCM, T, block_t)) {
+    // 32-channel stripes over each tile (FIR history in LDS)
     rc = launch_stripe(sa, STRIPE_HCM, st);
     if (rc) return rc;
   } else if (ntiles) {

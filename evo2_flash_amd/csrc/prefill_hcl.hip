@@ -394,8 +394,8 @@ static int hcl_prefill(const void *z, int64_t sz, const void *short_w,
                   static_cast<const bf16_t *>(conv_state), cs0, cs1, cs2, nullptr, 0,
                   nullptr, 0, 0, 0, residues, r0, r1, log_poles, l0, l1, ssm, m0, m1, m2,
                   static_cast<const bf16_t *>(D), static_cast<bf16_t *>(out), so, seq_table, nseq,
-                  blocks, sblk, static_cast<int>(H), num_blocks};
-    if (stripe_supported(sa, T, block_t)) {
+                  blocks, sblk, tile_table, ntiles, block_t, static_cast<int>(H), num_blocks};
+    if (stripe_supported(sa, STRIPE_HCL, T, block_t)) {
       int rc = launch_stripe(sa, STRIPE_HCL, st);
       if (rc) return rc;
       HclArgs wa{static_cast<const bf16_t *>(z), sz, nullptr, static_cast<const bf16_t *>(conv_state),

@@ -1,10 +1,11 @@
 // Single-pass ("stripe") prefill of the hcm and hcl mixer cores: a workgroup
-// owns 16 channels of one whole segment and sweeps it in 256-row sub-tiles,
-// so the LI scan carries its state inside the workgroup (no cross-tile carry
-// pass, z read once) and the 128-tap FIR keeps its history in LDS (no halo
-// re-read).  Kernels: prefill_stripe.hip.  The entry points of
+// sweeps a channel stripe row by row with its filter state in LDS and
+// registers.  hcl: 16 channels of a whole segment, so the LI scan carries
+// its state inside the workgroup (no carry pass, z read once).  hcm: 32
+// channels of one tile, the 128-tap history rebuilt from the 256 rows
+// before it.  Kernels: prefill_stripe.hip.  The entry points of
 // prefill_fir.hip and prefill_hcl.hip take this path when the tile table
-// holds whole segments (block_t >= T) and the layout allows it.
+// and the layout allow it.
 #pragma once
 
 #include "common.h"
@@ -24,16 +25,19 @@ struct StripeArgs {
   bf16_t *out; int64_t so;                  // g (T, H)
   const int32_t *seq; int64_t nseq;         // (nseq, 3) [start, end, has_init]
   const int32_t *blocks; int64_t sblk;
+  const int32_t *tiles; int64_t ntiles;     // hcm: (ntiles, 2) [segment, first row]
+  int block_t;                              // hcm: rows per tile
   int H;
   int64_t num_blocks;
 };
 
 enum StripeKind { STRIPE_HCM = 0, STRIPE_HCL = 1 };
 
-// True when the single-pass kernels can take this launch: every segment is
-// one tile (block_t >= T), H a multiple of 16, z and out 16-byte addressable
-// with row strides that keep a sub-tile's byte offsets in 32 bits.
-bool stripe_supported(const StripeArgs &a, int64_t T, int64_t block_t);
+// True when the single-pass kernels can take this launch: hcl with every
+// segment one tile (block_t >= T) and H a multiple of 16; hcm with tiles of
+// at least 256 rows and H a multiple of 32; z and out 16-byte addressable
+// with row strides that keep a step's byte offsets in 32 bits.
+bool stripe_supported(const StripeArgs &a, StripeKind kind, int64_t T, int64_t block_t);
 
 // Enqueues the single-pass kernel of `kind` (the conv and FIR windows are
 // left to the callers' window kernels; hcl writes the final LI state).

@@ -56,17 +56,39 @@ def stripe_block_t(num_tokens, hidden, max_segment=None):
     return (T + 63) // 64 * 64
 
 
+# The fused K=128 core on 32-channel stripes (H a multiple of 32): one
+# workgroup per (tile, 32 channels), the tile swept with its FIR history in
+# LDS after a 256-row lead-in.  Tiles are sized for about one workgroup per
+# compute unit (a 32k-token segment at H=4096: two 16384-row tiles).
+_STRIPE_FIR_GROUP = 32
+_STRIPE_FIR_MIN = 256
+
+
+def stripe_fir_block_t(num_tokens, hidden, max_segment=None):
+    """block_t of the 32-channel K=128 kernel, or None when H does not fit it."""
+    if num_tokens is None or hidden is None or int(num_tokens) <= 0:
+        return None
+    T, H = int(num_tokens), int(hidden)
+    if H % _STRIPE_FIR_GROUP:
+        return None
+    tiles = max(1, _STRIPE_CUS // (H // _STRIPE_FIR_GROUP))
+    bt = -(-T // tiles)
+    if max_segment is not None:
+        bt = min(bt, max(1, int(max_segment)))
+    return max(_STRIPE_FIR_MIN, -(-bt // _STRIPE_FIR_MIN) * _STRIPE_FIR_MIN)
+
+
 def fir_prefill_block_t(k, num_tokens=None, hidden=None, max_segment=None):
     """Rows per prefill tile for filter length k; the tile table is built for
-    this value.  For k = 128, a step whose work spreads over the GPU in whole
-    segments takes the single-pass kernel (`stripe_block_t`).  Otherwise, with
+    this value.  For k = 128 and H a multiple of 32 the tiles are sized for
+    the 32-channel kernel (`stripe_fir_block_t`).  Otherwise, with
     `num_tokens` and `hidden` it shrinks (to a multiple of 64) until the
     launch has enough workgroups to fill the GPU (counting the fused K=128
     core's four 16-channel workgroups per 64-channel block at tiles of 256
     rows or more); for filters longer than 8 taps it stops at 256 rows once
     the launch has 128 workgroups."""
     if int(k) == 128:
-        bt = stripe_block_t(num_tokens, hidden, max_segment)
+        bt = stripe_fir_block_t(num_tokens, hidden, max_segment)
         if bt is not None:
             return bt
     bt = _MAX_BLOCK_T.get(int(k), 1024)

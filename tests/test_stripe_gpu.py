@@ -7,6 +7,8 @@ csrc/prefill_stripe.hip) against the oracle.
   final states within 1e-3;
 * H a multiple of 16 but not of 64 (a 64-channel block with fewer than four
   16-channel workgroups) and the 1B width H=1920;
+* hcm on 32-channel stripes over tiles shorter than their segments (the
+  FIR history rebuilt from the 256 rows before a tile);
 * chunked prefill: prefill(L) against prefill(a) + continued prefill(L-a);
 * decode after a single-pass prefill matches the last row of prefill(L+1);
 * the 7B-shaped LI case (H=4096, one 32768-token segment) against a float64
@@ -175,11 +177,37 @@ def test_decode_after_single_pass(kind):
     assert max_rel_err(last.cpu(), full[L:].cpu()) <= 1e-2
 
 
+TILED_HCM = [
+    (256, [700, 5, 0, 300, 1, 290], [0, 1, 0, 1, 1, 0], 256),
+    (256, [1100, 130], [1, 0], 512),
+    (128, [2000, 257, 513], [1, 0, 1], 768),
+    (320, [5000, 3, 4097], [0, 1, 1], 1024),
+]
+
+
+@pytest.mark.parametrize("H,lens,has_init,block_t", TILED_HCM)
+def test_hcm_tiles_vs_oracle(H, lens, has_init, block_t):
+    """The 32-channel hcm kernel over tiles shorter than their segments: a
+    tile after the first rebuilds its FIR history from the 256 rows before it."""
+    nblk = len(lens) + 3
+    prm, z, slots, pool = _case("hcm", H, lens, nblk, seed=61 + H)
+    gp = clone_pool(pool, DEV)
+    print(f"hcm tiles H={H} lens={lens} block_t={block_t}", flush=True)
+    out = _run("hcm", prm, z, slots, gp, lens, has_init, H, bt=block_t).cpu()
+    ref = _oracle("hcm", prm, z, pool, lens, has_init, slots, H)
+    assert max_rel_err(out, ref) <= 1e-2
+    assert torch.equal(gp.kv_cache[0].cpu(), pool.kv_cache[0])
+    assert max_rel_err(gp.kv_cache[1].cpu(), pool.kv_cache[1]) <= 1e-2
+    assert torch.equal(gp.kv_cache[2].cpu(), pool.kv_cache[2])
+
+
 def test_block_t_choice():
-    """The 7B shape takes the single-pass kernels, the 1B width at one long
-    segment the tiled ones."""
+    """The 7B shape takes the single-pass kernels (hcl: one tile per
+    segment; hcm: two 16384-row tiles of 32-channel stripes), the 1B width
+    at one long segment the tiled LI scan."""
     assert hcl_block_t(32768, 4096) >= 32768
-    assert fir_prefill_block_t(128, 32768, 4096) >= 32768
+    assert fir_prefill_block_t(128, 32768, 4096) == 16384
+    assert fir_prefill_block_t(128, 131072, 8192) >= 131072
     assert fir_prefill_block_t(7, 32768, 4096) < 32768
     assert stripe_block_t(32768, 1920) is None
     assert stripe_block_t(32768, 1920, max_segment=8192) is not None
