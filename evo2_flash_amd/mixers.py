@@ -41,13 +41,13 @@ stamped afterwards.  The state pool then carries the speculative layout
 decode rows use the leading K_short-1 columns of the widened window.
 """
 
-import contextlib
 import os
 from typing import Optional
 
 import torch
 from torch import nn
 
+from . import engine
 from .decode import channel_major_taps, hyena_decode
 from .fp8 import Fp8StaticLinear
 from .fp8_emul import static_fp8_linear_emulated
@@ -65,35 +65,12 @@ from .verify import fir_snapshots, iir_snapshots
 _CHECK_VLLM_COUNTS = os.environ.get("EVO2_CHECK_VLLM_COUNTS") == "1"
 
 # ---------------------------------------------------------------- forward context
-# Layers register under their prefix here, as vLLM's
-# compilation_config.static_forward_context does (mixers.py:806-810).
-static_forward_context = {}
-
-
-class ForwardContext:
-    """What the mixers read from vLLM's forward context: `attn_metadata`,
-    either one metadata object for every layer or a dict keyed by prefix."""
-
-    def __init__(self):
-        self.attn_metadata = None
-
-
-_context = ForwardContext()
-
-
-def get_forward_context():
-    return _context
-
-
-@contextlib.contextmanager
-def set_forward_context(attn_metadata):
-    """Run a model step with `attn_metadata` visible to every mixer."""
-    prev = _context.attn_metadata
-    _context.attn_metadata = attn_metadata
-    try:
-        yield _context
-    finally:
-        _context.attn_metadata = prev
+# The engine binding (vLLM's forward context when vLLM imports, a local one
+# otherwise) lives in engine.py; these names are re-exported for callers.
+static_forward_context = engine.static_forward_context
+get_forward_context = engine.get_forward_context
+set_forward_context = engine.set_forward_context
+ForwardContext = engine.ForwardContext
 
 
 # ---------------------------------------------------------------- projections
@@ -186,22 +163,20 @@ class HyenaMixerBase(nn.Module):
                          if quant_config == "fp8" else Linear(h, h, bias=True, device=device))
         self.short_filter = nn.Parameter(torch.empty(3 * h, 1, self.k_short, device=device,
                                                      dtype=torch.bfloat16), requires_grad=False)
-        if self.prefix in static_forward_context:
-            raise ValueError(f"Duplicate layer name: {self.prefix}")
-        static_forward_context[self.prefix] = self
+        # the engine's static_forward_context and splitting_ops (mixers.py:806-820)
+        engine.register_layer(self.prefix, self)
         # bound by the engine: (conv, inner FIR, LI) native-layout slices
         self.kv_cache = (torch.tensor([]), torch.tensor([]))
 
     def forward(self, hidden_states, token_ids=None):
         output = torch.empty_like(hidden_states)
-        torch.ops.vllm.evo2_hyena_mixer(hidden_states, output, token_ids, self.prefix)
+        torch.ops.vllm.evo2_hyena_mixer(hidden_states, output, token_ids,
+                                        engine.layer_name(self.prefix))
         return output
 
     def _meta(self):
-        raw = get_forward_context().attn_metadata
-        if raw is None:
-            return None
-        return raw[self.prefix] if isinstance(raw, dict) else raw
+        """This layer's metadata from the forward context (mixers.py:852-856)."""
+        return engine.step_metadata(self.prefix)
 
     def _conv_state(self, i, width=None):
         """Dim-first view of state slice i (mixers.py:940-949): slices 0 and 1
@@ -576,14 +551,14 @@ class HyenaIIRMixer(HyenaMixerBase):
 
 
 # ---------------------------------------------------------------- operator
-HYENA_MIXER_OP = "vllm::evo2_hyena_mixer"
+HYENA_MIXER_OP = engine.HYENA_MIXER_OP
 
 
 def evo2_hyena_mixer(hidden_states: torch.Tensor, output: torch.Tensor,
                      token_ids: Optional[torch.Tensor], layer_name: str) -> None:
     """The mixer as one opaque operator that writes `output` in place
     (mixers.py:1404-1410)."""
-    layer = static_forward_context[layer_name]
+    layer = engine.lookup_layer(layer_name)
     res = layer._forward_impl(hidden_states, token_ids, output=output)
     if res is not output:
         output.copy_(res)
