@@ -210,6 +210,18 @@ SIGNATURES = {
         _c_p, _c_p, _c_p, _c_i64, _c_i64,         # out_col, qsl, computed, nreq, width
         _c_p, _c_p, _c_i64, _c_p,                 # prefill_blocks, seq_lens, npf, stream
     ],
+    "evo2_spec_plan": [
+        _c_p, _c_i64, _c_i64, _c_i64,             # slots + strides, ncols
+        _c_p, _c_p, _c_p, _c_p,                   # qsl, prev, sched, eng_acc
+        _c_i64, _c_i64, _c_i32,                   # nreq, width, null_all
+        _c_p, _c_p, _c_p, _c_p, _c_p, _c_p,       # ins, outs, starts, ends, acc, stream
+    ],
+    "evo2_spec_repair_prefill": [
+        _c_p, _c_i64, _c_i64,                     # stamps, stride, num_blocks
+        _c_p, _c_p, _c_p, _c_p, _c_i64,           # dst, src, need, has_init, npf
+        _c_p, _c_p,                               # take, faults
+        _c_p, _c_p, _c_p, _c_p, _c_p,             # slice pointers, strides, dims, sizes, stream
+    ],
 }
 
 RESTYPES = {"evo2_last_error": ctypes.c_char_p, "evo2_hcl_workspace_bytes": ctypes.c_int64,

@@ -55,8 +55,8 @@ from .hcl import hcl_block_t, hyena_hcl_prefill
 from .metadata import decode_state_indices, longest_prefill_segment, prefill_tables
 from .prefill import fir_prefill_block_t, hyena_fir_prefill
 from .short_conv import PAD_SLOT_ID, causal_conv1d_update
-from .speculative import (accepted_tokens, cache_safe_state_indices, decode_tensors,
-                          query_start_loc_d, record_stamps, spec_accepted)
+from .speculative import (packed_rows, pool_holds, record_stamps, repair_prefill_states,
+                          slot_matrix, spec_accepted, verify_plan)
 from .state import unified_state_dtype, unified_state_shape
 from .verify import fir_snapshots, iir_snapshots
 
@@ -255,59 +255,45 @@ class HyenaMixerBase(nn.Module):
         offset as there."""
         return 0 if self._stamp_faults is None else int(self._stamp_faults)
 
+    def _verify_plan(self, m):
+        """The step's verify plan (slot windows of 1 + num_spec positions,
+        row ranges, the engine's counts), shared by the step's layers."""
+        return verify_plan(m, int(m.num_decodes), 1 + self.num_spec, self.kv_cache[2].shape[0])
+
     def _spec_accepted(self, m):
-        """(num_decodes,) accepted count of the previous step from the stamps,
-        one launch (mixers.py:960-999): offset = computed tokens - stamp of
-        column 0, in [0, num_spec] for every request not on the null block;
-        returns offset + 1, clamped."""
-        nd = int(m.num_decodes)
-        computed = getattr(m, "num_computed_tokens_d", None)
-        if computed is None:
-            raise RuntimeError("speculative Hyena decode needs num_computed_tokens_d; it is "
-                               "supplied by metadata.HyenaMamba2MetadataBuilder")
-        slots = m.state_indices_tensor_d[:nd]
-        if slots.dim() == 1:
-            slots = slots[:, None]
-        # a slot matrix naming more blocks than the pool holds puts every
-        # request on the null block (mixers.py:527-541)
-        if self.kv_cache[2].shape[0] < slots.numel():
-            slots = None
-        counts = None
+        """Accepted count of the previous step per decode request, from the
+        position stamps in one launch (mixers.py:960-999): the live snapshot
+        sits at offset computed - stamp(column 0), accepted = offset + 1,
+        clamped to [1, 1 + num_spec]; out-of-range offsets off the null block
+        count as stamp faults."""
+        n = int(m.num_decodes)
+        done = getattr(m, "num_computed_tokens_d", None)
+        if done is None:
+            raise RuntimeError(f"{self.prefix}: a speculative step needs the computed-token "
+                               "counts (num_computed_tokens_d), which "
+                               "metadata.HyenaMamba2MetadataBuilder adds to the metadata")
+        rows = slot_matrix(m, n)[:n]
+        first = rows if pool_holds(rows.numel(), self.kv_cache[2].shape[0]) else None
+        check = None
         if _CHECK_VLLM_COUNTS and getattr(m, "num_accepted_tokens", None) is not None:
-            counts = accepted_tokens(m, nd, computed.device)
-        return spec_accepted(self._position_stamps(), slots, computed[:nd], self.num_spec,
-                             self._fault_counter(computed.device), counts)
+            check = self._verify_plan(m).engine_accepted
+        return spec_accepted(self._position_stamps(), first, done[:n], self.num_spec,
+                             self._fault_counter(done.device), check)
 
     def _repair_resumed_prefill_state(self, m):
-        """Align-mode prefix caching: a prefill row continuing from n computed
-        tokens must start from a block stamped n; where it does not and the
-        block of its last computed token is, copy that block (all three
-        slices) over it.  Rows that are fine copy onto themselves
-        (mixers.py:1001-1040)."""
-        if not self.num_spec or not int(m.num_prefills):
-            return
-        computed = getattr(m, "computed_before_p", None)
-        src = getattr(m, "state_src_block_p", None)
-        has_init = getattr(m, "has_initial_states_p", None)
-        if computed is None or src is None or has_init is None:
-            return
-        npf = int(m.num_prefills)
-        dst = m.state_indices_tensor_p[:npf].long()
-        src = src[:npf].long()
-        computed = computed[:npf].to(torch.float32)
-        stamps = self._position_stamps()
-        bad = (has_init[:npf].bool() & (stamps[dst] != computed) & (stamps[src] == computed)
-               & (src != 0) & (dst != 0))
-        take = torch.where(bad, src, dst)
-        for state in self.kv_cache:
-            state[dst] = state[take]
+        """Align-mode prefix caching: resumed prefill rows whose block is not
+        stamped with their computed count take the state of the block of
+        their last computed token (mixers.py:1001-1040), in two launches."""
+        if self.num_spec and int(m.num_prefills):
+            repair_prefill_states(self.kv_cache, self._position_stamps(), m,
+                                  self._fault_counter(self.kv_cache[2].device))
 
     def _resolve_accepted(self, m):
-        """Stamp-derived accepted counts for a speculative decode step, else
-        None; runs before the layer writes any state (mixers.py:1042-1047)."""
-        if self.num_spec and int(m.num_decodes) and self.is_speculative_decode(m):
-            return self._spec_accepted(m)
-        return None
+        """Stamp-derived accepted counts of a speculative step's decode rows,
+        resolved before the layer writes any state (mixers.py:1039-1047); None
+        for any other step."""
+        speculative = self.num_spec > 0 and int(m.num_decodes) > 0 and self.is_speculative_decode(m)
+        return self._spec_accepted(m) if speculative else None
 
     def _record_stamps(self, m):
         """Stamp every snapshot this step wrote, one launch: decode column p
@@ -323,7 +309,7 @@ class HyenaMixerBase(nn.Module):
             slots = m.state_indices_tensor_d[:nd]
             if slots.dim() == 1:
                 slots = slots[:, None]
-            qsl = query_start_loc_d(m, nd, stamps.device)
+            qsl = packed_rows(m, nd, stamps.device)
             computed = m.num_computed_tokens_d[:nd]
             # the written columns: prefix caching's window from the block of
             # the last scheduled token, else the slot row (mixers.py:444-456)
@@ -343,30 +329,34 @@ class HyenaMixerBase(nn.Module):
     def _spec_short_conv(self, z_d, m, accepted):
         """(x2, x1, v) of the decode rows of a speculative step through the
         widened short window (mixers.py:1153-1193)."""
-        conv_state = self._conv_state(0)
-        nreq = int(m.num_decodes)
-        slots = m.state_indices_tensor_d
-        idx = cache_safe_state_indices(slots, conv_state)
-        if idx.dim() == 1:
-            idx = idx[:, None]
+        window = self._conv_state(0)
+        n = int(m.num_decodes)
+        engine_rows = m.state_indices_tensor_d
+        rows = slot_matrix(m, n)
+        if engine_rows.dim() == 2 and not pool_holds(engine_rows.numel(), window.shape[0]):
+            rows = torch.zeros_like(rows)  # profiling-sized pool: the null block
         sched = getattr(m, "block_idx_last_scheduled_token", None)
         comp = getattr(m, "block_idx_last_computed_token", None)
-        acc = accepted if accepted is not None else accepted_tokens(m, nreq, z_d.device)
+        if accepted is None:
+            accepted = self._verify_plan(m).engine_accepted
         zf = causal_conv1d_update(
-            z_d, conv_state, self._short_w(), None, activation=None,
-            conv_state_indices=idx[:nreq],
-            block_idx_last_scheduled_token=None if sched is None else sched[:nreq],
-            initial_state_idx=None if comp is None else comp[:nreq],
-            num_accepted_tokens=acc, query_start_loc=query_start_loc_d(m, nreq, z_d.device),
-            max_query_len=idx.shape[1], pad_slot_id=PAD_SLOT_ID)
+            z_d, window, self._short_w(), None, activation=None,
+            conv_state_indices=rows[:n],
+            block_idx_last_scheduled_token=None if sched is None else sched[:n],
+            initial_state_idx=None if comp is None else comp[:n],
+            num_accepted_tokens=accepted, query_start_loc=packed_rows(m, n, z_d.device),
+            max_query_len=rows.shape[1], pad_slot_id=PAD_SLOT_ID)
         return zf[:, 0::3], zf[:, 1::3], zf[:, 2::3]
 
     def _spec_tensors(self, m, num_tokens, state, accepted):
-        """Verify metadata for the inner operator's snapshots (mixers.py:578-598)."""
-        ins, outs, starts, ends, acc = decode_tensors(m, num_tokens, 1 + self.num_spec,
-                                                      accepted)
-        return (cache_safe_state_indices(ins, state), cache_safe_state_indices(outs, state),
-                starts, ends, acc)
+        """(ins, outs, starts, ends, accepted) for the inner operator's
+        snapshots (mixers.py:578-598); `accepted` is the stamp-derived count,
+        or the engine's when there is none."""
+        plan = self._verify_plan(m)
+        if state.shape[0] != self.kv_cache[2].shape[0]:
+            raise ValueError(f"{self.prefix}: state slices of different pool sizes")
+        acc = plan.engine_accepted if accepted is None else accepted[:int(m.num_decodes)]
+        return plan.ins, plan.outs, plan.starts, plan.ends, acc
 
     @staticmethod
     def _unpad(out, hidden_states, n_actual):

@@ -1,4 +1,4 @@
-"""Host plumbing of speculative decode for the Hyena mixers (torch, no kernels).
+"""Host plumbing of speculative decode for the Hyena mixers.
 
 A verify step packs each decode request's anchor token and drafts into
 consecutive rows; request r owns rows query_start_loc_d[r] ..
@@ -13,14 +13,21 @@ Which snapshot is live is resolved from position stamps, not from vLLM's
 acceptance counts (mixers.py:17-28): every block carries in slice 2 row 0,
 last column, the number of tokens its snapshot represents; a request that
 has computed n' tokens finds its live snapshot at offset n' - stamp(column 0)
-(mixers.py:960-999).  Everything here is small index arithmetic on device
-tensors with no host synchronisation, so it can sit inside a captured step.
+(mixers.py:960-999).  Each piece is one small launch (csrc/spec.hip) over
+device tensors with no host synchronisation, so it can sit inside a
+captured step: the accepted counts from the stamps, the step's verify plan
+(snapshot blocks per position, packed row ranges, the engine's counts), the
+stamps a step writes, and align-mode prefix caching's repair of resumed
+prefill states.
 
 Stamp mismatches (a request whose stamps do not match its computed-token
 count) are counted in a device tensor the caller reads when it chooses
 (`HyenaMixerBase.stamp_faults`), where the reference raises a device-side
 assert: on ROCm such an assert aborts the whole process from inside a kernel.
 """
+
+import ctypes
+from typing import NamedTuple
 
 import torch
 
@@ -109,109 +116,143 @@ def record_stamps(stamps, slots, qsl, computed, width, out_col=None, prefill_blo
               _lib.stream_of(stamps))
 
 
-def accepted_tokens(m, num_reqs, device):
-    """vLLM's per-request accepted counts, >= 1; ones when absent
-    (mixers.py:431-441)."""
-    acc = getattr(m, "num_accepted_tokens", None)
-    if acc is None:
-        return torch.ones(num_reqs, device=device, dtype=torch.long)
-    if acc.numel() < num_reqs:
-        raise ValueError(f"num_accepted_tokens is too short: shape={tuple(acc.shape)}, "
-                         f"num_decodes={num_reqs}")
-    return acc[:num_reqs].to(dtype=torch.long).clamp_min(1)
+class VerifyPlan(NamedTuple):
+    """What the snapshot operators need about a step's decode requests,
+    besides the stamp-derived accepted counts: input and output snapshot
+    blocks per verifier position, the packed row range of each request, and
+    the engine's accepted counts (>= 1; ones when the step sends none)."""
+    ins: torch.Tensor        # (nreq, width) int32
+    outs: torch.Tensor       # (nreq, width) int32
+    starts: torch.Tensor     # (nreq,) int64
+    ends: torch.Tensor       # (nreq,) int64
+    engine_accepted: torch.Tensor  # (nreq,) int64
 
 
-def cache_all_decode_slots(m, slots, num_reqs, max_positions):
-    """Input and output slot windows from prefix caching's block pointers, or
-    the slot matrix itself for both (mixers.py:444-456)."""
-    previous = getattr(m, "block_idx_last_scheduled_token_prev_step", None)
-    scheduled = getattr(m, "block_idx_last_scheduled_token", None)
-    if previous is None or scheduled is None:
-        return slots, slots
-    width = slots.shape[1] if max_positions is None else min(slots.shape[1], max_positions)
-    offsets = torch.arange(width, device=slots.device, dtype=torch.long)
-    ins = slots.gather(1, previous[:num_reqs, None].long() + offsets)
-    outs = slots.gather(1, scheduled[:num_reqs, None].long() + offsets)
-    return ins, outs
-
-
-def decode_tensors(m, num_tokens, max_positions=None, accepted=None):
-    """(ins, outs, starts, ends, accepted) of the packed decode requests, all
-    on the device (mixers.py:459-524).  `accepted` defaults to vLLM's counts;
-    the mixers pass the stamp-derived ones."""
+def slot_matrix(m, nreq):
+    """The decode requests' slot rows as a 2-D view (one column when the
+    engine sends a vector)."""
     slots = m.state_indices_tensor_d
-    if slots.dim() == 1:
-        slots = slots[:, None]
-    if slots.dim() != 2:
-        raise ValueError(f"state_indices_tensor_d must be rank 1 or 2, got "
-                         f"shape={tuple(slots.shape)}")
-    num_reqs = int(m.num_decodes)
-    if slots.shape[0] < num_reqs:
-        raise ValueError(f"decode state rows={slots.shape[0]} smaller than "
-                         f"num_decodes={num_reqs}")
-    starts = getattr(m, "query_start_loc_d", None)
-    if starts is None:
-        if num_tokens != num_reqs:
-            raise ValueError("packed multi-token decode requires query_start_loc_d: "
-                             f"num_decode_tokens={num_tokens}, num_decodes={num_reqs}")
-        starts = torch.arange(num_reqs + 1, device=slots.device, dtype=torch.int64)
-    else:
-        if starts.numel() < num_reqs + 1:
-            raise ValueError(f"query_start_loc_d is too short: shape={tuple(starts.shape)}, "
-                             f"num_decodes={num_reqs}")
-    if accepted is None:
-        accepted = accepted_tokens(m, num_reqs, slots.device)
-    else:
-        accepted = accepted[:num_reqs].to(dtype=torch.long)
-    ins, outs = cache_all_decode_slots(m, slots[:num_reqs], num_reqs, max_positions)
-    first, last = _row_bounds(m, starts, num_reqs)
-    return ins, outs, first, last, accepted
+    if slots is None or slots.dim() not in (1, 2):
+        raise ValueError("state_indices_tensor_d must be a vector or a matrix of slot rows")
+    slots = slots[:, None] if slots.dim() == 1 else slots
+    if slots.shape[0] < nreq:
+        raise ValueError(f"{nreq} decode requests but {slots.shape[0]} slot rows")
+    return slots
 
 
-def _row_bounds(m, qsl, num_reqs):
-    """int64 (starts, ends) of the packed decode rows, computed once per
-    step: every layer of a step sees the same metadata, so the pair is kept
-    on it with the tensor it came from (held, so no other tensor can take
-    its address) and that tensor's version counter (an in-place update
-    recomputes)."""
-    cache = getattr(m, "_evo2_row_bounds", None)
-    if (cache is not None and cache[0] is qsl and cache[1] == qsl._version
-            and cache[2] == num_reqs):
-        return cache[3], cache[4]
-    s = qsl[:num_reqs + 1].to(torch.int64)
-    first, last = s[:-1], s[1:]
-    try:
-        m._evo2_row_bounds = (qsl, qsl._version, num_reqs, first, last)
-    except AttributeError:   # a metadata object that takes no new attributes
-        pass
-    return first, last
+def pool_holds(named, pool_blocks):
+    """False when a slot matrix naming `named` blocks is bigger than the
+    pool: the engine's profiling pass sizes the pool for one block per
+    request but sends one slot per verifier position, and every request then
+    sits on the null block (mixers.py:527-541).  Shape-only, so fixed under
+    capture."""
+    return int(named) <= int(pool_blocks)
 
 
-def cache_safe_state_indices(indices, state):
-    """The null block for every entry when a slot matrix names more blocks
-    than the pool holds: the engine's profiling pass allocates one block per
-    request but passes one index per verifier position (mixers.py:527-541).
-    Shape-only, so constant under graph capture."""
-    if indices.dim() == 2 and state.shape[0] < indices.numel():
-        return torch.zeros_like(indices)
-    return indices
-
-
-def query_start_loc_d(m, num_reqs, device):
-    """The decode rows' packed starts, or one row per request when the step
-    carries none (the form `decode_tensors` accepts)."""
+def packed_rows(m, nreq, device):
+    """(nreq + 1,) packed row starts of the decode requests: the engine's
+    query_start_loc_d, or one row per request when it sends none."""
     qsl = getattr(m, "query_start_loc_d", None)
-    if qsl is None:
-        if int(m.num_decode_tokens) != num_reqs:
-            raise ValueError("packed multi-token decode requires query_start_loc_d: "
-                             f"num_decode_tokens={int(m.num_decode_tokens)}, "
-                             f"num_decodes={num_reqs}")
-        return torch.arange(num_reqs + 1, device=device, dtype=torch.int32)
-    if qsl.numel() < num_reqs + 1:
-        raise ValueError(f"query_start_loc_d is too short: shape={tuple(qsl.shape)}, "
-                         f"num_decodes={num_reqs}")
-    return qsl[:num_reqs + 1]
+    if qsl is not None:
+        if qsl.numel() <= nreq:
+            raise ValueError(f"query_start_loc_d has {qsl.numel()} entries for {nreq} requests")
+        return qsl[:nreq + 1]
+    if int(m.num_decode_tokens) != nreq:
+        raise ValueError(f"{int(m.num_decode_tokens)} decode tokens in {nreq} requests need "
+                         "query_start_loc_d")
+    return torch.arange(nreq + 1, device=device, dtype=torch.int32)
 
 
-__all__ = ["spec_accepted", "record_stamps", "accepted_tokens", "cache_all_decode_slots",
-           "decode_tensors", "cache_safe_state_indices", "query_start_loc_d"]
+def _block_pointers(m, nreq):
+    """Prefix caching's block columns of the previous and this step's last
+    scheduled token, both or neither."""
+    prev = getattr(m, "block_idx_last_scheduled_token_prev_step", None)
+    sched = getattr(m, "block_idx_last_scheduled_token", None)
+    if prev is None or sched is None:
+        return None, None
+    return prev[:nreq], sched[:nreq]
+
+
+_PLAN_ATTR = "_evo2_verify_plan"
+
+
+def verify_plan(m, nreq, max_positions, pool_blocks):
+    """The step's `VerifyPlan`, one launch (`evo2_spec_plan`).  Slot windows
+    are the slot row itself, or with prefix caching's block pointers the
+    `max_positions` columns from each pointer; a pool smaller than the slot
+    matrix puts every request on the null block.  Kept on the metadata object
+    for the step's other layers while its input tensors are unchanged (their
+    version counters), and rebuilt on every call during graph capture so the
+    launch is part of the graph."""
+    slots = slot_matrix(m, nreq)
+    device = slots.device
+    rows = packed_rows(m, nreq, device)
+    qsl = rows if getattr(m, "query_start_loc_d", None) is not None else None  # else r, r + 1
+    prev, sched = _block_pointers(m, nreq)
+    eng = getattr(m, "num_accepted_tokens", None)
+    if eng is not None and eng.numel() < nreq:
+        raise ValueError(f"num_accepted_tokens has {eng.numel()} entries for {nreq} requests")
+    width = slots.shape[1] if prev is None else min(slots.shape[1], int(max_positions))
+    holds = pool_holds(nreq * width, pool_blocks)
+    # the engine's own tensors (views made here are new objects every call)
+    inputs = tuple(getattr(m, f, None) for f in (
+        "state_indices_tensor_d", "query_start_loc_d", "block_idx_last_scheduled_token_prev_step",
+        "block_idx_last_scheduled_token", "num_accepted_tokens"))
+    key = (nreq, width, holds) + tuple(None if t is None else (id(t), t._version) for t in inputs)
+    capturing = torch.cuda.is_current_stream_capturing()
+    memo = getattr(m, _PLAN_ATTR, None)
+    if memo is not None and memo[0] == key and not capturing:
+        return memo[2]
+    _lib.require_device(slots, qsl, prev, sched, eng)
+    qsl32, prev32, sched32, eng32 = (None if t is None else _i32(t[:nreq + 1] if t is qsl else t[:nreq])
+                                     for t in (qsl, prev, sched, eng))
+    slots32 = slots[:nreq] if slots.dtype == torch.int32 else slots[:nreq].to(torch.int32)
+    ins = torch.empty(nreq, width, dtype=torch.int32, device=device)
+    outs = torch.empty_like(ins)
+    bounds = torch.empty(3, nreq, dtype=torch.int64, device=device)
+    _lib.call("evo2_spec_plan", _lib.ptr(slots32), slots32.stride(0), slots32.stride(1),
+              slots32.shape[1], _lib.ptr(qsl32), _lib.ptr(prev32), _lib.ptr(sched32),
+              _lib.ptr(eng32), nreq, width, 0 if holds else 1, _lib.ptr(ins), _lib.ptr(outs),
+              _lib.ptr(bounds[0]), _lib.ptr(bounds[1]), _lib.ptr(bounds[2]),
+              _lib.stream_of(slots))
+    plan = VerifyPlan(ins, outs, bounds[0], bounds[1], bounds[2])
+    try:
+        # the inputs stay referenced, so no other tensor can take their ids
+        setattr(m, _PLAN_ATTR, (key, inputs, plan))
+    except (AttributeError, TypeError):
+        pass
+    return plan
+
+
+def repair_prefill_states(kv_cache, stamps, m, faults):
+    """Align-mode prefix caching: a prefill row resuming from n computed
+    tokens whose block is not stamped n, while the block of its last
+    computed token is, takes that block's three slices (mixers.py:1001-1040).
+    Two launches (decide, then copy only the rows that need it); a row whose
+    repair would race another's counts in `faults` instead."""
+    npf = int(m.num_prefills)
+    need = getattr(m, "computed_before_p", None)
+    src = getattr(m, "state_src_block_p", None)
+    flags = getattr(m, "has_initial_states_p", None)
+    if not npf or need is None or src is None or flags is None:
+        return
+    dst = m.state_indices_tensor_p
+    _lib.require_device(stamps, dst, src, need, flags, faults)
+    dst32, src32, need32 = (_i32(t[:npf]) for t in (dst, src, need))
+    init8 = flags[:npf].to(torch.uint8).contiguous()
+    take = torch.empty(npf, dtype=torch.int32, device=stamps.device)
+    ptrs = (ctypes.c_void_p * 3)(*[t.data_ptr() for t in kv_cache])
+    strides = (ctypes.c_int64 * 9)(*[st for t in kv_cache for st in t.stride()])
+    dims = (ctypes.c_int64 * 6)(*[d for t in kv_cache for d in t.shape[1:]])
+    sizes = (ctypes.c_int32 * 3)(*[t.element_size() for t in kv_cache])
+    for t in kv_cache:
+        if t.dim() != 3:
+            raise ValueError("state slices must be (blocks, d1, d2) views")
+    _lib.call("evo2_spec_repair_prefill", _lib.ptr(stamps), stamps.stride(0), stamps.shape[0],
+              _lib.ptr(dst32), _lib.ptr(src32), _lib.ptr(need32), _lib.ptr(init8), npf,
+              _lib.ptr(take), _lib.ptr(faults), ptrs, strides, dims, sizes,
+              _lib.stream_of(stamps))
+
+
+__all__ = ["spec_accepted", "record_stamps", "VerifyPlan", "verify_plan", "slot_matrix",
+           "pool_holds", "packed_rows", "repair_prefill_states"]

@@ -553,6 +553,56 @@ int evo2_spec_record_stamps(float *stamps, int64_t ss, int64_t num_blocks,
                             const int32_t *prefill_blocks, const int32_t *seq_lens,
                             int64_t npf, void *stream);
 
+/*
+ * Per-step verify plan of nreq speculative decode requests, one launch:
+ *   ins, outs  (nreq, width) int32: the input and output snapshot blocks of
+ *              position p.  With both block pointers (prev, sched: prefix
+ *              caching's block columns of the previous step's and this
+ *              step's last scheduled token) slot-row columns prev[r] + p and
+ *              sched[r] + p, else column p for both.  A column outside
+ *              [0, ncols), and every entry when null_all != 0, is block 0.
+ *   starts, ends (nreq,) int64: packed rows [qsl[r], qsl[r+1]) (qsl NULL:
+ *              one row per request, [r, r + 1)).
+ *   acc        (nreq,) int64: max(eng_acc[r], 1), or 1 with eng_acc NULL.
+ * slots (nreq, ncols) int32 at element strides si0, si1; qsl (nreq + 1,),
+ * prev, sched, eng_acc (nreq,) int32 or NULL (prev and sched together).
+ *
+ * Replaces the reference's decode-request plumbing (evo2_flash/mixers.py:
+ * 431-541: accepted counts, cache-all slot windows, the packed row range and
+ * the null-block rule for profiling-sized pools).
+ */
+int evo2_spec_plan(const int32_t *slots, int64_t si0, int64_t si1, int64_t ncols,
+                   const int32_t *qsl, const int32_t *prev, const int32_t *sched,
+                   const int32_t *eng_acc, int64_t nreq, int64_t width, int32_t null_all,
+                   int32_t *ins, int32_t *outs, int64_t *starts, int64_t *ends, int64_t *acc,
+                   void *stream);
+
+/*
+ * Align-mode repair of resumed prefill states, two launches.  Prefill row
+ * j < npf (has_init[j] nonzero) continues from need[j] computed tokens in
+ * block dst[j]; when dst[j]'s position stamp (stamps[b * ss]) is not need[j]
+ * and block src[j]'s is, all three state slices of src[j] are copied over
+ * dst[j].  Rows on the null block, blocks outside [0, num_blocks) and
+ * dst == src are left alone.  A row whose source is another repaired row's
+ * destination, or whose destination another repaired row also writes, is
+ * not repaired and adds one to *faults (int64).  take (npf,) int32 is the
+ * caller's workspace (the block each row copies from, -1 for none).
+ * Slice k: slice_ptr[k] base of the (blocks, d1, d2) view, element strides
+ * slice_strides[3k .. 3k+2], dims slice_dims[2k], slice_dims[2k+1], element
+ * size slice_es[k] (2 or 4 bytes).  The pointer and size arrays are host
+ * memory.
+ *
+ * Replaces the reference's _repair_resumed_prefill_state
+ * (evo2_flash/mixers.py:1001-1037), which copies every prefill row's state
+ * over itself or its source each step.
+ */
+int evo2_spec_repair_prefill(const float *stamps, int64_t ss, int64_t num_blocks,
+                             const int32_t *dst, const int32_t *src, const int32_t *need,
+                             const uint8_t *has_init, int64_t npf, int32_t *take,
+                             void *faults, void *const *slice_ptr,
+                             const int64_t *slice_strides, const int64_t *slice_dims,
+                             const int32_t *slice_es, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -21,7 +21,7 @@ __all__ = [
     "iir_verify_emulated", "STATE_ACC_BUDGET", "fast_accum_mm", "fp8_linear_fast_accum",
     "causal_conv1d_update_ref", "causal_conv1d_ref", "iir_final_state_recurrence",
     "causal_conv1d_update_spec_ref", "mixer_decode_speculative",
-    "spec_accepted_ref", "record_stamps_ref",
+    "spec_accepted_ref", "record_stamps_ref", "verify_plan_ref", "repair_prefill_ref",
 ]
 
 # mixers.py:72-74: bound on the (H, blk, L) temporary of the LI final state.
@@ -538,6 +538,54 @@ def record_stamps_ref(stamps, slots, qsl, computed, width, out_col=None, prefill
     for b, n in zip(prefill_blocks, seq_lens):
         put(int(b), int(n))
     return out
+
+
+def verify_plan_ref(slots, nreq, width, qsl=None, prev=None, sched=None, eng_acc=None,
+                    null_all=False):
+    """(ins, outs, starts, ends, acc) of a step's speculative decode requests
+    as lists, following the reference's _decode_tensors and its helpers
+    (mixers.py:431-541).  slots: rows of block ids.  Without both block
+    pointers ins = outs = the slot row; with them, width columns from
+    prev[r] and sched[r] (the reference's gather; a column outside the row
+    is the null block here, where torch's gather would raise).  The packed
+    rows are qsl[r] .. qsl[r+1], or r .. r+1 without qsl; acc =
+    max(eng_acc[r], 1), or 1 without counts.  null_all: the profiling-pool
+    rule, every block the null block (mixers.py:527-541)."""
+    def window(r, base):
+        row = slots[r]
+        out = []
+        for p in range(width):
+            c = base + p
+            out.append(0 if null_all or c < 0 or c >= len(row) else int(row[c]))
+        return out
+    paged = prev is not None and sched is not None
+    ins = [window(r, int(prev[r]) if paged else 0) for r in range(nreq)]
+    outs = [window(r, int(sched[r]) if paged else 0) for r in range(nreq)]
+    starts = [int(qsl[r]) if qsl is not None else r for r in range(nreq)]
+    ends = [int(qsl[r + 1]) if qsl is not None else r + 1 for r in range(nreq)]
+    acc = [max(int(eng_acc[r]), 1) if eng_acc is not None else 1 for r in range(nreq)]
+    return ins, outs, starts, ends, acc
+
+
+def repair_prefill_ref(slices, stamps, dst, src, need, has_init):
+    """Align-mode repair of resumed prefill states (mixers.py:1001-1037), on
+    copies: row j (has_init) whose block dst[j] is not stamped need[j] while
+    src[j] is takes src[j]'s contents in every slice; both blocks must be off
+    the null block.  All sources are read before any destination is written
+    (the reference's gather-then-scatter).  Returns (new slices, repaired
+    rows).  `stamps` lists each block's stamp."""
+    take = []
+    for j in range(len(dst)):
+        d, s_ = int(dst[j]), int(src[j])
+        bad = (bool(has_init[j]) and d != 0 and s_ != 0 and float(stamps[d]) != float(need[j])
+               and float(stamps[s_]) == float(need[j]))
+        take.append(s_ if bad else d)
+    out = [t.clone() for t in slices]
+    for t_new, t_old in zip(out, slices):
+        gathered = [t_old[b].clone() for b in take]
+        for j, d in enumerate(dst):
+            t_new[int(d)] = gathered[j]
+    return out, [j for j in range(len(dst)) if take[j] != int(dst[j])]
 
 
 # ------------------------------------------------------------ speculative verify

@@ -305,3 +305,93 @@ def test_stamp_kernels_vs_oracle(seed, with_counts, shifted):
                                    width, None if out_col is None else out_col.tolist(),
                                    pf_blocks.tolist(), pf_lens.tolist())
     assert stamps.cpu().tolist() == ref
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+@pytest.mark.parametrize("paged", [False, True])
+@pytest.mark.parametrize("packed", [False, True])
+def test_verify_plan_kernel_vs_oracle(seed, paged, packed):
+    """The step's verify plan (one launch) against `oracle.verify_plan_ref`:
+    slot windows with and without prefix caching's block pointers (some
+    running past the slot row), packed or one-row requests, the engine's
+    counts (zeros clamped to 1), and the profiling-pool rule; exact."""
+    from evo2_flash_amd.speculative import verify_plan
+    g = torch.Generator().manual_seed(seed)
+    nreq, cols, width = 9, 6, 4
+    slots = torch.randint(0, 50, (nreq, cols), generator=g, dtype=torch.int32)
+    lens = torch.randint(1, width + 1, (nreq,), generator=g)
+    qsl = torch.cat([torch.zeros(1, dtype=torch.int64), lens.cumsum(0)]).to(torch.int32)
+    prev = torch.randint(0, cols - 1, (nreq,), generator=g, dtype=torch.int32)
+    sched = torch.randint(0, cols, (nreq,), generator=g, dtype=torch.int32)
+    eng = torch.randint(0, 4, (nreq,), generator=g, dtype=torch.int32)
+    for pool, eng_on in ((100, True), (40, False)):   # 40 < 9 x 4: the profiling pool
+        m = HyenaMamba2Metadata(num_decodes=nreq, num_decode_tokens=int(qsl[-1]) if packed else nreq)
+        m.state_indices_tensor_d = slots.to(DEV)
+        m.query_start_loc_d = qsl.to(DEV) if packed else None
+        if paged:
+            m.block_idx_last_scheduled_token_prev_step = prev.to(DEV)
+            m.block_idx_last_scheduled_token = sched.to(DEV)
+        m.num_accepted_tokens = eng.to(DEV) if eng_on else None
+        plan = verify_plan(m, nreq, width, pool)
+        w = width if paged else cols
+        ref = oracle.verify_plan_ref(slots.tolist(), nreq, w, qsl=qsl.tolist() if packed else None,
+                                     prev=prev.tolist() if paged else None,
+                                     sched=sched.tolist() if paged else None,
+                                     eng_acc=eng.tolist() if eng_on else None,
+                                     null_all=pool < nreq * w)
+        got = (plan.ins.tolist(), plan.outs.tolist(), plan.starts.tolist(), plan.ends.tolist(),
+               plan.engine_accepted.tolist())
+        assert got == tuple(ref), (pool, eng_on)
+        assert verify_plan(m, nreq, width, pool) is plan   # kept for the step's other layers
+        m.state_indices_tensor_d.add_(0)                    # an in-place update rebuilds it
+        assert verify_plan(m, nreq, width, pool) is not plan
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_repair_kernel_vs_oracle(seed):
+    """Align-mode repair (two launches) against `oracle.repair_prefill_ref` on
+    a random speculative pool: repaired rows take all three slices of their
+    source bitwise, every other block is untouched; a row whose source is
+    another repaired row's destination is left alone and counted as a fault."""
+    from evo2_flash_amd.speculative import repair_prefill_states
+    g = torch.Generator().manual_seed(seed)
+    nb, H = 24, 128
+    pool = HyenaStatePool(nb, H, "cpu", num_spec=3)
+    pool.raw.copy_(torch.randint(0, 255, pool.raw.shape, generator=g, dtype=torch.uint8))
+    st = pool.stamps()
+    st.copy_(torch.randint(0, 6, (nb,), generator=g).float())
+    # row: dst, src, need -- and what happens
+    #  0: 2 <- 3, need 3, dst stale, src right      repaired
+    #  1: 4 <- 6, need 5, dst already right         untouched
+    #  2: 7 <- 8, need 99, neither block right      untouched
+    #  3: 9 <- 10, need 2, dst stale, src right     repaired
+    #  4: 11 <- 12, fresh prefill (no initial state) untouched
+    #  5: null destination                          untouched
+    #  6: null source                               untouched
+    #  7: 15 <- 9, need 4: wants block 9, which row 3 repairs: refused, a fault
+    dst = [2, 4, 7, 9, 11, 0, 13, 15]
+    src = [3, 6, 8, 10, 12, 5, 0, 9]
+    need = [3, 5, 99, 2, 1, 1, 1, 4]
+    init = [1, 1, 1, 1, 0, 1, 1, 1]
+    for b, v in ((2, 0), (3, 3), (4, 5), (6, 5), (9, 4), (10, 2), (15, 1), (12, 1), (11, 0)):
+        st[b] = float(v)
+    gp = HyenaStatePool(nb, H, DEV, num_spec=3)
+    gp.raw.copy_(pool.raw)
+    m = HyenaMamba2Metadata(num_prefills=len(dst))
+    m.state_indices_tensor_p = torch.tensor(dst, dtype=torch.int32, device=DEV)
+    m.state_src_block_p = torch.tensor(src, dtype=torch.int64, device=DEV)
+    m.computed_before_p = torch.tensor(need, dtype=torch.int64, device=DEV)
+    m.has_initial_states_p = torch.tensor(init, dtype=torch.bool, device=DEV)
+    faults = torch.zeros((), dtype=torch.int64, device=DEV)
+    repair_prefill_states(gp.kv_cache, gp.stamps(), m, faults)
+    flat = [t.reshape(nb, -1) for t in pool.kv_cache]
+    ref_slices, rows = oracle.repair_prefill_ref(flat, st.tolist(), dst, src, need, init)
+    # the oracle's gather-then-scatter repairs the clashing row 7 as well;
+    # the kernel refuses it and counts one fault
+    assert rows == [0, 3, 7]
+    expect = [t.clone() for t in ref_slices]
+    for t_exp, t_old in zip(expect, flat):
+        t_exp[dst[7]] = t_old[dst[7]]
+    for k in range(3):
+        assert torch.equal(_bits(gp.kv_cache[k].reshape(nb, -1).cpu()), _bits(expect[k])), k
+    assert int(faults) == 1

@@ -6,9 +6,10 @@ layout the reference states (mixers.py:222-240), and by the rollback
 invariant the layout exists for: after any accepted prefix of a verify step,
 the next step computes what one-token-at-a-time decoding of the accepted
 tokens would.  The position-stamp rollback of the mixers (mixers.py:952-1074)
-is torch index arithmetic and runs here on CPU tensors: stamps written per
-snapshot, accepted counts resolved from them, mismatches counted, and the
-align-mode repair of a resumed prefill.
+is small launches on the GPU; here the oracle's restatements of it are pinned
+by hand-worked cases: stamps written per snapshot, accepted counts resolved
+from them, mismatches counted, the step's verify plan, and the align-mode
+repair of a resumed prefill.
 """
 
 import pytest
@@ -19,7 +20,7 @@ from evo2_flash_amd.config import HyenaConfig
 from evo2_flash_amd.metadata import (HyenaMamba2Metadata, HyenaMamba2MetadataBuilder,
                                      Mamba2Metadata, build_metadata)
 from evo2_flash_amd.mixers import make_mixer
-from evo2_flash_amd.speculative import cache_safe_state_indices, decode_tensors
+from evo2_flash_amd.speculative import pool_holds
 from evo2_flash_amd.state import HyenaStatePool, page_bytes, unified_state_shape
 
 
@@ -203,28 +204,34 @@ def test_resolve_needs_computed_counts():
     assert plain._resolve_accepted(m) is None
 
 
-def test_repair_resumed_prefill_state():
-    """A prefill row resuming from n computed tokens whose block is not
-    stamped n takes its state (all three slices) from the block of its last
-    computed token when that one is stamped n (mixers.py:1001-1040)."""
-    mixer, pool = _mixer("hcl")
+def test_repair_resumed_prefill_ref():
+    """The oracle's align-mode repair (mixers.py:1001-1040), hand-worked: a
+    prefill row resuming from n computed tokens whose block is not stamped n
+    takes its state (all three slices) from the block of its last computed
+    token when that one is stamped n; a row already right, and one with
+    neither block stamped n, are untouched.  The GPU kernels are checked
+    against this in test_speculative_gpu.py."""
+    pool = HyenaStatePool(10, 128, "cpu", num_spec=3)
     g = torch.Generator().manual_seed(5)
     pool.raw.copy_(torch.randint(0, 255, pool.raw.shape, generator=g, dtype=torch.uint8))
     st = pool.stamps()
     st[2], st[3] = 5.0, 40.0     # row 0: dst 2 stale, src 3 good  -> repaired
     st[4], st[6] = 40.0, 40.0    # row 1: dst 4 already right      -> untouched
     st[7], st[8] = 1.0, 2.0      # row 2: neither matches          -> untouched
-    before = pool.raw.clone()
-    m = build_metadata(prefill_lens=[3, 3, 3], prefill_slots=[2, 4, 7], has_init=[1, 1, 1],
-                       device="cpu")
-    m.computed_before_p = torch.tensor([40, 40, 40])
-    m.state_src_block_p = torch.tensor([3, 6, 8])
-    mixer._repair_resumed_prefill_state(m)
-    for i in range(3):   # bitwise (random bytes hold NaNs)
-        assert torch.equal(pool.kv_cache[i][2].contiguous().view(torch.uint8),
-                           pool.kv_cache[i][3].contiguous().view(torch.uint8))
-    changed = (pool.raw != before).any(dim=1).nonzero().view(-1).tolist()
-    assert changed == [2]
+    slices = [t.contiguous().view(torch.uint8) if t.dtype != torch.uint8 else t
+              for t in (pool.kv_cache[0].view(10, -1), pool.kv_cache[1].reshape(10, -1),
+                        pool.kv_cache[2].reshape(10, -1))]
+    new, rows = oracle.repair_prefill_ref(slices, st.tolist(), [2, 4, 7], [3, 6, 8],
+                                          [40, 40, 40], [1, 1, 1])
+    assert rows == [0]
+    for old, upd in zip(slices, new):
+        assert torch.equal(upd[2], old[3])
+        keep = [b for b in range(10) if b != 2]
+        assert torch.equal(upd[keep], old[keep])
+    # a null destination or source, or a fresh row, is never repaired
+    _, rows = oracle.repair_prefill_ref(slices, st.tolist(), [0, 2, 2], [3, 0, 3], [40] * 3,
+                                        [1, 1, 0])
+    assert rows == []
 
 
 def test_metadata_builder():
@@ -248,21 +255,23 @@ def test_metadata_builder():
     assert plain.computed_before_p is None and plain.state_src_block_p is None
 
 
-def test_decode_tensors_and_cache_all_slots():
-    m = _spec_meta([[1, 2, 3, 4, 5, 6], [7, 8, 9, 10, 11, 12]], [2, 3], [0, 0])
-    ins, outs, starts, ends, acc = decode_tensors(m, 5, 4)
-    assert torch.equal(ins, outs) and ins.shape == (2, 6)
-    assert starts.tolist() == [0, 2] and ends.tolist() == [2, 5] and acc.tolist() == [1, 1]
-    m.num_accepted_tokens = torch.tensor([3, 0])
-    assert decode_tensors(m, 5, 4)[4].tolist() == [3, 1]      # clamped to >= 1
-    m.block_idx_last_scheduled_token_prev_step = torch.tensor([0, 2])
-    m.block_idx_last_scheduled_token = torch.tensor([1, 1])
-    ins, outs, *_ = decode_tensors(m, 5, 4)
-    assert ins.tolist() == [[1, 2, 3, 4], [9, 10, 11, 12]]
-    assert outs.tolist() == [[2, 3, 4, 5], [8, 9, 10, 11]]
-    with pytest.raises(ValueError, match="query_start_loc_d"):
-        m.query_start_loc_d = None
-        decode_tensors(m, 5, 4)
-    # profiling-sized pools map a wide slot matrix to the null block
-    assert cache_safe_state_indices(torch.ones(2, 4, dtype=torch.int32),
-                                    torch.zeros(5, 3)).sum() == 0
+def test_verify_plan_ref_and_pool_rule():
+    """The oracle's verify plan (mixers.py:431-541), hand-worked: without
+    block pointers the slot row is both the input and the output window;
+    with them, windows of `width` columns from each pointer; the engine's
+    accepted counts are clamped to >= 1; a profiling-sized pool puts every
+    request on the null block."""
+    slots = [[1, 2, 3, 4, 5, 6], [7, 8, 9, 10, 11, 12]]
+    ins, outs, starts, ends, acc = oracle.verify_plan_ref(slots, 2, 6, qsl=[0, 2, 5])
+    assert ins == outs == slots
+    assert starts == [0, 2] and ends == [2, 5] and acc == [1, 1]
+    assert oracle.verify_plan_ref(slots, 2, 6, eng_acc=[3, 0])[4] == [3, 1]
+    ins, outs, starts, ends, _ = oracle.verify_plan_ref(slots, 2, 4, prev=[0, 2], sched=[1, 1])
+    assert ins == [[1, 2, 3, 4], [9, 10, 11, 12]]
+    assert outs == [[2, 3, 4, 5], [8, 9, 10, 11]]
+    assert starts == [0, 1] and ends == [1, 2]
+    # a window running past the row reads the null block
+    assert oracle.verify_plan_ref(slots, 2, 4, prev=[4, 0], sched=[0, 0])[0][0] == [5, 6, 0, 0]
+    assert oracle.verify_plan_ref(slots, 2, 6, null_all=True)[0] == [[0] * 6] * 2
+    # the pool rule: a slot matrix naming more blocks than the pool holds
+    assert pool_holds(8, 8) and not pool_holds(9, 8)
