@@ -387,6 +387,10 @@ __global__ __launch_bounds__(256) void fp8_gemm_persist_kernel(GemmArgs p, int t
     int bn, bm;
     persist_tile(static_cast<int>(blockIdx.x) + j * static_cast<int>(gridDim.x), tiles_n, tiles_m,
                  grouped != 0, bn, bm);
+    // The order is a bijection onto the grid (checked on the host for every
+    // grid up to 64 x 40 tiles); a tile outside it stores nothing rather than
+    // past the output (the operand loads are bounded by their descriptors).
+    if (bn < 0 || bn >= tiles_n || bm < 0 || bm >= tiles_m) return;  // wave-uniform
     // whole tiles only (the host checks M and N are multiples of 256 and the
     // output rows 8-byte aligned)
     const int n0 = bn * G_BN, m0 = bm * G_BM;

@@ -680,6 +680,33 @@ def test_fast_accum_known_answers():
     assert _fa([]) == 0.0
 
 
+def test_fp8_linear_fast_accum_scales_known_answer():
+    """The emulated static W8A8 linear's quantisation and scale epilogue
+    (fp8_emul_triton.py:181-191), hand-worked with non-unit scales.
+    x / s_in must be exact E4M3 values, the products exact, the sum below
+    the fast-accumulation ulp, and the epilogue acc * s_in * s_w then rounds
+    once to bf16:
+      x = (1, 2, -0.5, 3, 0 ...), s_in = 0.5 -> (2, 4, -1, 6, 0 ...)
+      row 0: w = (1, 0.5, 2, -1)      -> acc = 2 + 2 - 2 - 6 = -4
+      row 1: w = (0.25, 0.125, 4, 1)  -> acc = 0.5 + 0.5 - 4 + 6 = 3
+      s_w = 0.375 -> out = acc * 0.1875 = (-0.75, 0.5625), exact in bf16;
+    and a saturating case: x = 300 with s_in = 0.5 clamps to 448, so the
+    output is 448 * w * s_in * s_w, not 600 * w * s_in * s_w."""
+    pad = lambda rows: torch.nn.functional.pad(torch.tensor(rows), (0, 28))  # K = 32
+    x = pad([[1.0, 2.0, -0.5, 3.0]]).to(torch.bfloat16)
+    w = pad([[1.0, 0.5, 2.0, -1.0], [0.25, 0.125, 4.0, 1.0]]).to(torch.float8_e4m3fn)
+    out = oracle.fp8_linear_fast_accum(x, w, 0.5, 0.375)
+    assert out.dtype == torch.bfloat16 and out.shape == (1, 2)
+    assert out.float().tolist() == [[-0.75, 0.5625]]
+    # the scales are not applied to each other first: a non-dyadic s_w rounds
+    # only in the final bf16 cast: acc = 3, 3 * 0.5 * 0.1 = 0.15 -> bf16(0.15)
+    out = oracle.fp8_linear_fast_accum(x, w[1:], 0.5, 0.1)
+    assert out.float().item() == torch.tensor(3 * 0.5 * 0.1).to(torch.bfloat16).float().item()
+    sat = oracle.fp8_linear_fast_accum(pad([[300.0, 0, 0, 0]]).to(torch.bfloat16), w[:1],
+                                       0.5, 0.375)
+    assert sat.float().item() == 448.0 * 1.0 * 0.5 * 0.375
+
+
 def test_fast_accum_close_to_fp32_but_not_equal():
     g = torch.Generator().manual_seed(3)
     a = (torch.randn(16, 256, generator=g) * 4).to(torch.float8_e4m3fn).float()

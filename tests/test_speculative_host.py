@@ -22,6 +22,7 @@ from evo2_flash_amd.metadata import (HyenaMamba2Metadata, HyenaMamba2MetadataBui
 from evo2_flash_amd.mixers import make_mixer
 from evo2_flash_amd.speculative import pool_holds
 from evo2_flash_amd.state import HyenaStatePool, page_bytes, unified_state_shape
+from evo2_flash_amd.synthetic import mixer_params
 
 
 def _rand_window(nb, dim, width, seed):
@@ -275,3 +276,96 @@ def test_verify_plan_ref_and_pool_rule():
     assert oracle.verify_plan_ref(slots, 2, 6, null_all=True)[0] == [[0] * 6] * 2
     # the pool rule: a slot matrix naming more blocks than the pool holds
     assert pool_holds(8, 8) and not pool_holds(9, 8)
+
+
+def _spec_pool(H, nb, nspec, seed):
+    g = torch.Generator().manual_seed(seed)
+    pool = HyenaStatePool(nb, H, "cpu", num_spec=nspec)
+    pool.kv_cache[0].copy_(torch.randn(pool.kv_cache[0].shape, generator=g).to(torch.bfloat16))
+    pool.kv_cache[1].copy_(torch.randn(pool.kv_cache[1].shape, generator=g)
+                           .to(torch.bfloat16).float())
+    pool.kv_cache[2].copy_(torch.randn(pool.kv_cache[2].shape, generator=g) * 5)
+    return pool
+
+
+def _clone(pool, nspec):
+    p = HyenaStatePool(pool.num_blocks, pool.hidden, "cpu", num_spec=nspec)
+    p.raw.copy_(pool.raw)
+    return p
+
+
+def _operator(kind, prm, H):
+    """(inner, log_poles, poles, state view of a pool)"""
+    if kind == "hcl":
+        lp = prm["log_poles"][..., 0]
+        return prm["residues"], lp, torch.exp(lp.float()), lambda p: p.ssm_view()
+    K = prm["conv"].shape[-1]
+    return prm["conv"].view(H, K), None, None, lambda p: p.inner_view()
+
+
+@pytest.mark.parametrize("kind", ["hcs", "hcm", "hcl"])
+@pytest.mark.parametrize("emulate", [True, False])
+def test_speculative_composition_at_one_token(kind, emulate):
+    """One token per request, previous step fully accepted (accepted = 1):
+    the oracle's speculative composition (widened window, snapshot operator,
+    D, gate) equals the plain decode composition bit for bit -- the kernel-
+    order emulations (`hyena_decode_emulated`) or the reference's torch
+    paths (`mixer_decode_unfused`) -- outputs and the written inner state."""
+    H, nb, nspec = 64, 8, 3
+    prm = mixer_params(kind, H, 3, in_proj_fp8=False)
+    sw = prm["short_filter"].view(3 * H, 3)
+    inner, lp, poles, view = _operator(kind, prm, H)
+    pool = _spec_pool(H, nb, nspec, 1)
+    g = torch.Generator().manual_seed(2)
+    z = (torch.randn(3, 3 * H, generator=g) * 1.3).to(torch.bfloat16)
+    slots = torch.tensor([[2, 3, 4, 5], [6, 7, 1, 1], [1, 1, 1, 1]])
+    p1, p2 = _clone(pool, nspec), _clone(pool, nspec)
+    gs = oracle.mixer_decode_speculative(z, sw, p1.conv_view(), inner, view(p1), prm.get("D"),
+                                         slots, [0, 1, 2, 3], [1, 1, 1], 1, poles=poles,
+                                         emulate_kernels=emulate)
+    window = p2.conv_view()[..., :2]
+    if emulate:
+        gd = oracle.hyena_decode_emulated(z, sw, window, slots[:, 0], inner, view(p2),
+                                          prm.get("D"), lp)
+    else:
+        gd = oracle.mixer_decode_unfused(z, sw, window, slots[:, 0].tolist(), inner,
+                                         view(p2), prm.get("D"), lp)
+    assert torch.equal(gs.view(torch.int16), gd.view(torch.int16))
+    for b in (2, 6):
+        assert torch.equal(view(p1)[b], view(p2)[b])
+
+
+@pytest.mark.parametrize("kind", ["hcs", "hcm", "hcl"])
+@pytest.mark.parametrize("emulate", [True, False])
+def test_fully_accepted_step_equals_chained_decodes(kind, emulate):
+    """A verify step of Q tokens per request equals Q one-token decodes run in
+    turn on the request's block, bit for bit: every output row, and the
+    snapshot in the step's last column equals the state after the Q-th
+    decode."""
+    H, nb, nspec, Q = 64, 10, 3, 4
+    prm = mixer_params(kind, H, 5, in_proj_fp8=False)
+    sw = prm["short_filter"].view(3 * H, 3)
+    inner, lp, poles, view = _operator(kind, prm, H)
+    pool = _spec_pool(H, nb, nspec, 4)
+    g = torch.Generator().manual_seed(6)
+    slots = torch.tensor([[2, 3, 4, 5], [6, 7, 8, 9]])
+    z = (torch.randn(2 * Q, 3 * H, generator=g) * 1.3).to(torch.bfloat16)
+    p1 = _clone(pool, nspec)
+    gs = oracle.mixer_decode_speculative(z, sw, p1.conv_view(), inner, view(p1), prm.get("D"),
+                                         slots, [0, Q, 2 * Q], [1, 1], Q, poles=poles,
+                                         emulate_kernels=emulate)
+    width = inner.shape[1] - 1 if kind != "hcl" else 16
+    for r in range(2):
+        p2 = _clone(pool, nspec)
+        blk = int(slots[r, 0])
+        for p in range(Q):
+            row = z[r * Q + p:r * Q + p + 1]
+            window = p2.conv_view()[..., :2]
+            if emulate:
+                y = oracle.hyena_decode_emulated(row, sw, window, torch.tensor([blk]), inner,
+                                                 view(p2), prm.get("D"), lp)
+            else:
+                y = oracle.mixer_decode_unfused(row, sw, window, [blk], inner, view(p2),
+                                                prm.get("D"), lp)
+            assert torch.equal(y.view(torch.int16), gs[r * Q + p:r * Q + p + 1].view(torch.int16)), (r, p)
+        assert torch.equal(view(p2)[blk][:, :width], view(p1)[int(slots[r, Q - 1])][:, :width])
