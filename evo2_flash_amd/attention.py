@@ -62,7 +62,9 @@ def paged_decode_attention(q, k_pages, v_pages, block_table, positions, scale, w
     v_pages (pages, heads, 16, head_dim) bf16; block_table (>= B, max_pages)
     int32 (position l of sequence b is in page block_table[b, l // 16]);
     positions (B,) int64 (sequence b attends to 0..positions[b]).  Returns
-    (B, heads, head_dim) bf16."""
+    (B, heads, head_dim) bf16.  The kernel never reads through a table entry
+    outside [0, pages): the positions of such an entry are left out of the
+    softmax (check_block_table finds them on the host)."""
     _lib.require_device(q, k_pages, v_pages, block_table, positions, work)
     B, heads, hd = q.shape
     max_pages = block_table.shape[1]
@@ -84,11 +86,34 @@ def paged_decode_attention(q, k_pages, v_pages, block_table, positions, scale, w
               _lib.ptr(q), q.stride(0), q.stride(1),
               _lib.ptr(k_pages), k_pages.stride(0), k_pages.stride(1), k_pages.stride(2),
               _lib.ptr(v_pages), v_pages.stride(0), v_pages.stride(1), v_pages.stride(2),
-              _lib.ptr(block_table), block_table.stride(0),
+              k_pages.shape[0], _lib.ptr(block_table), block_table.stride(0),
               _lib.ptr(positions), _lib.ptr(work), work.numel() * 4,
               _lib.ptr(out), out.stride(0), out.stride(1),
               B, heads, hd, max_pages, float(scale), _lib.stream_of(q))
     return out
+
+
+def check_block_table(block_table, lengths, num_pages, first_page=1):
+    """Raise ValueError unless every page that sequence b's first lengths[b]
+    positions use (block_table[b, :ceil(lengths[b] / 16)]) lies in
+    [first_page, num_pages) (page 0 is the cache's null page).  For tables
+    built on the host; a device table is copied to the host first."""
+    table = block_table.detach().cpu()
+    lengths = [int(n) for n in (lengths.detach().cpu().tolist()
+                                if torch.is_tensor(lengths) else lengths)]
+    if table.dim() != 2 or len(lengths) > table.shape[0]:
+        raise ValueError(f"block_table {tuple(table.shape)} cannot serve {len(lengths)} sequences")
+    for b, n in enumerate(lengths):
+        npg = -(-n // PAGE)
+        if npg > table.shape[1]:
+            raise ValueError(f"sequence {b}: {n} positions need {npg} pages, the table has "
+                             f"{table.shape[1]}")
+        row = table[b, :npg]
+        bad = (row < first_page) | (row >= num_pages)
+        if bool(bad.any()):
+            j = int(bad.nonzero()[0, 0])
+            raise ValueError(f"sequence {b}: block_table[{b}, {j}] = {int(row[j])} is outside "
+                             f"[{first_page}, {num_pages})")
 
 
 class PagedKVCache:
@@ -180,5 +205,5 @@ def causal_prefill_attention(q, k, v, scale):
     return _causal_chunked(q, k, v, scale)
 
 
-__all__ = ["decode_attention", "workspace", "paged_decode_attention", "PagedKVCache",
-           "causal_prefill_attention", "PAGE"]
+__all__ = ["decode_attention", "workspace", "paged_decode_attention", "check_block_table",
+           "PagedKVCache", "causal_prefill_attention", "PAGE"]

@@ -14,6 +14,10 @@
 //
 //   out[b, h] = sum_l softmax_l(scale * q . k_l) v_l  over l <= positions[b]
 //
+// A table entry outside [0, num_pages) is never dereferenced: the positions
+// it would hold are left out of the softmax (a sequence with none left gets
+// zeros), so a stale or garbage entry gives a wrong row, not a fault.
+//
 // Split over the context (flash decoding): workgroup (c, h, b) takes the
 // 2048 positions of chunk c, computes its scores with 16-byte loads of eight
 // consecutive positions per lane (q in LDS), the chunk's max and exp-sum with
@@ -37,6 +41,7 @@ struct AttnArgs {
   const bf16_t *v; int64_t vb, vh, vl;       // (B, heads, L, hd) or (pages, heads, 16, hd);
                                              // dim stride 1 (vb: sequence or page)
   const int32_t *tbl; int64_t tbs;           // paged: (B, L / 16) block table, row stride
+  int64_t num_pages;                         // paged: entries outside [0, num_pages) masked
   const int64_t *pos;                        // (B,) this step's position; length pos + 1
   float *part;                               // (B, heads, nchunk, hd + 2): o, max, sum
   bf16_t *out; int64_t ob, oh;               // (B, heads, hd), dim stride 1
@@ -71,8 +76,10 @@ __global__ __launch_bounds__(AT_T) void attn_chunk_kernel(AttnArgs p) {
   }
   if (t < HD) qs[t] = bf2f(p.q[(int64_t)b * p.qb + (int64_t)h * p.qh + t]);
   if constexpr (PAGED) {  // the chunk's pages that hold positions below l1
-    if (t < AT_CHUNK / AT_PAGE && l0 + AT_PAGE * t < l1)
-      pages[t] = p.tbl[(int64_t)b * p.tbs + l0 / AT_PAGE + t];
+    if (t < AT_CHUNK / AT_PAGE && l0 + AT_PAGE * t < l1) {
+      const int32_t pg = p.tbl[(int64_t)b * p.tbs + l0 / AT_PAGE + t];
+      pages[t] = pg >= 0 && pg < p.num_pages ? pg : -1;  // -1: masked
+    }
   }
   __syncthreads();
 
@@ -80,10 +87,11 @@ __global__ __launch_bounds__(AT_T) void attn_chunk_kernel(AttnArgs p) {
   // starts below l1 inside the cache; in the paged cache the eight lie in
   // one page)
   const int lb = l0 + 8 * t;
+  const bool live = lb < l1 && (!PAGED || pages[(lb - l0) / AT_PAGE] >= 0);
   float s[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) s[e] = 0.0f;
-  if (lb < l1) {
+  if (live) {
     const bf16_t *kr =
         PAGED ? p.k + (int64_t)pages[(lb - l0) / AT_PAGE] * p.kb + (int64_t)h * p.kh + lb % AT_PAGE
               : p.k + (int64_t)b * p.kb + (int64_t)h * p.kh + lb;
@@ -100,7 +108,7 @@ __global__ __launch_bounds__(AT_T) void attn_chunk_kernel(AttnArgs p) {
   float mx = -INFINITY;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    s[e] = lb + e < l1 ? s[e] * p.scale : -INFINITY;
+    s[e] = live && lb + e < l1 ? s[e] * p.scale : -INFINITY;
     mx = fmaxf(mx, s[e]);
   }
   for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
@@ -108,11 +116,11 @@ __global__ __launch_bounds__(AT_T) void attn_chunk_kernel(AttnArgs p) {
   __syncthreads();
   mx = red[0];
 #pragma unroll
-  for (int w = 1; w < AT_T / 64; ++w) mx = fmaxf(mx, red[w]);  // finite: l0 < l1
+  for (int w = 1; w < AT_T / 64; ++w) mx = fmaxf(mx, red[w]);  // -inf only if all masked
   float sum = 0.0f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    const float pe = lb + e < l1 ? expf(s[e] - mx) : 0.0f;
+    const float pe = live && lb + e < l1 ? expf(s[e] - mx) : 0.0f;
     ps[8 * t + e] = pe;
     sum += pe;
   }
@@ -133,9 +141,10 @@ __global__ __launch_bounds__(AT_T) void attn_chunk_kernel(AttnArgs p) {
   {
     const bf16_t *vr = p.v + (PAGED ? 0 : (int64_t)b * p.vb) + (int64_t)h * p.vh + 8 * g;
     for (int l = l0 + wave * RW + r; l < l1; l += (AT_T / 64) * RW) {
-      const bf16_t *row =
-          PAGED ? vr + (int64_t)pages[(l - l0) / AT_PAGE] * p.vb + (int64_t)(l % AT_PAGE) * p.vl
-                : vr + (int64_t)l * p.vl;
+      const int pg = PAGED ? pages[(l - l0) / AT_PAGE] : 0;
+      if (PAGED && pg < 0) continue;  // masked page: weight 0, never read
+      const bf16_t *row = PAGED ? vr + (int64_t)pg * p.vb + (int64_t)(l % AT_PAGE) * p.vl
+                                : vr + (int64_t)l * p.vl;
       const uint4 vv = *reinterpret_cast<const uint4 *>(row);
       const float pl = ps[l - l0];
       o[0] += pl * lo_bf(vv.x); o[1] += pl * hi_bf(vv.x);
@@ -179,11 +188,12 @@ __global__ __launch_bounds__(HD) void attn_merge_kernel(AttnArgs p) {
   for (int c = 0; c < nc; ++c) M = fmaxf(M, part[c * (HD + 2) + HD]);
   float tot = 0.0f, o = 0.0f;
   for (int c = 0; c < nc; ++c) {
-    const float f = expf(part[c * (HD + 2) + HD] - M);
+    const float mc = part[c * (HD + 2) + HD];
+    const float f = mc == -INFINITY ? 0.0f : expf(mc - M);  // a chunk of masked pages
     tot += f * part[c * (HD + 2) + HD + 1];
     o += f * part[c * (HD + 2) + d];
   }
-  p.out[(int64_t)b * p.ob + (int64_t)h * p.oh + d] = f2bf(nc > 0 ? o / tot : 0.0f);
+  p.out[(int64_t)b * p.ob + (int64_t)h * p.oh + d] = f2bf(tot > 0.0f ? o / tot : 0.0f);
 }
 
 template <int HD, bool PAGED>
@@ -229,7 +239,7 @@ extern "C" int evo2_decode_attention(const void *q, int64_t qb, int64_t qh,
       vl % 8 || vh % 8 || vb % 8 || reinterpret_cast<uintptr_t>(v) % 16 || L > 0x7fffffff)
     return fail(EVO2_ERR_UNSUPPORTED, "decode_attention: cache strides or alignment not supported");
   AttnArgs a{static_cast<const bf16_t *>(q), qb, qh, static_cast<const bf16_t *>(k), kb, kh, kd,
-             static_cast<const bf16_t *>(v), vb, vh, vl, nullptr, 0, positions, workspace,
+             static_cast<const bf16_t *>(v), vb, vh, vl, nullptr, 0, 0, positions, workspace,
              static_cast<bf16_t *>(out), ob, oh, scale, static_cast<int>(heads),
              static_cast<int>(L), static_cast<int>(cdiv(L, AT_CHUNK))};
   hipStream_t st = static_cast<hipStream_t>(stream);
@@ -239,16 +249,18 @@ extern "C" int evo2_decode_attention(const void *q, int64_t qb, int64_t qh,
 extern "C" int evo2_paged_decode_attention(const void *q, int64_t qb, int64_t qh,
                                            const void *k_pages, int64_t kp, int64_t kh, int64_t kd,
                                            const void *v_pages, int64_t vp, int64_t vh, int64_t vl,
-                                           const int32_t *block_table, int64_t tbs,
+                                           int64_t num_pages, const int32_t *block_table,
+                                           int64_t tbs,
                                            const int64_t *positions, float *workspace,
                                            int64_t workspace_bytes, void *out, int64_t ob,
                                            int64_t oh, int64_t B, int64_t heads,
                                            int64_t head_dim, int64_t max_pages, float scale,
                                            void *stream) {
   if (B < 0 || heads <= 0 || max_pages <= 0 || B > 65535 || heads > 65535 ||
-      max_pages > (int64_t(1) << 26))
-    return fail(EVO2_ERR_INVALID, "paged_decode_attention: bad sizes B=%lld heads=%lld pages=%lld",
-                (long long)B, (long long)heads, (long long)max_pages);
+      max_pages > (int64_t(1) << 26) || num_pages <= 0)
+    return fail(EVO2_ERR_INVALID,
+                "paged_decode_attention: bad sizes B=%lld heads=%lld pages=%lld num_pages=%lld",
+                (long long)B, (long long)heads, (long long)max_pages, (long long)num_pages);
   if (head_dim != 64 && head_dim != 128)
     return fail(EVO2_ERR_UNSUPPORTED, "paged_decode_attention: head_dim %lld (64 or 128)",
                 (long long)head_dim);
@@ -265,7 +277,7 @@ extern "C" int evo2_paged_decode_attention(const void *q, int64_t qb, int64_t qh
                 "paged_decode_attention: page strides or alignment not supported");
   AttnArgs a{static_cast<const bf16_t *>(q), qb, qh, static_cast<const bf16_t *>(k_pages), kp,
              kh, kd, static_cast<const bf16_t *>(v_pages), vp, vh, vl, block_table, tbs,
-             positions, workspace, static_cast<bf16_t *>(out), ob, oh, scale,
+             num_pages, positions, workspace, static_cast<bf16_t *>(out), ob, oh, scale,
              static_cast<int>(heads), static_cast<int>(L), static_cast<int>(cdiv(L, AT_CHUNK))};
   hipStream_t st = static_cast<hipStream_t>(stream);
   return head_dim == 64 ? launch_attn<64, true>(a, B, st) : launch_attn<128, true>(a, B, st);

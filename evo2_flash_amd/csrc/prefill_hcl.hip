@@ -475,13 +475,27 @@ static std::mutex g_scratch_mu;
 static float *g_scratch_dev[HCL_MAX_DEVICES];
 
 // This device's address of `scratch` (looked up on the first call made with
-// the device current).
-static int scratch_for_current_device(float **out) {
+// the device current).  The kernels run on the stream's device, so a stream
+// of another device than the current one is refused: its kernels would be
+// handed the current device's address.
+static int scratch_for_current_device(hipStream_t stream, float **out) {
   int dev = -1;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess)
     return fail(EVO2_ERR_DEVICE, "hyena_hcl_prefill_noalloc: hipGetDevice failed: %s",
                 hipGetErrorString(e));
+  if (stream) {  // the null stream belongs to the current device
+    hipDevice_t sdev = -1;
+    e = hipStreamGetDevice(stream, &sdev);
+    if (e != hipSuccess)
+      return fail(EVO2_ERR_DEVICE, "hyena_hcl_prefill_noalloc: hipStreamGetDevice failed: %s",
+                  hipGetErrorString(e));
+    if (sdev != dev)
+      return fail(EVO2_ERR_INVALID,
+                  "hyena_hcl_prefill_noalloc: the stream is on device %d but device %d is "
+                  "current; make the stream's device current first",
+                  static_cast<int>(sdev), dev);
+  }
   if (dev < 0 || dev >= HCL_MAX_DEVICES)
     return fail(EVO2_ERR_UNSUPPORTED, "hyena_hcl_prefill_noalloc: device %d beyond %d", dev,
                 HCL_MAX_DEVICES);
@@ -520,7 +534,7 @@ extern "C" int evo2_hyena_hcl_prefill_noalloc(
                 "tiles)", (long long)ntiles, (long long)H, (long long)need,
                 (long long)HCL_SCRATCH_BYTES);
   float *work = nullptr;
-  int rc = scratch_for_current_device(&work);
+  int rc = scratch_for_current_device(static_cast<hipStream_t>(stream), &work);
   if (rc) return rc;
   return hcl_prefill(z, sz, short_w, conv_state, cs0, cs1, cs2, residues, r0, r1, log_poles,
                      l0, l1, ssm, m0, m1, m2, D, seq_table, nseq, blocks, sblk, tile_table,

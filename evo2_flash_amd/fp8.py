@@ -169,6 +169,16 @@ class Fp8StaticLinear(nn.Module):
         # the decode copy below).
         self.weight.weight_loader = self._load_weight
 
+    # The decode-layout copy costs N*K bytes per projection.  False keeps
+    # every call on the row-major weight (the same result bits) and makes no
+    # copy, for deployments that cannot spare the memory.
+    decode_copies = True
+
+    def process_weights_after_loading(self):
+        """Make the decode copy now (or rewrite it in place), so that it exists
+        before an engine measures free memory to size its pools."""
+        self.decode_weight()
+
     def _load_weight(self, param, loaded):
         """Copy a checkpoint tensor into the weight and rewrite the decode copy
         in place (a HIP graph captured before the reload reads the new
@@ -194,12 +204,15 @@ class Fp8StaticLinear(nn.Module):
         self._decode_w = ((self.weight.data_ptr(), self.weight._version), wp)
 
     def decode_weight(self):
-        """The weight in the decode layout, made on first use and again after
-        the weight changes (kept beside the checkpoint copy; not state).  None
-        while a HIP graph is being captured and no copy exists yet, and for
-        shapes without a decode layout."""
+        """The weight in the decode layout (kept beside the checkpoint copy;
+        not state).  Made once; after the weight changes in place it is
+        rewritten into the same buffer, so a HIP graph captured on it reads
+        the new weight once one eager call (or refresh_decode_weight()) has
+        run.  None while a HIP graph is being captured and the copy is
+        missing or stale, for shapes without a decode layout, and when
+        decode_copies is off."""
         w = self.weight
-        if not packable(*w.shape) or not w.is_cuda:
+        if not self.decode_copies or not packable(*w.shape) or not w.is_cuda:
             return None
         key = (w.data_ptr(), w._version)
         cached = getattr(self, "_decode_w", None)
@@ -207,6 +220,10 @@ class Fp8StaticLinear(nn.Module):
             return cached[1]
         if torch.cuda.is_current_stream_capturing():
             return None
+        if cached is not None:
+            self.refresh_decode_weight()  # in place when shape and device match
+            if self._decode_w is not None:
+                return self._decode_w[1]
         wp = fp8_pack_weight(w.detach())
         self._decode_w = (key, wp)
         return wp

@@ -174,6 +174,13 @@ class HyenaMixerBase(nn.Module):
                                         engine.layer_name(self.prefix))
         return output
 
+    def process_weights_after_loading(self):
+        """Make the decode copies of the fp8 projections after loading, before
+        an engine sizes its memory pools from what is free."""
+        for proj in (self.in_proj, self.out_proj):
+            if isinstance(proj, Fp8StaticLinear):
+                proj.process_weights_after_loading()
+
     def _meta(self):
         """This layer's metadata from the forward context (mixers.py:852-856)."""
         return engine.step_metadata(self.prefix)
@@ -420,6 +427,7 @@ class HyenaFIRMixer(HyenaMixerBase):
         rewritten in place on a reload, so a HIP graph captured before it
         still reads the current taps.  `conv`'s weight_loader calls this on
         every load; code that writes `conv` by other means calls it after."""
+        super().process_weights_after_loading()
         taps = channel_major_taps(self.conv.detach().view(self.hidden, self.k_inner))
         old = self._decode_taps
         if (old is not None and old.shape == taps.shape and old.stride() == taps.stride()
@@ -487,9 +495,6 @@ class HyenaIIRMixer(HyenaMixerBase):
                                      requires_grad=False)
         self.D = nn.Parameter(torch.empty(h, device=device, dtype=torch.bfloat16),
                               requires_grad=False)
-
-    def process_weights_after_loading(self):
-        pass
 
     def _ssm_state(self):
         """Slice 2 without the speculative stamp column: (blocks, H, S) fp32,

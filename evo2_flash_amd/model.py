@@ -28,8 +28,8 @@ Weights are random, seeded, in the benchmark's distributions.
 import torch
 from torch import nn
 
-from .attention import (PAGE, PagedKVCache, causal_prefill_attention, paged_decode_attention,
-                        workspace as attention_workspace)
+from .attention import (PAGE, PagedKVCache, causal_prefill_attention, check_block_table,
+                        paged_decode_attention, workspace as attention_workspace)
 from .metadata import build_metadata
 from .mixers import Linear, load_mixer_params, make_mixer, set_forward_context
 from .norm import Evo2RMSNorm
@@ -181,6 +181,7 @@ class Evo2DecodeModel(nn.Module):
         table = torch.empty(max_batch, self.max_pages, dtype=torch.int32)
         table[:, :sp] = perm[:sp].to(torch.int32)
         table[:, sp:] = perm[sp:].to(torch.int32).view(max_batch, own)
+        check_block_table(table, [self.max_pages * PAGE] * max_batch, num_pages)
         self.block_table = table.to(device)
         self.shared_prefix = shared_prefix
         layers, self.pools = [], {}

@@ -330,7 +330,9 @@ int evo2_decode_attention(const void *q, int64_t qb, int64_t qh,
  *   value pages (pages, heads, 16, head_dim): strides vp, vh, vl; dim stride 1
  * Sequence b attends to positions 0..positions[b] (< max_pages * 16); the
  * workspace is evo2_decode_attention_workspace_bytes(B, heads, head_dim,
- * max_pages * 16) bytes.
+ * max_pages * 16) bytes.  num_pages is the number of pages the cache holds:
+ * a table entry outside [0, num_pages) is never read through; the positions
+ * it names are left out of the softmax (zeros for a sequence left with none).
  *
  * Serves the attention layers of Evo2Attention at decode
  * (evo2_flash/model.py:104-153) over the paged cache layout the serving
@@ -339,7 +341,7 @@ int evo2_decode_attention(const void *q, int64_t qb, int64_t qh,
 int evo2_paged_decode_attention(const void *q, int64_t qb, int64_t qh,
                                 const void *k_pages, int64_t kp, int64_t kh, int64_t kd,
                                 const void *v_pages, int64_t vp, int64_t vh, int64_t vl,
-                                const int32_t *block_table, int64_t tbs,
+                                int64_t num_pages, const int32_t *block_table, int64_t tbs,
                                 const int64_t *positions, float *workspace,
                                 int64_t workspace_bytes, void *out, int64_t ob, int64_t oh,
                                 int64_t B, int64_t heads, int64_t head_dim, int64_t max_pages,

@@ -88,3 +88,43 @@ def test_paged_decode_attention_vs_fp32(hd, max_pages, pos):
                                  positions.to(DEV), hd ** -0.5)
     assert out.shape == (B, nh, hd)
     assert max_rel_err(out.cpu(), ref) <= 1e-2
+
+
+def test_paged_decode_attention_masks_entries_outside_the_cache():
+    """Table entries outside [0, pages) (-1, pages, a large id) are never read
+    through: their positions drop out of the softmax, and a sequence with no
+    position left gets zeros."""
+    g = torch.Generator().manual_seed(3)
+    hd, nh, max_pages = 64, 4, 140
+    pos = [2239, 2239, 300, 40]
+    B = len(pos)
+    num_pages = B * max_pages + 1
+    table = (torch.randperm(num_pages - 1, generator=g)[:B * max_pages] + 1).to(torch.int32)
+    table = table.view(B, max_pages).clone()
+    table[0, 5] = -1
+    table[0, 130] = num_pages            # in the second 2048-position chunk
+    table[1, :128] = 1 << 30             # the whole first chunk of sequence 1
+    table[2, 3] = -7
+    table[3, :3] = -1                    # every page sequence 3 uses
+    cache = PagedKVCache(num_pages, nh, hd, "cpu")
+    cache.k.copy_((torch.randn(cache.k.shape, generator=g) * 0.5).to(bf))
+    cache.v.copy_((torch.randn(cache.v.shape, generator=g) * 0.5).to(bf))
+    q = torch.randn(B, nh, hd, generator=g).to(bf)
+    positions = torch.tensor(pos, dtype=torch.int64)
+    ref = torch.zeros(B, nh, hd)
+    for b in range(B):
+        keep = [l for l in range(pos[b] + 1) if 0 <= int(table[b, l // PAGE]) < num_pages]
+        if not keep:
+            continue
+        pg = table[b, [l // PAGE for l in keep]].long()
+        off = torch.tensor([l % PAGE for l in keep])
+        k = cache.k[pg, :, :, off].float()          # (n, heads, hd)
+        v = cache.v[pg, :, off, :].float()          # (n, heads, hd)
+        s = torch.einsum("hd,nhd->hn", q[b].float(), k) * hd ** -0.5
+        ref[b] = torch.einsum("hn,nhd->hd", torch.softmax(s, dim=-1), v)
+    print("paged decode_attention masked table entries", flush=True)
+    out = paged_decode_attention(q.to(DEV), cache.k.to(DEV), cache.v.to(DEV), table.to(DEV),
+                                 positions.to(DEV), hd ** -0.5).cpu()
+    assert torch.isfinite(out.float()).all()
+    assert torch.equal(out[3], torch.zeros(nh, hd, dtype=bf))
+    assert max_rel_err(out[:3], ref[:3]) <= 1e-2

@@ -183,7 +183,7 @@ def test_linear_module_decode_copy():
     y, _ = lin(x)
     ref = static_fp8_linear(x, lin.weight, lin.input_scale, lin.weight_scale, lin.bias)
     assert torch.equal(y.view(torch.int16), ref.view(torch.int16))
-    assert lin.decode_weight() is not first
+    assert lin.decode_weight() is first  # rewritten into the same buffer
     # the engine's loader path and a write through .data (which leaves the
     # version counter alone) followed by refresh_decode_weight()
     kept = lin.decode_weight()
@@ -224,11 +224,46 @@ def test_linear_decode_copy_in_graph():
         with torch.cuda.graph(graph, stream=s):
             lin(x, out=out)
     torch.cuda.current_stream().wait_stream(s)
-    for w in (w8, quantize_weight_e4m3(torch.randn(N, K, generator=gen, device=DEV) * 0.02)[0]):
-        lin.weight.weight_loader(lin.weight, w)
+    eager = torch.empty_like(out)
+    for how in ("loader", "loader", "copy_"):
+        w = quantize_weight_e4m3(torch.randn(N, K, generator=gen, device=DEV) * 0.02)[0]
+        if how == "loader":
+            lin.weight.weight_loader(lin.weight, w)
+        else:
+            # a plain in-place write: the next eager call rewrites the copy in
+            # the buffer the graph holds
+            with torch.no_grad():
+                lin.weight.copy_(w)
+            lin(x, out=eager)
         for _ in range(3):
             out.zero_()
             graph.replay()
             torch.cuda.synchronize()
             ref = static_fp8_linear(x, lin.weight, lin.input_scale, lin.weight_scale)
-            assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+            assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), how
+
+
+def test_linear_decode_copy_after_loading():
+    """process_weights_after_loading makes the decode copy before any decode
+    call (an engine sizes its pools after loading); with decode_copies off
+    none is made and the row-major GEMM gives the same bits."""
+    from evo2_flash_amd.fp8 import Fp8StaticLinear
+    N, K = 1024, 512
+    gen = torch.Generator(device=DEV).manual_seed(13)
+    w8, ws = quantize_weight_e4m3(torch.randn(N, K, generator=gen, device=DEV) * 0.02)
+    x = torch.randn(4, K, generator=gen, device=DEV).to(torch.bfloat16)
+    outs = []
+    for copies in (True, False):
+        lin = Fp8StaticLinear(K, N, bias=False, device=DEV)
+        lin.decode_copies = copies
+        lin.weight.weight_loader(lin.weight, w8)
+        with torch.no_grad():
+            lin.weight_scale.copy_(ws)
+            lin.input_scale.fill_(6.0 / 448)
+        lin.process_weights_after_loading()
+        made = getattr(lin, "_decode_w", None)
+        assert (made is not None) == copies
+        if copies:
+            assert made[1].shape == (N, K) and lin.decode_weight() is made[1]
+        outs.append(lin(x)[0])
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))

@@ -229,3 +229,23 @@ def test_packed_weight_rules():
     assert not streams_weight(8192, 12288)
     assert packable(12288, 4096) and packable(16, 128)
     assert not packable(12280, 4096) and not packable(4096, 4000)
+
+
+def test_check_block_table():
+    """The host check of a paged-attention block table: every page a
+    sequence's positions use lies in [1, num_pages); pages past a sequence's
+    length are not looked at."""
+    from evo2_flash_amd.attention import check_block_table
+    table = torch.tensor([[3, 1, 2, 0], [4, 5, 9, -1]], dtype=torch.int32)
+    check_block_table(table, [48, 32], 6)          # 3 pages and 2 pages
+    check_block_table(table, torch.tensor([1, 0]), 6)
+    with pytest.raises(ValueError, match=r"block_table\[1, 2\] = 9 is outside \[1, 6\)"):
+        check_block_table(table, [48, 48], 6)
+    with pytest.raises(ValueError, match=r"block_table\[0, 3\] = 0"):
+        check_block_table(table, [64, 16], 6)
+    with pytest.raises(ValueError, match=r"block_table\[1, 3\] = -1"):
+        check_block_table(table, [16, 64], 10)
+    with pytest.raises(ValueError, match="need 5 pages"):
+        check_block_table(table, [65, 16], 10)
+    with pytest.raises(ValueError, match="cannot serve 3"):
+        check_block_table(table, [16, 16, 16], 10)
