@@ -225,19 +225,40 @@ __global__ __launch_bounds__(256) void fp8_gemm_kernel(GemmArgs p) {
 // ---------------------------------------------------------------------------
 // Persistent form of the same tile.  One workgroup per CU walks the output
 // tiles t = blockIdx.x, blockIdx.x + gridDim.x, ..., and its global -> LDS
-// ring runs straight across tile boundaries: the slices of the next tile are
-// already loading while the current one finishes its last steps and writes
-// its epilogue, so a tile's start-up latency is paid once per workgroup
-// rather than once per tile.  Four ring stages (32 KB of W and 32 KB of X
-// each), refilled three K steps ahead; the unrolled step pattern (stage,
-// fragment buffer) repeats every four steps, which divides the K steps of a
-// tile (K a multiple of 256).  Tile order: workgroup b runs on XCD b mod 8,
-// so with a grid of 256 the 32 tiles an XCD runs at once are made one block
-// of 4 W tiles x 8 X tiles, whose operands that XCD's L2 then serves 8 and 4
-// times over.  A round of 256 tiles covers 8 such blocks; when the block
-// count is not a multiple of 8, the blocks left after the last whole round
-// are handed out tile by tile in block order.
-constexpr int P_STAGES = 4;
+// pipeline runs straight across tile boundaries: the first slice of the next
+// tile is already loading while the current one finishes and writes its
+// epilogue, so a tile's start-up latency is paid once per workgroup rather
+// than once per tile.
+//
+// K moves in slices of 128 bytes: each row's slice is one whole 128-byte
+// line, so a direct-to-LDS instruction (64 lanes x 16 bytes = 8 rows) asks
+// for 8 full lines.  Two stages of 32 KB of W and 32 KB of X; slice k + 2 is
+// loaded into the stage of slice k as soon as every wave has read slice k,
+// and a slice takes two v_mfma_f32_32x32x64_f8f6f4 sub-steps (64 bytes of K
+// each), so a load has a whole slice of matrix work (~1.1 us) to land and
+// the workgroup meets at one barrier per slice.  LDS rows are 128 bytes;
+// 16-byte chunk c of row r sits at c ^ ((r >> 1) & 7), which spreads the 16
+// rows a b128 read serves per cycle over all 64 banks.
+//
+// Tile order: workgroup b runs on XCD b mod 8, so with a grid of 256 the 32
+// tiles an XCD runs at once are made one block of 4 W tiles x 8 X tiles,
+// whose operands that XCD's L2 then serves 8 and 4 times over.  A round of
+// 256 tiles covers 8 such blocks; when the block count is not a multiple of
+// 8, the blocks left after the last whole round are handed out tile by tile
+// in block order.
+// The lane's index in its wave, computed afresh (two VALU instructions) where
+// code off the hot loop needs it, rather than kept live across the loop in
+// a VGPR the compiler would spill: a spill reload waits for every operand
+// load in flight.  In an asm statement, so it is not hoisted and shared.
+__device__ __forceinline__ int lane_now() {
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
+}
+
+constexpr int Q_BK = 128;               // bytes of K per slice
+constexpr int Q_STAGE = G_BN * Q_BK;    // bytes per operand per stage
+constexpr int Q_KALIGN = 2 * Q_BK;      // K granularity: whole slice pairs per tile
 
 // The grouped order needs a grid of 256 and whole 4 x 8 blocks.
 __host__ __device__ inline bool persist_grouped(int ncu, int tiles_n, int tiles_m) {
@@ -269,10 +290,15 @@ __host__ __device__ inline void persist_tile(int t, int tiles_n, int tiles_m, bo
 
 __global__ __launch_bounds__(256) void fp8_gemm_persist_kernel(GemmArgs p, int tiles_n, int tiles_m,
                                                                int grouped) {
-  __shared__ __align__(16) uint8_t w0[G_STAGE], w1[G_STAGE], w2[G_STAGE], w3[G_STAGE];
-  __shared__ __align__(16) uint8_t x0[G_STAGE], x1[G_STAGE], x2[G_STAGE], x3[G_STAGE];
-  constexpr int DB = 4;       // 1 KB DMA blocks per operand, wave and stage
-  constexpr int DMA = 2 * DB; // refill loads per wave and step
+  __shared__ __align__(16) uint8_t w0[Q_STAGE], w1[Q_STAGE];
+  __shared__ __align__(16) uint8_t x0[Q_STAGE], x1[Q_STAGE];
+  // The bias of even and odd tiles, loaded direct-to-LDS a whole tile ahead
+  // of the epilogue that adds it (64 lanes x 16 bytes: the tile's 256
+  // columns and the next 256, unused).  Reading it then never waits on the
+  // memory pipe, where a load would also wait for the next tile's operand
+  // loads and the stores before it.
+  __shared__ __align__(16) bf16_t bias0[512], bias1[512];
+  constexpr int DB = Q_STAGE / 4 / 1024;  // 1 KB DMA blocks per operand, wave and slice (8)
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -280,45 +306,55 @@ __global__ __launch_bounds__(256) void fp8_gemm_persist_kernel(GemmArgs p, int t
   const int wn = (wave & 1) * 128;   // wave's W rows
   const int wm = (wave >> 1) * 128;  // wave's X rows
   const int total = tiles_n * tiles_m;
-  const int KT = p.K / G_BK;
-  const int ntile = (total - static_cast<int>(blockIdx.x) + static_cast<int>(gridDim.x) - 1) /
-                    static_cast<int>(gridDim.x);
+  const int KT = p.K / Q_BK;  // slices per tile, even
+  int grid = static_cast<int>(gridDim.x);
+  asm volatile("" : "+s"(grid));  // kept in an SGPR, not reloaded from the dispatch packet
+  const int ntile = (total - static_cast<int>(blockIdx.x) + grid - 1) / grid;
   const int nsteps = ntile * KT;
 
   // Operands through buffer descriptors over the whole matrices (their byte
-  // extents fit 32 bits, checked on the host): a 32-bit lane offset for the
-  // lane's row and chunk within the DMA tile, the K offset in an SGPR.
+  // extents fit 32 bits, checked on the host).
   const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint8_t *>(p.w), 0, static_cast<int>((int64_t)(p.N - 1) * p.sw + p.K), 0x00020000);
   const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint8_t *>(p.x), 0, static_cast<int>((int64_t)(p.M - 1) * p.sx + p.K), 0x00020000);
-  // DMA: one wave instruction fills 1 KB = 16 rows of 64 bytes; lane i writes
-  // row i/4, physical chunk i%4, which holds logical chunk (i%4) ^ ((row >> 2) & 3).
-  int vw[DB], vx[DB];  // lane offsets of the tile the refills are loading
+  // bias reads past column N return zero
+  const __amdgpu_buffer_rsrc_t brs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<bf16_t *>(p.bias), 0, 2 * p.N, 0x00020000);
+
+  // DMA: one wave instruction fills 1 KB = 8 rows of 128 bytes; lane i writes
+  // row i / 8, physical chunk i % 8, which holds logical chunk
+  // (i % 8) ^ ((row >> 1) & 7).  Block j of a wave covers rows
+  // 8 (DB wave + j) + i / 8, whose swizzle is ((i / 16) + 4 (j & 1)) & 7: two
+  // lane offsets per operand (even and odd blocks, row within the block and
+  // chunk), the block's row offset and the K offset in SGPRs.
+  int lw[2], lx[2];
+  {
+    const int r = lane >> 3;
+#pragma unroll
+    for (int par = 0; par < 2; ++par) {
+      const int chunk = ((lane & 7) ^ (((lane >> 4) + 4 * par) & 7)) << 4;
+      lw[par] = r * static_cast<int>(p.sw) + chunk;
+      lx[par] = r * static_cast<int>(p.sx) + chunk;
+    }
+  }
+  int tw = 0, tx = 0;  // byte offsets of the wave's first DMA row in the tile being loaded
   auto dma_tile = [&](int j) __attribute__((always_inline)) {
     int bn, bm;
-    persist_tile(static_cast<int>(blockIdx.x) + j * static_cast<int>(gridDim.x), tiles_n, tiles_m,
-                 grouped != 0, bn, bm);
-#pragma unroll
-    for (int i = 0; i < DB; ++i) {
-      const int row = (wave * DB + i) * 16 + lane / 4;
-      const int chunk = ((lane & 3) ^ ((row >> 2) & 3)) << 4;
-      vw[i] = (bn * G_BN + row) * static_cast<int>(p.sw) + chunk;
-      vx[i] = (bm * G_BM + row) * static_cast<int>(p.sx) + chunk;
-    }
+    persist_tile(static_cast<int>(blockIdx.x) + j * grid, tiles_n, tiles_m, grouped != 0, bn, bm);
+    tw = (bn * G_BN + DB * 8 * wave) * static_cast<int>(p.sw);
+    tx = (bm * G_BM + DB * 8 * wave) * static_cast<int>(p.sx);
   };
   auto stage_w = [&](auto stage) __attribute__((always_inline)) -> uint8_t * {
-    constexpr int S = decltype(stage)::value;
-    return S == 0 ? w0 : S == 1 ? w1 : S == 2 ? w2 : w3;
+    return decltype(stage)::value ? w1 : w0;
   };
   auto stage_x = [&](auto stage) __attribute__((always_inline)) -> uint8_t * {
-    constexpr int S = decltype(stage)::value;
-    return S == 0 ? x0 : S == 1 ? x1 : S == 2 ? x2 : x3;
+    return decltype(stage)::value ? x1 : x0;
   };
-  // Slice q of this workgroup's step sequence (tile q / KT, K step q % KT)
-  // into a stage; slices past the end re-read the last one, so every step
-  // issues the same loads and the wait counts stay exact.
-  int dma_t = 0;  // tile whose offsets vw / vx hold
+  // Slice q of this workgroup's sequence (tile q / KT, K slice q % KT) into
+  // a stage; slices past the end re-read the last one, so every step issues
+  // the same loads and the wait counts stay exact.
+  int dma_t = 0;  // tile whose offsets tw / tx hold
   auto issue = [&](auto stage, int q) __attribute__((always_inline)) {
     q = min(q, nsteps - 1);
     const int tq = q / KT;  // uniform
@@ -326,39 +362,43 @@ __global__ __launch_bounds__(256) void fp8_gemm_persist_kernel(GemmArgs p, int t
       dma_t = tq;
       dma_tile(tq);
     }
-    const int koff = (q - tq * KT) * G_BK;
-    uint8_t *lw = stage_w(stage);
-    uint8_t *lx = stage_x(stage);
+    const int koff = (q - tq * KT) * Q_BK;
+    uint8_t *lwp = stage_w(stage);
+    uint8_t *lxp = stage_x(stage);
 #pragma unroll
     for (int j = 0; j < DB; ++j) {
       const int blk = wave * DB + j;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(wrs, (lds_void *)(lw + blk * 1024), 16, vw[j], koff, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, (lds_void *)(lx + blk * 1024), 16, vx[j], koff, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(wrs, (lds_void *)(lwp + blk * 1024), 16, lw[j & 1],
+                                               tw + 8 * j * static_cast<int>(p.sw) + koff, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, (lds_void *)(lxp + blk * 1024), 16, lx[j & 1],
+                                               tx + 8 * j * static_cast<int>(p.sx) + koff, 0, 0);
     }
   };
 
-  const int g = lane >> 5;   // lane group: k bytes [32g, 32g + 32) of the step
+  const int g = lane >> 5;   // lane group: k bytes [32g, 32g + 32) of a sub-step
   const int lr = lane & 31;  // row within a 32-row MFMA tile
-  auto frag_off = [&](int r, int half) __attribute__((always_inline)) {
-    return r * G_BK + (((2 * g + half) ^ ((r >> 2) & 3)) << 4);
-  };
-  auto read_frags = [&](auto stage, i32x8 fa[4], i32x8 fb[4]) __attribute__((always_inline)) {
-    const uint8_t *lw = stage_w(stage);
-    const uint8_t *lx = stage_x(stage);
-    // in the order the next step consumes them (tn-major MFMAs: every X
-    // fragment and W fragment 0 first)
+  const int sw = (lr >> 1) & 7;  // swizzle of every row this lane reads
+  // Fragments of sub-step h of a stage: row r = base + 32 t + lr, logical
+  // chunks 4h + 2g and 4h + 2g + 1.
+  auto read_frags = [&](auto stage, auto sub, i32x8 fa[4], i32x8 fb[4]) __attribute__((always_inline)) {
+    constexpr int H = decltype(sub)::value;
+    const uint8_t *lwp = stage_w(stage);
+    const uint8_t *lxp = stage_x(stage);
+    const int c0 = ((4 * H + 2 * g) ^ sw) << 4, c1 = ((4 * H + 2 * g + 1) ^ sw) << 4;
+    // in the order the MFMAs consume them (tn-major: every X fragment and W
+    // fragment 0 first)
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      const int rx = wm + 32 * t + lr;
-      const uint4 b0 = *reinterpret_cast<const uint4 *>(lx + frag_off(rx, 0));
-      const uint4 b1 = *reinterpret_cast<const uint4 *>(lx + frag_off(rx, 1));
+      const uint8_t *row = lxp + (wm + 32 * t + lr) * Q_BK;
+      const uint4 b0 = *reinterpret_cast<const uint4 *>(row + c0);
+      const uint4 b1 = *reinterpret_cast<const uint4 *>(row + c1);
       fb[t] = i32x8{(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w, (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
     }
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      const int rw = wn + 32 * t + lr;
-      const uint4 a0 = *reinterpret_cast<const uint4 *>(lw + frag_off(rw, 0));
-      const uint4 a1 = *reinterpret_cast<const uint4 *>(lw + frag_off(rw, 1));
+      const uint8_t *row = lwp + (wn + 32 * t + lr) * Q_BK;
+      const uint4 a0 = *reinterpret_cast<const uint4 *>(row + c0);
+      const uint4 a1 = *reinterpret_cast<const uint4 *>(row + c1);
       fa[t] = i32x8{(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w, (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
     }
   };
@@ -381,89 +421,121 @@ __global__ __launch_bounds__(256) void fp8_gemm_persist_kernel(GemmArgs p, int t
                                                                        0, 0, 0, 0, 0, 0);
   };
   const float scale = p.sx_scale[0] * p.sw_scale[0];
+  // Wave 0 loads the bias of tile j into the buffer of its parity.
+  auto load_bias = [&](auto par, int j) __attribute__((always_inline)) {
+    if (!p.bias || wave != 0) return;  // uniform
+    int bn, bm;
+    persist_tile(static_cast<int>(blockIdx.x) + j * grid, tiles_n, tiles_m, grouped != 0, bn, bm);
+    bf16_t *lb = decltype(par)::value ? bias1 : bias0;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(brs, (lds_void *)lb, 16, 16 * lane_now(), 2 * bn * G_BN,
+                                             0, 0);
+  };
   // Epilogue of tile j: lane holds, for X row m = m0 + wm + 32 tm + lr, the
   // W rows n = n0 + wn + 32 tn + 8 q + 4 g + i (i < 4) in acc[tn][tm][4 q + i].
-  auto epilogue = [&](int j) __attribute__((always_inline)) {
+  // Every store address is one of four row pointers plus a constant.
+  auto epilogue = [&](auto par, int j) __attribute__((always_inline)) {
     int bn, bm;
-    persist_tile(static_cast<int>(blockIdx.x) + j * static_cast<int>(gridDim.x), tiles_n, tiles_m,
-                 grouped != 0, bn, bm);
+    persist_tile(static_cast<int>(blockIdx.x) + j * grid, tiles_n, tiles_m, grouped != 0, bn, bm);
     // The order is a bijection onto the grid (checked on the host for every
     // grid up to 64 x 40 tiles); a tile outside it stores nothing rather than
     // past the output (the operand loads are bounded by their descriptors).
     if (bn < 0 || bn >= tiles_n || bm < 0 || bm >= tiles_m) return;  // wave-uniform
     // whole tiles only (the host checks M and N are multiples of 256 and the
     // output rows 8-byte aligned)
-    const int n0 = bn * G_BN, m0 = bm * G_BM;
+    const int ln = lane_now();
+    const int elr = ln & 31, eg = ln >> 5;
+    bf16_t *obase = p.out + (int64_t)(bm * G_BM + wm + elr) * p.so + bn * G_BN + wn + 4 * eg;
+    const bf16_t *lb = (decltype(par)::value ? bias1 : bias0) + wn + 4 * eg;
+    const bool has_bias = p.bias != nullptr;
 #pragma unroll
     for (int tm = 0; tm < 4; ++tm) {
-      bf16_t *orow = p.out + (int64_t)(m0 + wm + 32 * tm + lr) * p.so;
+      bf16_t *orow = obase + (int64_t)(32 * tm) * p.so;
 #pragma unroll
       for (int tn = 0; tn < 4; ++tn) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          const int n = n0 + wn + 32 * tn + 8 * q + 4 * g;
           float v[4];
 #pragma unroll
           for (int i = 0; i < 4; ++i) v[i] = acc[tn][tm][4 * q + i] * scale;
-          if (p.bias) {
-            const uint2 bb = *reinterpret_cast<const uint2 *>(p.bias + n);
+          if (has_bias) {
+            const uint2 bb = *reinterpret_cast<const uint2 *>(lb + 32 * tn + 8 * q);
             v[0] += lo_bf(bb.x);
             v[1] += hi_bf(bb.x);
             v[2] += lo_bf(bb.y);
             v[3] += hi_bf(bb.y);
           }
-          *reinterpret_cast<uint2 *>(orow + n) = make_uint2(pack_bf(v[0], v[1]), pack_bf(v[2], v[3]));
+          *reinterpret_cast<uint2 *>(orow + 32 * tn + 8 * q) =
+              make_uint2(pack_bf(v[0], v[1]), pack_bf(v[2], v[3]));
         }
       }
     }
   };
 
-  // Step s: MFMAs of slice s (stage s % 4, fragments read during step s - 1)
-  // while reading slice s + 1's fragments; first wait for slice s + 1's loads
-  // (slice s + 2 stays in flight) and a barrier (every wave's loads for s + 1
-  // have landed; every wave has read slice s - 1, whose stage is refilled
-  // with slice s + 3 right after).  The first step after an epilogue also has
-  // its stores outstanding, and loads and stores retire in order: waiting for
-  // at most 63 then covers slices s + 1 and s + 2 and one store.
+  // Step k (slice k in stage S = k % 2):
+  //   sub-step 0: MFMAs of (k, 0) from fragments read during step k - 1,
+  //     while reading (k, 1);
+  //   then every wave waits for its loads of slice k + 1 and its reads of
+  //     slice k, and meets the others at the barrier: slice k + 1 is in LDS
+  //     and nobody reads stage S again, which is refilled with slice k + 2;
+  //   sub-step 1: MFMAs of (k, 1) while reading (k + 1, 0) from the other
+  //     stage.
+  // The first step after an epilogue also has its 64 stores outstanding,
+  // issued after the loads of slice k + 1: loads and stores retire in order,
+  // so waiting for at most 63 covers the loads.
   i32x8 fa[2][4], fb[2][4];
-  auto step = [&](auto stage, auto fbuf, int s, bool after_epilogue) __attribute__((always_inline)) {
-    constexpr int S = decltype(stage)::value;
-    constexpr int B = decltype(fbuf)::value;
-    if (after_epilogue) vmcnt_wait<63>();
-    else vmcnt_wait<DMA>();
-    __builtin_amdgcn_s_barrier();
-    issue(std::integral_constant<int, (S + 3) % P_STAGES>{}, s + 3);
-    read_frags(std::integral_constant<int, (S + 1) % P_STAGES>{}, fa[B ^ 1], fb[B ^ 1]);
-    mma(fa[B], fb[B]);
+  auto interleave = [&](bool dma) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      if (i < DMA) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+      if (dma) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
     }
   };
-
-  dma_tile(0);
   using std::integral_constant;
-  issue(integral_constant<int, 0>{}, 0);
-  issue(integral_constant<int, 1>{}, 1);
-  issue(integral_constant<int, 2>{}, 2);
-  vmcnt_wait<2 * DMA>();  // slice 0 (slices 1 and 2 in flight)
+  using I0 = integral_constant<int, 0>;
+  using I1 = integral_constant<int, 1>;
+  auto step = [&](auto stage, int k, bool after_epilogue) __attribute__((always_inline)) {
+    constexpr int S = decltype(stage)::value;
+    read_frags(stage, I1{}, fa[1], fb[1]);
+    mma(fa[0], fb[0]);
+    interleave(false);
+    if (after_epilogue) vmcnt_wait<63>();
+    else vmcnt_wait<0>();
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    issue(stage, k + 2);
+    read_frags(integral_constant<int, S ^ 1>{}, I0{}, fa[0], fb[0]);
+    mma(fa[1], fb[1]);
+    interleave(true);
+  };
+
+  using P0 = integral_constant<int, 0>;
+  using P1 = integral_constant<int, 1>;
+  load_bias(P0{}, 0);
+  dma_tile(0);
+  issue(I0{}, 0);
+  issue(I1{}, 1);
+  vmcnt_wait<2 * DB>();  // slice 0 (slice 1 in flight; the bias before them)
   __builtin_amdgcn_s_barrier();
-  read_frags(integral_constant<int, 0>{}, fa[0], fb[0]);
+  read_frags(I0{}, I0{}, fa[0], fb[0]);
   zero_acc();
   int s = 0;
-  for (int j = 0; j < ntile; ++j) {
-    // K steps of tile j in fours (KT is a multiple of 4): the stage and
-    // fragment buffer of a step are fixed by its position in the four
-    for (int k = 0; k < KT; k += 4, s += 4) {
-      step(integral_constant<int, 0>{}, integral_constant<int, 0>{}, s, k == 0 && j > 0);
-      step(integral_constant<int, 1>{}, integral_constant<int, 1>{}, s + 1, false);
-      step(integral_constant<int, 2>{}, integral_constant<int, 0>{}, s + 2, false);
-      step(integral_constant<int, 3>{}, integral_constant<int, 1>{}, s + 3, false);
+  // Tile j of parity P: first the bias of tile j + 1 into the other buffer
+  // (its previous contents, tile j - 1's, were added before this tile
+  // began), then the slices in pairs (KT is even, so every tile starts in
+  // stage 0), then the epilogue with this buffer.
+  auto tile = [&](auto par, int j) __attribute__((always_inline)) {
+    constexpr int P = decltype(par)::value;
+    if (j + 1 < ntile) load_bias(integral_constant<int, P ^ 1>{}, j + 1);
+    for (int k = 0; k < KT; k += 2, s += 2) {
+      step(I0{}, s, k == 0 && j > 0);
+      step(I1{}, s + 1, false);
     }
-    epilogue(j);
+    epilogue(par, j);
     zero_acc();
+  };
+  for (int j = 0; j < ntile; j += 2) {
+    tile(P0{}, j);
+    if (j + 1 < ntile) tile(P1{}, j + 1);
   }
   // No direct-to-LDS write may still be landing when the workgroup's LDS is
   // handed to the next one.
@@ -834,7 +906,7 @@ extern "C" int evo2_fp8_gemm(const void *x8, int64_t sx, const void *w8, int64_t
   const int ncu = cu_count();
   // the persistent form once every CU has a tile; its ring needs K to be a
   // multiple of four K steps and the operands to fit 32-bit buffer offsets
-  if (ncu > 0 && tiles_n * tiles_m >= ncu && K % (P_STAGES * G_BK) == 0 &&
+  if (ncu > 0 && tiles_n * tiles_m >= ncu && K % Q_KALIGN == 0 &&
       M % G_BM == 0 && N % G_BN == 0 && so % 4 == 0 && reinterpret_cast<uintptr_t>(out) % 8 == 0 &&
       (!bias || reinterpret_cast<uintptr_t>(bias) % 8 == 0) &&
       (N - 1) * sw + K < (int64_t(1) << 31) && (M - 1) * sx + K < (int64_t(1) << 31)) {
