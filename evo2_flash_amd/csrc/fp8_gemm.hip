@@ -441,10 +441,14 @@ __global__ __launch_bounds__(256) void fp8_gemm_persist_kernel(GemmArgs p, int t
     // past the output (the operand loads are bounded by their descriptors).
     if (bn < 0 || bn >= tiles_n || bm < 0 || bm >= tiles_m) return;  // wave-uniform
     // whole tiles only (the host checks M and N are multiples of 256 and the
-    // output rows 8-byte aligned)
+    // output rows 16-byte aligned)
+    // Lanes l and l + 32 hold the same row: for each pair of column groups
+    // (q, q + 1) they swap halves (v_permlane32_swap) so that lane l ends up
+    // with columns 16 p .. 16 p + 7 and lane l + 32 with 16 p + 8 .. 16 p + 15,
+    // and each stores 16 contiguous bytes: half as many store requests.
     const int ln = lane_now();
     const int elr = ln & 31, eg = ln >> 5;
-    bf16_t *obase = p.out + (int64_t)(bm * G_BM + wm + elr) * p.so + bn * G_BN + wn + 4 * eg;
+    bf16_t *obase = p.out + (int64_t)(bm * G_BM + wm + elr) * p.so + bn * G_BN + wn + 8 * eg;
     const bf16_t *lb = (decltype(par)::value ? bias1 : bias0) + wn + 4 * eg;
     const bool has_bias = p.bias != nullptr;
 #pragma unroll
@@ -452,6 +456,7 @@ __global__ __launch_bounds__(256) void fp8_gemm_persist_kernel(GemmArgs p, int t
       bf16_t *orow = obase + (int64_t)(32 * tm) * p.so;
 #pragma unroll
       for (int tn = 0; tn < 4; ++tn) {
+        uint32_t pk[4][2];  // column group q, packed pairs
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           float v[4];
@@ -464,8 +469,16 @@ __global__ __launch_bounds__(256) void fp8_gemm_persist_kernel(GemmArgs p, int t
             v[2] += lo_bf(bb.y);
             v[3] += hi_bf(bb.y);
           }
-          *reinterpret_cast<uint2 *>(orow + 32 * tn + 8 * q) =
-              make_uint2(pack_bf(v[0], v[1]), pack_bf(v[2], v[3]));
+          pk[q][0] = pack_bf(v[0], v[1]);
+          pk[q][1] = pack_bf(v[2], v[3]);
+        }
+#pragma unroll
+        for (int pq = 0; pq < 2; ++pq) {
+          // swap(x, y): lanes < 32 keep x and get x of lane + 32; lanes >= 32
+          // get y of lane - 32 and keep y
+          const auto s0 = __builtin_amdgcn_permlane32_swap(pk[2 * pq][0], pk[2 * pq + 1][0], false, false);
+          const auto s1 = __builtin_amdgcn_permlane32_swap(pk[2 * pq][1], pk[2 * pq + 1][1], false, false);
+          *reinterpret_cast<uint4 *>(orow + 32 * tn + 16 * pq) = make_uint4(s0[0], s1[0], s0[1], s1[1]);
         }
       }
     }
@@ -907,7 +920,7 @@ extern "C" int evo2_fp8_gemm(const void *x8, int64_t sx, const void *w8, int64_t
   // the persistent form once every CU has a tile; its ring needs K to be a
   // multiple of four K steps and the operands to fit 32-bit buffer offsets
   if (ncu > 0 && tiles_n * tiles_m >= ncu && K % Q_KALIGN == 0 &&
-      M % G_BM == 0 && N % G_BN == 0 && so % 4 == 0 && reinterpret_cast<uintptr_t>(out) % 8 == 0 &&
+      M % G_BM == 0 && N % G_BN == 0 && so % 8 == 0 && reinterpret_cast<uintptr_t>(out) % 16 == 0 &&
       (!bias || reinterpret_cast<uintptr_t>(bias) % 8 == 0) &&
       (N - 1) * sw + K < (int64_t(1) << 31) && (M - 1) * sx + K < (int64_t(1) << 31)) {
     const int grouped = persist_grouped(ncu, static_cast<int>(tiles_n), static_cast<int>(tiles_m));
