@@ -25,7 +25,7 @@ Also measured in the same run and reported in the same JSON line:
     of the reference torch decode path timed on the host cores.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--no-prefill] [--no-gemm]
-                    [--no-verify] [--no-model] [--no-model40b]
+                    [--no-verify] [--no-model] [--no-model40b] [--model-steps N]
                     [--only decode|verify|prefill|gemm|copy|model|config0|model_prefill|model40b]
 """
 
@@ -230,6 +230,8 @@ def bench_decode(steps, warmup, dev, seed=1234):
 # ---------------------------------------------------------------- whole model
 CTX_7B = 8192 + 512   # prompt plus the decode steps of the 7B workload
 PROMPT_7B = 8192
+STEPS_7B = 512        # decode steps of the 7B workload
+STEPS_40B = 8         # timed decode steps of the 40B workload (of its 256)
 ACGT = (65, 67, 71, 84)
 
 
@@ -287,18 +289,23 @@ def bench_model(steps, dev, B=B_DECODE, seed=21):
     from evo2_flash_amd.model import Evo2DecodeModel, decode_flops_bytes
 
     cfg = evo2_7b()
-    model = Evo2DecodeModel(cfg, max_batch=B, max_ctx=CTX_7B, device=dev, rope_theta=10000.0,
-                            rope_factor=128.0, name=f"bench_model_b{B}", page_seed=seed)
+    # one page beyond the workload: _graph_decode runs two untimed steps first
+    model = Evo2DecodeModel(cfg, max_batch=B, max_ctx=CTX_7B + 16, device=dev,
+                            rope_theta=10000.0, rope_factor=128.0, name=f"bench_model_b{B}",
+                            page_seed=seed)
     model.init_random(seed, state_scale=0.0, kv_scale=0.0)
     prompts = _acgt((B, PROMPT_7B), dev, seed + 1)
     _, t_pre = _sync_time(lambda: model.prefill(prompts, chunk_seqs=8))
-    n = min(steps, 500)
+    n = steps
+    if PROMPT_7B + n + 2 > CTX_7B + 16:
+        raise ValueError(f"{n} decode steps run past the cache")
     ms = _graph_decode(model, B, PROMPT_7B, n, dev, seed + 2)
     wbytes, kvbytes = decode_flops_bytes(cfg, B, PROMPT_7B + n)
     del model
     torch.cuda.empty_cache()
     return {"tok_s": round(B / (ms * 1e-3), 1), "ms_per_step": round(ms, 3), "batch": B,
-            "context": f"{PROMPT_7B}..{PROMPT_7B + n}", "layers": 32,
+            "context": f"{PROMPT_7B}..{PROMPT_7B + n + 1} (timed: the last {n} steps)",
+            "steps": n, "layers": 32,
             "prefill": {"prompt_tokens": B * PROMPT_7B, "s": round(t_pre, 2),
                         "tok_s": round(B * PROMPT_7B / t_pre, 1)},
             "bytes_per_step": {"weights": wbytes, "kv_cache": kvbytes},
@@ -378,9 +385,15 @@ def bench_model40b(steps, dev, B=32, L=131072, seed=41):
     prompt = _acgt((L,), dev, seed + 1)
     logits, t_pre = _sync_time(lambda: model.prefill_shared(prompt))
     finite = bool(torch.isfinite(logits).all())
-    n = min(steps, 256)
+    n = steps
+    if n + 2 > 256:
+        raise ValueError(f"{n} decode steps run past the cache")
     ms = _graph_decode(model, B, L, n, dev, seed + 2)
     wbytes, kvbytes = decode_flops_bytes(cfg, B, L + n)
+    # the prompt's pages once, each sequence's own positions once: what the
+    # step reads from distinct HBM addresses (the logical figure counts the
+    # shared prompt once per sequence)
+    _, kv_unique = decode_flops_bytes(cfg, 1, L + B * n)
     fl = prefill_flops(cfg, L)
     del model
     torch.cuda.empty_cache()
@@ -388,8 +401,13 @@ def bench_model40b(steps, dev, B=32, L=131072, seed=41):
                         "TFLOPs": round(fl / t_pre / 1e12, 1), "logits_finite": finite},
             "decode": {"batch": B, "steps": n, "ms_per_step": round(ms, 3),
                        "tok_s": round(B / (ms * 1e-3), 1),
-                       "bytes_per_step": {"weights": wbytes, "kv_cache": kvbytes},
-                       "achieved_GBs": round((wbytes + kvbytes) / (ms * 1e-3) / 1e9, 1)},
+                       "bytes_per_step": {"weights": wbytes, "kv_cache_logical": kvbytes,
+                                          "kv_cache_unique": kv_unique},
+                       "logical_GBs": round((wbytes + kvbytes) / (ms * 1e-3) / 1e9, 1),
+                       "unique_GBs": round((wbytes + kv_unique) / (ms * 1e-3) / 1e9, 1),
+                       "steps_note": f"{n} of the workload's 256 steps: a step costs the same "
+                                     f"at every position of 131072..131328 (the KV grows by "
+                                     f"0.2%), and 256 steps would hold the GPU ~1 minute"},
             "kv": "one prompt's 16-position pages shared by all sequences through the block "
                   "table, then one page run per sequence",
             "residual_scale": 1e6}
@@ -891,6 +909,9 @@ def main(argv=None):
     ap.add_argument("--no-model40b", action="store_true",
                     help="skip the 40B-shaped whole model (131072-token prefill, then B=32 "
                          "decode; ~20 s, ~150 GB of HBM)")
+    ap.add_argument("--model-steps", type=int, default=STEPS_7B,
+                    help="decode steps of the 7B whole-model leg (the workload's 512 by default; "
+                         "fewer for profiling)")
     ap.add_argument("--only", choices=["decode", "verify", "prefill", "gemm", "copy", "model",
                                        "config0", "model_prefill", "model40b"],
                     default=None,
@@ -916,15 +937,15 @@ def main(argv=None):
     gem = bench_gemm(max(5, args.steps // 4), dev) if run("gemm", args.no_gemm) else None
     cf0 = (bench_config0(max(5, args.steps // 4), dev, cpu=not (args.no_cpu or args.only))
            if run("config0", False) else None)
-    mod = _guarded(bench_model, max(16, args.steps // 2), dev) if run("model", args.no_model) else None
+    mod = _guarded(bench_model, args.model_steps, dev) if run("model", args.no_model) else None
     mpre = _guarded(bench_model_prefill, dev) if run("model_prefill", args.no_model) else None
-    m40 = (_guarded(bench_model40b, 8, dev) if run("model40b", args.no_model or args.no_model40b)
+    m40 = (_guarded(bench_model40b, STEPS_40B, dev) if run("model40b", args.no_model or args.no_model40b)
            else None)
     if mod and "error" not in mod:
         # the reference's one published whole-step figure: a plain decode step
         # of the 7B model at batch 8 under full CUDA graphs, 7.85 ms on
         # H100/H200, context length not stated (api.py:384-385)
-        mod["batch8"] = _guarded(bench_model, max(16, args.steps // 2), dev, B=8)
+        mod["batch8"] = _guarded(bench_model, args.model_steps, dev, B=8)
         mod["batch8"]["reference"] = {"ms_per_step": 7.85, "hardware": "H100/H200",
                                       "source": "api.py:384-385",
                                       "note": "plain decode, whole 7B model, batch 8; "
