@@ -33,7 +33,7 @@ from .attention import (PAGE, PagedKVCache, causal_prefill_attention, check_bloc
 from .metadata import build_metadata
 from .mixers import Linear, load_mixer_params, make_mixer, set_forward_context
 from .norm import Evo2RMSNorm
-from .state import HyenaStatePool
+from .state import HyenaStatePool, get_mamba_state_copy_func
 from .synthetic import mixer_params
 
 
@@ -158,6 +158,11 @@ class Evo2DecodeModel(nn.Module):
     every Hyena layer's pool (block 0 is the null block) and KV pages
     `block_table[b]` in every attention layer (a seeded random permutation
     of pages 1..; page 0 is never used)."""
+
+    @classmethod
+    def get_mamba_state_copy_func(cls):
+        """The state slices' prefix-caching copy rules (model.py:285-304)."""
+        return get_mamba_state_copy_func()
 
     def __init__(self, config, max_batch, max_ctx, device, rope_theta=10000.0, rope_factor=1.0,
                  name="evo2", page_seed=0, shared_prefix=0):

@@ -15,9 +15,56 @@ conv window widens to K_short-1+num_spec columns and the LI slice gains a
 tokens the block's snapshot represents (mixers.py:952-958).
 """
 
+from typing import NamedTuple
+
 import torch
 
 NULL_BLOCK = 0
+
+
+class MambaCopySpec(NamedTuple):
+    """A cached state to move between blocks: its first element's address
+    and its element count (the engine copies them to the start of the
+    destination block's state in the same slice)."""
+    start_addr: int
+    num_elements: int
+
+
+def _conv_source(state, block_ids, cur_block_idx, num_accepted_tokens):
+    # native (blocks, state_len, dim): after a verify step the block's window
+    # is [older inputs, d_1 .. d_q]; the K-1 inputs before the next token
+    # start num_accepted_tokens - 1 columns in
+    return state[block_ids[cur_block_idx], num_accepted_tokens - 1:]
+
+
+def _temporal_source(state, block_ids, cur_block_idx, num_accepted_tokens):
+    # one whole snapshot per verifier position, in consecutive blocks
+    return state[block_ids[cur_block_idx + num_accepted_tokens - 1]]
+
+
+def get_conv_copy_spec(state, block_ids, cur_block_idx, num_accepted_tokens):
+    """Copy rule of the sliding conv window (slice 0)."""
+    src = _conv_source(state, block_ids, cur_block_idx, num_accepted_tokens)
+    return MambaCopySpec(src.data_ptr(), src.numel())
+
+
+def get_temporal_copy_spec(state, block_ids, cur_block_idx, num_accepted_tokens):
+    """Copy rule of a temporal snapshot slice (slices 1 and 2)."""
+    src = _temporal_source(state, block_ids, cur_block_idx, num_accepted_tokens)
+    return MambaCopySpec(src.data_ptr(), src.numel())
+
+
+def get_mamba_state_copy_func():
+    """One copy rule per state slice (model.py:285-304): the sliding window
+    for the conv slice, a whole snapshot for the inner-FIR and LI slices.
+    vLLM's own rules when vLLM imports (its model runner consumes their spec
+    type), else this module's, which follow the same arguments and layout."""
+    try:
+        from vllm.model_executor.layers.mamba.mamba_utils import (get_conv_copy_spec as conv,
+                                                                  get_temporal_copy_spec as temp)
+    except ImportError:
+        conv, temp = get_conv_copy_spec, get_temporal_copy_spec
+    return (conv, temp, temp)
 
 
 def unified_state_shape(hidden, k_short=3, k_inner_max=128, state_size=16, num_spec=0):
@@ -102,6 +149,16 @@ class HyenaStatePool:
         if not self.num_spec:
             raise ValueError("position stamps exist only with speculative decoding (num_spec > 0)")
         return self.kv_cache[2][:, 0, -1]
+
+    def copy_cached_state(self, block_ids, cur_block_idx, num_accepted_tokens, dst_block):
+        """Apply the three copy rules to this pool, the way the engine does on
+        its prefix-caching path: each slice's source (get_mamba_state_copy_func)
+        goes to the start of `dst_block`'s state in that slice."""
+        for state, src_of in zip(self.kv_cache, (_conv_source, _temporal_source, _temporal_source)):
+            src = src_of(state, block_ids, cur_block_idx, num_accepted_tokens)
+            n = src.numel()
+            state[dst_block].reshape(-1)[:n].copy_(src.reshape(-1))
+        return self
 
     def zero_(self):
         self.raw.zero_()

@@ -369,3 +369,47 @@ def test_fully_accepted_step_equals_chained_decodes(kind, emulate):
                                                 prm.get("D"), lp)
             assert torch.equal(y.view(torch.int16), gs[r * Q + p:r * Q + p + 1].view(torch.int16)), (r, p)
         assert torch.equal(view(p2)[blk][:, :width], view(p1)[int(slots[r, Q - 1])][:, :width])
+
+
+@pytest.mark.parametrize("kind", ["hcs", "hcm", "hcl"])
+@pytest.mark.parametrize("accepted", [1, 2, 4])
+def test_state_copy_rules_resume_after_partial_acceptance(kind, accepted):
+    """The prefix-caching copy rules (model.py:285-304): after a verify step
+    of Q tokens over blocks b_0 .. b_{Q-1}, copying each slice by its rule
+    (sliding window from b_0 offset by accepted - 1, snapshot from
+    b_{accepted-1}) into a fresh block and decoding the next token there
+    gives, bit for bit, what decoding the accepted tokens and then that token
+    one at a time gives.  A wrong window offset or snapshot block fails it."""
+    from evo2_flash_amd.state import (MambaCopySpec, get_conv_copy_spec,
+                                      get_mamba_state_copy_func, get_temporal_copy_spec)
+    H, nb, nspec, Q = 64, 12, 3, 4
+    prm = mixer_params(kind, H, 7, in_proj_fp8=False)
+    sw = prm["short_filter"].view(3 * H, 3)
+    inner, lp, poles, view = _operator(kind, prm, H)
+    pool = _spec_pool(H, nb, nspec, 8)
+    g = torch.Generator().manual_seed(9)
+    blocks = [2, 3, 4, 5]
+    z = (torch.randn(Q + 1, 3 * H, generator=g) * 1.3).to(torch.bfloat16)
+    spec = _clone(pool, nspec)
+    oracle.mixer_decode_speculative(z[:Q], sw, spec.conv_view(), inner, view(spec),
+                                    prm.get("D"), torch.tensor([blocks]), [0, Q], [1], Q,
+                                    poles=poles, emulate_kernels=True)
+    rules = get_mamba_state_copy_func()
+    assert rules == (get_conv_copy_spec, get_temporal_copy_spec, get_temporal_copy_spec)
+    for state, rule in zip(spec.kv_cache, rules):
+        cs = rule(state, blocks, 0, accepted)
+        assert isinstance(cs, MambaCopySpec) and cs.num_elements > 0
+    dst = 10
+    spec.copy_cached_state(blocks, 0, accepted, dst)
+    y_spec = oracle.hyena_decode_emulated(z[Q:Q + 1], sw, spec.conv_view()[..., :2],
+                                          torch.tensor([dst]), inner, view(spec),
+                                          prm.get("D"), lp)
+    chain = _clone(pool, nspec)
+    for p in list(range(accepted)) + [Q]:
+        y = oracle.hyena_decode_emulated(z[p:p + 1], sw, chain.conv_view()[..., :2],
+                                         torch.tensor([blocks[0]]), inner, view(chain),
+                                         prm.get("D"), lp)
+    assert torch.equal(y.view(torch.int16), y_spec.view(torch.int16))
+    width = inner.shape[1] - 1 if kind != "hcl" else 16
+    assert torch.equal(view(chain)[blocks[0]][:, :width], view(spec)[dst][:, :width])
+    assert torch.equal(chain.conv_view()[blocks[0]][:, :2], spec.conv_view()[dst][:, :2])
