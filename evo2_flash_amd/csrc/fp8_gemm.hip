@@ -22,6 +22,7 @@
 // chunk c of row r sits at c ^ ((r >> 2) & 3): a b128 read is served 16
 // lanes (16 consecutive rows) at a time over 64 banks, and the swizzle puts
 // those 16 rows' chunks in 16 different bank groups.
+#include <algorithm>
 #include <type_traits>
 
 #include "common.h"
@@ -818,6 +819,34 @@ __global__ __launch_bounds__(256) void fp8_quantize_kernel(const bf16_t *x, int6
   }
 }
 
+// The same for rows of whole 16-element chunks with 16-byte aligned rows:
+// a thread converts 16 values (two 16-byte loads, one 16-byte store), the
+// grid strides over the (rows x K / 16) chunks.
+__global__ __launch_bounds__(256) void fp8_quantize16_kernel(const bf16_t *x, int64_t sx,
+                                                             uint8_t *q, int64_t sq,
+                                                             const float *scale, int64_t chunks,
+                                                             int cpr) {
+  const float s = scale[0];
+  for (int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x; c < chunks;
+       c += (int64_t)gridDim.x * 256) {
+    const int64_t r = c / cpr;
+    const int k = static_cast<int>(c - r * cpr) * 16;
+    const uint4 *xp = reinterpret_cast<const uint4 *>(x + r * sx + k);
+    const uint4 a = xp[0], b = xp[1];
+    const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    int out[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float v[4] = {lo_bf(w[2 * j]), hi_bf(w[2 * j]), lo_bf(w[2 * j + 1]), hi_bf(w[2 * j + 1])};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = fminf(fmaxf(v[i] / s, -448.0f), 448.0f);
+      int packed = __builtin_amdgcn_cvt_pk_fp8_f32(v[0], v[1], 0, false);
+      out[j] = __builtin_amdgcn_cvt_pk_fp8_f32(v[2], v[3], packed, true);
+    }
+    *reinterpret_cast<int4 *>(q + r * sq + k) = make_int4(out[0], out[1], out[2], out[3]);
+  }
+}
+
 }  // namespace evo2
 
 using namespace evo2;
@@ -880,6 +909,15 @@ extern "C" int evo2_fp8_quantize(const void *x, int64_t sx, void *q, int64_t sq,
       if (rc) return rc;
     }
     return EVO2_OK;
+  }
+  if (K % 16 == 0 && sx % 8 == 0 && sq % 16 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+      reinterpret_cast<uintptr_t>(q) % 16 == 0) {
+    const int64_t chunks = rows * (K / 16);
+    const int64_t blocks = std::min<int64_t>(cdiv(chunks, 256), 8192);
+    hipLaunchKernelGGL(fp8_quantize16_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), static_cast<const bf16_t *>(x), sx,
+                       static_cast<uint8_t *>(q), sq, scale, chunks, static_cast<int>(K / 16));
+    return check_launch("fp8_quantize");
   }
   dim3 grid(static_cast<unsigned>(cdiv(K, 1024)), static_cast<unsigned>(rows));
   hipLaunchKernelGGL(fp8_quantize_kernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream),

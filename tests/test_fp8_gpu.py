@@ -29,14 +29,24 @@ DEV = "cuda"
 E4M3 = torch.float8_e4m3fn
 
 
-def test_quantize_bitexact():
+@pytest.mark.parametrize("rows,K,row_stride", [(4, 1027, None),    # 4-element kernel
+                                              (4, 1024, None),    # 16-element kernel
+                                              (3, 4096, 4104),    # strided rows, 16-element
+                                              (3, 4096, 4100)])   # rows not 16-byte aligned
+def test_quantize_bitexact(rows, K, row_stride):
     g = torch.Generator().manual_seed(0)
-    x = torch.cat([torch.randn(4096, generator=g) * 3,
-                   torch.tensor([0.0, -0.0, 1e-9, 448.0, 449.0, -1e4, 1e4, 0.0087890625,
-                                 0.009765625, 240.0, 248.0, 256.0])]).to(torch.bfloat16)
-    x = x[: (x.numel() // 4) * 4].reshape(4, -1)
+    n = rows * K
+    special = torch.tensor([0.0, -0.0, 1e-9, 448.0, 449.0, -1e4, 1e4, 0.0087890625,
+                            0.009765625, 240.0, 248.0, 256.0])
+    x = torch.cat([torch.randn(n - special.numel(), generator=g) * 3, special])
+    x = x[torch.randperm(n, generator=g)].to(torch.bfloat16).reshape(rows, K)
     scale = torch.tensor([0.75])
-    q = quantize_input(x.to(DEV), scale.to(DEV)).cpu()
+    xd = x.to(DEV)
+    if row_stride is not None:
+        wide = torch.zeros(rows, row_stride, dtype=torch.bfloat16, device=DEV)
+        wide[:, :K] = xd
+        xd = wide[:, :K]
+    q = quantize_input(xd, scale.to(DEV)).cpu()
     ref = oracle.quantize_input(x, scale)
     assert torch.equal(q.view(torch.uint8), ref.view(torch.uint8))
 
