@@ -7,6 +7,8 @@ the KV cache in 16-position pages of a random block table:
   state pools within the mixer tolerance after every step;
 * a prefill of two prompts: last-position logits within 2e-2, Hyena states
   and the KV pages of the prompt against the composition;
+* both of the above also at the 7B model's layer shape (H=4096, 32 heads,
+  MLP 11264, fp8 in_proj), where the stripe prefill kernels run;
 * prefill(L) followed by one decode step equals prefill(L + 1) at the last
   position (logits and states), which ties the prefill and decode paths of
   every layer kind to each other;
@@ -69,33 +71,38 @@ def _mlp_ref(layer, post):
     return _lin((z1.float() * z2.float()).to(bf), layer.mlp.l3.weight.cpu())
 
 
-def test_decode_steps_vs_cpu_composition():
-    H, B = 256, 3
-    cfg = _cfg5(H)
+def _decode_vs_composition(cfg, B, pos0, steps, name, seed=11, win_tol=2e-2, li_tol=1e-3):
+    """`steps` decode steps of B sequences from positions pos0 against the
+    CPU composition: logits within 2e-2 and the Hyena state pools within the
+    mixer tolerances after every step: `win_tol` for the FIR windows (the
+    step's new column is u = x1 v), `li_tol` for the LI states (one step adds
+    u to p s, so a bf16 step of z from the fp8 in_proj moves every pole of a
+    channel by the same du)."""
+    H = cfg.hidden_size
     model = Evo2DecodeModel(cfg, max_batch=B, max_ctx=32, device=DEV, rope_theta=10000.0,
-                            rope_factor=4.0, name="harness_test")
-    model.init_random(seed=11, state_scale=0.5, kv_scale=0.5)
+                            rope_factor=4.0, name=name)
+    model.init_random(seed=seed, state_scale=0.5, kv_scale=0.5)
     # CPU copies of every state the step touches
     pools = {}
     for i, p in model.pools.items():
         c = HyenaStatePool(p.num_blocks, H, "cpu")
         c.raw.copy_(p.raw.cpu())
         pools[i] = c
-    attn = model.layers[3].mixer
-    kc, vc = (t.cpu() for t in attn.cache.dense(model.block_table, B, 32))
+    caches = {i: tuple(t.cpu() for t in layer.mixer.cache.dense(model.block_table, B, 32))
+              for i, layer in enumerate(model.layers) if layer.kind == "attn"}
     emb = model.embed.detach().cpu()
     g = torch.Generator().manual_seed(3)
-    pos = torch.tensor([10, 4, 17])
+    pos = torch.tensor(pos0)
     slots = model.slots.cpu().tolist()
-    for step in range(3):
-        tok = torch.randint(0, 512, (B,), generator=g)
-        print(f"harness decode step {step}", flush=True)
+    for step in range(steps):
+        tok = torch.randint(0, cfg.vocab_size, (B,), generator=g)
+        print(f"{name}: decode step {step}", flush=True)
         logits = model.decode_step(tok.to(DEV), pos.to(DEV)).cpu()
         x = emb[tok]
         for i, layer in enumerate(model.layers):
             pre = oracle.rms_norm(x, layer.pre_norm.weight.cpu(), cfg.rms_norm_eps)
             if layer.kind == "attn":
-                m = _attn_ref(attn, pre, pos, kc, vc)
+                m = _attn_ref(layer.mixer, pre, pos, *caches[i])
             else:
                 prm = {k: v.detach().cpu() for k, v in layer.mixer.named_parameters()}
                 m = oracle_mixer_step(layer.kind, prm, pre, pools[i], slots, [], [], [], H)
@@ -105,9 +112,31 @@ def test_decode_steps_vs_cpu_composition():
         ref = _lin(oracle.rms_norm(x, model.norm.weight.cpu(), cfg.rms_norm_eps), emb)
         assert max_rel_err(logits, ref) <= 2e-2, step
         for i, p in model.pools.items():
-            assert max_rel_err(p.kv_cache[1].cpu(), pools[i].kv_cache[1]) <= 2e-2, (step, i)
-            assert max_rel_err(p.kv_cache[2].cpu(), pools[i].kv_cache[2]) <= 1e-3, (step, i)
+            assert max_rel_err(p.kv_cache[1].cpu(), pools[i].kv_cache[1]) <= win_tol, (step, i)
+            assert max_rel_err(p.kv_cache[2].cpu(), pools[i].kv_cache[2]) <= li_tol, (step, i)
         pos = pos + 1
+
+
+def test_decode_steps_vs_cpu_composition():
+    _decode_vs_composition(_cfg5(256), 3, [10, 4, 17], 3, "harness_test")
+
+
+def test_decode_steps_7b_layer_shape():
+    """The same check at the 7B model's layer shape (H=4096, 32 heads of 128,
+    MLP 11264, fp8 in_proj): one layer of each Hyena kind and an attention
+    layer, two decode steps of three sequences."""
+    cfg = HyenaConfig(hidden_size=4096, num_hidden_layers=5, num_attention_heads=32,
+                      intermediate_size=11264, vocab_size=512, hcs_layer_idxs=[0, 4],
+                      hcm_layer_idxs=[1], hcl_layer_idxs=[2], attn_layer_idxs=[3],
+                      use_fp8_input_projections=True)
+    # K = 4096 in_proj sums move a few z entries by a bf16 step or two against
+    # the CPU's fp32 products, and u = x1 v carries that into the windows' new
+    # column and every pole of an LI channel; the last layer's input also
+    # carries the bf16 differences of four layers and their MLPs at H=4096.
+    # States within 5e-2 here (a wrong slot, layer or window column is O(1);
+    # the per-kernel tests pin the mixer cores tightly), logits within 2e-2.
+    _decode_vs_composition(cfg, 3, [20, 5, 12], 2, "harness_7b_shape", seed=13, win_tol=5e-2,
+                           li_tol=5e-2)
 
 
 def test_decode_step_graph_replays():
@@ -172,27 +201,28 @@ def _prefill_attn_ref(a, x, nseq, L):
     return _lin(o, a.o_proj.weight.cpu(), a.o_proj.bias.cpu()), k, v
 
 
-def test_prefill_vs_cpu_composition():
-    """Two fresh 45-token prompts through the model: last-position logits,
-    the Hyena states written for each sequence and the KV pages of the
-    prompt against the CPU composition."""
-    H, B, L = 256, 2, 45
-    cfg = _cfg5(H)
-    model = Evo2DecodeModel(cfg, max_batch=3, max_ctx=64, device=DEV, rope_theta=10000.0,
-                            rope_factor=4.0, name="harness_prefill", page_seed=3)
-    model.init_random(seed=12, state_scale=0.0, kv_scale=0.0)
+def _prefill_vs_composition(cfg, B, L, name, seed=12, state_tol=2e-2):
+    """Fresh L-token prompts of B sequences: last-position logits, the Hyena
+    states written for each sequence (within `state_tol`) and every attention
+    layer's KV pages against the CPU composition."""
+    H = cfg.hidden_size
+    model = Evo2DecodeModel(cfg, max_batch=B + 1, max_ctx=L + 32, device=DEV, rope_theta=10000.0,
+                            rope_factor=4.0, name=name, page_seed=3)
+    model.init_random(seed=seed, state_scale=0.0, kv_scale=0.0)
     g = torch.Generator().manual_seed(5)
     tok = torch.tensor([65, 67, 71, 84])[torch.randint(0, 4, (B, L), generator=g)]
-    print("harness prefill", flush=True)
+    print(f"{name}: prefill {B} x {L}", flush=True)
     logits = model.prefill(tok.to(DEV), chunk_seqs=2).cpu()
     emb = model.embed.detach().cpu()
     pools = {i: HyenaStatePool(p.num_blocks, H, "cpu") for i, p in model.pools.items()}
     slots = model.slots.cpu()[:B].tolist()
     x = emb[tok.reshape(-1)]
+    kv_ref = {}
     for i, layer in enumerate(model.layers):
         pre = oracle.rms_norm(x, layer.pre_norm.weight.cpu(), cfg.rms_norm_eps)
         if layer.kind == "attn":
             m, k_ref, v_ref = _prefill_attn_ref(layer.mixer, pre, B, L)
+            kv_ref[i] = (k_ref, v_ref)
         else:
             prm = {k: v.detach().cpu() for k, v in layer.mixer.named_parameters()}
             m = oracle_mixer_step(layer.kind, prm, pre, pools[i], [], [L] * B, slots, [0] * B, H)
@@ -202,11 +232,29 @@ def test_prefill_vs_cpu_composition():
     ref = _lin(oracle.rms_norm(last, model.norm.weight.cpu(), cfg.rms_norm_eps), emb)
     assert max_rel_err(logits, ref) <= 2e-2
     for i, p in model.pools.items():
-        assert max_rel_err(p.kv_cache[1].cpu(), pools[i].kv_cache[1]) <= 2e-2, i
-        assert max_rel_err(p.kv_cache[2].cpu(), pools[i].kv_cache[2]) <= 2e-2, i
-    kd, vd = model.layers[3].mixer.cache.dense(model.block_table, B, L)
-    assert max_rel_err(kd.cpu(), k_ref.transpose(-1, -2)) <= 2e-2
-    assert max_rel_err(vd.cpu(), v_ref) <= 2e-2
+        assert max_rel_err(p.kv_cache[1].cpu(), pools[i].kv_cache[1]) <= state_tol, i
+        assert max_rel_err(p.kv_cache[2].cpu(), pools[i].kv_cache[2]) <= state_tol, i
+    for i, (k_ref, v_ref) in kv_ref.items():
+        kd, vd = model.layers[i].mixer.cache.dense(model.block_table, B, L)
+        assert max_rel_err(kd.cpu(), k_ref.transpose(-1, -2)) <= 2e-2, i
+        assert max_rel_err(vd.cpu(), v_ref) <= 2e-2, i
+
+
+def test_prefill_vs_cpu_composition():
+    """Two fresh 45-token prompts through the five-layer model."""
+    _prefill_vs_composition(_cfg5(256), 2, 45, "harness_prefill")
+
+
+def test_prefill_7b_layer_shape():
+    """Two 300-token prompts at the 7B model's layer shape (the stripe
+    prefill kernels take both Hyena cores at this size)."""
+    cfg = HyenaConfig(hidden_size=4096, num_hidden_layers=5, num_attention_heads=32,
+                      intermediate_size=11264, vocab_size=512, hcs_layer_idxs=[0, 4],
+                      hcm_layer_idxs=[1], hcl_layer_idxs=[2], attn_layer_idxs=[3],
+                      use_fp8_input_projections=True)
+    # the last layer's states carry the bf16 differences of the four layers
+    # before it at H=4096 (see test_decode_steps_7b_layer_shape)
+    _prefill_vs_composition(cfg, 2, 300, "harness_prefill_7b_shape", seed=14, state_tol=5e-2)
 
 
 def test_prefill_then_decode_matches_longer_prefill():
