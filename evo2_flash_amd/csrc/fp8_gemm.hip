@@ -433,7 +433,9 @@ __global__ __launch_bounds__(256) void fp8_gemm_persist_kernel(GemmArgs p, int t
   };
   // Epilogue of tile j: lane holds, for X row m = m0 + wm + 32 tm + lr, the
   // W rows n = n0 + wn + 32 tn + 8 q + 4 g + i (i < 4) in acc[tn][tm][4 q + i].
-  // Every store address is one of four row pointers plus a constant.
+  // Every store address is one of four row pointers plus a constant; a lane
+  // issues EPI_STORES 16-byte stores (4 tm x 4 tn x 2 pairs).
+  constexpr int EPI_STORES = 4 * 4 * 2;
   auto epilogue = [&](auto par, int j) __attribute__((always_inline)) {
     int bn, bm;
     persist_tile(static_cast<int>(blockIdx.x) + j * grid, tiles_n, tiles_m, grouped != 0, bn, bm);
@@ -493,9 +495,10 @@ __global__ __launch_bounds__(256) void fp8_gemm_persist_kernel(GemmArgs p, int t
   //     and nobody reads stage S again, which is refilled with slice k + 2;
   //   sub-step 1: MFMAs of (k, 1) while reading (k + 1, 0) from the other
   //     stage.
-  // The first step after an epilogue also has its 64 stores outstanding,
+  // The first step after an epilogue also has the epilogue's EPI_STORES
+  // stores outstanding (and, in wave 0, the next bias load after them), all
   // issued after the loads of slice k + 1: loads and stores retire in order,
-  // so waiting for at most 63 covers the loads.
+  // so waiting until at most EPI_STORES remain covers the loads.
   i32x8 fa[2][4], fb[2][4];
   auto interleave = [&](bool dma) __attribute__((always_inline)) {
 #pragma unroll
@@ -513,7 +516,7 @@ __global__ __launch_bounds__(256) void fp8_gemm_persist_kernel(GemmArgs p, int t
     read_frags(stage, I1{}, fa[1], fb[1]);
     mma(fa[0], fb[0]);
     interleave(false);
-    if (after_epilogue) vmcnt_wait<63>();
+    if (after_epilogue) vmcnt_wait<EPI_STORES>();
     else vmcnt_wait<0>();
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     issue(stage, k + 2);
