@@ -83,8 +83,10 @@ struct StripeGeo {
   static_assert(zloads(1) == zloads(NF - 1) && NF * (NF + 3) >= ZINS, "featurizer wave load counts");
   static constexpr int HIST = 144;               // hcm: history rows a batch's windows reach
   // u ring rows: hcl keeps two batches; hcm the history, a batch being read
-  // and the step being written meanwhile
-  static constexpr int UR = CH == 16 ? 2 * BATCH : HIST + BATCH + STEP;
+  // and the step being written meanwhile, rounded up to a multiple of 128
+  // rows: a wrap then moves a read by whole 256-byte bank rows, which keeps
+  // the matrix waves' 16-byte reads on distinct banks
+  static constexpr int UR = CH == 16 ? 2 * BATCH : (HIST + BATCH + STEP + 127) / 128 * 128;
   static constexpr int UP = UR + 8;              // u ring pitch (bf16)
   static constexpr int XR = BATCH + STEP;        // x2 ring rows: a batch and the step after it
   static constexpr int XP = XR + 8;              // x2 ring pitch (bf16)
@@ -94,7 +96,8 @@ struct StripeGeo {
   static_assert(UR % 16 == 0 && XR % 16 == 0, "16-row groups never wrap");
   static constexpr int NGB = SPB == 1 ? 2 : 1;   // output buffers (stores run one step after the epilogue)
   static constexpr int SIB = 64 / CH;            // workgroups per 64-channel block
-  static constexpr int NSLOT = 3;                // z slots: two steps in flight
+  static constexpr int NSLOT = 3;                // z slots: two steps in flight (a
+                                                 // fourth measured no faster for hcl)
   static constexpr int KS = 5;                   // hcm: k-steps over the 160-row window
   static constexpr int TAPW = 176;               // hcm: zero-padded taps per channel for the A build
   static constexpr int ETAB = 17;                // hcl: p^m for m = 0..16 per pole
@@ -394,8 +397,9 @@ __global__ __launch_bounds__(StripeGeo<CHW>::NT, 1) void stripe_kernel(StripeArg
 
   // ---- matrix waves: inner filter and epilogue of batch m into gbuf.  gbuf
   // row pr = 16 i + n holds batch row 16 n + i; this wave's four channels
-  // are 8-byte piece mw of it, placed at piece mw ^ (n >> SH) so that the 16
-  // lanes writing one output row index fall on distinct banks
+  // are 8-byte piece mw of it, placed at piece mw ^ (n >> SH) ^ NPC / 2 [i / 4
+  // odd] so that the 32 lanes of one write (n < 16, i = 4 g + k for g = 0, 1:
+  // rows 64 apart) fall on distinct banks
   constexpr int NPC = CH / 4;              // 8-byte pieces per gbuf row
   constexpr int SH = CH == 16 ? 3 : 2;     // n >> SH takes NPC / 2 ... values
   auto matrix = [&](int m) __attribute__((always_inline)) {
@@ -488,7 +492,7 @@ __global__ __launch_bounds__(StripeGeo<CHW>::NT, 1) void stripe_kernel(StripeArg
       gq[cc][1] = pack_bf(gv[2], gv[3]);
     }
     bf16_t *gb = gbuf + (G::NGB == 2 ? (m & 1) : 0) * G::BATCH * CH;
-    const int piece = mw ^ (l16 >> SH);
+    const int piece = mw ^ (l16 >> SH) ^ ((g & 1) * (NPC / 2));
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       uint32_t b[4];
@@ -512,10 +516,11 @@ __global__ __launch_bounds__(StripeGeo<CHW>::NT, 1) void stripe_kernel(StripeArg
     for (int k = 0; k < NCK / (64 * G::NM); ++k) {
       const int q = mt + 64 * G::NM * k, pr = q / CPR, ck = q % CPR;
       const int n = pr & 15;
-      // pieces 2 ck, 2 ck + 1 of the row sit at (2 ck) ^ (n >> SH) and its
-      // neighbour, swapped when that index is odd
+      // pieces 2 ck, 2 ck + 1 of the row sit at (2 ck) ^ (n >> SH) ^ NPC / 2
+      // [(pr >> 6) odd] and its neighbour, swapped when n >> SH is odd
       const int sw = n >> SH;
-      uint4 v = *reinterpret_cast<const uint4 *>(gb + pr * CH + 4 * ((2 * ck) ^ (sw & ~1)));
+      const int hi = ((pr >> 6) & 1) * (NPC / 2);
+      uint4 v = *reinterpret_cast<const uint4 *>(gb + pr * CH + 4 * ((2 * ck) ^ (sw & ~1) ^ hi));
       if (sw & 1) v = make_uint4(v.z, v.w, v.x, v.y);
       const int r = 16 * n + (pr >> 4);
       const int t = sb + G::BATCH * m + r;  // >= t0 for batches with outputs
