@@ -548,9 +548,15 @@ def _bench_verify_mixers(reps, dev, H, B, Q, seed):
 
 
 # ---------------------------------------------------------------- prefill
-def bench_prefill(reps, dev, L=L_PREFILL, H=H_7B, seed=77):
-    """One fresh L-token sequence through one mixer core of each kind; the
-    27-layer step is 9 x (hcs + hcm + hcl)."""
+def bench_prefill(reps, dev, L=L_PREFILL, H=H_7B, seed=77, warmup=1):
+    """One fresh L-token sequence through the 27 Hyena mixer cores of the 7B
+    layer map, launched in layer order (9 each of hcs, hcm, hcl, interleaved
+    as in the model).  `warmup` untimed passes, then `reps` passes timed as a
+    whole (the step), then `reps` passes with an event between launches (the
+    per-kind figures).  Timing each kind alone, back to back, measured the
+    hcl core up to ~15% slower than inside the layer sequence: sustained
+    back-to-back runs of it lower the clock."""
+    from evo2_flash_amd.config import evo2_7b
     from evo2_flash_amd.hcl import hcl_block_t, hyena_hcl_prefill
     from evo2_flash_amd.metadata import build_metadata, prefill_tables
     from evo2_flash_amd.prefill import fir_prefill_block_t, hyena_fir_prefill
@@ -562,7 +568,7 @@ def bench_prefill(reps, dev, L=L_PREFILL, H=H_7B, seed=77):
     m = build_metadata(prefill_lens=[L], prefill_slots=[1], has_init=[0], device=dev)
     pool = HyenaStatePool(2, H, dev)
     stream = torch.cuda.current_stream()
-    res = {}
+    fns, block_t = {}, {}
     for kind in ("hcs", "hcm", "hcl"):
         prm = mixer_params(kind, H, seed, device=dev, in_proj_fp8=False)
         sw = prm["short_filter"].view(3 * H, 3)
@@ -583,20 +589,54 @@ def bench_prefill(reps, dev, L=L_PREFILL, H=H_7B, seed=77):
             def fn(prm=prm, sw=sw, bt=bt, seq_t=seq_t, til_t=til_t, w=w, K=K):
                 return hyena_fir_prefill(z, sw, pool.conv_view(), w, pool.inner_view(K - 1),
                                          prm.get("D"), seq_t, m.state_indices_tensor_p, til_t, bt)
-        fn()
-        torch.cuda.synchronize()
-        avg, med = _timed(fn, reps, stream)
-        nbytes = prefill_bytes(L, H)
-        res[kind] = {"avg_us": round(avg, 2), "median_us": round(med, 2), "block_t": bt,
+        fns[kind], block_t[kind] = fn, bt
+    cfg = evo2_7b()
+    order = [cfg.layer_kind(i) for i in range(cfg.num_hidden_layers)]
+    order = [k for k in order if k != "attn"]
+    assert len(order) == 27 and all(order.count(k) == 9 for k in fns), order
+    for _ in range(max(1, warmup)):
+        for k in order:
+            fns[k]()
+    torch.cuda.synchronize()
+    # the step: whole passes between two events
+    steps = []
+    for _ in range(reps):
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for k in order:
+            fns[k]()
+        b.record(stream)
+        steps.append((a, b))
+    # per kind: an event after every launch
+    passes = []
+    for _ in range(reps):
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(order) + 1)]
+        ev[0].record(stream)
+        for j, k in enumerate(order):
+            fns[k]()
+            ev[j + 1].record(stream)
+        passes.append(ev)
+    torch.cuda.synchronize()
+    step_us = statistics.mean(a.elapsed_time(b) * 1e3 for a, b in steps)
+    per = {k: [] for k in fns}
+    for ev in passes:
+        for j, k in enumerate(order):
+            per[k].append(ev[j].elapsed_time(ev[j + 1]) * 1e3)
+    nbytes = prefill_bytes(L, H)
+    res = {}
+    for kind in ("hcs", "hcm", "hcl"):
+        avg, med = statistics.mean(per[kind]), statistics.median(per[kind])
+        res[kind] = {"avg_us": round(avg, 2), "median_us": round(med, 2), "block_t": block_t[kind],
                      "bytes": nbytes, "achieved_GBs": round(nbytes / (avg * 1e-6) / 1e9, 1),
                      "frac": round(nbytes / (avg * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
-    step_us = 9 * sum(v["avg_us"] for v in res.values())
-    ideal_us = 27 * prefill_bytes(L, H) / (HBM_PEAK_GBS * 1e3)
+    ideal_us = 27 * nbytes / (HBM_PEAK_GBS * 1e3)
     del z
     return {"scope": "the 27 Hyena mixer cores of the 7B layer map, z -> g (short filter, "
-                     "gate, inner FIR or modal scan, D, x2); in_proj, out_proj, norms, MLPs "
-                     "and attention are in model_prefill",
+                     "gate, inner FIR or modal scan, D, x2), launched in layer order; in_proj, "
+                     "out_proj, norms, MLPs and attention are in model_prefill",
             "tok_s": round(L / (step_us * 1e-6), 1), "us_per_step": round(step_us, 1),
+            "sum_of_kinds_us": round(9 * sum(v["avg_us"] for v in res.values()), 1),
             "L": L, "mixer_frac": round(ideal_us / step_us, 4), "per_kind": res}
 
 
@@ -933,7 +973,8 @@ def main(argv=None):
     run = lambda leg, flag: (args.only == leg) or (args.only is None and not flag)  # noqa: E731
     dec = bench_decode(args.steps, args.warmup, dev) if run("decode", False) else None
     ver = bench_verify(max(8, args.steps // 2), dev) if run("verify", args.no_verify) else None
-    pre = bench_prefill(max(3, args.steps // 8), dev) if run("prefill", args.no_prefill) else None
+    pre = (bench_prefill(max(3, args.steps // 8), dev, warmup=args.warmup)
+           if run("prefill", args.no_prefill) else None)
     gem = bench_gemm(max(5, args.steps // 4), dev) if run("gemm", args.no_gemm) else None
     cf0 = (bench_config0(max(5, args.steps // 4), dev, cpu=not (args.no_cpu or args.only))
            if run("config0", False) else None)
