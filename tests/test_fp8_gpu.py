@@ -136,7 +136,7 @@ def test_config3_shapes(N):
     out = fp8_gemm(x8, w8, xs, ws)
     ref = (x8.float() @ w8.float().t()) * (xs * ws)
     assert max_rel_err(out, ref) <= 2e-2
-    # dequantised bf16 reference of the unquantised activations, as the north star states it
+    # the dequantised reference bf16((A8 s_a) @ (W8 s_w)^T), operands rounded to bf16 first
     ref_bf = ((x8.float() * xs).to(torch.bfloat16).float() @ (w8.float() * ws).to(torch.bfloat16).float().t())
     assert max_rel_err(out, ref_bf) <= 2e-2
 
