@@ -60,6 +60,8 @@ __global__ __launch_bounds__(256) void fp8_gemm_kernel(GemmArgs p) {
   const int m0 = blockIdx.y * G_BM;
   const int wn = (wave & 1) * 128;   // wave quadrant in W rows
   const int wm = (wave >> 1) * 128;  // wave quadrant in X rows
+  // the scales first, as scalar loads whose latency the K loop hides
+  const float scale = p.sx_scale[0] * p.sw_scale[0];
 
   // DMA: one wave instruction fills 1 KB = 16 rows of 64 bytes; lane i
   // writes row i/4, physical chunk i%4, which holds logical chunk
@@ -191,7 +193,6 @@ __global__ __launch_bounds__(256) void fp8_gemm_kernel(GemmArgs p) {
 
   // Epilogue: lane holds, for X row m = m0 + wm + 32 tm + lr, the W rows
   // n = n0 + wn + 32 tn + 8 q + 4 g + i (i < 4) in acc[tn][tm][4 q + i].
-  const float scale = p.sx_scale[0] * p.sw_scale[0];
   const bool full = m0 + G_BM <= p.M && n0 + G_BN <= p.N && (p.so % 4) == 0 &&
                     (reinterpret_cast<uintptr_t>(p.out) & 7) == 0;
 #pragma unroll
@@ -619,6 +620,10 @@ __global__ __launch_bounds__(256) void fp8_gemm_small_kernel(GemmArgs p) {
   int bx, by;
   if (!stream_tile((p.N + 16 * WPG - 1) / (16 * WPG), (p.M + S_ROWS - 1) / S_ROWS, bx, by))
     return;  // uniform: grid padding
+  // the scales before any load that writes LDS: read here the compiler makes
+  // them scalar loads, whose latency passes under the K loop (read after it,
+  // they were vector loads the epilogue waited for)
+  const float scale = p.sx_scale[0] * p.sw_scale[0];
   const int n0 = bx * 16 * WPG;
   const int m0 = by * S_ROWS;  // 64-row block of the activations
   const int mrows = p.M - m0;          // >= 1 (the grid covers M exactly)
@@ -738,7 +743,6 @@ __global__ __launch_bounds__(256) void fp8_gemm_small_kernel(GemmArgs p) {
   vmcnt_wait<0>();  // no DMA may still target this workgroup's LDS
 
   // lane holds out[m0 + 16 t + lr][n = n0 + 16 wave + 4 g + i] in acc[t][i]
-  const float scale = p.sx_scale[0] * p.sw_scale[0];
   const int n = n0 + 16 * wave + 4 * g;  // (n0 + 16 * wave: this wave's W rows)
   float bias[4] = {0.f, 0.f, 0.f, 0.f};
   if (p.bias) {
