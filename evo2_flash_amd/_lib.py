@@ -145,6 +145,7 @@ SIGNATURES = {
         _c_p, _c_i64, _c_i64, _c_i64,             # value pages + strides (page, h, l)
         _c_i64,                                   # num_pages
         _c_p, _c_i64,                             # block table, row stride
+        _c_i64,                                   # shared_pages
         _c_p, _c_p, _c_i64,                       # positions, workspace, bytes
         _c_p, _c_i64, _c_i64,                     # out + strides (b, h)
         _c_i64, _c_i64, _c_i64, _c_i64, _c_f, _c_p,  # B, heads, head_dim, max_pages, scale, stream

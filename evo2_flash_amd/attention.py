@@ -57,14 +57,19 @@ def decode_attention(q, k_cache, v_cache, positions, scale, work=None):
     return out
 
 
-def paged_decode_attention(q, k_pages, v_pages, block_table, positions, scale, work=None):
+def paged_decode_attention(q, k_pages, v_pages, block_table, positions, scale, work=None,
+                           shared_pages=0):
     """q (B, heads, head_dim) bf16; k_pages (pages, heads, head_dim, 16) and
     v_pages (pages, heads, 16, head_dim) bf16; block_table (>= B, max_pages)
     int32 (position l of sequence b is in page block_table[b, l // 16]);
     positions (B,) int64 (sequence b attends to 0..positions[b]).  Returns
     (B, heads, head_dim) bf16.  The kernel never reads through a table entry
     outside [0, pages): the positions of such an entry are left out of the
-    softmax (check_block_table finds them on the host)."""
+    softmax (check_block_table finds them on the host).  shared_pages: the
+    first shared_pages entries of every row name the same pages (a prompt
+    shared by all B sequences; shared_prefix_pages finds it on the host):
+    those chunks read each page once for several sequences, with the same
+    result bits."""
     _lib.require_device(q, k_pages, v_pages, block_table, positions, work)
     B, heads, hd = q.shape
     max_pages = block_table.shape[1]
@@ -86,11 +91,23 @@ def paged_decode_attention(q, k_pages, v_pages, block_table, positions, scale, w
               _lib.ptr(q), q.stride(0), q.stride(1),
               _lib.ptr(k_pages), k_pages.stride(0), k_pages.stride(1), k_pages.stride(2),
               _lib.ptr(v_pages), v_pages.stride(0), v_pages.stride(1), v_pages.stride(2),
-              k_pages.shape[0], _lib.ptr(block_table), block_table.stride(0),
+              k_pages.shape[0], _lib.ptr(block_table), block_table.stride(0), int(shared_pages),
               _lib.ptr(positions), _lib.ptr(work), work.numel() * 4,
               _lib.ptr(out), out.stride(0), out.stride(1),
               B, heads, hd, max_pages, float(scale), _lib.stream_of(q))
     return out
+
+
+def shared_prefix_pages(block_table, B):
+    """The number of leading entries that rows 0..B-1 of the block table
+    share (the pages of a prompt behind all B sequences).  For tables built
+    on the host; a device table is copied to the host first."""
+    table = block_table.detach().cpu()[:B]
+    if B <= 1:
+        return 0
+    same = (table == table[0:1]).all(dim=0)
+    diff = (~same).nonzero()
+    return int(diff[0, 0]) if diff.numel() else int(table.shape[1])
 
 
 def check_block_table(block_table, lengths, num_pages, first_page=1):

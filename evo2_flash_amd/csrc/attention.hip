@@ -30,7 +30,10 @@
 // sequences at the same pages (a shared prompt), those pages stream from HBM
 // once per pair and from L2 for the other sequences (32 sequences sharing a
 // 131072-position prompt: 23.0 -> 8.0 ms per layer; 64 sequences with pages
-// of their own: 1.70 -> 1.68 ms).
+// of their own: 1.70 -> 1.68 ms).  When the caller declares the shared
+// leading pages, the chunks inside them take four sequences per workgroup,
+// each key and value load serving all four (8.0 -> 5.4 ms per layer, the
+// same bits).
 #include "common.h"
 
 namespace evo2 {
@@ -61,47 +64,72 @@ __device__ __forceinline__ int valid_len(const AttnArgs &p, int b) {
   return static_cast<int>(n < 0 ? 0 : (n > p.L ? p.L : n));
 }
 
-template <int HD, bool PAGED>
-__global__ __launch_bounds__(AT_T) void attn_chunk_kernel(AttnArgs p) {
-  __shared__ float qs[HD];
-  __shared__ float ps[AT_CHUNK];
-  __shared__ float red[AT_T / 64];
-  __shared__ float osum[AT_T / 64][HD];
+// Chunks c_first .. c_first + c_count - 1 of NQ sequences b0 .. b0 + NQ - 1
+// (those below B) and one head per workgroup.  With NQ > 1 (paged cache only)
+// the sequences read the pages of row b0: the caller passes NQ > 1 only for
+// chunks whose pages every sequence shares, and each key and value load then
+// serves NQ queries.  Every query's arithmetic (score sums over d in order,
+// the block reductions, the value sums over l in order) is the NQ = 1
+// kernel's, so a chunk's partials do not depend on NQ.
+template <int HD, bool PAGED, int NQ>
+__global__ __launch_bounds__(AT_T) void attn_chunk_kernel(AttnArgs p, int c_first, int c_count) {
+  static_assert(NQ == 1 || PAGED, "shared chunks are a paged-cache case");
+  __shared__ float qs[NQ][HD];
+  __shared__ float ps[NQ][AT_CHUNK];
+  __shared__ float red[NQ][AT_T / 64];
+  __shared__ float osum[NQ][AT_T / 64][HD];
   __shared__ int32_t pages[PAGED ? AT_CHUNK / AT_PAGE : 1];
-  int c, h, b;
+  const int G = (p.B + NQ - 1) / NQ;  // sequence groups
+  int c, h, b0;
   if (p.pair_major) {
-    // (chunk, head) pair P and sequence b: the B workgroups of a pair run
-    // back to back on one XCD (workgroup w runs on XCD w mod 8), so where
+    // (chunk, head) pair P and sequence group gi: the G workgroups of a pair
+    // run back to back on one XCD (workgroup w runs on XCD w mod 8), so where
     // sequences share pages (one prompt behind many sequences) the pair's
     // keys and values come from HBM once and from that XCD's L2 for the rest
     const int w = blockIdx.x;
     const int j = w >> 3;
-    b = j % p.B;
-    const int P = (j / p.B) * 8 + (w & 7);
-    if (P >= p.nchunk * p.heads) return;  // uniform: padding
-    c = P % p.nchunk;
-    h = P / p.nchunk;
+    const int P = (j / G) * 8 + (w & 7);
+    if (P >= c_count * p.heads) return;  // uniform: padding
+    b0 = (j % G) * NQ;
+    c = c_first + P % c_count;
+    h = P / c_count;
   } else {
-    c = blockIdx.x;
+    c = c_first + blockIdx.x;
     h = blockIdx.y;
-    b = blockIdx.z;
+    b0 = blockIdx.z * NQ;
   }
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int n = valid_len(p, b);
-  const int l0 = c * AT_CHUNK, l1 = min(l0 + AT_CHUNK, n);
-  float *part = p.part + (((int64_t)b * p.heads + h) * p.nchunk + c) * (HD + 2);
-  if (l0 >= l1) {  // uniform: an empty chunk contributes nothing
-    if (t < HD) part[t] = 0.0f;
-    if (t == 0) {
-      part[HD] = -INFINITY;
-      part[HD + 1] = 0.0f;
+  const int l0 = c * AT_CHUNK;
+  int l1[NQ];
+  int l1max = l0;
+#pragma unroll
+  for (int qi = 0; qi < NQ; ++qi) {
+    l1[qi] = b0 + qi < p.B ? min(l0 + AT_CHUNK, valid_len(p, b0 + qi)) : l0;
+    l1max = max(l1max, l1[qi]);
+  }
+  auto part_of = [&](int qi) -> float * {
+    return p.part + (((int64_t)(b0 + qi) * p.heads + h) * p.nchunk + c) * (HD + 2);
+  };
+  if (l0 >= l1max) {  // uniform: an empty chunk contributes nothing
+#pragma unroll
+    for (int qi = 0; qi < NQ; ++qi) {
+      if (b0 + qi >= p.B) break;
+      float *part = part_of(qi);
+      if (t < HD) part[t] = 0.0f;
+      if (t == 0) {
+        part[HD] = -INFINITY;
+        part[HD + 1] = 0.0f;
+      }
     }
     return;
   }
-  if (t < HD) qs[t] = bf2f(p.q[(int64_t)b * p.qb + (int64_t)h * p.qh + t]);
-  if constexpr (PAGED) {  // the chunk's pages that hold positions below l1
-    if (t < AT_CHUNK / AT_PAGE && l0 + AT_PAGE * t < l1) {
-      const int32_t pg = p.tbl[(int64_t)b * p.tbs + l0 / AT_PAGE + t];
+  for (int i = t; i < NQ * HD; i += AT_T) {
+    const int qi = i / HD, d = i - HD * qi;
+    qs[qi][d] = b0 + qi < p.B ? bf2f(p.q[(int64_t)(b0 + qi) * p.qb + (int64_t)h * p.qh + d]) : 0.0f;
+  }
+  if constexpr (PAGED) {  // the chunk's pages that hold positions below l1max
+    if (t < AT_CHUNK / AT_PAGE && l0 + AT_PAGE * t < l1max) {
+      const int32_t pg = p.tbl[(int64_t)b0 * p.tbs + l0 / AT_PAGE + t];
       pages[t] = pg >= 0 && pg < p.num_pages ? pg : -1;  // -1: masked
     }
   }
@@ -111,46 +139,62 @@ __global__ __launch_bounds__(AT_T) void attn_chunk_kernel(AttnArgs p) {
   // starts below l1 inside the cache; in the paged cache the eight lie in
   // one page)
   const int lb = l0 + 8 * t;
-  const bool live = lb < l1 && (!PAGED || pages[(lb - l0) / AT_PAGE] >= 0);
-  float s[8];
+  const bool live = lb < l1max && (!PAGED || pages[(lb - l0) / AT_PAGE] >= 0);
+  float s[NQ][8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) s[e] = 0.0f;
+  for (int qi = 0; qi < NQ; ++qi)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s[qi][e] = 0.0f;
   if (live) {
     const bf16_t *kr =
         PAGED ? p.k + (int64_t)pages[(lb - l0) / AT_PAGE] * p.kb + (int64_t)h * p.kh + lb % AT_PAGE
-              : p.k + (int64_t)b * p.kb + (int64_t)h * p.kh + lb;
+              : p.k + (int64_t)b0 * p.kb + (int64_t)h * p.kh + lb;
 #pragma unroll 8
     for (int d = 0; d < HD; ++d) {
       const uint4 kv = *reinterpret_cast<const uint4 *>(kr + (int64_t)d * p.kd);
-      const float qd = qs[d];
-      s[0] += qd * lo_bf(kv.x); s[1] += qd * hi_bf(kv.x);
-      s[2] += qd * lo_bf(kv.y); s[3] += qd * hi_bf(kv.y);
-      s[4] += qd * lo_bf(kv.z); s[5] += qd * hi_bf(kv.z);
-      s[6] += qd * lo_bf(kv.w); s[7] += qd * hi_bf(kv.w);
+#pragma unroll
+      for (int qi = 0; qi < NQ; ++qi) {
+        const float qd = qs[qi][d];
+        s[qi][0] += qd * lo_bf(kv.x); s[qi][1] += qd * hi_bf(kv.x);
+        s[qi][2] += qd * lo_bf(kv.y); s[qi][3] += qd * hi_bf(kv.y);
+        s[qi][4] += qd * lo_bf(kv.z); s[qi][5] += qd * hi_bf(kv.z);
+        s[qi][6] += qd * lo_bf(kv.w); s[qi][7] += qd * hi_bf(kv.w);
+      }
     }
   }
-  float mx = -INFINITY;
+  float mx[NQ];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    s[e] = live && lb + e < l1 ? s[e] * p.scale : -INFINITY;
-    mx = fmaxf(mx, s[e]);
+  for (int qi = 0; qi < NQ; ++qi) {
+    mx[qi] = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      s[qi][e] = live && lb + e < l1[qi] ? s[qi][e] * p.scale : -INFINITY;
+      mx[qi] = fmaxf(mx[qi], s[qi][e]);
+    }
+    for (int o = 32; o > 0; o >>= 1) mx[qi] = fmaxf(mx[qi], __shfl_xor(mx[qi], o));
+    if (lane == 0) red[qi][wave] = mx[qi];
   }
-  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-  if (lane == 0) red[wave] = mx;
   __syncthreads();
-  mx = red[0];
+  float sum[NQ];
 #pragma unroll
-  for (int w = 1; w < AT_T / 64; ++w) mx = fmaxf(mx, red[w]);  // -inf only if all masked
-  float sum = 0.0f;
+  for (int qi = 0; qi < NQ; ++qi) {
+    mx[qi] = red[qi][0];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const float pe = live && lb + e < l1 ? expf(s[e] - mx) : 0.0f;
-    ps[8 * t + e] = pe;
-    sum += pe;
+    for (int w = 1; w < AT_T / 64; ++w) mx[qi] = fmaxf(mx[qi], red[qi][w]);  // -inf only if all masked
+    sum[qi] = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float pe = live && lb + e < l1[qi] ? expf(s[qi][e] - mx[qi]) : 0.0f;
+      ps[qi][8 * t + e] = pe;
+      sum[qi] += pe;
+    }
+    for (int o = 32; o > 0; o >>= 1) sum[qi] += __shfl_xor(sum[qi], o);
   }
-  for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
   __syncthreads();  // ps complete; every wave has read red
-  if (lane == 0) red[wave] = sum;
+  if (lane == 0) {
+#pragma unroll
+    for (int qi = 0; qi < NQ; ++qi) red[qi][wave] = sum[qi];
+  }
 
   // o[d] = sum_l p_l v[l][d]: 16-byte loads of eight dims; a wave covers
   // RW = 64 / (HD / 8) rows per instruction (lane = row group r, dim block
@@ -159,45 +203,59 @@ __global__ __launch_bounds__(AT_T) void attn_chunk_kernel(AttnArgs p) {
   constexpr int GPR = HD / 8;         // lanes per row
   constexpr int RW = 64 / GPR;        // rows per wave instruction
   const int r = lane / GPR, g = lane % GPR;
-  float o[8];
+  float o[NQ][8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) o[e] = 0.0f;
+  for (int qi = 0; qi < NQ; ++qi)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[qi][e] = 0.0f;
   {
-    const bf16_t *vr = p.v + (PAGED ? 0 : (int64_t)b * p.vb) + (int64_t)h * p.vh + 8 * g;
-    for (int l = l0 + wave * RW + r; l < l1; l += (AT_T / 64) * RW) {
+    const bf16_t *vr = p.v + (PAGED ? 0 : (int64_t)b0 * p.vb) + (int64_t)h * p.vh + 8 * g;
+    for (int l = l0 + wave * RW + r; l < l1max; l += (AT_T / 64) * RW) {
       const int pg = PAGED ? pages[(l - l0) / AT_PAGE] : 0;
       if (PAGED && pg < 0) continue;  // masked page: weight 0, never read
       const bf16_t *row = PAGED ? vr + (int64_t)pg * p.vb + (int64_t)(l % AT_PAGE) * p.vl
                                 : vr + (int64_t)l * p.vl;
       const uint4 vv = *reinterpret_cast<const uint4 *>(row);
-      const float pl = ps[l - l0];
-      o[0] += pl * lo_bf(vv.x); o[1] += pl * hi_bf(vv.x);
-      o[2] += pl * lo_bf(vv.y); o[3] += pl * hi_bf(vv.y);
-      o[4] += pl * lo_bf(vv.z); o[5] += pl * hi_bf(vv.z);
-      o[6] += pl * lo_bf(vv.w); o[7] += pl * hi_bf(vv.w);
+#pragma unroll
+      for (int qi = 0; qi < NQ; ++qi) {
+        if (NQ > 1 && l >= l1[qi]) continue;  // past this query's positions
+        const float pl = ps[qi][l - l0];
+        o[qi][0] += pl * lo_bf(vv.x); o[qi][1] += pl * hi_bf(vv.x);
+        o[qi][2] += pl * lo_bf(vv.y); o[qi][3] += pl * hi_bf(vv.y);
+        o[qi][4] += pl * lo_bf(vv.z); o[qi][5] += pl * hi_bf(vv.z);
+        o[qi][6] += pl * lo_bf(vv.w); o[qi][7] += pl * hi_bf(vv.w);
+      }
     }
   }
 #pragma unroll
-  for (int sh = GPR; sh < 64; sh <<= 1)
+  for (int qi = 0; qi < NQ; ++qi) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) o[e] += __shfl_xor(o[e], sh);
-  if (r == 0) {
+    for (int sh = GPR; sh < 64; sh <<= 1)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) osum[wave][8 * g + e] = o[e];
+      for (int e = 0; e < 8; ++e) o[qi][e] += __shfl_xor(o[qi][e], sh);
+    if (r == 0) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) osum[qi][wave][8 * g + e] = o[qi][e];
+    }
   }
   __syncthreads();
-  if (t < HD) {
-    float o = osum[0][t];
 #pragma unroll
-    for (int w = 1; w < AT_T / 64; ++w) o += osum[w][t];
-    part[t] = o;
-  }
-  if (t == 0) {
-    float tot = red[0];
+  for (int qi = 0; qi < NQ; ++qi) {
+    if (b0 + qi >= p.B) break;
+    float *part = part_of(qi);
+    if (t < HD) {
+      float ov = osum[qi][0][t];
 #pragma unroll
-    for (int w = 1; w < AT_T / 64; ++w) tot += red[w];
-    part[HD] = mx;
-    part[HD + 1] = tot;
+      for (int w = 1; w < AT_T / 64; ++w) ov += osum[qi][w][t];
+      part[t] = ov;
+    }
+    if (t == 0) {
+      float tot = red[qi][0];
+#pragma unroll
+      for (int w = 1; w < AT_T / 64; ++w) tot += red[qi][w];
+      part[HD] = mx[qi];
+      part[HD + 1] = tot;
+    }
   }
 }
 
@@ -220,23 +278,44 @@ __global__ __launch_bounds__(HD) void attn_merge_kernel(AttnArgs p) {
   p.out[(int64_t)b * p.ob + (int64_t)h * p.oh + d] = f2bf(tot > 0.0f ? o / tot : 0.0f);
 }
 
-template <int HD, bool PAGED>
-static int launch_attn(AttnArgs a, int64_t B, hipStream_t st) {
-  a.B = static_cast<int>(B);
-  const int64_t wgs = cdiv(static_cast<int64_t>(a.nchunk) * a.heads, 8) * 8 * B;
+// Chunks [c_first, c_first + c_count) with NQ sequences per workgroup.
+template <int HD, bool PAGED, int NQ>
+static void launch_chunks(const AttnArgs &a, int c_first, int c_count, hipStream_t st) {
+  const int64_t groups = cdiv(static_cast<int64_t>(a.B), NQ);
+  const int64_t wgs = cdiv(static_cast<int64_t>(c_count) * a.heads, 8) * 8 * groups;
+  AttnArgs b = a;
 #ifdef ATTN_GRID3
-  a.pair_major = 0;
+  b.pair_major = 0;
 #else
-  a.pair_major = wgs <= 0x7fffffff;
+  b.pair_major = wgs <= 0x7fffffff;
 #endif
-  if (a.pair_major)
-    hipLaunchKernelGGL((attn_chunk_kernel<HD, PAGED>), dim3(static_cast<unsigned>(wgs)), dim3(AT_T), 0,
-                       st, a);
+  if (b.pair_major)
+    hipLaunchKernelGGL((attn_chunk_kernel<HD, PAGED, NQ>), dim3(static_cast<unsigned>(wgs)), dim3(AT_T),
+                       0, st, b, c_first, c_count);
   else
-    hipLaunchKernelGGL((attn_chunk_kernel<HD, PAGED>),
-                       dim3(a.nchunk, a.heads, static_cast<unsigned>(B)), dim3(AT_T), 0, st, a);
-  int rc = check_launch("decode_attention chunks");
-  if (rc) return rc;
+    hipLaunchKernelGGL((attn_chunk_kernel<HD, PAGED, NQ>),
+                       dim3(static_cast<unsigned>(c_count), a.heads, static_cast<unsigned>(groups)),
+                       dim3(AT_T), 0, st, b, c_first, c_count);
+}
+
+// Sequences per workgroup on the chunks every sequence shares.
+constexpr int AT_SHARED_NQ = 4;
+
+template <int HD, bool PAGED>
+static int launch_attn(AttnArgs a, int64_t B, int shared_chunks, hipStream_t st) {
+  a.B = static_cast<int>(B);
+  if constexpr (PAGED) {
+    if (shared_chunks > 0) {
+      launch_chunks<HD, true, AT_SHARED_NQ>(a, 0, shared_chunks, st);
+      int rc = check_launch("decode_attention shared chunks");
+      if (rc) return rc;
+    }
+  }
+  if (shared_chunks < a.nchunk) {
+    launch_chunks<HD, PAGED, 1>(a, shared_chunks, a.nchunk - shared_chunks, st);
+    int rc = check_launch("decode_attention chunks");
+    if (rc) return rc;
+  }
   hipLaunchKernelGGL(attn_merge_kernel<HD>, dim3(a.heads, static_cast<unsigned>(B)), dim3(HD), 0, st, a);
   return check_launch("decode_attention merge");
 }
@@ -278,24 +357,27 @@ extern "C" int evo2_decode_attention(const void *q, int64_t qb, int64_t qh,
              static_cast<bf16_t *>(out), ob, oh, scale, static_cast<int>(heads),
              static_cast<int>(L), static_cast<int>(cdiv(L, AT_CHUNK))};
   hipStream_t st = static_cast<hipStream_t>(stream);
-  return head_dim == 64 ? launch_attn<64, false>(a, B, st) : launch_attn<128, false>(a, B, st);
+  return head_dim == 64 ? launch_attn<64, false>(a, B, 0, st) : launch_attn<128, false>(a, B, 0, st);
 }
 
 extern "C" int evo2_paged_decode_attention(const void *q, int64_t qb, int64_t qh,
                                            const void *k_pages, int64_t kp, int64_t kh, int64_t kd,
                                            const void *v_pages, int64_t vp, int64_t vh, int64_t vl,
                                            int64_t num_pages, const int32_t *block_table,
-                                           int64_t tbs,
+                                           int64_t tbs, int64_t shared_pages,
                                            const int64_t *positions, float *workspace,
                                            int64_t workspace_bytes, void *out, int64_t ob,
                                            int64_t oh, int64_t B, int64_t heads,
                                            int64_t head_dim, int64_t max_pages, float scale,
                                            void *stream) {
   if (B < 0 || heads <= 0 || max_pages <= 0 || B > 65535 || heads > 65535 ||
-      max_pages > (int64_t(1) << 26) || num_pages <= 0)
+      max_pages > (int64_t(1) << 26) || num_pages <= 0 || shared_pages < 0 ||
+      shared_pages > max_pages)
     return fail(EVO2_ERR_INVALID,
-                "paged_decode_attention: bad sizes B=%lld heads=%lld pages=%lld num_pages=%lld",
-                (long long)B, (long long)heads, (long long)max_pages, (long long)num_pages);
+                "paged_decode_attention: bad sizes B=%lld heads=%lld pages=%lld num_pages=%lld "
+                "shared_pages=%lld",
+                (long long)B, (long long)heads, (long long)max_pages, (long long)num_pages,
+                (long long)shared_pages);
   if (head_dim != 64 && head_dim != 128)
     return fail(EVO2_ERR_UNSUPPORTED, "paged_decode_attention: head_dim %lld (64 or 128)",
                 (long long)head_dim);
@@ -315,5 +397,8 @@ extern "C" int evo2_paged_decode_attention(const void *q, int64_t qb, int64_t qh
              num_pages, positions, workspace, static_cast<bf16_t *>(out), ob, oh, scale,
              static_cast<int>(heads), static_cast<int>(L), static_cast<int>(cdiv(L, AT_CHUNK))};
   hipStream_t st = static_cast<hipStream_t>(stream);
-  return head_dim == 64 ? launch_attn<64, true>(a, B, st) : launch_attn<128, true>(a, B, st);
+  // chunks that lie wholly inside the shared prefix
+  const int shared_chunks = static_cast<int>(shared_pages * AT_PAGE / AT_CHUNK);
+  return head_dim == 64 ? launch_attn<64, true>(a, B, shared_chunks, st)
+                        : launch_attn<128, true>(a, B, shared_chunks, st);
 }

@@ -29,7 +29,8 @@ import torch
 from torch import nn
 
 from .attention import (PAGE, PagedKVCache, causal_prefill_attention, check_block_table,
-                        paged_decode_attention, workspace as attention_workspace)
+                        paged_decode_attention, shared_prefix_pages,
+                        workspace as attention_workspace)
 from .metadata import build_metadata
 from .mixers import Linear, load_mixer_params, make_mixer, set_forward_context
 from .norm import Evo2RMSNorm
@@ -83,6 +84,7 @@ class Evo2Attention(nn.Module):
         self.register_buffer("inv_freq", 1.0 / rope_theta ** (
             torch.arange(0, self.hd, 2, device=device, dtype=torch.float32) / self.hd))
         self.cache = PagedKVCache(num_pages, self.heads, self.hd, device)
+        self.shared_pages = 0  # leading block-table entries every sequence shares
         self._attn_ws = attention_workspace(max_batch, self.heads, self.hd, max_pages * PAGE,
                                             device)
 
@@ -99,7 +101,8 @@ class Evo2Attention(nn.Module):
         q, k, v = self._qkv(x, positions)
         self.cache.append(k, v.contiguous(), block_table, positions)
         out = paged_decode_attention(q.contiguous(), self.cache.k, self.cache.v, block_table,
-                                     positions, self.hd ** -0.5, self._attn_ws)  # (B, nh, hd)
+                                     positions, self.hd ** -0.5, self._attn_ws,
+                                     shared_pages=self.shared_pages)  # (B, nh, hd)
         o, _ = self.o_proj(out.reshape(B, self.heads * self.hd))
         return o
 
@@ -187,6 +190,9 @@ class Evo2DecodeModel(nn.Module):
         table[:, :sp] = perm[:sp].to(torch.int32)
         table[:, sp:] = perm[sp:].to(torch.int32).view(max_batch, own)
         check_block_table(table, [self.max_pages * PAGE] * max_batch, num_pages)
+        # the table's shared leading pages (the shared prompt's, whole pages of
+        # it when max_batch > 1), declared to the decode attention
+        shared_pages = min(sp, shared_prefix_pages(table, max_batch))
         self.block_table = table.to(device)
         self.shared_prefix = shared_prefix
         layers, self.pools = [], {}
@@ -194,6 +200,7 @@ class Evo2DecodeModel(nn.Module):
             if config.layer_kind(i) == "attn":
                 mixer = Evo2Attention(config, num_pages, self.max_pages, max_batch, rope_theta,
                                       rope_factor, device)
+                mixer.shared_pages = shared_pages
             else:
                 mixer = make_mixer(config, i, prefix=f"{name}.layers.{i}.mixer", device=device)
                 pool = HyenaStatePool(max_batch + 1, h, device)

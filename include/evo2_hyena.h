@@ -333,6 +333,12 @@ int evo2_decode_attention(const void *q, int64_t qb, int64_t qh,
  * max_pages * 16) bytes.  num_pages is the number of pages the cache holds:
  * a table entry outside [0, num_pages) is never read through; the positions
  * it names are left out of the softmax (zeros for a sequence left with none).
+ * shared_pages (0 <= shared_pages <= max_pages) declares that the first
+ * shared_pages entries of every row name the same pages (one prompt behind
+ * all B sequences): the chunks of 2048 positions inside that prefix then
+ * read each page once for four sequences.  The result does not depend on it
+ * (the same bits); a wrong declaration computes those chunks with row 0's
+ * pages for every sequence.
  *
  * Serves the attention layers of Evo2Attention at decode
  * (evo2_flash/model.py:104-153) over the paged cache layout the serving
@@ -342,6 +348,7 @@ int evo2_paged_decode_attention(const void *q, int64_t qb, int64_t qh,
                                 const void *k_pages, int64_t kp, int64_t kh, int64_t kd,
                                 const void *v_pages, int64_t vp, int64_t vh, int64_t vl,
                                 int64_t num_pages, const int32_t *block_table, int64_t tbs,
+                                int64_t shared_pages,
                                 const int64_t *positions, float *workspace,
                                 int64_t workspace_bytes, void *out, int64_t ob, int64_t oh,
                                 int64_t B, int64_t heads, int64_t head_dim, int64_t max_pages,

@@ -5,14 +5,15 @@ positions 0..positions[b].  Bar: max |out - ref| / max |ref| <= 1e-2 per case
 128; contexts of one and several 2048-position chunks; lengths ending inside a
 chunk, at a chunk edge and at the cache end; a batch slice of a larger cache
 (the harness's k_cache[:B]); the 7B attention shape (32 heads of 128) at the
-benchmark's context.
+benchmark's context; a prompt's pages shared by every sequence, with and
+without the sharing declared (bitwise the same).
 """
 
 import pytest
 import torch
 
 from evo2_flash_amd.attention import (PAGE, PagedKVCache, decode_attention,
-                                     paged_decode_attention, workspace)
+                                     paged_decode_attention, shared_prefix_pages, workspace)
 
 from _cases import max_rel_err
 
@@ -128,3 +129,43 @@ def test_paged_decode_attention_masks_entries_outside_the_cache():
     assert torch.isfinite(out.float()).all()
     assert torch.equal(out[3], torch.zeros(nh, hd, dtype=bf))
     assert max_rel_err(out[:3], ref[:3]) <= 1e-2
+
+
+@pytest.mark.parametrize("B", [6, 8])
+def test_paged_decode_attention_shared_prompt(B):
+    """Rows sharing their first pages (one prompt behind every sequence), one
+    shared entry masked, one sequence shorter than the shared prompt: with
+    the sharing declared, the chunks inside the prompt read each page once
+    for four sequences and the result is the same bits as without it, and
+    matches fp32 attention over the pages."""
+    g = torch.Generator().manual_seed(11 + B)
+    hd, nh, sp, own = 128, 4, 392, 24          # 392 shared pages: three whole chunks and a part
+    max_pages = sp + own
+    num_pages = sp + B * own + 1
+    perm = torch.randperm(num_pages - 1, generator=g) + 1
+    table = torch.empty(B, max_pages, dtype=torch.int32)
+    table[:, :sp] = perm[:sp].to(torch.int32)
+    table[:, sp:] = perm[sp:].to(torch.int32).view(B, own)
+    table[:, 70] = -1                           # masked for every sequence (inside chunk 0)
+    pos = [sp * PAGE + 5, max_pages * PAGE - 1, 5000, sp * PAGE + 300, 4095, 2047, 6300, 6271][:B]
+    cache = PagedKVCache(num_pages, nh, hd, "cpu")
+    cache.k.copy_((torch.randn(cache.k.shape, generator=g) * 0.5).to(bf))
+    cache.v.copy_((torch.randn(cache.v.shape, generator=g) * 0.5).to(bf))
+    q = torch.randn(B, nh, hd, generator=g).to(bf)
+    positions = torch.tensor(pos, dtype=torch.int64)
+    assert shared_prefix_pages(table, B) == sp
+    ref = torch.zeros(B, nh, hd)
+    for b in range(B):
+        keep = [l for l in range(pos[b] + 1) if int(table[b, l // PAGE]) >= 0]
+        pg = table[b, [l // PAGE for l in keep]].long()
+        off = torch.tensor([l % PAGE for l in keep])
+        k = cache.k[pg, :, :, off].float()
+        v = cache.v[pg, :, off, :].float()
+        s = torch.einsum("hd,nhd->hn", q[b].float(), k) * hd ** -0.5
+        ref[b] = torch.einsum("hn,nhd->hd", torch.softmax(s, dim=-1), v)
+    args = (q.to(DEV), cache.k.to(DEV), cache.v.to(DEV), table.to(DEV), positions.to(DEV), hd ** -0.5)
+    print(f"paged decode_attention shared prompt B={B}", flush=True)
+    plain = paged_decode_attention(*args).cpu()
+    shared = paged_decode_attention(*args, shared_pages=sp).cpu()
+    assert torch.equal(plain.view(torch.int16), shared.view(torch.int16))
+    assert max_rel_err(shared, ref) <= 1e-2

@@ -249,3 +249,15 @@ def test_check_block_table():
         check_block_table(table, [65, 16], 10)
     with pytest.raises(ValueError, match="cannot serve 3"):
         check_block_table(table, [16, 16, 16], 10)
+
+
+def test_shared_prefix_pages():
+    """The leading block-table entries that the first B rows share."""
+    from evo2_flash_amd.attention import shared_prefix_pages
+    table = torch.tensor([[7, 8, 9, 1, 2], [7, 8, 9, 3, 4], [7, 8, 5, 6, 0]], dtype=torch.int32)
+    assert shared_prefix_pages(table, 2) == 3
+    assert shared_prefix_pages(table, 3) == 2
+    assert shared_prefix_pages(table, 1) == 0
+    same = torch.tensor([[1, 2], [1, 2]], dtype=torch.int32)
+    assert shared_prefix_pages(same, 2) == 2
+    assert shared_prefix_pages(torch.tensor([[1, 2], [3, 2]], dtype=torch.int32), 2) == 0
