@@ -68,8 +68,9 @@ def paged_decode_attention(q, k_pages, v_pages, block_table, positions, scale, w
     softmax (check_block_table finds them on the host).  shared_pages: the
     first shared_pages entries of every row name the same pages (a prompt
     shared by all B sequences; shared_prefix_pages finds it on the host):
-    those chunks read each page once for several sequences, with the same
-    result bits."""
+    those chunks read each page once for several sequences (head_dim 128: up
+    to 32 on the matrix cores, the sums in another order, within a bf16
+    rounding step of the undeclared result; 64: four, the same bits)."""
     _lib.require_device(q, k_pages, v_pages, block_table, positions, work)
     B, heads, hd = q.shape
     max_pages = block_table.shape[1]

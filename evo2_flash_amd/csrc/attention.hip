@@ -31,9 +31,13 @@
 // once per pair and from L2 for the other sequences (32 sequences sharing a
 // 131072-position prompt: 23.0 -> 8.0 ms per layer; 64 sequences with pages
 // of their own: 1.70 -> 1.68 ms).  When the caller declares the shared
-// leading pages, the chunks inside them take four sequences per workgroup,
-// each key and value load serving all four (8.0 -> 5.4 ms per layer, the
-// same bits).
+// leading pages, the chunks inside them take 32 sequences per workgroup on
+// the matrix cores at head_dim 128 (below: 8.0 -> 0.84 ms per layer), and
+// four per workgroup on the VALU at head_dim 64 (each key and value load
+// serving all four, the same bits as one per workgroup).
+#include <type_traits>
+#include <utility>
+
 #include "common.h"
 
 namespace evo2 {
@@ -64,6 +68,32 @@ __device__ __forceinline__ int valid_len(const AttnArgs &p, int b) {
   return static_cast<int>(n < 0 ? 0 : (n > p.L ? p.L : n));
 }
 
+// The (chunk c, head h, first sequence b0) of this workgroup, false for the
+// padding of the pair-major grid.  Pair-major: (chunk, head) pair P and
+// sequence group j % G; the G workgroups of a pair run back to back on one
+// XCD (workgroup w runs on XCD w mod 8), so where sequences share pages (one
+// prompt behind many sequences) the pair's keys and values come from HBM
+// once and from that XCD's L2 for the rest.  Otherwise the grid is (chunk,
+// head, sequence group).
+__device__ __forceinline__ bool chunk_of(const AttnArgs &p, int nq, int c_first, int c_count, int &c,
+                                         int &h, int &b0) {
+  const int G = (p.B + nq - 1) / nq;  // sequence groups
+  if (p.pair_major) {
+    const int w = blockIdx.x;
+    const int j = w >> 3;
+    const int P = (j / G) * 8 + (w & 7);
+    if (P >= c_count * p.heads) return false;
+    b0 = (j % G) * nq;
+    c = c_first + P % c_count;
+    h = P / c_count;
+  } else {
+    c = c_first + blockIdx.x;
+    h = blockIdx.y;
+    b0 = blockIdx.z * nq;
+  }
+  return true;
+}
+
 // Chunks c_first .. c_first + c_count - 1 of NQ sequences b0 .. b0 + NQ - 1
 // (those below B) and one head per workgroup.  With NQ > 1 (paged cache only)
 // the sequences read the pages of row b0: the caller passes NQ > 1 only for
@@ -79,25 +109,8 @@ __global__ __launch_bounds__(AT_T) void attn_chunk_kernel(AttnArgs p, int c_firs
   __shared__ float red[NQ][AT_T / 64];
   __shared__ float osum[NQ][AT_T / 64][HD];
   __shared__ int32_t pages[PAGED ? AT_CHUNK / AT_PAGE : 1];
-  const int G = (p.B + NQ - 1) / NQ;  // sequence groups
   int c, h, b0;
-  if (p.pair_major) {
-    // (chunk, head) pair P and sequence group gi: the G workgroups of a pair
-    // run back to back on one XCD (workgroup w runs on XCD w mod 8), so where
-    // sequences share pages (one prompt behind many sequences) the pair's
-    // keys and values come from HBM once and from that XCD's L2 for the rest
-    const int w = blockIdx.x;
-    const int j = w >> 3;
-    const int P = (j / G) * 8 + (w & 7);
-    if (P >= c_count * p.heads) return;  // uniform: padding
-    b0 = (j % G) * NQ;
-    c = c_first + P % c_count;
-    h = P / c_count;
-  } else {
-    c = c_first + blockIdx.x;
-    h = blockIdx.y;
-    b0 = blockIdx.z * NQ;
-  }
+  if (!chunk_of(p, NQ, c_first, c_count, c, h, b0)) return;  // uniform: padding
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int l0 = c * AT_CHUNK;
   int l1[NQ];
@@ -259,6 +272,378 @@ __global__ __launch_bounds__(AT_T) void attn_chunk_kernel(AttnArgs p, int c_firs
   }
 }
 
+// Shared-prompt chunks on the matrix cores (head_dim 128): one workgroup per
+// (chunk, head) and 32 sequences, whose pages are those of row b0 (the
+// caller passes only chunks every sequence shares).  Each wave takes the
+// 128-position blocks w, w + 4, .. of the chunk with a running max and sum
+// (online softmax), on v_mfma_f32_16x16x32_bf16:
+//  * scores S^T = K Q^T: eight 16-row tiles, tile t row m = position 8 m + t
+//    of the block, so lane (m, g) loads 16 bytes (positions 8 m .. 8 m + 7)
+//    of one key dim at a time; eight such loads (dims 32 kk + 4 j + g, j =
+//    0..7: four neighbouring dims per page line) transposed in registers
+//    give the A operands of all eight tiles for k-step kk, and Q's B operand
+//    takes the same dims.  Lane (n, g) then holds the scores of positions
+//    32 g .. 32 g + 31 for sequences n and 16 + n;
+//  * o^T = V^T P^T: dim tile e row m = dim 8 m + e; lane (m, g) loads eight
+//    16-byte value rows (positions 32 g + 8 kp + j, dims 8 m .. + 7) and
+//    transposes them the same way; the B operand is the lane's own
+//    probabilities of those positions, split into bf16 high and low parts
+//    (~16 bits), so no lane exchanges data except for the max and sum.
+// Products of bf16 are exact and sums fp32, as in the one-sequence kernel;
+// the order of the sums differs, and the probabilities are exp2 of scores
+// kept in log2 units.  The four waves' (max, sum, o) meet in LDS for the
+// chunk's partials.
+// The key and value rows reach the lanes through a per-wave queue of
+// direct-to-LDS loads (four 8 KB groups in flight, no registers held), read
+// back with each lane's own 16 bytes, so the sweep streams while the matrix
+// cores and the softmax work.  Blocks that every sequence attends to in full
+// skip the masks.  At the 40B shape (32 sequences, 64 heads, a 131072-position
+// prompt: 4.3 GB of keys and values per layer) one launch takes ~0.84 ms, the
+// memory stream alone ~0.83; the four-sequence VALU kernel took 5.4 ms.
+constexpr int AS_NQ = 32;   // sequences per workgroup
+constexpr int AS_BLK = 128; // positions per wave block
+
+typedef __attribute__((ext_vector_type(8))) __bf16 abf16x8_t;
+typedef __attribute__((ext_vector_type(4))) float af32x4_t;
+typedef __attribute__((ext_vector_type(4))) unsigned int au32x4_t;
+typedef __attribute__((address_space(3))) void alds_void;
+
+// f(integral_constant<int, 0>) .. f(integral_constant<int, N - 1>): the
+// index is a constant expression inside f.
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_seq(F &f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F &&f) {
+  static_for_seq(f, std::make_integer_sequence<int, N>{});
+}
+
+// Eight 16-byte LDS reads at byte address a + 1024 j, then a wait for them.
+// Inline assembly: the compiler would otherwise wait for every direct-to-LDS
+// load in flight before any LDS read; the caller waits for the ones it reads.
+__device__ __forceinline__ void lds_read8(au32x4_t (&r)[8], uint32_t a) {
+  asm volatile(
+      "ds_read_b128 %0, %8\n"
+      "ds_read_b128 %1, %8 offset:1024\n"
+      "ds_read_b128 %2, %8 offset:2048\n"
+      "ds_read_b128 %3, %8 offset:3072\n"
+      "ds_read_b128 %4, %8 offset:4096\n"
+      "ds_read_b128 %5, %8 offset:5120\n"
+      "ds_read_b128 %6, %8 offset:6144\n"
+      "ds_read_b128 %7, %8 offset:7168\n"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6]),
+        "=&v"(r[7])
+      : "v"(a)
+      : "memory");
+}
+
+// Element t of the eight 16-byte rows r[0..7] (row j holds elements 0..7 in
+// order) as one operand: (r[0][t], .., r[7][t]).
+template <int T>
+__device__ __forceinline__ abf16x8_t column8(const au32x4_t (&r)[8]) {
+  au32x4_t o;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t a = r[2 * i][T / 2], b = r[2 * i + 1][T / 2];
+    o[i] = T & 1 ? __builtin_amdgcn_perm(b, a, 0x07060302u) : __builtin_amdgcn_perm(b, a, 0x05040100u);
+  }
+  return __builtin_bit_cast(abf16x8_t, o);
+}
+
+__global__ __launch_bounds__(AT_T, 1) void attn_shared_mfma_kernel(AttnArgs p, int c_count) {
+  constexpr int HD = 128;
+  constexpr int NW = AT_T / 64;
+  __shared__ int32_t pages[AT_CHUNK / AT_PAGE];
+  __shared__ float wm[NW][AS_NQ], wl[NW][AS_NQ];
+  __shared__ int whole[AT_CHUNK / AS_BLK];  // block needs no masks
+  // Per wave, four 8 KB slots of a load queue (one group of eight 1 KB
+  // direct-to-LDS loads each); after the sweep slots 0 and 1 hold the
+  // wave's o for sequences 0..15 and 16..31.  Separate arrays, so the
+  // compiler's wait for a slot's loads counts only that slot's.
+  __shared__ float ring0[NW][2048], ring1[NW][2048], ring2[NW][2048], ring3[NW][2048];
+  int c, h, b0;
+  if (!chunk_of(p, AS_NQ, 0, c_count, c, h, b0)) return;  // uniform: padding
+  const int t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int n = lane & 15, g = lane >> 4;
+  const int l0 = c * AT_CHUNK;
+  int l1max = l0;             // end of the positions any sequence of the group attends to
+  int l1min = l0 + AT_CHUNK;  // end of those every sequence attends to
+  for (int qi = 0; qi < AS_NQ && b0 + qi < p.B; ++qi) {
+    const int e = min(l0 + AT_CHUNK, valid_len(p, b0 + qi));
+    l1max = max(l1max, e);
+    l1min = min(l1min, e);
+  }
+  int l1[2];       // this lane's sequences b0 + n and b0 + 16 + n
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    const int b = b0 + 16 * nt + n;
+    l1[nt] = b < p.B ? min(l0 + AT_CHUNK, valid_len(p, b)) : l0;
+  }
+  float *const part0 = p.part + ((int64_t)b0 * p.heads + h) * p.nchunk * (HD + 2) + (int64_t)c * (HD + 2);
+  const int64_t qstride = (int64_t)p.heads * p.nchunk * (HD + 2);  // between sequences
+  if (l0 >= l1max) {  // uniform: an empty chunk contributes nothing
+    for (int i = t; i < AS_NQ * (HD + 2); i += AT_T) {
+      const int qi = i / (HD + 2), d = i - qi * (HD + 2);
+      if (b0 + qi < p.B) part0[qi * qstride + d] = d == HD ? -INFINITY : 0.0f;
+    }
+    return;
+  }
+  if (t < AT_CHUNK / AT_PAGE) {  // the chunk's pages below l1max; -1: masked
+    int32_t pg = -1;
+    if (l0 + AT_PAGE * t < l1max) {
+      pg = p.tbl[(int64_t)b0 * p.tbs + l0 / AT_PAGE + t];
+      if (pg < 0 || pg >= p.num_pages) pg = -1;
+    }
+    pages[t] = pg;
+    // a block whose pages are all in the cache and whose positions every
+    // sequence attends to needs no masks
+    const uint64_t bad = __ballot(pg < 0);
+    if ((t & 7) == 0) whole[t / 8] = ((bad >> (t & 56)) & 0xff) == 0 && l0 + AS_BLK * (t / 8 + 1) <= l1min;
+  }
+  // Q as the B operand of the score products: k-slot (g, j) of k-step kk is
+  // dim 32 kk + 4 j + g
+  abf16x8_t qop[HD / 32][2];
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    const int b = b0 + 16 * nt + n;
+    const bf16_t *qr = p.q + (int64_t)(b < p.B ? b : b0) * p.qb + (int64_t)h * p.qh + g;
+#pragma unroll
+    for (int kk = 0; kk < HD / 32; ++kk)
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        qop[kk][nt][j] = __builtin_bit_cast(__bf16, b < p.B ? qr[32 * kk + 4 * j] : bf16_t(0));
+  }
+  __syncthreads();
+
+  float mrun[2] = {-INFINITY, -INFINITY}, lrun[2] = {0.0f, 0.0f};
+  af32x4_t acc[8][2];  // o^T: dim tile e (dims 32 g + 8 i + e in lane (n, g)), sequence tile nt
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) acc[e][nt] = af32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  // The wave's key and value rows pass through its slots: group kk of a
+  // block (keys of k-step kk, then values of k-step kk) goes to slot kk, and
+  // a group is requested as soon as the group before it in that slot has
+  // been read, so four groups (32 KB) stay in flight.  Loads carry no
+  // per-lane branch: a masked page's lanes read page 0 (its keys meet masked
+  // scores only, its values are zeroed after the read).  Each page is read
+  // once per launch, so the loads carry the non-temporal hint (5% faster).
+  auto slot = [&](auto r) __attribute__((always_inline)) -> float * {
+    constexpr int R = decltype(r)::value;
+    return R == 0 ? ring0[wave] : R == 1 ? ring1[wave] : R == 2 ? ring2[wave] : ring3[wave];
+  };
+  // keys of k-step kk: lane (m, g) reads dims 32 kk + 4 j + g of positions
+  // 8 m .. 8 m + 7 of the block
+  auto kreq = [&](int blk, auto kk) __attribute__((always_inline)) {
+    const int kpg = pages[(AS_BLK / AT_PAGE) * blk + (n >> 1)];
+    const bf16_t *kr = p.k + (int64_t)max(kpg, 0) * p.kb + (int64_t)h * p.kh + 8 * (n & 1) +
+                       (int64_t)(32 * kk + g) * p.kd;
+    float *dst = slot(kk);
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      __builtin_amdgcn_global_load_lds(kr + (int64_t)(4 * j) * p.kd, (alds_void *)(dst + 256 * j), 16, 0, CPOL_NT);
+  };
+  // values of k-step kp: lane (m, g) reads dims 8 m .. 8 m + 7 of positions
+  // lb + 32 g + 8 kp + j (page pb + 2 g + kp / 2, row 8 (kp % 2) + j)
+  auto vreq = [&](int blk, auto kp) __attribute__((always_inline)) {
+    const int vpg = pages[(AS_BLK / AT_PAGE) * blk + 2 * g + kp / 2];
+    const bf16_t *vr = p.v + (int64_t)max(vpg, 0) * p.vb + (int64_t)h * p.vh +
+                       (int64_t)(8 * (kp & 1)) * p.vl + 8 * n;
+    float *dst = slot(kp);
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      __builtin_amdgcn_global_load_lds(vr + (int64_t)j * p.vl, (alds_void *)(dst + 256 * j), 16, 0, CPOL_NT);
+  };
+  // this lane's 16 bytes of each load of a slot's group, once no more than
+  // `after` groups requested later are in flight; the slot is then free for
+  // the next group (the reads have returned before it is requested)
+  auto take = [&](au32x4_t(&r)[8], auto sl, auto after) __attribute__((always_inline)) {
+    vmcnt_wait<8 * decltype(after)::value>();
+    lds_read8(r, static_cast<uint32_t>(reinterpret_cast<uintptr_t>(slot(sl) + 4 * lane)));
+  };
+  using std::integral_constant;
+  const int nblk = (l1max - l0 + AS_BLK - 1) / AS_BLK;  // blocks holding positions below l1max
+  if (wave < nblk) static_for<HD / 32>([&](auto kk) __attribute__((always_inline)) { kreq(wave, kk); });
+  // The running max is kept in log2 units of the scaled score, so each
+  // probability is one FMA and one v_exp_f32 (exp2).
+  const float c2 = p.scale * 1.4426950408889634f;
+  // One block of the sweep; MASK: some position of the block is masked for
+  // some sequence (a page outside the cache, or past a sequence's end).
+  auto block = [&](int blk, auto mask_c) __attribute__((always_inline)) {
+    constexpr bool MASK = decltype(mask_c)::value;
+    const int lb = l0 + AS_BLK * blk;
+    const int pb = (AS_BLK / AT_PAGE) * blk;  // the block's first page in the chunk
+    int vpg[4];
+    if constexpr (MASK) {
+#pragma unroll
+      for (int kp = 0; kp < 4; ++kp) vpg[kp] = pages[pb + 2 * g + kp / 2];
+    }
+    // scores
+    af32x4_t s[8][2];
+#pragma unroll
+    for (int tt = 0; tt < 8; ++tt)
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) s[tt][nt] = af32x4_t{0.f, 0.f, 0.f, 0.f};
+    static_for<HD / 32>([&](auto kk) __attribute__((always_inline)) {
+      au32x4_t kv[8];
+      // after keys kk: keys kk + 1 .. 3 and values 0 .. kk - 1
+      take(kv, kk, integral_constant<int, 3>{});
+      vreq(blk, kk);
+#define EVO2_SCORE_TILE(T)                                                              \
+  {                                                                                     \
+    const abf16x8_t a = column8<T>(kv);                                                 \
+    s[T][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qop[kk][0], s[T][0], 0, 0, 0); \
+    s[T][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qop[kk][1], s[T][1], 0, 0, 0); \
+  }
+      EVO2_SCORE_TILE(0) EVO2_SCORE_TILE(1) EVO2_SCORE_TILE(2) EVO2_SCORE_TILE(3)
+      EVO2_SCORE_TILE(4) EVO2_SCORE_TILE(5) EVO2_SCORE_TILE(6) EVO2_SCORE_TILE(7)
+#undef EVO2_SCORE_TILE
+    });
+    // s[tt][nt][i]: position lb + 32 g + 8 i + tt, sequence 16 nt + n; its
+    // page pb + 2 g + i / 2.  Scores become scale log2(e) q.k (-inf where
+    // masked), then probabilities exp2(score - running max).
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      float bm = -INFINITY;
+#pragma unroll
+      for (int tt = 0; tt < 8; ++tt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float v = s[tt][nt][i] * c2;
+          if constexpr (MASK) {
+            const int l = lb + 32 * g + 8 * i + tt;
+            v = vpg[i] >= 0 && l < l1[nt] ? v : -INFINITY;
+          }
+          s[tt][nt][i] = v;
+          bm = fmaxf(bm, v);
+        }
+      bm = fmaxf(bm, __shfl_xor(bm, 16));
+      bm = fmaxf(bm, __shfl_xor(bm, 32));
+      const float mn = fmaxf(mrun[nt], bm);
+      // while everything so far is masked, mn is -inf: subtract 0 instead
+      // (every probability is then exp2(-inf) = 0)
+      const float msub = mn == -INFINITY ? 0.0f : mn;
+      const float alpha = __builtin_amdgcn_exp2f(mrun[nt] - msub);  // 0 while nothing came before
+      float ls = 0.0f;
+#pragma unroll
+      for (int tt = 0; tt < 8; ++tt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float pe = __builtin_amdgcn_exp2f(s[tt][nt][i] - msub);
+          s[tt][nt][i] = pe;
+          ls += pe;
+        }
+      lrun[nt] = fmaf(lrun[nt], alpha, ls);  // this lane's positions only
+      mrun[nt] = mn;
+      if (__any(alpha != 1.0f)) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e][nt] *= alpha;
+      }
+    }
+    // o^T += V^T P^T over k-steps kp: k-slot (g, j) is position lb + 32 g + 8 kp + j
+    const bool more = blk + NW < nblk;  // uniform
+    static_for<4>([&](auto kp) __attribute__((always_inline)) {
+      constexpr int KP = decltype(kp)::value;
+      au32x4_t vv[8];
+      // after values kp: values kp + 1 .. 3 and, with a next block, its keys 0 .. kp - 1
+      if (more) {
+        take(vv, kp, integral_constant<int, 3>{});
+        kreq(blk + NW, kp);
+      } else {
+        take(vv, kp, integral_constant<int, 3 - KP>{});
+      }
+      if constexpr (MASK) {
+        const int lv = lb + 32 * g + 8 * KP;
+#pragma unroll
+        for (int j = 0; j < 8; ++j)  // masked pages and positions at or past l1max: zero
+          if (vpg[KP] < 0 || lv + j >= l1max) vv[j] = au32x4_t{0u, 0u, 0u, 0u};
+      }
+      // probabilities as bf16 high and low parts (k-slot j = tile j's element KP)
+      au32x4_t phu[2], plu[2];
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const float a = s[2 * jj][nt][KP], b = s[2 * jj + 1][nt][KP];
+          const uint32_t hi = pack_bf(a, b);
+          phu[nt][jj] = hi;
+          plu[nt][jj] = pack_bf(a - lo_bf(hi), b - hi_bf(hi));
+        }
+      abf16x8_t ph[2], pl[2];
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        ph[nt] = __builtin_bit_cast(abf16x8_t, phu[nt]);
+        pl[nt] = __builtin_bit_cast(abf16x8_t, plu[nt]);
+      }
+#define EVO2_VALUE_TILE(E)                                                                  \
+  {                                                                                         \
+    const abf16x8_t a = column8<E>(vv);                                                     \
+    acc[E][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, ph[0], acc[E][0], 0, 0, 0);      \
+    acc[E][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pl[0], acc[E][0], 0, 0, 0);      \
+    acc[E][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, ph[1], acc[E][1], 0, 0, 0);      \
+    acc[E][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pl[1], acc[E][1], 0, 0, 0);      \
+  }
+      EVO2_VALUE_TILE(0) EVO2_VALUE_TILE(1) EVO2_VALUE_TILE(2) EVO2_VALUE_TILE(3)
+      EVO2_VALUE_TILE(4) EVO2_VALUE_TILE(5) EVO2_VALUE_TILE(6) EVO2_VALUE_TILE(7)
+#undef EVO2_VALUE_TILE
+    });
+  };
+  for (int blk = wave; blk < nblk; blk += NW) {
+    if (whole[blk]) block(blk, std::false_type{});  // uniform
+    else block(blk, std::true_type{});
+  }
+
+  // the waves' partials into LDS (o in the wave's slots 0 and 1, whose
+  // loads have all been read), then the chunk's (o, max, sum) per sequence
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    float l = lrun[nt];
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    if (g == 0) {
+      wm[wave][16 * nt + n] = mrun[nt] * 0.6931471805599453f;  // log2 units -> natural
+      wl[wave][16 * nt + n] = l;
+    }
+    float *wo = nt == 0 ? ring0[wave] : ring1[wave];  // (sequence n, dim) rows of HD
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) wo[n * HD + 32 * g + 8 * i + e] = acc[e][nt][i];
+  }
+  __syncthreads();
+  {
+    constexpr int TPQ = AT_T / AS_NQ;  // threads per sequence
+    constexpr int DPT = HD / TPQ;      // dims per thread
+    const int qi = t / TPQ, d0 = (t % TPQ) * DPT;
+    if (b0 + qi < p.B) {
+      float M = wm[0][qi];
+#pragma unroll
+      for (int w = 1; w < NW; ++w) M = fmaxf(M, wm[w][qi]);
+      float f[NW];
+#pragma unroll
+      for (int w = 0; w < NW; ++w) f[w] = wm[w][qi] == -INFINITY ? 0.0f : expf(wm[w][qi] - M);
+      float *part = part0 + qi * qstride;
+#pragma unroll
+      for (int d = 0; d < DPT; ++d) {
+        float o = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) o = fmaf(f[w], (qi < 16 ? ring0[w] : ring1[w])[(qi & 15) * HD + d0 + d], o);
+        part[d0 + d] = o;
+      }
+      if (t % TPQ == 0) {
+        float tot = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) tot = fmaf(f[w], wl[w][qi], tot);
+        part[HD] = M;
+        part[HD + 1] = tot;
+      }
+    }
+  }
+}
+
 // Merge the chunks of (sequence b, head h): lane d of HD.
 template <int HD>
 __global__ __launch_bounds__(HD) void attn_merge_kernel(AttnArgs p) {
@@ -298,7 +683,8 @@ static void launch_chunks(const AttnArgs &a, int c_first, int c_count, hipStream
                        dim3(AT_T), 0, st, b, c_first, c_count);
 }
 
-// Sequences per workgroup on the chunks every sequence shares.
+// Sequences per workgroup of the one-load-many-queries VALU kernel on the
+// chunks every sequence shares (head_dim 64; 128 takes the matrix cores).
 constexpr int AT_SHARED_NQ = 4;
 
 template <int HD, bool PAGED>
@@ -306,7 +692,21 @@ static int launch_attn(AttnArgs a, int64_t B, int shared_chunks, hipStream_t st)
   a.B = static_cast<int>(B);
   if constexpr (PAGED) {
     if (shared_chunks > 0) {
-      launch_chunks<HD, true, AT_SHARED_NQ>(a, 0, shared_chunks, st);
+      if constexpr (HD == 128) {
+        const int64_t wgs = cdiv(static_cast<int64_t>(shared_chunks) * a.heads, 8) * 8 * cdiv(B, AS_NQ);
+        AttnArgs b = a;
+        b.pair_major = wgs <= 0x7fffffff;
+        if (b.pair_major)
+          hipLaunchKernelGGL(attn_shared_mfma_kernel, dim3(static_cast<unsigned>(wgs)), dim3(AT_T), 0, st, b,
+                             shared_chunks);
+        else
+          hipLaunchKernelGGL(attn_shared_mfma_kernel,
+                             dim3(static_cast<unsigned>(shared_chunks), a.heads,
+                                  static_cast<unsigned>(cdiv(B, AS_NQ))),
+                             dim3(AT_T), 0, st, b, shared_chunks);
+      } else {
+        launch_chunks<HD, true, AT_SHARED_NQ>(a, 0, shared_chunks, st);
+      }
       int rc = check_launch("decode_attention shared chunks");
       if (rc) return rc;
     }

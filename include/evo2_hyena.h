@@ -336,9 +336,10 @@ int evo2_decode_attention(const void *q, int64_t qb, int64_t qh,
  * shared_pages (0 <= shared_pages <= max_pages) declares that the first
  * shared_pages entries of every row name the same pages (one prompt behind
  * all B sequences): the chunks of 2048 positions inside that prefix then
- * read each page once for four sequences.  The result does not depend on it
- * (the same bits); a wrong declaration computes those chunks with row 0's
- * pages for every sequence.
+ * read each page once for up to 32 sequences (head_dim 128, on the matrix
+ * cores: the sums in another order, within a bf16 rounding step of the
+ * undeclared result) or four (head_dim 64, the same bits).  A wrong
+ * declaration computes those chunks with row 0's pages for every sequence.
  *
  * Serves the attention layers of Evo2Attention at decode
  * (evo2_flash/model.py:104-153) over the paged cache layout the serving
