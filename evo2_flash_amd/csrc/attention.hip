@@ -18,23 +18,25 @@
 // it would hold are left out of the softmax (a sequence with none left gets
 // zeros), so a stale or garbage entry gives a wrong row, not a fault.
 //
-// Split over the context (flash decoding): workgroup (c, h, b) takes the
-// 2048 positions of chunk c, computes its scores with 16-byte loads of eight
-// consecutive positions per lane (q in LDS), the chunk's max and exp-sum with
-// a block reduction, then sum_l p_l v_l with 16-byte loads of eight dims per
-// lane, and writes (o, max, sum) to a workspace; a second launch merges the
-// chunks of each (sequence, head).  Keys and values are each read once
-// (6.2 TB/s at 64 sequences x 32 heads x 8704 positions); everything is fp32
-// until the bf16 output.  The workgroups of one (chunk, head) pair are
-// dispatched back to back on one XCD: where the block table points many
-// sequences at the same pages (a shared prompt), those pages stream from HBM
-// once per pair and from L2 for the other sequences (32 sequences sharing a
-// 131072-position prompt: 23.0 -> 8.0 ms per layer; 64 sequences with pages
-// of their own: 1.70 -> 1.68 ms).  When the caller declares the shared
-// leading pages, the chunks inside them take 32 sequences per workgroup on
-// the matrix cores at head_dim 128 (below: 8.0 -> 0.84 ms per layer), and
-// four per workgroup on the VALU at head_dim 64 (each key and value load
-// serving all four, the same bits as one per workgroup).
+// Split over the context (flash decoding): a workgroup takes the 2048
+// positions of one chunk c for head h and writes (o, max, sum) to a
+// workspace; a second launch merges the chunks of each (sequence, head).
+// Keys and values are each read once; everything is fp32 until the bf16
+// output.  Two chunk kernels:
+//  * the VALU kernel (contiguous cache, and paged at head_dim 64): workgroup
+//    (c, h, b) computes its scores with 16-byte loads of eight consecutive
+//    positions per lane (q in LDS), the chunk's max and exp-sum with a block
+//    reduction, then sum_l p_l v_l with 16-byte loads of eight dims per lane
+//    (6.2 TB/s at 64 sequences x 32 heads x 8704 positions, contiguous);
+//  * the matrix-core kernel (paged, head_dim 128; below): one sequence per
+//    workgroup, or 32 on chunks whose pages the caller declares shared by
+//    every sequence (a prompt behind all of them), each key and value byte
+//    then read once for all 32.
+// The workgroups of one (chunk, head) pair are dispatched back to back on
+// one XCD, so pages that several workgroups of a pair read stream from HBM
+// once per pair and from L2 for the rest.  At head_dim 64 declared shared
+// chunks take four sequences per VALU workgroup, each load serving all four
+// (the same bits as one per workgroup).
 #include <type_traits>
 #include <utility>
 
@@ -272,34 +274,41 @@ __global__ __launch_bounds__(AT_T) void attn_chunk_kernel(AttnArgs p, int c_firs
   }
 }
 
-// Shared-prompt chunks on the matrix cores (head_dim 128): one workgroup per
-// (chunk, head) and 32 sequences, whose pages are those of row b0 (the
-// caller passes only chunks every sequence shares).  Each wave takes the
-// 128-position blocks w, w + 4, .. of the chunk with a running max and sum
-// (online softmax), on v_mfma_f32_16x16x32_bf16:
+// Paged chunks on the matrix cores (head_dim 128): one workgroup per (chunk,
+// head) and group of gq sequences whose pages are those of row b0: 32
+// sequences in two 16-sequence tiles for chunks every sequence shares (the
+// caller passes only such chunks), one sequence in one tile for the rest
+// (fifteen idle query slots: the launch is bound by its loads, not by the
+// matrix cores).  Each wave takes the 128-position blocks w, w + 4, .. of the
+// chunk with a running max and sum (online softmax), on
+// v_mfma_f32_16x16x32_bf16:
 //  * scores S^T = K Q^T: eight 16-row tiles, tile t row m = position 8 m + t
 //    of the block, so lane (m, g) loads 16 bytes (positions 8 m .. 8 m + 7)
 //    of one key dim at a time; eight such loads (dims 32 kk + 4 j + g, j =
 //    0..7: four neighbouring dims per page line) transposed in registers
 //    give the A operands of all eight tiles for k-step kk, and Q's B operand
 //    takes the same dims.  Lane (n, g) then holds the scores of positions
-//    32 g .. 32 g + 31 for sequences n and 16 + n;
+//    32 g .. 32 g + 31 for query slots n and 16 + n;
 //  * o^T = V^T P^T: dim tile e row m = dim 8 m + e; lane (m, g) loads eight
 //    16-byte value rows (positions 32 g + 8 kp + j, dims 8 m .. + 7) and
 //    transposes them the same way; the B operand is the lane's own
 //    probabilities of those positions, split into bf16 high and low parts
 //    (~16 bits), so no lane exchanges data except for the max and sum.
-// Products of bf16 are exact and sums fp32, as in the one-sequence kernel;
-// the order of the sums differs, and the probabilities are exp2 of scores
-// kept in log2 units.  The four waves' (max, sum, o) meet in LDS for the
-// chunk's partials.
+// Products of bf16 are exact and sums fp32, as in the VALU kernel; the order
+// of the sums differs, and the probabilities are exp2 of scores kept in log2
+// units.  The four waves' (max, sum, o) meet in LDS for the chunk's partials.
 // The key and value rows reach the lanes through a per-wave queue of
 // direct-to-LDS loads (four 8 KB groups in flight, no registers held), read
 // back with each lane's own 16 bytes, so the sweep streams while the matrix
 // cores and the softmax work.  Blocks that every sequence attends to in full
-// skip the masks.  At the 40B shape (32 sequences, 64 heads, a 131072-position
-// prompt: 4.3 GB of keys and values per layer) one launch takes ~0.84 ms, the
-// memory stream alone ~0.83; the four-sequence VALU kernel took 5.4 ms.
+// skip the masks.  Measured on one MI355X: the 40B shape's shared prompt (32
+// sequences, 64 heads, 131072 positions: 4.3 GB of keys and values per layer)
+// ~0.86 ms per launch (the four-sequence VALU kernel 5.4 ms); 64 sequences of
+// 32 heads with 8700 positions of their own (8.6 GB) 1.36 ms against 1.66 ms
+// on the VALU kernel (6.7 TB/s).  Pages that many sequences share without
+// the caller declaring them stream from L2 once per sequence and cost the
+// one-tile form its arithmetic: 32 sequences on one 131072-position prompt
+// take 10.6 ms there against 7.9 ms on the VALU kernel.
 constexpr int AS_NQ = 32;   // sequences per workgroup
 constexpr int AS_BLK = 128; // positions per wave block
 
@@ -352,7 +361,9 @@ __device__ __forceinline__ abf16x8_t column8(const au32x4_t (&r)[8]) {
   return __builtin_bit_cast(abf16x8_t, o);
 }
 
-__global__ __launch_bounds__(AT_T, 1) void attn_shared_mfma_kernel(AttnArgs p, int c_count) {
+template <int CPOL, int NQT>
+__global__ __launch_bounds__(AT_T, 1) void attn_mfma_kernel(AttnArgs p, int c_first, int c_count, int gq) {
+  static_assert(NQT == 1 || NQT == 2, "one or two 16-sequence tiles");
   constexpr int HD = 128;
   constexpr int NW = AT_T / 64;
   __shared__ int32_t pages[AT_CHUNK / AT_PAGE];
@@ -364,29 +375,28 @@ __global__ __launch_bounds__(AT_T, 1) void attn_shared_mfma_kernel(AttnArgs p, i
   // compiler's wait for a slot's loads counts only that slot's.
   __shared__ float ring0[NW][2048], ring1[NW][2048], ring2[NW][2048], ring3[NW][2048];
   int c, h, b0;
-  if (!chunk_of(p, AS_NQ, 0, c_count, c, h, b0)) return;  // uniform: padding
+  if (!chunk_of(p, gq, c_first, c_count, c, h, b0)) return;  // uniform: padding
+  // query slot qi holds sequence b0 + qi if qi < gq and b0 + qi < B
+  auto live = [&](int qi) { return qi < gq && b0 + qi < p.B; };
   const int t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int n = lane & 15, g = lane >> 4;
   const int l0 = c * AT_CHUNK;
   int l1max = l0;             // end of the positions any sequence of the group attends to
   int l1min = l0 + AT_CHUNK;  // end of those every sequence attends to
-  for (int qi = 0; qi < AS_NQ && b0 + qi < p.B; ++qi) {
+  for (int qi = 0; live(qi); ++qi) {
     const int e = min(l0 + AT_CHUNK, valid_len(p, b0 + qi));
     l1max = max(l1max, e);
     l1min = min(l1min, e);
   }
-  int l1[2];       // this lane's sequences b0 + n and b0 + 16 + n
+  int l1[NQT];     // this lane's query slots n and 16 + n
 #pragma unroll
-  for (int nt = 0; nt < 2; ++nt) {
-    const int b = b0 + 16 * nt + n;
-    l1[nt] = b < p.B ? min(l0 + AT_CHUNK, valid_len(p, b)) : l0;
-  }
+  for (int nt = 0; nt < NQT; ++nt) l1[nt] = live(16 * nt + n) ? min(l0 + AT_CHUNK, valid_len(p, b0 + 16 * nt + n)) : l0;
   float *const part0 = p.part + ((int64_t)b0 * p.heads + h) * p.nchunk * (HD + 2) + (int64_t)c * (HD + 2);
   const int64_t qstride = (int64_t)p.heads * p.nchunk * (HD + 2);  // between sequences
   if (l0 >= l1max) {  // uniform: an empty chunk contributes nothing
-    for (int i = t; i < AS_NQ * (HD + 2); i += AT_T) {
+    for (int i = t; i < 16 * NQT * (HD + 2); i += AT_T) {
       const int qi = i / (HD + 2), d = i - qi * (HD + 2);
-      if (b0 + qi < p.B) part0[qi * qstride + d] = d == HD ? -INFINITY : 0.0f;
+      if (live(qi)) part0[qi * qstride + d] = d == HD ? -INFINITY : 0.0f;
     }
     return;
   }
@@ -404,25 +414,30 @@ __global__ __launch_bounds__(AT_T, 1) void attn_shared_mfma_kernel(AttnArgs p, i
   }
   // Q as the B operand of the score products: k-slot (g, j) of k-step kk is
   // dim 32 kk + 4 j + g
-  abf16x8_t qop[HD / 32][2];
+  abf16x8_t qop[HD / 32][NQT];
 #pragma unroll
-  for (int nt = 0; nt < 2; ++nt) {
-    const int b = b0 + 16 * nt + n;
-    const bf16_t *qr = p.q + (int64_t)(b < p.B ? b : b0) * p.qb + (int64_t)h * p.qh + g;
+  for (int nt = 0; nt < NQT; ++nt) {
+    const bool ok = live(16 * nt + n);
+    const bf16_t *qr = p.q + (int64_t)(ok ? b0 + 16 * nt + n : b0) * p.qb + (int64_t)h * p.qh + g;
 #pragma unroll
     for (int kk = 0; kk < HD / 32; ++kk)
 #pragma unroll
       for (int j = 0; j < 8; ++j)
-        qop[kk][nt][j] = __builtin_bit_cast(__bf16, b < p.B ? qr[32 * kk + 4 * j] : bf16_t(0));
+        qop[kk][nt][j] = __builtin_bit_cast(__bf16, ok ? qr[32 * kk + 4 * j] : bf16_t(0));
   }
   __syncthreads();
 
-  float mrun[2] = {-INFINITY, -INFINITY}, lrun[2] = {0.0f, 0.0f};
-  af32x4_t acc[8][2];  // o^T: dim tile e (dims 32 g + 8 i + e in lane (n, g)), sequence tile nt
+  float mrun[NQT], lrun[NQT];
+  af32x4_t acc[8][NQT];  // o^T: dim tile e (dims 32 g + 8 i + e in lane (n, g)), sequence tile nt
+#pragma unroll
+  for (int nt = 0; nt < NQT; ++nt) {
+    mrun[nt] = -INFINITY;
+    lrun[nt] = 0.0f;
+  }
 #pragma unroll
   for (int e = 0; e < 8; ++e)
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) acc[e][nt] = af32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int nt = 0; nt < NQT; ++nt) acc[e][nt] = af32x4_t{0.f, 0.f, 0.f, 0.f};
 
   // The wave's key and value rows pass through its slots: group kk of a
   // block (keys of k-step kk, then values of k-step kk) goes to slot kk, and
@@ -444,7 +459,7 @@ __global__ __launch_bounds__(AT_T, 1) void attn_shared_mfma_kernel(AttnArgs p, i
     float *dst = slot(kk);
 #pragma unroll
     for (int j = 0; j < 8; ++j)
-      __builtin_amdgcn_global_load_lds(kr + (int64_t)(4 * j) * p.kd, (alds_void *)(dst + 256 * j), 16, 0, CPOL_NT);
+      __builtin_amdgcn_global_load_lds(kr + (int64_t)(4 * j) * p.kd, (alds_void *)(dst + 256 * j), 16, 0, CPOL);
   };
   // values of k-step kp: lane (m, g) reads dims 8 m .. 8 m + 7 of positions
   // lb + 32 g + 8 kp + j (page pb + 2 g + kp / 2, row 8 (kp % 2) + j)
@@ -455,7 +470,7 @@ __global__ __launch_bounds__(AT_T, 1) void attn_shared_mfma_kernel(AttnArgs p, i
     float *dst = slot(kp);
 #pragma unroll
     for (int j = 0; j < 8; ++j)
-      __builtin_amdgcn_global_load_lds(vr + (int64_t)j * p.vl, (alds_void *)(dst + 256 * j), 16, 0, CPOL_NT);
+      __builtin_amdgcn_global_load_lds(vr + (int64_t)j * p.vl, (alds_void *)(dst + 256 * j), 16, 0, CPOL);
   };
   // this lane's 16 bytes of each load of a slot's group, once no more than
   // `after` groups requested later are in flight; the slot is then free for
@@ -482,21 +497,21 @@ __global__ __launch_bounds__(AT_T, 1) void attn_shared_mfma_kernel(AttnArgs p, i
       for (int kp = 0; kp < 4; ++kp) vpg[kp] = pages[pb + 2 * g + kp / 2];
     }
     // scores
-    af32x4_t s[8][2];
+    af32x4_t s[8][NQT];
 #pragma unroll
     for (int tt = 0; tt < 8; ++tt)
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt) s[tt][nt] = af32x4_t{0.f, 0.f, 0.f, 0.f};
+      for (int nt = 0; nt < NQT; ++nt) s[tt][nt] = af32x4_t{0.f, 0.f, 0.f, 0.f};
     static_for<HD / 32>([&](auto kk) __attribute__((always_inline)) {
       au32x4_t kv[8];
       // after keys kk: keys kk + 1 .. 3 and values 0 .. kk - 1
       take(kv, kk, integral_constant<int, 3>{});
       vreq(blk, kk);
-#define EVO2_SCORE_TILE(T)                                                              \
-  {                                                                                     \
-    const abf16x8_t a = column8<T>(kv);                                                 \
-    s[T][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qop[kk][0], s[T][0], 0, 0, 0); \
-    s[T][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qop[kk][1], s[T][1], 0, 0, 0); \
+#define EVO2_SCORE_TILE(T)                                                                  \
+  {                                                                                         \
+    const abf16x8_t a = column8<T>(kv);                                                     \
+    for (int nt = 0; nt < NQT; ++nt)                                                        \
+      s[T][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qop[kk][nt], s[T][nt], 0, 0, 0); \
   }
       EVO2_SCORE_TILE(0) EVO2_SCORE_TILE(1) EVO2_SCORE_TILE(2) EVO2_SCORE_TILE(3)
       EVO2_SCORE_TILE(4) EVO2_SCORE_TILE(5) EVO2_SCORE_TILE(6) EVO2_SCORE_TILE(7)
@@ -506,7 +521,7 @@ __global__ __launch_bounds__(AT_T, 1) void attn_shared_mfma_kernel(AttnArgs p, i
     // page pb + 2 g + i / 2.  Scores become scale log2(e) q.k (-inf where
     // masked), then probabilities exp2(score - running max).
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
+    for (int nt = 0; nt < NQT; ++nt) {
       float bm = -INFINITY;
 #pragma unroll
       for (int tt = 0; tt < 8; ++tt)
@@ -562,9 +577,9 @@ __global__ __launch_bounds__(AT_T, 1) void attn_shared_mfma_kernel(AttnArgs p, i
           if (vpg[KP] < 0 || lv + j >= l1max) vv[j] = au32x4_t{0u, 0u, 0u, 0u};
       }
       // probabilities as bf16 high and low parts (k-slot j = tile j's element KP)
-      au32x4_t phu[2], plu[2];
+      au32x4_t phu[NQT], plu[NQT];
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt)
+      for (int nt = 0; nt < NQT; ++nt)
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
           const float a = s[2 * jj][nt][KP], b = s[2 * jj + 1][nt][KP];
@@ -572,19 +587,19 @@ __global__ __launch_bounds__(AT_T, 1) void attn_shared_mfma_kernel(AttnArgs p, i
           phu[nt][jj] = hi;
           plu[nt][jj] = pack_bf(a - lo_bf(hi), b - hi_bf(hi));
         }
-      abf16x8_t ph[2], pl[2];
+      abf16x8_t ph[NQT], pl[NQT];
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
+      for (int nt = 0; nt < NQT; ++nt) {
         ph[nt] = __builtin_bit_cast(abf16x8_t, phu[nt]);
         pl[nt] = __builtin_bit_cast(abf16x8_t, plu[nt]);
       }
 #define EVO2_VALUE_TILE(E)                                                                  \
   {                                                                                         \
     const abf16x8_t a = column8<E>(vv);                                                     \
-    acc[E][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, ph[0], acc[E][0], 0, 0, 0);      \
-    acc[E][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pl[0], acc[E][0], 0, 0, 0);      \
-    acc[E][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, ph[1], acc[E][1], 0, 0, 0);      \
-    acc[E][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pl[1], acc[E][1], 0, 0, 0);      \
+    for (int nt = 0; nt < NQT; ++nt) {                                                      \
+      acc[E][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, ph[nt], acc[E][nt], 0, 0, 0); \
+      acc[E][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pl[nt], acc[E][nt], 0, 0, 0); \
+    }                                                                                       \
   }
       EVO2_VALUE_TILE(0) EVO2_VALUE_TILE(1) EVO2_VALUE_TILE(2) EVO2_VALUE_TILE(3)
       EVO2_VALUE_TILE(4) EVO2_VALUE_TILE(5) EVO2_VALUE_TILE(6) EVO2_VALUE_TILE(7)
@@ -599,7 +614,7 @@ __global__ __launch_bounds__(AT_T, 1) void attn_shared_mfma_kernel(AttnArgs p, i
   // the waves' partials into LDS (o in the wave's slots 0 and 1, whose
   // loads have all been read), then the chunk's (o, max, sum) per sequence
 #pragma unroll
-  for (int nt = 0; nt < 2; ++nt) {
+  for (int nt = 0; nt < NQT; ++nt) {
     float l = lrun[nt];
     l += __shfl_xor(l, 16);
     l += __shfl_xor(l, 32);
@@ -615,10 +630,10 @@ __global__ __launch_bounds__(AT_T, 1) void attn_shared_mfma_kernel(AttnArgs p, i
   }
   __syncthreads();
   {
-    constexpr int TPQ = AT_T / AS_NQ;  // threads per sequence
+    constexpr int TPQ = AT_T / (16 * NQT);  // threads per sequence
     constexpr int DPT = HD / TPQ;      // dims per thread
     const int qi = t / TPQ, d0 = (t % TPQ) * DPT;
-    if (b0 + qi < p.B) {
+    if (live(qi)) {
       float M = wm[0][qi];
 #pragma unroll
       for (int w = 1; w < NW; ++w) M = fmaxf(M, wm[w][qi]);
@@ -683,6 +698,23 @@ static void launch_chunks(const AttnArgs &a, int c_first, int c_count, hipStream
                        dim3(AT_T), 0, st, b, c_first, c_count);
 }
 
+// Chunks [c_first, c_first + c_count) on the matrix-core kernel, gq sequences
+// per workgroup.
+template <int CPOL, int NQT>
+static void launch_mfma(const AttnArgs &a, int c_first, int c_count, int gq, hipStream_t st) {
+  const int64_t groups = cdiv(static_cast<int64_t>(a.B), gq);
+  const int64_t wgs = cdiv(static_cast<int64_t>(c_count) * a.heads, 8) * 8 * groups;
+  AttnArgs b = a;
+  b.pair_major = wgs <= 0x7fffffff;
+  if (b.pair_major)
+    hipLaunchKernelGGL((attn_mfma_kernel<CPOL, NQT>), dim3(static_cast<unsigned>(wgs)), dim3(AT_T), 0, st, b, c_first, c_count,
+                       gq);
+  else
+    hipLaunchKernelGGL((attn_mfma_kernel<CPOL, NQT>),
+                       dim3(static_cast<unsigned>(c_count), a.heads, static_cast<unsigned>(groups)), dim3(AT_T),
+                       0, st, b, c_first, c_count, gq);
+}
+
 // Sequences per workgroup of the one-load-many-queries VALU kernel on the
 // chunks every sequence shares (head_dim 64; 128 takes the matrix cores).
 constexpr int AT_SHARED_NQ = 4;
@@ -693,17 +725,7 @@ static int launch_attn(AttnArgs a, int64_t B, int shared_chunks, hipStream_t st)
   if constexpr (PAGED) {
     if (shared_chunks > 0) {
       if constexpr (HD == 128) {
-        const int64_t wgs = cdiv(static_cast<int64_t>(shared_chunks) * a.heads, 8) * 8 * cdiv(B, AS_NQ);
-        AttnArgs b = a;
-        b.pair_major = wgs <= 0x7fffffff;
-        if (b.pair_major)
-          hipLaunchKernelGGL(attn_shared_mfma_kernel, dim3(static_cast<unsigned>(wgs)), dim3(AT_T), 0, st, b,
-                             shared_chunks);
-        else
-          hipLaunchKernelGGL(attn_shared_mfma_kernel,
-                             dim3(static_cast<unsigned>(shared_chunks), a.heads,
-                                  static_cast<unsigned>(cdiv(B, AS_NQ))),
-                             dim3(AT_T), 0, st, b, shared_chunks);
+        launch_mfma<CPOL_NT, 2>(a, 0, shared_chunks, AS_NQ, st);
       } else {
         launch_chunks<HD, true, AT_SHARED_NQ>(a, 0, shared_chunks, st);
       }
@@ -712,7 +734,10 @@ static int launch_attn(AttnArgs a, int64_t B, int shared_chunks, hipStream_t st)
     }
   }
   if (shared_chunks < a.nchunk) {
-    launch_chunks<HD, PAGED, 1>(a, shared_chunks, a.nchunk - shared_chunks, st);
+    if constexpr (PAGED && HD == 128)
+      launch_mfma<CPOL_NT, 1>(a, shared_chunks, a.nchunk - shared_chunks, 1, st);
+    else
+      launch_chunks<HD, PAGED, 1>(a, shared_chunks, a.nchunk - shared_chunks, st);
     int rc = check_launch("decode_attention chunks");
     if (rc) return rc;
   }

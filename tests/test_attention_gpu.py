@@ -94,12 +94,14 @@ def test_paged_decode_attention_vs_fp32(hd, max_pages, pos):
     assert max_rel_err(out.cpu(), ref) <= 1e-2
 
 
-def test_paged_decode_attention_masks_entries_outside_the_cache():
+@pytest.mark.parametrize("hd", [64, 128])
+def test_paged_decode_attention_masks_entries_outside_the_cache(hd):
     """Table entries outside [0, pages) (-1, pages, a large id) are never read
     through: their positions drop out of the softmax, and a sequence with no
-    position left gets zeros."""
+    position left gets zeros (head_dim 64: the VALU kernel; 128: the
+    matrix-core kernel)."""
     g = torch.Generator().manual_seed(3)
-    hd, nh, max_pages = 64, 4, 140
+    nh, max_pages = 4, 140
     pos = [2239, 2239, 300, 40]
     B = len(pos)
     num_pages = B * max_pages + 1
@@ -126,7 +128,7 @@ def test_paged_decode_attention_masks_entries_outside_the_cache():
         v = cache.v[pg, :, off, :].float()          # (n, heads, hd)
         s = torch.einsum("hd,nhd->hn", q[b].float(), k) * hd ** -0.5
         ref[b] = torch.einsum("hn,nhd->hd", torch.softmax(s, dim=-1), v)
-    print("paged decode_attention masked table entries", flush=True)
+    print(f"paged decode_attention masked table entries hd={hd}", flush=True)
     out = paged_decode_attention(q.to(DEV), cache.k.to(DEV), cache.v.to(DEV), table.to(DEV),
                                  positions.to(DEV), hd ** -0.5).cpu()
     assert torch.isfinite(out.float()).all()
