@@ -734,7 +734,15 @@ static int launch_attn(AttnArgs a, int64_t B, int shared_chunks, hipStream_t st)
     }
   }
   if (shared_chunks < a.nchunk) {
-    if constexpr (PAGED && HD == 128)
+    // The matrix-core kernel holds one workgroup per CU (its load queue fills
+    // the LDS), which pays off when there are whole chunks to stream; a
+    // region of own pages shorter than two chunks (a few positions per
+    // sequence past a shared prompt) runs faster on the VALU kernel, many
+    // workgroups per CU (40B shape, 32 x 64 heads, ~10 positions each: 17.6
+    // against 56.4 us).
+    bool mfma = false;
+    if constexpr (PAGED && HD == 128) mfma = a.nchunk - shared_chunks >= 2;
+    if (mfma)
       launch_mfma<CPOL_NT, 1>(a, shared_chunks, a.nchunk - shared_chunks, 1, st);
     else
       launch_chunks<HD, PAGED, 1>(a, shared_chunks, a.nchunk - shared_chunks, st);
