@@ -150,6 +150,10 @@ SIGNATURES = {
         _c_p, _c_i64, _c_i64,                     # out + strides (b, h)
         _c_i64, _c_i64, _c_i64, _c_i64, _c_f, _c_p,  # B, heads, head_dim, max_pages, scale, stream
     ],
+    "evo2_prefill_attention": [
+        _c_p, _c_p, _c_p, _c_p,                   # q, k, vt, out
+        _c_i64, _c_i64, _c_i64, _c_i64, _c_f, _c_p,  # N, heads, L, head_dim, scale, stream
+    ],
     "evo2_fp8_quantize": [_c_p, _c_i64, _c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_p],
     "evo2_rms_norm": [
         _c_p, _c_i64, _c_p, _c_i64,               # x, sx, residual, sr

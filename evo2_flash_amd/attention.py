@@ -9,9 +9,12 @@ past each sequence's own masked.  Keys and values are each read once (the
 context is split into 2048-position chunks whose partial softmax sums are
 merged by a second launch); the arithmetic is fp32 up to the bf16 output.
 
-Prefill attention (a prompt against itself, causal) is torch: its fused
-attention kernels where the platform has them for the inputs, else a
-chunked product with contiguous operands and an fp32 softmax.
+Prefill attention (a prompt against itself, causal) runs on the HIP kernel
+in csrc/attention_prefill.hip at head_dim 128 (the values transposed once
+per call; fp32 scores and softmax, bf16 softmax weights in the value
+product); other head dims on torch's fused attention kernels where the
+platform has them for the inputs, else a chunked product with contiguous
+operands and an fp32 softmax.
 """
 
 import torch
@@ -203,11 +206,35 @@ def _causal_chunked(q, k, v, scale, chunk=512):
     return out.view(N, nh, L, hd)
 
 
+def prefill_attention(q, k, v, scale):
+    """Causal self-attention of prompts on this build's HIP kernel: q, k, v
+    (N, heads, L, 128) bf16 with L a multiple of 8 -> (N, heads, L, 128)
+    bf16.  The values are handed over transposed (one copy)."""
+    _lib.require_device(q, k, v)
+    N, nh, L, hd = q.shape
+    if k.shape != q.shape or v.shape != q.shape:
+        raise ValueError(f"q, k, v shapes {tuple(q.shape)}, {tuple(k.shape)}, {tuple(v.shape)} differ")
+    if hd != 128 or L % 8:
+        raise ValueError(f"prefill_attention takes head_dim 128 and L a multiple of 8, got {hd}, {L}")
+    if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
+        raise ValueError("prefill_attention takes bf16 q, k, v")
+    q = q.contiguous()
+    k = k.contiguous()
+    vt = v.transpose(-1, -2).contiguous()
+    out = torch.empty_like(q)
+    _lib.call("evo2_prefill_attention", _lib.ptr(q), _lib.ptr(k), _lib.ptr(vt), _lib.ptr(out),
+              N, nh, L, hd, float(scale), _lib.stream_of(q))
+    return out
+
+
 def causal_prefill_attention(q, k, v, scale):
     """Causal self-attention of prompts: q, k, v (N, heads, L, head_dim) bf16
-    -> (N, heads, L, head_dim).  torch's fused kernels (flash or
-    memory-efficient) where they accept the inputs; never its unfused math
-    path, which multiplies by a transposed view."""
+    -> (N, heads, L, head_dim).  head_dim 128 with L a multiple of 8 runs on
+    prefill_attention (this build's kernel); other shapes on torch's fused
+    kernels (flash or memory-efficient) where they accept the inputs, never
+    its unfused math path, which multiplies by a transposed view."""
+    if q.shape[-1] == 128 and q.shape[-2] % 8 == 0 and q.shape[-2] > 0 and q.is_cuda:
+        return prefill_attention(q, k, v, scale)
     global _FUSED_SDPA
     if _FUSED_SDPA is not False:
         from torch.nn.attention import SDPBackend, sdpa_kernel
@@ -224,4 +251,4 @@ def causal_prefill_attention(q, k, v, scale):
 
 
 __all__ = ["decode_attention", "workspace", "paged_decode_attention", "check_block_table",
-           "PagedKVCache", "causal_prefill_attention", "PAGE"]
+           "PagedKVCache", "causal_prefill_attention", "prefill_attention", "PAGE"]

@@ -37,10 +37,7 @@
 // once per pair and from L2 for the rest.  At head_dim 64 declared shared
 // chunks take four sequences per VALU workgroup, each load serving all four
 // (the same bits as one per workgroup).
-#include <type_traits>
-#include <utility>
-
-#include "common.h"
+#include "attn_common.h"
 
 namespace evo2 {
 
@@ -312,42 +309,6 @@ __global__ __launch_bounds__(AT_T) void attn_chunk_kernel(AttnArgs p, int c_firs
 constexpr int AS_NQ = 32;   // sequences per workgroup
 constexpr int AS_BLK = 128; // positions per wave block
 
-typedef __attribute__((ext_vector_type(8))) __bf16 abf16x8_t;
-typedef __attribute__((ext_vector_type(4))) float af32x4_t;
-typedef __attribute__((ext_vector_type(4))) unsigned int au32x4_t;
-typedef __attribute__((address_space(3))) void alds_void;
-
-// f(integral_constant<int, 0>) .. f(integral_constant<int, N - 1>): the
-// index is a constant expression inside f.
-template <typename F, int... I>
-__device__ __forceinline__ void static_for_seq(F &f, std::integer_sequence<int, I...>) {
-  (f(std::integral_constant<int, I>{}), ...);
-}
-template <int N, typename F>
-__device__ __forceinline__ void static_for(F &&f) {
-  static_for_seq(f, std::make_integer_sequence<int, N>{});
-}
-
-// Eight 16-byte LDS reads at byte address a + 1024 j, then a wait for them.
-// Inline assembly: the compiler would otherwise wait for every direct-to-LDS
-// load in flight before any LDS read; the caller waits for the ones it reads.
-__device__ __forceinline__ void lds_read8(au32x4_t (&r)[8], uint32_t a) {
-  asm volatile(
-      "ds_read_b128 %0, %8\n"
-      "ds_read_b128 %1, %8 offset:1024\n"
-      "ds_read_b128 %2, %8 offset:2048\n"
-      "ds_read_b128 %3, %8 offset:3072\n"
-      "ds_read_b128 %4, %8 offset:4096\n"
-      "ds_read_b128 %5, %8 offset:5120\n"
-      "ds_read_b128 %6, %8 offset:6144\n"
-      "ds_read_b128 %7, %8 offset:7168\n"
-      "s_waitcnt lgkmcnt(0)"
-      : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6]),
-        "=&v"(r[7])
-      : "v"(a)
-      : "memory");
-}
-
 // Element t of the eight 16-byte rows r[0..7] (row j holds elements 0..7 in
 // order) as one operand: (r[0][t], .., r[7][t]).
 template <int T>
@@ -477,7 +438,7 @@ __global__ __launch_bounds__(AT_T, 1) void attn_mfma_kernel(AttnArgs p, int c_fi
   // the next group (the reads have returned before it is requested)
   auto take = [&](au32x4_t(&r)[8], auto sl, auto after) __attribute__((always_inline)) {
     vmcnt_wait<8 * decltype(after)::value>();
-    lds_read8(r, static_cast<uint32_t>(reinterpret_cast<uintptr_t>(slot(sl) + 4 * lane)));
+    lds_read8<1024>(r, lds_addr(slot(sl) + 4 * lane));
   };
   using std::integral_constant;
   const int nblk = (l1max - l0 + AS_BLK - 1) / AS_BLK;  // blocks holding positions below l1max

@@ -356,6 +356,22 @@ int evo2_paged_decode_attention(const void *q, int64_t qb, int64_t qh,
                                 float scale, void *stream);
 
 /*
+ * Causal self-attention of prompts, the prefill form of the attention layers:
+ *   out[n, h, i] = sum_{j <= i} softmax_j(scale q[n, h, i] . k[n, h, j]) v[n, h, j]
+ *   q, k, out (N, heads, L, head_dim) bf16, contiguous;
+ *   vt        (N, heads, head_dim, L) bf16, contiguous: the values transposed.
+ * head_dim 128, L a multiple of 8, 16-byte aligned pointers.  Scores, the
+ * softmax and the weighted sum are fp32, the softmax weights enter the value
+ * product as bf16 (flash attention's rounding), the output is bf16.
+ *
+ * Serves the attention layers of Evo2Attention at prefill
+ * (evo2_flash/model.py:104-153; vLLM's flash attention there, outside the
+ * mixer path).
+ */
+int evo2_prefill_attention(const void *q, const void *k, const void *vt, void *out, int64_t N,
+                           int64_t heads, int64_t L, int64_t head_dim, float scale, void *stream);
+
+/*
  * Static per-tensor activation quantisation for the fp8 projections:
  * q = e4m3fn(clamp(x / scale[0], -448, 448)), round to nearest even.
  *   x (rows, K) bf16, row stride sx; q (rows, K) e4m3 bytes, row stride sq.

@@ -9,7 +9,9 @@ benchmark's context; a prompt's pages shared by every sequence, with and
 without the sharing declared (head_dim 64: bitwise the same; 128, the
 matrix-core kernel: within a bf16 rounding step of the undeclared result,
 nearly all elements the same bits), for one partial and two groups of 32
-sequences.
+sequences.  Causal prefill attention (head_dim 128, the matrix-core kernel)
+against fp32 attention on the CPU at several prompt lengths, and with
+peaked scores.
 """
 
 import pytest
@@ -185,3 +187,49 @@ def test_paged_decode_attention_shared_prompt(B, hd):
         assert (plain.view(torch.int16) != shared.view(torch.int16)).float().mean() <= 0.01
     assert max_rel_err(shared, ref) <= 1e-2
     assert max_rel_err(plain, ref) <= 1e-2
+
+
+def _causal_ref(q, k, v, scale):
+    """fp32 causal attention on the CPU: (N, heads, L, hd)."""
+    qf, kf, vf = q.float(), k.float(), v.float()
+    L = q.shape[-2]
+    s = torch.matmul(qf, kf.transpose(-1, -2).contiguous()) * scale
+    s.masked_fill_(torch.ones(L, L, dtype=torch.bool).triu(1), float("-inf"))
+    return torch.matmul(torch.softmax(s, dim=-1), vf)
+
+
+@pytest.mark.parametrize("N,nh,L", [(1, 2, 8), (2, 3, 200), (1, 2, 392), (1, 4, 1024), (1, 2, 4104)])
+def test_prefill_attention_vs_fp32(N, nh, L):
+    """Causal prefill attention on the matrix-core kernel against fp32
+    attention on the CPU: one partial 128-query block, several, prompts
+    ending inside a key block, and a prompt past 4096 (the last query block
+    partly outside it).  Bar 1e-2 (bf16 output and bf16 softmax weights)."""
+    from evo2_flash_amd.attention import prefill_attention
+    g = torch.Generator().manual_seed(L + nh)
+    hd = 128
+    q = torch.randn(N, nh, L, hd, generator=g).to(bf)
+    k = torch.randn(N, nh, L, hd, generator=g).to(bf)
+    v = torch.randn(N, nh, L, hd, generator=g).to(bf)
+    ref = _causal_ref(q, k, v, hd ** -0.5)
+    print(f"prefill_attention N={N} heads={nh} L={L}", flush=True)
+    out = prefill_attention(q.to(DEV), k.to(DEV), v.to(DEV), hd ** -0.5).cpu()
+    assert out.shape == q.shape and out.dtype == bf
+    assert torch.isfinite(out.float()).all()
+    assert max_rel_err(out, ref) <= 1e-2
+
+
+def test_prefill_attention_peaked_scores():
+    """Large scores (a softmax close to one-hot, and rows whose running max
+    jumps late in the sweep): the online rescaling keeps the sums exact
+    enough."""
+    from evo2_flash_amd.attention import prefill_attention
+    g = torch.Generator().manual_seed(5)
+    N, nh, L, hd = 1, 2, 640, 128
+    q = (torch.randn(N, nh, L, hd, generator=g) * 4).to(bf)
+    k = (torch.randn(N, nh, L, hd, generator=g) * 4).to(bf)
+    k[:, :, 600] *= 3                  # a late key that dominates the rows after it
+    v = torch.randn(N, nh, L, hd, generator=g).to(bf)
+    ref = _causal_ref(q, k, v, hd ** -0.5)
+    print("prefill_attention peaked scores", flush=True)
+    out = prefill_attention(q.to(DEV), k.to(DEV), v.to(DEV), hd ** -0.5).cpu()
+    assert max_rel_err(out, ref) <= 1e-2
