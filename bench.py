@@ -15,8 +15,13 @@ Also measured in the same run and reported in the same JSON line:
     (M=64) against HBM;
   * verify: the inner operators of a speculative verify step (64 requests
     of 4 tokens, a state snapshot per token) against HBM;
-  * model_decode: the whole 7B-shaped model at decode (the mixers in their
-    decoder layers, attention and MLPs in torch), end-to-end tokens/s;
+  * model_decode: the whole 7B-shaped model at decode (the mixers and the
+    paged decode attention on this build's kernels, projections and MLPs in
+    torch), end-to-end tokens/s; model_prefill and model_40b the same
+    harness at prefill and at the 40B shape;
+  * attn_prefill: the harness's causal prefill attention kernel at the 7B
+    prompt (and the 40B one with --only attn_prefill), with torch's fused
+    attention on the same inputs as a reference;
   * config0_prefill: one mixer core of each kind at H=1920 over one fresh
     2048-token sequence, tokens/s per block on the GPU and for the oracle's
     restatement of the reference torch path on the host cores;
@@ -26,7 +31,8 @@ Also measured in the same run and reported in the same JSON line:
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--no-prefill] [--no-gemm]
                     [--no-verify] [--no-model] [--no-model40b] [--model-steps N]
-                    [--only decode|verify|prefill|gemm|copy|model|config0|model_prefill|model40b]
+                    [--only decode|verify|prefill|gemm|copy|model|config0|model_prefill|model40b|
+                            attn_prefill]
 """
 
 import argparse
@@ -364,7 +370,47 @@ def bench_model_prefill(dev, L=L_PREFILL, reps=3, seed=31):
             "layer_us": {k: round(v, 1) for k, v in per.items()},
             "instrumented_ms": round(t_inst * 1e3, 2),
             "note": "whole 7B-shaped model, batch 1; Hyena layers = in_proj + mixer core + "
-                    "out_proj on this build's kernels; attention, MLP and norms' GEMMs in torch"}
+                    "out_proj and the causal attention on this build's kernels; attention "
+                    "projections, MLP and norms' GEMMs in torch"}
+
+
+def bench_attn_prefill(dev, shapes=((32, L_PREFILL),), reps=3, seed=51):
+    """The harness's causal prefill attention (head_dim 128, one sequence) on
+    this build's kernel, and torch's fused attention on the same inputs as a
+    reference (not on any product path): ms per call and TFLOP/s of the
+    causal half (4 L^2 d heads / 2)."""
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    from evo2_flash_amd.attention import prefill_attention
+
+    out = {}
+    for heads, L in shapes:
+        g = torch.Generator(device=dev).manual_seed(seed)
+        q, k, v = (torch.randn(1, heads, L, 128, generator=g, device=dev).to(torch.bfloat16)
+                   for _ in range(3))
+        scale = 128 ** -0.5
+        flop = 4 * heads * L * L * 128 / 2
+
+        def ref():
+            with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+                return torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=True,
+                                                                        scale=scale)
+        r = {}
+        for name, fn in (("kernel", lambda: prefill_attention(q, k, v, scale)), ("torch", ref)):
+            try:
+                fn()
+                times = [_sync_time(fn)[1] for _ in range(reps)]
+                t = statistics.median(times)
+                r[name + "_ms"] = round(t * 1e3, 3)
+                r[name + "_TFLOPs"] = round(flop / t / 1e12, 1)
+            except RuntimeError as e:  # torch's fused kernels may refuse the inputs
+                r[name + "_error"] = str(e).splitlines()[0][:120]
+        out[f"{heads}x{L}"] = r
+        del q, k, v
+        torch.cuda.empty_cache()
+    out["note"] = ("kernel: csrc/attention_prefill.hip (values transposed once per call, "
+                   "included); torch: scaled_dot_product_attention's fused kernels")
+    return out
 
 
 def bench_model40b(steps, dev, B=32, L=131072, seed=41):
@@ -953,7 +999,7 @@ def main(argv=None):
                     help="decode steps of the 7B whole-model leg (the workload's 512 by default; "
                          "fewer for profiling)")
     ap.add_argument("--only", choices=["decode", "verify", "prefill", "gemm", "copy", "model",
-                                       "config0", "model_prefill", "model40b"],
+                                       "config0", "model_prefill", "model40b", "attn_prefill"],
                     default=None,
                     help="run one leg only (for profiling); `copy` runs a plain 1 GiB "
                          "device copy, the reference dispatch for scaling HBM counters")
@@ -980,6 +1026,10 @@ def main(argv=None):
            if run("config0", False) else None)
     mod = _guarded(bench_model, args.model_steps, dev) if run("model", args.no_model) else None
     mpre = _guarded(bench_model_prefill, dev) if run("model_prefill", args.no_model) else None
+    # the 40B shape (64 heads, 131072 positions: ~0.8 s of torch's kernel) only when asked
+    apre = (_guarded(bench_attn_prefill, dev, **({"shapes": ((32, L_PREFILL), (64, 131072))}
+                                               if args.only == "attn_prefill" else {}))
+            if run("attn_prefill", args.no_model) else None)
     m40 = (_guarded(bench_model40b, STEPS_40B, dev) if run("model40b", args.no_model or args.no_model40b)
            else None)
     if mod and "error" not in mod:
@@ -1033,6 +1083,8 @@ def main(argv=None):
             mpre["mixer_core_us"] = pre["us_per_step"]
             mpre["mixer_core_share"] = round(pre["us_per_step"] / (mpre["ms"] * 1e3), 4)
         line["model_prefill"] = mpre
+    if apre:
+        line["attn_prefill"] = apre
     if m40:
         line["model_40b"] = m40
     if cf0:
