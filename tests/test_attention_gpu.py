@@ -198,12 +198,15 @@ def _causal_ref(q, k, v, scale):
     return torch.matmul(torch.softmax(s, dim=-1), vf)
 
 
-@pytest.mark.parametrize("N,nh,L", [(1, 2, 8), (2, 3, 200), (1, 2, 392), (1, 4, 1024), (1, 2, 4104)])
+@pytest.mark.parametrize("N,nh,L", [(1, 2, 8), (2, 3, 200), (1, 2, 392), (1, 4, 1024), (1, 2, 4104),
+                                    (1, 8, 1032), (2, 16, 520)])
 def test_prefill_attention_vs_fp32(N, nh, L):
     """Causal prefill attention on the matrix-core kernel against fp32
-    attention on the CPU: one partial 128-query block, several, prompts
-    ending inside a key block, and a prompt past 4096 (the last query block
-    partly outside it).  Bar 1e-2 (bf16 output and bf16 softmax weights)."""
+    attention on the CPU: one partial 256-query block, several, prompts
+    ending inside a key block, a prompt past 4096 (the last query block
+    partly outside it), and head counts that split over the eight XCDs (the
+    head-per-XCD grid), with two sequences.  Bar 1e-2 (bf16 output and bf16
+    softmax weights)."""
     from evo2_flash_amd.attention import prefill_attention
     g = torch.Generator().manual_seed(L + nh)
     hd = 128
