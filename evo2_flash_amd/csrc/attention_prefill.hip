@@ -98,8 +98,9 @@ __global__ __launch_bounds__(AP_NW * 64, 1) void attn_prefill_kernel(PrefillArgs
   for (int jj = 0; jj < 32 / AP_NW; ++jj) {
     const int j = (32 / AP_NW) * wave + jj;
     const int r = 4 * j + (lane >> 4);
-    koff[jj] = static_cast<uint32_t>(r * AP_HD + 8 * ((lane & 15) ^ ((r >> 2) & 15))) * 2;
-    voff[jj] = static_cast<uint32_t>(r * L + 8 * ((lane & 15) ^ ((r >> 3) & 15))) * 2;
+    // byte offsets below 256 L < 2^32 (checked on the host), in 32 bits unsigned
+    koff[jj] = (static_cast<uint32_t>(r) * AP_HD + 8u * ((lane & 15) ^ ((r >> 2) & 15))) * 2u;
+    voff[jj] = (static_cast<uint32_t>(r) * static_cast<uint32_t>(L) + 8u * ((lane & 15) ^ ((r >> 3) & 15))) * 2u;
   }
   auto issue = [&](int b) __attribute__((always_inline)) {
     const int kb0 = b * AP_KB;
@@ -108,8 +109,10 @@ __global__ __launch_bounds__(AP_NW * 64, 1) void attn_prefill_kernel(PrefillArgs
 #pragma unroll
     for (int jj = 0; jj < 32 / AP_NW; ++jj) {
       const int j = (32 / AP_NW) * wave + jj;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (alds_void *)(kd + 512 * j), 16, koff[jj], kb0 * AP_HD * 2, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (alds_void *)(vd + 512 * j), 16, voff[jj], kb0 * 2, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (alds_void *)(kd + 512 * j), 16, koff[jj],
+                                               static_cast<int>(static_cast<uint32_t>(kb0) * (AP_HD * 2u)), 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (alds_void *)(vd + 512 * j), 16, voff[jj],
+                                               static_cast<int>(static_cast<uint32_t>(kb0) * 2u), 0, 0);
     }
   };
 
@@ -282,7 +285,7 @@ extern "C" int evo2_prefill_attention(const void *q, const void *k, const void *
                                       int64_t heads, int64_t L, int64_t head_dim, float scale,
                                       void *stream) {
   // a (sequence, head) plane of 256 L bytes is addressed by 32-bit buffer offsets
-  if (N < 0 || heads <= 0 || L < 0 || N > 65535 || heads > 65535 || L > (int64_t(1) << 24))
+  if (N < 0 || heads <= 0 || L < 0 || N > 65535 || heads > 65535 || L * 256 > int64_t(0xffffffff))
     return fail(EVO2_ERR_INVALID, "prefill_attention: bad sizes N=%lld heads=%lld L=%lld", (long long)N,
                 (long long)heads, (long long)L);
   if (head_dim != AP_HD)

@@ -360,7 +360,8 @@ int evo2_paged_decode_attention(const void *q, int64_t qb, int64_t qh,
  *   out[n, h, i] = sum_{j <= i} softmax_j(scale q[n, h, i] . k[n, h, j]) v[n, h, j]
  *   q, k, out (N, heads, L, head_dim) bf16, contiguous;
  *   vt        (N, heads, head_dim, L) bf16, contiguous: the values transposed.
- * head_dim 128, L a multiple of 8, 16-byte aligned pointers.  Scores, the
+ * head_dim 128, L a multiple of 8 with 256 L < 2^32, 16-byte aligned
+ * pointers, scale > 0.  Scores, the
  * softmax and the weighted sum are fp32, the softmax weights enter the value
  * product as bf16 (flash attention's rounding), the output is bf16.
  *

@@ -97,6 +97,17 @@ def test_validation_before_launch():
     rc = lib.evo2_hyena_hcl_prefill(n, 0, n, n, 0, 0, 0, n, 0, 0, n, 0, 0, n, 0, 0, 0, n, n, 1, n,
                                     0, n, 1, n, 40, n, 0, n, 0, 10, 4096, 2, n)
     assert rc == EVO2_ERR_INVALID and b"block_t" in lib.evo2_last_error()
+    # prefill attention: a (sequence, head) plane of 256 L bytes must fit 32-bit offsets,
+    # head_dim 128 only, L a multiple of 8, a positive scale
+    rc = lib.evo2_prefill_attention(n, n, n, n, 1, 32, 1 << 24, 128, 0.088, n)
+    assert rc == EVO2_ERR_INVALID and b"bad sizes" in lib.evo2_last_error()
+    rc = lib.evo2_prefill_attention(n, n, n, n, 1, 32, 4096, 64, 0.125, n)
+    assert rc == EVO2_ERR_UNSUPPORTED and b"128 only" in lib.evo2_last_error()
+    rc = lib.evo2_prefill_attention(n, n, n, n, 1, 32, 4096, 128, -1.0, n)
+    assert rc == EVO2_ERR_INVALID and b"positive" in lib.evo2_last_error()
+    rc = lib.evo2_prefill_attention(n, n, n, n, 1, 32, 4100, 128, 0.088, n)
+    assert rc == EVO2_ERR_INVALID  # null pointers, checked before L % 8
+    assert lib.evo2_prefill_attention(n, n, n, n, 0, 32, 4096, 128, 0.088, n) == EVO2_OK
 
 
 def test_wrappers_refuse_cpu_tensors():
