@@ -627,9 +627,13 @@ __global__ __launch_bounds__(HD) void attn_merge_kernel(AttnArgs p) {
   const int n = valid_len(p, b);
   const int nc = (n + AT_CHUNK - 1) / AT_CHUNK;
   const float *part = p.part + ((int64_t)b * p.heads + h) * p.nchunk * (HD + 2);
+  // unrolled so that several chunks' loads are in flight (the sums stay in
+  // chunk order)
   float M = -INFINITY;
+#pragma unroll 8
   for (int c = 0; c < nc; ++c) M = fmaxf(M, part[c * (HD + 2) + HD]);
   float tot = 0.0f, o = 0.0f;
+#pragma unroll 8
   for (int c = 0; c < nc; ++c) {
     const float mc = part[c * (HD + 2) + HD];
     const float f = mc == -INFINITY ? 0.0f : expf(mc - M);  // a chunk of masked pages
