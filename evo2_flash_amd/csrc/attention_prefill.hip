@@ -8,27 +8,30 @@
 // registers.
 //
 // A workgroup takes 256 queries of one (sequence, head): eight waves of 32
-// (two 16-query tiles; the workgroups of one XCD take whole heads when the
-// heads split evenly over the eight), and sweeps the key blocks of 128 keys at or before its
-// last query; each block's keys (128 x 256 B) and values (128 dims x 256 B)
-// come through LDS by direct-to-LDS loads, double-buffered, one barrier per
-// block.  Per wave and block, on v_mfma_f32_16x16x32_bf16:
-//  * scores S^T = K Q^T: eight 16-key tiles, tile t row m = key 8 m + t of the
-//    block; lane (m, g) reads 16 bytes of key 8 m + t (dims 32 kk + 8 g ..
+// (two 16-query tiles, two waves a SIMD; the workgroups of one XCD take whole
+// heads when the heads split evenly over the eight), and sweeps the key
+// blocks of 128 keys at or before its last query; each block's keys (128 x
+// 256 B) and values (128 dims x 256 B) come through LDS by direct-to-LDS
+// loads, double-buffered, one barrier per block.  A wave takes a block in two
+// halves of 64 keys, on v_mfma_f32_16x16x32_bf16:
+//  * scores S^T = K Q^T: four 16-key tiles, tile t row m = key 4 m + t of
+//    the half; lane (m, g) reads 16 bytes of that key (dims 32 kk + 8 g ..
 //    + 7), Q's B operand the same dims of its query.  Lane (n, g) then holds
-//    the scores of keys 32 g .. 32 g + 31 for queries n and 16 + n;
+//    the scores of keys 16 g .. 16 g + 15 of the half for queries n and
+//    16 + n;
 //  * o^T += V^T P^T: dim tile e row m = dim 8 m + e; lane (m, g) reads 16
-//    bytes of value row 8 m + e (keys 32 g + 8 kp .. + 7); the B operand is
-//    the lane's own probabilities of those keys as bf16.
+//    bytes of value row 8 m + e (keys 16 g + 8 kp .. + 7 of the half); the B
+//    operand is the lane's own probabilities of those keys as bf16.
 // Online softmax in fp32 with exp2 of scores kept in log2 units; a row's
-// reference max moves (and its sums are rescaled) only when a block's max
-// exceeds it by more than AP_SLACK, so the probabilities stay below 2^AP_SLACK
-// and most blocks rescale nothing.  The probabilities enter the value
-// product rounded to bf16, as in flash attention, and the row sums are the
-// same bf16 probabilities summed by one more product (an all-ones operand),
-// so numerator and denominator use the same values.  LDS rows are 256 bytes; 16-byte chunk c of row r sits at
-// c ^ ((r >> 3) & 15), which puts the 16 rows a read serves on distinct bank
-// groups.
+// reference max moves (and its sums are rescaled) only when a half's max
+// exceeds it by more than AP_SLACK, so the probabilities stay below
+// 2^AP_SLACK and most halves rescale nothing.  The probabilities enter the
+// value product rounded to bf16, as in flash attention, and the row sums are
+// the same bf16 probabilities summed by one more product (an all-ones
+// operand), so numerator and denominator use the same values.  LDS rows are
+// 256 bytes; 16-byte chunk c of key row r sits at c ^ ((r >> 2) & 15), of
+// value row r at c ^ ((r >> 3) & 15), which puts the 16 rows a read serves
+// on distinct bank groups.
 #include "attn_common.h"
 
 namespace evo2 {
@@ -85,14 +88,16 @@ __global__ __launch_bounds__(AP_NW * 64, 1) void attn_prefill_kernel(PrefillArgs
   // of 1 KB each; wave w issues loads 4 w .. 4 w + 3 of both.  Lane i of
   // load j fills LDS row r = 4 j + i / 16, position i % 16, which holds chunk
   // (i % 16) ^ ((r >> 2) & 15) of key row kb0 + r (keys) or chunk
-  // (i % 16) ^ ((r >> 3) & 15), keys kb0 + 8 c .., of dim row r (values).  Buffer loads over the (sequence, head)
-  // plane: a lane's offset within the block is fixed, the block's in an
-  // SGPR; key rows past the prompt read zeros (past the plane), value chunks
-  // past it the next row's first keys or zeros, finite values whose
-  // probabilities are 0.
+  // (i % 16) ^ ((r >> 3) & 15), keys kb0 + 8 c .., of dim row r (values).
+  // Buffer loads over the (sequence, head) plane: a lane's offset within the
+  // block is fixed, the block's in an SGPR; key rows past the prompt read
+  // zeros (past the plane), value chunks past it the next row's first keys
+  // or zeros, finite values whose probabilities are 0.
   const uint32_t pbytes = static_cast<uint32_t>(p.plane * 2);
-  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16_t *>(k), 0, pbytes, 0x00020000);
-  const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16_t *>(vt), 0, pbytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t krs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16_t *>(k), 0, pbytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t vrs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16_t *>(vt), 0, pbytes, 0x00020000);
   uint32_t koff[32 / AP_NW], voff[32 / AP_NW];
 #pragma unroll
   for (int jj = 0; jj < 32 / AP_NW; ++jj) {
@@ -100,7 +105,8 @@ __global__ __launch_bounds__(AP_NW * 64, 1) void attn_prefill_kernel(PrefillArgs
     const int r = 4 * j + (lane >> 4);
     // byte offsets below 256 L < 2^32 (checked on the host), in 32 bits unsigned
     koff[jj] = (static_cast<uint32_t>(r) * AP_HD + 8u * ((lane & 15) ^ ((r >> 2) & 15))) * 2u;
-    voff[jj] = (static_cast<uint32_t>(r) * static_cast<uint32_t>(L) + 8u * ((lane & 15) ^ ((r >> 3) & 15))) * 2u;
+    voff[jj] =
+        (static_cast<uint32_t>(r) * static_cast<uint32_t>(L) + 8u * ((lane & 15) ^ ((r >> 3) & 15))) * 2u;
   }
   auto issue = [&](int b) __attribute__((always_inline)) {
     const int kb0 = b * AP_KB;
