@@ -405,22 +405,17 @@ __global__ __launch_bounds__(256) void fp8_gemm_persist_kernel(GemmArgs p, int t
     }
   };
 
+  // The accumulators of a tile start at its first MFMAs, which take C = 0
+  // (no clearing between tiles), so they are not live across tiles.
   f32x16 acc[4][4];
-  auto zero_acc = [&]() __attribute__((always_inline)) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
-  };
-  auto mma = [&](const i32x8 fa[4], const i32x8 fb[4]) __attribute__((always_inline)) {
+  const f32x16 zero16 = {};
+  auto mma = [&](const i32x8 fa[4], const i32x8 fb[4], auto first) __attribute__((always_inline)) {
 #pragma unroll
     for (int tn = 0; tn < 4; ++tn)
 #pragma unroll
       for (int tm = 0; tm < 4; ++tm)
-        acc[tn][tm] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa[tn], fb[tm], acc[tn][tm],
-                                                                       0, 0, 0, 0, 0, 0);
+        acc[tn][tm] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+            fa[tn], fb[tm], decltype(first)::value ? zero16 : acc[tn][tm], 0, 0, 0, 0, 0, 0);
   };
   const float scale = p.sx_scale[0] * p.sw_scale[0];
   // Wave 0 loads the bias of tile j into the buffer of its parity.
@@ -512,17 +507,20 @@ __global__ __launch_bounds__(256) void fp8_gemm_persist_kernel(GemmArgs p, int t
   using std::integral_constant;
   using I0 = integral_constant<int, 0>;
   using I1 = integral_constant<int, 1>;
-  auto step = [&](auto stage, int k, bool after_epilogue) __attribute__((always_inline)) {
+  using F0 = integral_constant<bool, false>;
+  using F1 = integral_constant<bool, true>;
+  // first: slice 0 of a tile, whose sub-step 0 starts the accumulators
+  auto step = [&](auto stage, int k, bool after_epilogue, auto first) __attribute__((always_inline)) {
     constexpr int S = decltype(stage)::value;
     read_frags(stage, I1{}, fa[1], fb[1]);
-    mma(fa[0], fb[0]);
+    mma(fa[0], fb[0], first);
     interleave(false);
     if (after_epilogue) vmcnt_wait<EPI_STORES>();
     else vmcnt_wait<0>();
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     issue(stage, k + 2);
     read_frags(integral_constant<int, S ^ 1>{}, I0{}, fa[0], fb[0]);
-    mma(fa[1], fb[1]);
+    mma(fa[1], fb[1], F0{});
     interleave(true);
   };
 
@@ -535,21 +533,23 @@ __global__ __launch_bounds__(256) void fp8_gemm_persist_kernel(GemmArgs p, int t
   vmcnt_wait<2 * DB>();  // slice 0 (slice 1 in flight; the bias before them)
   __builtin_amdgcn_s_barrier();
   read_frags(I0{}, I0{}, fa[0], fb[0]);
-  zero_acc();
   int s = 0;
   // Tile j of parity P: first the bias of tile j + 1 into the other buffer
   // (its previous contents, tile j - 1's, were added before this tile
   // began), then the slices in pairs (KT is even, so every tile starts in
-  // stage 0), then the epilogue with this buffer.
+  // stage 0; the first pair starts the accumulators), then the epilogue
+  // with this buffer.
   auto tile = [&](auto par, int j) __attribute__((always_inline)) {
     constexpr int P = decltype(par)::value;
     if (j + 1 < ntile) load_bias(integral_constant<int, P ^ 1>{}, j + 1);
-    for (int k = 0; k < KT; k += 2, s += 2) {
-      step(I0{}, s, k == 0 && j > 0);
-      step(I1{}, s + 1, false);
+    step(I0{}, s, j > 0, F1{});
+    step(I1{}, s + 1, false, F0{});
+    s += 2;
+    for (int k = 2; k < KT; k += 2, s += 2) {
+      step(I0{}, s, false, F0{});
+      step(I1{}, s + 1, false, F0{});
     }
     epilogue(par, j);
-    zero_acc();
   };
   for (int j = 0; j < ntile; j += 2) {
     tile(P0{}, j);
