@@ -83,8 +83,11 @@ def test_gemm_known_answer(M, N, K):
 # order); (2048, 12288) has 8 x 48 = 384 tiles, twelve blocks of 4 x 8, so
 # the XCD-block order's second round is half full and its last four blocks
 # go out tile by tile; (3328, 5120) has 13 x 20 = 260 tiles over 256
-# workgroups (row-major order, four workgroups take a second tile).
-@pytest.mark.parametrize("M,N,K", [(2048, 8192, 512), (2048, 12288, 512), (3328, 5120, 768)])
+# workgroups (row-major order, four workgroups take a second tile);
+# (2048, 12288, 256) has tiles of one slice pair, the one that starts the
+# accumulators.
+@pytest.mark.parametrize("M,N,K", [(2048, 8192, 512), (2048, 12288, 512), (3328, 5120, 768),
+                                   (2048, 12288, 256)])
 def test_gemm_known_answer_persistent(M, N, K):
     g = torch.Generator().manual_seed(M + N + K)
     x8 = _small_int_e4m3((M, K), g)
