@@ -146,6 +146,9 @@ __global__ __launch_bounds__(StripeGeo<CHW>::NT, 1) void stripe_kernel(StripeArg
   __shared__ __align__(16) bf16_t xbuf[CH * XP];
   __shared__ __align__(16) bf16_t gbuf[G::NGB * G::BATCH * CH];
   __shared__ float sfin[HCL ? CH * 16 : 1];                  // hcl: state before the last chunk
+  // hcl: per channel the scan's multipliers p^16, p^32, p^64, p^128 of the 16
+  // poles, [channel][j][pole] for p^(16 2^j)
+  __shared__ __align__(16) float pmul[HCL ? CH * 4 * 16 : 1];
 
   // ---- workgroup -> (tile, CH-channel group)
   const int L = blockIdx.x;
@@ -302,6 +305,13 @@ __global__ __launch_bounds__(StripeGeo<CHW>::NT, 1) void stripe_kernel(StripeArg
       float acc = 0.f;  // sum over poles in order (triton_hcl.py:77-85)
       for (int q = 0; q < 16; ++q) acc = fmaf(R[ch * 16 + q], E[(ch * 16 + q) * ETAB + m], acc);
       Hf[i] = acc;
+      // pole m's scan multipliers, squared in the order the scan applies them
+      float pm = E[(ch * 16 + m) * ETAB + 16];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        pmul[(ch * 4 + j) * 16 + m] = pm;
+        pm *= pm;
+      }
     }
     __syncthreads();
     if (!is_f) {
@@ -420,26 +430,24 @@ __global__ __launch_bounds__(StripeGeo<CHW>::NT, 1) void stripe_kernel(StripeArg
         // the state entering the batch joins chunk 0's end state, then an
         // inclusive scan over the 16 chunks of each pole, X(n) += p^(16 d) X(n - d),
         // leaves the state at the end of every chunk
-        float x[4], mm[4];
+        float x[4];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          mm[k] = P16[cc][k];
-          x[k] = fmaf(l16 == 0 ? mm[k] : 0.f, carry[cc][k], X[k]);
-        }
+        for (int k = 0; k < 4; ++k) x[k] = fmaf(l16 == 0 ? P16[cc][k] : 0.f, carry[cc][k], X[k]);
 #pragma unroll
-        for (int k = 0; k < 4; ++k) x[k] = fmaf(mm[k], row_shr<1>(x[k]), x[k]);
+        for (int k = 0; k < 4; ++k) x[k] = fmaf(P16[cc][k], row_shr<1>(x[k]), x[k]);
+        // p^32, p^64, p^128 of this lane's poles 4 g .. 4 g + 3 from the table
+        const float *pmc = pmul + (4 * mw + cc) * 64 + 4 * g;
+        const float4 m2 = *reinterpret_cast<const float4 *>(pmc + 16);
+        const float4 m4 = *reinterpret_cast<const float4 *>(pmc + 32);
+        const float4 m8 = *reinterpret_cast<const float4 *>(pmc + 48);
+        const float mm2[4] = {m2.x, m2.y, m2.z, m2.w}, mm4[4] = {m4.x, m4.y, m4.z, m4.w};
+        const float mm8[4] = {m8.x, m8.y, m8.z, m8.w};
 #pragma unroll
-        for (int k = 0; k < 4; ++k) mm[k] *= mm[k];
+        for (int k = 0; k < 4; ++k) x[k] = fmaf(mm2[k], row_shr<2>(x[k]), x[k]);
 #pragma unroll
-        for (int k = 0; k < 4; ++k) x[k] = fmaf(mm[k], row_shr<2>(x[k]), x[k]);
+        for (int k = 0; k < 4; ++k) x[k] = fmaf(mm4[k], row_shr<4>(x[k]), x[k]);
 #pragma unroll
-        for (int k = 0; k < 4; ++k) mm[k] *= mm[k];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) x[k] = fmaf(mm[k], row_shr<4>(x[k]), x[k]);
-#pragma unroll
-        for (int k = 0; k < 4; ++k) mm[k] *= mm[k];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) x[k] = fmaf(mm[k], row_shr<8>(x[k]), x[k]);
+        for (int k = 0; k < 4; ++k) x[k] = fmaf(mm8[k], row_shr<8>(x[k]), x[k]);
         // the state before chunk n (chunk 0: the entering state), and the
         // state leaving the batch
         float sp[4];
@@ -455,12 +463,15 @@ __global__ __launch_bounds__(StripeGeo<CHW>::NT, 1) void stripe_kernel(StripeArg
           for (int k = 0; k < 4; ++k) sfin[ch * 16 + 4 * g + k] = sp[k];
         }
         // B operand: K index 8 g + 2 k + h = (pole 4 g + k, high / low part)
-        sbf16x8_t Bs;
+        // (hi = bf16(s) is exact in fp32, so packing (hi, s - hi) rounds only the
+        // low part: the bits of bf_hi and bf_lo)
+        si32x4_t bsw;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-          Bs[2 * k] = bf_hi(sp[k]);
-          Bs[2 * k + 1] = bf_lo(sp[k]);
+          const float hi = rbf_valu(sp[k]);  // sp: a DPP move, an ordinary VALU result
+          bsw[k] = static_cast<int>(pack_bf(hi, sp[k] - hi));
         }
+        const sbf16x8_t Bs = __builtin_bit_cast(sbf16x8_t, bsw);
         Y = __builtin_amdgcn_mfma_f32_16x16x32_bf16(AC[cc], Bs, Y, 0, 0, 0);
         Y = __builtin_amdgcn_mfma_f32_16x16x32_bf16(AC2[cc], Bs, Y, 0, 0, 0);
       } else {
@@ -483,7 +494,7 @@ __global__ __launch_bounds__(StripeGeo<CHW>::NT, 1) void stripe_kernel(StripeArg
         const uint2 u4 = *reinterpret_cast<const uint2 *>(up);
         const float uu[4] = {lo_bf(u4.x), hi_bf(u4.x), lo_bf(u4.y), hi_bf(u4.y)};
 #pragma unroll
-        for (int k = 0; k < 4; ++k) gv[k] = xx[k] * rbf(rbf(Y[k]) + rbf(dv[cc] * uu[k]));
+        for (int k = 0; k < 4; ++k) gv[k] = xx[k] * rbf_valu(rbf(Y[k]) + rbf_valu(dv[cc] * uu[k]));
       } else {
 #pragma unroll
         for (int k = 0; k < 4; ++k) gv[k] = xx[k] * rbf(Y[k]);
